@@ -1,0 +1,399 @@
+/*
+ * oasis_hip.h -- C ABI of liboasis_hip.so, the MI355X (gfx950) implementation of the
+ * Oasis-500M DiT denoising step and ViT VAE decoder.
+ *
+ * Conventions (all entry points):
+ *   - Plain device pointers, caller-owned, row-major and contiguous unless a leading
+ *     dimension ("ld") is given. Nothing here allocates device memory; everything is
+ *     stream-ordered on the given HIP stream (hipStream_t passed as void*, NULL = the
+ *     default stream) and may be captured into a hipGraph.
+ *   - Return OASIS_OK (0) or a negative OASIS_ERR_* code; oasis_last_error() returns
+ *     the message of the last failure on the calling thread.
+ *   - dtype codes: OASIS_F32 (fp32) and OASIS_BF16 (bfloat16).
+ *
+ * Reference citations are paths into zoecarver/open-oasis.
+ */
+#ifndef OASIS_HIP_H
+#define OASIS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OASIS_ABI_VERSION 1
+#define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
+
+enum {
+  OASIS_OK = 0,
+  OASIS_ERR_NULL = -1,   /* a required pointer is NULL */
+  OASIS_ERR_SHAPE = -2,  /* unsupported or inconsistent shape */
+  OASIS_ERR_DTYPE = -3,  /* unsupported dtype code */
+  OASIS_ERR_LAUNCH = -4, /* HIP reported an error */
+  OASIS_ERR_ARG = -5     /* other invalid argument */
+};
+
+enum { OASIS_F32 = 0, OASIS_BF16 = 1 };
+
+typedef void* oasis_stream_t;
+
+const char* oasis_last_error(void);
+int oasis_abi_version(void);
+
+/* ======================================================================
+ * Reference kernel surface (destination passing: inputs first, outputs last).
+ * Elementwise kernels take flat tensors of n elements, all of one dtype.
+ * ==================================================================== */
+
+/* out = x * sigmoid(x).  Replaces silu_kernel(x, out)  (src/silu.py:8-9). */
+int oasis_silu(const void* x, void* out, int64_t n, int dtype, oasis_stream_t stream);
+
+/* out = x * (scale + 1) + shift.
+ * Replaces adaln_modulate_kernel(x, shift, scale, out)  (src/adaln_modulate.py:8-9). */
+int oasis_adaln_modulate(const void* x, const void* shift, const void* scale, void* out,
+                         int64_t n, int dtype, oasis_stream_t stream);
+
+/* out = residual + x * gate.
+ * Replaces gated_residual_kernel(residual, x, gate, out)  (src/gated_residual.py:16-17). */
+int oasis_gated_residual(const void* residual, const void* x, const void* gate, void* out,
+                         int64_t n, int dtype, oasis_stream_t stream);
+
+/* out = residual + (x + bias) * gate.
+ * Replaces bias_gated_residual_kernel(residual, x, bias, gate, out)
+ * (src/gated_residual.py:65-66). */
+int oasis_bias_gated_residual(const void* residual, const void* x, const void* bias,
+                              const void* gate, void* out, int64_t n, int dtype,
+                              oasis_stream_t stream);
+
+/* out = (x - mean) / sqrt(var + eps) * weight + bias over the last dim (cols).
+ * weight/bias are fp32 whatever dtype is; their rows are read at weight + r*wb_ld (wb_ld = 0 for a [cols] vector,
+ * cols for the reference's row-expanded [rows, cols] tensors).
+ * Replaces make_layernorm_kernel(dim_tiles)(x, weight, ln_bias, scaler, mean_scale, out)
+ * (src/layernorm.py:15-17; instance layernorm_d1024, oasis_inference.py:172).
+ * scaler/mean_scale are Tensix reduction constants and have no counterpart here. */
+int oasis_layernorm(const void* x, const void* weight, const void* bias, int64_t wb_ld,
+                    void* out, int64_t rows, int64_t cols, float eps, int dtype,
+                    oasis_stream_t stream);
+
+/* out[M,N] = x[M,K] @ w.  w_layout 0: w is [K,N] (the reference layout), 1: w is [N,K].
+ * x and w are bf16; out is fp32 or bf16 (out_dtype).
+ * Replaces make_linear_kernel(k_chunk)(x, w, out)  (src/linear.py:10-12; instance
+ * linear_k32, oasis_inference.py:171). */
+int oasis_linear(const void* x, const void* w, void* out, int64_t M, int64_t K, int64_t N,
+                 int w_layout, int out_dtype, oasis_stream_t stream);
+
+/* out[r, :] = silu_cond[0, :] @ w[K,N] + b[N] for r in [0, out_rows) (row expansion).
+ * All fp32 except w (bf16).
+ * Replaces make_adaln_matmul_expand_kernel(k_tiles, n_repeat)(silu_cond, adaln_w,
+ * adaln_b, out)  (src/adaln_matmul_expand.py:13-15). */
+int oasis_adaln_matmul_expand(const float* silu_cond, const void* w, const float* b,
+                              float* out, int64_t K, int64_t N, int64_t out_rows,
+                              oasis_stream_t stream);
+
+/* RoPE on the Q and K columns of qkv plus head split.
+ *   qkv:  [rows, ld_qkv], Q at cols [0,D), K at [D,2D), V at [2D,3D), D = n_heads*64.
+ *         Extra columns (the reference's Q_swap/K_swap) are ignored: the pair swap of
+ *         rotate_half is done in registers.
+ *   cos/sinp: fp32 tables; the value for row r, head h, dim d is at
+ *         tab[pos*tab_ld + h*tab_head_stride + d] with pos = (r / pos_div) % pos_mod.
+ *         sinp carries the rotate_half sign (-sin at even d, +sin at odd d).
+ *   mode 0 (heads-first): out row (f*n_heads + h)*seq + p for r = f*seq + p
+ *         (spatial / VAE layout, make_rope_layout_kernel and make_vae_rope_kernel);
+ *   mode 1 (token-major): out row r, cols h*64..h*64+63 (make_rope_temporal_kernel).
+ *   dtype applies to qkv and the three outputs; head_dim must be 64.
+ * Replaces make_rope_layout_kernel(...)(qkv_full, cos_tab, sin_tab, q_out, k_out, v_out)
+ * (src/rope_layout_kernel.py:16-22), make_rope_temporal_kernel(...)(same)
+ * (src/rope_layout_kernel.py:89-97) and make_vae_rope_kernel(...)(same)
+ * (src/vae_rope.py:8-10). */
+int oasis_rope_layout(const void* qkv, int64_t ld_qkv, const float* cos, const float* sinp,
+                      int64_t tab_ld, int64_t tab_head_stride, int64_t pos_div,
+                      int64_t pos_mod, void* q_out, void* k_out, void* v_out, int64_t rows,
+                      int64_t seq, int64_t n_heads, int64_t head_dim, int mode, int dtype,
+                      oasis_stream_t stream);
+
+/* Multi-head attention with heads stacked along rows:
+ *   Q,out: [n_heads_total*sq, head_dim]; K,V: [n_heads_total*skv, head_dim].
+ *   out = softmax(Q K^T * scale + bias) V per head; bias is an optional fp32
+ *   [sq, skv] additive mask shared by all heads (NULL for none); causal != 0 masks
+ *   keys j > i. dtype applies to Q, K, V and out; head_dim must be 64.
+ * Replaces make_sdpa_kernel(...)(Q_all, K_all, V_all, scaler, attn_scratch, out)
+ * (src/sdpa.py:27-41) and make_sdpa_causal_kernel(...)(Q_all, K_all, V_all, scaler,
+ * bias, attn_scratch, out) (src/sdpa_causal.py:17-23). */
+int oasis_sdpa(const void* Q, const void* K, const void* V, void* out, int64_t n_heads_total,
+               int64_t sq, int64_t skv, int64_t head_dim, float scale, const float* bias,
+               int causal, int dtype, oasis_stream_t stream);
+
+/* ======================================================================
+ * Hot-path building blocks (used by the composite entry points below).
+ * ==================================================================== */
+
+enum {
+  OASIS_EPI_STORE_F32 = 0,    /* out_f32[m, n] = acc + bias                        */
+  OASIS_EPI_STORE_BF16 = 1,   /* out_bf16[m, n] = acc + bias                       */
+  OASIS_EPI_GELU_TANH = 2,    /* out_bf16[m, n] = gelu_tanh(acc + bias)            */
+  OASIS_EPI_GELU_ERF = 3,     /* out_bf16[m, n] = gelu_erf(acc + bias)             */
+  OASIS_EPI_GATED_RES = 4,    /* out_f32[m, n] += gate[f(m), n] * (acc + bias)     */
+  OASIS_EPI_RESIDUAL = 5,     /* out_f32[m, n] += acc + bias                       */
+  OASIS_EPI_QKV_ROPE = 6,     /* RoPE on Q,K + head split into q/k/v (bf16)         */
+  OASIS_EPI_UNPATCHIFY = 7    /* VAE predictor -> clamp(-1,1) CHW frame (fp32)      */
+};
+
+/* Row m is token p of frame f = m / rows_per_frame (p = m % rows_per_frame);
+ * frame f is frame t = f % frames_per_stream of stream b = f / frames_per_stream. */
+typedef struct {
+  int kind;
+  int n_heads;              /* QKV_ROPE: heads (head_dim is 64)                   */
+  const float* bias;        /* [N] fp32 or NULL                                   */
+  float* out_f32;           /* STORE_F32 / GATED_RES / RESIDUAL / UNPATCHIFY      */
+  void* out_bf16;           /* STORE_BF16 / GELU_*                                */
+  int64_t ld_out;           /* leading dimension of out_* (elements)              */
+  const float* gate;        /* GATED_RES: gate row of frame f at gate + f*gate_fstride */
+  int64_t gate_fstride;
+  int64_t rows_per_frame;
+  int64_t frames_per_stream;
+  /* QKV_ROPE: element offset of (b, t, p, h, d) = b*s_b + t*s_t + p*s_p + h*s_h + d
+   * in each of q/k/v; RoPE position = t if rope_by_frame else p; tables [pos][64]. */
+  void* q;
+  void* k;
+  void* v;
+  const float* rope_cos;
+  const float* rope_sinp;
+  int rope_by_frame;
+  int unpatch_grid_w;       /* UNPATCHIFY: patches per row of the latent grid      */
+  int64_t s_b, s_t, s_p, s_h;
+  int unpatch_patch;        /* UNPATCHIFY: patch edge (20)                         */
+  int unpatch_channels;     /* UNPATCHIFY: channels (3)                            */
+} oasis_epilogue_t;
+
+/* acc[M,N] = A[M,K] @ B[N,K]^T (bf16 in, fp32 accumulate) followed by the epilogue.
+ * K % 64 == 0, N % 8 == 0. */
+int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                    int64_t N, int64_t K, const oasis_epilogue_t* epi, oasis_stream_t stream);
+
+/* y_bf16[m, :] = LN(x[m, :]) * scale_p1[f(m), :] + shift[f(m), :], f(m) = m / rows_per_frame,
+ * frame rows of shift/scale_p1 at + f*ada_fstride.  scale_p1 already holds (1 + scale).
+ * LN has no affine, eps as given.  (ttnn.layer_norm + addcmul,
+ * oasis_inference.py:1053-1056,1168-1171.) */
+int oasis_ln_modulate(const float* x, int64_t M, int64_t D, const float* shift,
+                      const float* scale_p1, int64_t ada_fstride, int64_t rows_per_frame,
+                      void* y_bf16, float eps, oasis_stream_t stream);
+
+/* y_bf16 = LN(x) * w + b (affine LayerNorm of the VAE, oasis_inference.py:1559,1592,1611). */
+int oasis_ln_affine(const float* x, int64_t M, int64_t D, const float* w, const float* b,
+                    void* y_bf16, float eps, oasis_stream_t stream);
+
+/* Non-causal multi-head attention, heads-first inputs, token-major output:
+ *   q,k,v: bf16 [n_frames*n_heads, L, 64]; out: bf16 [n_frames*L, n_heads*64].
+ * (spatial SDPA, src/sdpa.py; VAE SDPA, oasis_inference.py:1575-1577.) */
+int oasis_attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames,
+                    int64_t L, int64_t n_heads, float scale, oasis_stream_t stream);
+
+/* Causal attention over the T frames of each (stream, position, head) group:
+ *   q,k,v: bf16 [B, P, n_heads, T, 64]; out: bf16 [B*T*P, n_heads*64] token-major.
+ * (temporal SDPA, src/sdpa_causal.py with the bias of oasis_inference.py:843-857.) */
+int oasis_temporal_attention(const void* q, const void* k, const void* v, void* out,
+                             int64_t B, int64_t T, int64_t P, int64_t n_heads, float scale,
+                             oasis_stream_t stream);
+
+enum { OASIS_ACT_NONE = 0, OASIS_ACT_SILU = 1 };
+
+/* Skinny GEMM for R <= 16 rows: out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]).
+ * x fp32 [R, ldx], W bf16 [N, K] (K % 64 == 0), b fp32 [N] or NULL, out fp32 [R, ld_out].
+ * x is split into bf16 hi + lo parts, so the product keeps ~16 mantissa bits of x.
+ * accumulate != 0 adds into out. (adaLN GEMMs, oasis_inference.py:983-993, and the
+ * conditioning MLP, oasis_inference.py:1406-1427.) */
+int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N,
+                    int64_t K, const float* b, float* out, int64_t ld_out, int act_in,
+                    int act_out, int accumulate, oasis_stream_t stream);
+
+/* out[r, :] = [cos(t_r f), sin(t_r f)], f_i = exp(-ln(10000) i / (dim/2)), dim even.
+ * (timestep_embedding, oasis_inference.py:307-311.) */
+int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, float* out,
+                             oasis_stream_t stream);
+
+/* out[m, n] = b[n] + sum_k x[m, k] W[n, k] in fp32 (W bf16 [N, K], K <= 256), for the
+ * small-K projections: patch embed (K=64, oasis_inference.py:1911) and the VAE
+ * post_quant linear (K=32, oasis_inference.py:1551). */
+int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W,
+                       int64_t N, const float* b, float* out, int64_t ld_out,
+                       oasis_stream_t stream);
+
+/* chunk <- c4*x0 + c5*eps with x0 = c0*chunk - c1*v, eps = (c2*chunk - x0)*c3, n elements.
+ * (DDIM update, oasis_inference.py:1919-1931.) */
+int oasis_ddim_update(float* chunk, const float* v, int64_t n, float c0, float c1, float c2,
+                      float c3, float c4, float c5, oasis_stream_t stream);
+
+/* DiT patch rows [gh*gw, 4*C] (cols (p,q,c)) -> VAE latent [(2gh)*(2gw), out_cols] scaled by
+ * inv_scale, channels in cols [0, C), zeros after.
+ * (bridge_unpatchify, oasis_inference.py:1651-1709.) */
+int oasis_bridge(const float* chunk, float* latent, int64_t gh, int64_t gw, int64_t C,
+                 int64_t out_cols, float inv_scale, oasis_stream_t stream);
+
+/* [gh*gw, 3*ps*ps] patches (cols (c,p,q)) -> clamp([3, gh*ps, gw*ps], -1, 1).
+ * (vae_unpatchify + clamp, oasis_inference.py:1636-1645,2292.) */
+int oasis_vae_unpatchify(const float* patches, float* frame, int64_t gh, int64_t gw,
+                         int64_t ps, oasis_stream_t stream);
+
+/* ======================================================================
+ * Composite entry points: the DiT step, the VAE decoder and the DDIM frame.
+ * ==================================================================== */
+
+/* Device pointers of one DiT (weights bf16 [out, in], biases and tables fp32).
+ * Sub-block j = 2*i + (0 spatial | 1 temporal) of block i.
+ * ada_w/ada_b hold every sub-block's adaLN projection back to back, then the final
+ * layer's: rows [j*6D, (j+1)*6D) for sub-block j, [n_sub*6D, n_sub*6D + 2D) for the
+ * final layer, with +1 folded into the bias of each scale chunk. */
+typedef struct {
+  int n_sub;                 /* 2 * blocks                                         */
+  int d_model;               /* 1024                                               */
+  int n_heads;               /* 16 (head_dim 64)                                   */
+  int d_mlp;                 /* 4096                                               */
+  int grid_h, grid_w;        /* 9 x 16 patches                                     */
+  int patch_dim;             /* 64 = 2*2*16                                        */
+  int freq_dim;              /* 256                                                */
+  int ext_dim_pad;           /* 64 (25 action dims zero-padded)                    */
+  const void* ada_w;         /* [n_sub*6D + 2D, D]                                 */
+  const float* ada_b;
+  const void* qkv_w[OASIS_MAX_SUB];   /* [3D, D], no bias                          */
+  const void* out_w[OASIS_MAX_SUB];   /* [D, D]                                    */
+  const float* out_b[OASIS_MAX_SUB];
+  const void* fc1_w[OASIS_MAX_SUB];   /* [Dm, D]                                   */
+  const float* fc1_b[OASIS_MAX_SUB];
+  const void* fc2_w[OASIS_MAX_SUB];   /* [D, Dm]                                   */
+  const float* fc2_b[OASIS_MAX_SUB];
+  const void* final_w;       /* [64, D]                                            */
+  const float* final_b;
+  const void* xemb_w;        /* [D, 64] patch embed with columns in (p, q, c) order */
+  const float* xemb_b;
+  const void* temb_w0;       /* [D, 256]                                           */
+  const float* temb_b0;
+  const void* temb_w2;       /* [D, D]                                             */
+  const float* temb_b2;
+  const void* ext_w;         /* [D, ext_dim_pad]                                   */
+  const float* ext_b;
+  const float* s_cos;        /* [grid_h*grid_w, 64] spatial RoPE (sin with sign)  */
+  const float* s_sinp;
+  const float* t_cos;        /* [t_max, 64] temporal RoPE                          */
+  const float* t_sinp;
+  int t_max;
+} oasis_dit_weights_t;
+
+/* Activation workspace for up to max_rows = B*T*P tokens (caller-allocated). */
+typedef struct {
+  int64_t max_rows;
+  float* x;        /* [max_rows, D] fp32 residual stream                          */
+  void* h;         /* [max_rows, D] bf16 normalised + modulated                   */
+  void* q;         /* [max_rows, D] bf16 each                                     */
+  void* k;
+  void* v;
+  void* attn;      /* [max_rows, D] bf16                                          */
+  void* mlp;       /* [max_rows, Dm] bf16                                         */
+} oasis_dit_buffers_t;
+
+/* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action), then
+ * ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b for every sub-block and the final layer.
+ *   t: fp32 [R]; action: fp32 [R, ext_dim_pad]; tfreq: fp32 [R, freq_dim] scratch;
+ *   hid: fp32 [R, D] scratch; cond: fp32 [R, D]; ada: fp32 [R, n_sub*6D + 2D].  R <= 16.
+ * (compute_cond_for_frame, oasis_inference.py:1406-1427; build_per_frame_adaln,
+ * oasis_inference.py:971-993; silu_kernel call, oasis_inference.py:1459-1463.) */
+int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action,
+                           int64_t R, float* tfreq, float* hid, float* cond, float* ada,
+                           oasis_stream_t stream);
+
+/* Sub-blocks [j0, j1) of the DiT on x[B*T*P, D] in place (j even: spatial, odd: temporal),
+ * ada as in oasis_dit_forward.  (run_sub_block, oasis_inference.py:995-1215.) */
+int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
+                         int64_t T, const float* ada, int64_t ada_fstride, int64_t j0, int64_t j1,
+                         oasis_stream_t stream);
+
+/* Final layer on x[M, D]: v_out[M, 64] = (LN(x) * scale_p1 + shift) @ final_w^T + final_b.
+ * (oasis_inference.py:1497-1521.) */
+int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M,
+                    const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream);
+
+/* One DiT forward over B streams of T frames: x[B*T*P, D] holds the embedded tokens on
+ * entry and the final hidden state on exit; v_out: fp32 [B*T*P, 64].
+ * ada: adaLN rows, frame f = b*T + t at ada + f*ada_fstride.
+ * (dit_forward_device, oasis_inference.py:1438-1526.) */
+int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                      int64_t B, int64_t T, const float* ada, int64_t ada_fstride,
+                      float* v_out, oasis_stream_t stream);
+
+typedef struct {
+  int depth;                 /* 12                                                 */
+  int d_model;               /* 1024                                               */
+  int n_heads;               /* 16                                                 */
+  int d_mlp;                 /* 4096                                               */
+  int latent_dim;            /* 32                                                 */
+  int grid_h, grid_w;        /* 18 x 32                                            */
+  int patch;                 /* 20                                                 */
+  const void* pq_w;          /* [D, latent_dim]                                    */
+  const float* pq_b;
+  const float* n1_w[OASIS_MAX_SUB];
+  const float* n1_b[OASIS_MAX_SUB];
+  const void* qkv_w[OASIS_MAX_SUB];   /* [3D, D]                                   */
+  const float* qkv_b[OASIS_MAX_SUB];
+  const void* proj_w[OASIS_MAX_SUB];
+  const float* proj_b[OASIS_MAX_SUB];
+  const float* n2_w[OASIS_MAX_SUB];
+  const float* n2_b[OASIS_MAX_SUB];
+  const void* fc1_w[OASIS_MAX_SUB];
+  const float* fc1_b[OASIS_MAX_SUB];
+  const void* fc2_w[OASIS_MAX_SUB];
+  const float* fc2_b[OASIS_MAX_SUB];
+  const float* norm_w;
+  const float* norm_b;
+  const void* pred_w;        /* [3*patch*patch, D]                                 */
+  const float* pred_b;
+  const float* rope_cos;     /* [grid_h*grid_w, 64]                                */
+  const float* rope_sinp;
+} oasis_vae_weights_t;
+
+typedef struct {
+  float* x;        /* [L, D] fp32   */
+  void* h;         /* [L, D] bf16   */
+  void* q;         /* [L, D] bf16   */
+  void* k;
+  void* v;
+  void* attn;      /* [L, D] bf16   */
+  void* mlp;       /* [L, Dm] bf16  */
+} oasis_vae_buffers_t;
+
+/* latent fp32 [L, latent_dim] -> frame fp32 [3, grid_h*patch, grid_w*patch] in [-1, 1].
+ * (vae_decode_forward, oasis_inference.py:1546-1618, + vae_unpatchify and clamp.) */
+int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf,
+                     const float* latent, float* frame, oasis_stream_t stream);
+
+/* One generated frame at T=2: n_steps DDIM v-prediction steps, then bridge + VAE decode.
+ *   chunk: fp32 [P, 64] noise in, denoised latent patches out;
+ *   ctx_z: fp32 [P, D] embedded context frame;
+ *   ada: fp32 rows [1 + n_steps, n_sub*6D + 2D]: row 0 the context frame, row 1+i the
+ *        generated frame at step i (see oasis_dit_conditioning);
+ *   coeffs: HOST array of n_steps x 6 DDIM coefficients (oasis_ddim_update order);
+ *   v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae latent_dim] scratch;
+ *   frame: fp32 [3, H, W] output.
+ * (ddim_step_fn and the traced frame, oasis_inference.py:1909-1932,2131-2148.) */
+int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                     const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                     float* chunk, const float* ctx_z, const float* ada, int64_t n_steps,
+                     const float* coeffs, float* v_out, float* latent, float* frame,
+                     oasis_stream_t stream);
+
+/* ---- hipGraph capture of any sequence of the calls above on one stream ---------
+ * Replaces ttnn.begin_trace_capture / end_trace_capture / execute_trace / release_trace
+ * (oasis_inference.py:2133-2146,2224; play.py:405-411). The stream must not be the
+ * legacy default stream. */
+int oasis_graph_begin(oasis_stream_t stream);
+int oasis_graph_end(oasis_stream_t stream, void** graph_exec);
+int oasis_graph_launch(void* graph_exec, oasis_stream_t stream);
+int oasis_graph_destroy(void* graph_exec);
+
+/* Blocks until all work queued on the stream is done (host helper for tests). */
+int oasis_stream_sync(oasis_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OASIS_HIP_H */

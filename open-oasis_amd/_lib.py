@@ -1,0 +1,167 @@
+"""ctypes binding of liboasis_hip.so (the C ABI declared in include/oasis_hip.h).
+
+The library is loaded from ``lib/liboasis_hip.so`` next to this file. There is no
+fallback: if it is missing, or no GPU is visible when a kernel is called, the call
+raises. Build it with ``python open-oasis_amd/build.py`` (or ``__graft_entry__.build()``).
+"""
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "liboasis_hip.so")
+
+OASIS_OK = 0
+F32, BF16 = 0, 1
+MAX_SUB = 64
+
+EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
+EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
+ACT_NONE, ACT_SILU = 0, 1
+
+
+class OasisError(RuntimeError):
+    """A liboasis_hip call returned an error code."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__("%s failed (code %d): %s" % (fn, code, msg))
+        self.code = code
+
+
+c_p = ctypes.c_void_p
+c_i64 = ctypes.c_int64
+c_i = ctypes.c_int
+c_f = ctypes.c_float
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [
+        ("kind", c_i), ("n_heads", c_i), ("bias", c_p), ("out_f32", c_p), ("out_bf16", c_p),
+        ("ld_out", c_i64), ("gate", c_p), ("gate_fstride", c_i64), ("rows_per_frame", c_i64),
+        ("frames_per_stream", c_i64), ("q", c_p), ("k", c_p), ("v", c_p), ("rope_cos", c_p),
+        ("rope_sinp", c_p), ("rope_by_frame", c_i), ("unpatch_grid_w", c_i),
+        ("s_b", c_i64), ("s_t", c_i64), ("s_p", c_i64), ("s_h", c_i64),
+        ("unpatch_patch", c_i), ("unpatch_channels", c_i),
+    ]
+
+
+class DiTWeights(ctypes.Structure):
+    _fields_ = [
+        ("n_sub", c_i), ("d_model", c_i), ("n_heads", c_i), ("d_mlp", c_i), ("grid_h", c_i),
+        ("grid_w", c_i), ("patch_dim", c_i), ("freq_dim", c_i), ("ext_dim_pad", c_i),
+        ("ada_w", c_p), ("ada_b", c_p),
+        ("qkv_w", c_p * MAX_SUB), ("out_w", c_p * MAX_SUB), ("out_b", c_p * MAX_SUB),
+        ("fc1_w", c_p * MAX_SUB), ("fc1_b", c_p * MAX_SUB), ("fc2_w", c_p * MAX_SUB),
+        ("fc2_b", c_p * MAX_SUB),
+        ("final_w", c_p), ("final_b", c_p), ("xemb_w", c_p), ("xemb_b", c_p),
+        ("temb_w0", c_p), ("temb_b0", c_p), ("temb_w2", c_p), ("temb_b2", c_p),
+        ("ext_w", c_p), ("ext_b", c_p),
+        ("s_cos", c_p), ("s_sinp", c_p), ("t_cos", c_p), ("t_sinp", c_p), ("t_max", c_i),
+    ]
+
+
+class DiTBuffers(ctypes.Structure):
+    _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p),
+                ("attn", c_p), ("mlp", c_p)]
+
+
+class VAEWeights(ctypes.Structure):
+    _fields_ = [
+        ("depth", c_i), ("d_model", c_i), ("n_heads", c_i), ("d_mlp", c_i), ("latent_dim", c_i),
+        ("grid_h", c_i), ("grid_w", c_i), ("patch", c_i),
+        ("pq_w", c_p), ("pq_b", c_p),
+        ("n1_w", c_p * MAX_SUB), ("n1_b", c_p * MAX_SUB), ("qkv_w", c_p * MAX_SUB),
+        ("qkv_b", c_p * MAX_SUB), ("proj_w", c_p * MAX_SUB), ("proj_b", c_p * MAX_SUB),
+        ("n2_w", c_p * MAX_SUB), ("n2_b", c_p * MAX_SUB), ("fc1_w", c_p * MAX_SUB),
+        ("fc1_b", c_p * MAX_SUB), ("fc2_w", c_p * MAX_SUB), ("fc2_b", c_p * MAX_SUB),
+        ("norm_w", c_p), ("norm_b", c_p), ("pred_w", c_p), ("pred_b", c_p),
+        ("rope_cos", c_p), ("rope_sinp", c_p),
+    ]
+
+
+class VAEBuffers(ctypes.Structure):
+    _fields_ = [("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p), ("attn", c_p),
+                ("mlp", c_p)]
+
+
+P = ctypes.POINTER
+# name -> argtypes (every function returns int except oasis_last_error)
+SIGNATURES = {
+    "oasis_abi_version": [],
+    "oasis_silu": [c_p, c_p, c_i64, c_i, c_p],
+    "oasis_adaln_modulate": [c_p, c_p, c_p, c_p, c_i64, c_i, c_p],
+    "oasis_gated_residual": [c_p, c_p, c_p, c_p, c_i64, c_i, c_p],
+    "oasis_bias_gated_residual": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i, c_p],
+    "oasis_layernorm": [c_p, c_p, c_p, c_i64, c_p, c_i64, c_i64, c_f, c_i, c_p],
+    "oasis_linear": [c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i, c_i, c_p],
+    "oasis_adaln_matmul_expand": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_p],
+    "oasis_rope_layout": [c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p,
+                          c_i64, c_i64, c_i64, c_i64, c_i, c_i, c_p],
+    "oasis_sdpa": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_i, c_i, c_p],
+    "oasis_gemm_bf16": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_p],
+    "oasis_ln_modulate": [c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_f, c_p],
+    "oasis_ln_affine": [c_p, c_i64, c_i64, c_p, c_p, c_p, c_f, c_p],
+    "oasis_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_f, c_p],
+    "oasis_temporal_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
+    "oasis_gemv_bf16": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
+    "oasis_timestep_embedding": [c_p, c_i64, c_i64, c_p, c_p],
+    "oasis_small_linear": [c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_p],
+    "oasis_ddim_update": [c_p, c_p, c_i64, c_f, c_f, c_f, c_f, c_f, c_f, c_p],
+    "oasis_bridge": [c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
+    "oasis_vae_unpatchify": [c_p, c_p, c_i64, c_i64, c_i64, c_p],
+    "oasis_dit_conditioning": [P(DiTWeights), c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p],
+    "oasis_dit_forward": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_p, c_p],
+    "oasis_dit_sub_blocks": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p],
+    "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],
+    "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
+    "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), c_p, c_p,
+                         c_p, c_i64, c_p, c_p, c_p, c_p, c_p],
+    "oasis_graph_begin": [c_p],
+    "oasis_graph_end": [c_p, P(c_p)],
+    "oasis_graph_launch": [c_p, c_p],
+    "oasis_graph_destroy": [c_p],
+    "oasis_stream_sync": [c_p],
+}
+
+_LIB = None
+
+
+def lib():
+    """Load (once) and return the ctypes handle. Raises if the library is not built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError("liboasis_hip.so is not built (%s); run open-oasis_amd/build.py" % LIB_PATH)
+        h = ctypes.CDLL(LIB_PATH)
+        h.oasis_last_error.restype = ctypes.c_char_p
+        h.oasis_last_error.argtypes = []
+        for name, argt in SIGNATURES.items():
+            f = getattr(h, name)
+            f.argtypes = argt
+            f.restype = c_i
+        _LIB = h
+    return _LIB
+
+
+def exported_names():
+    """Names of the C entry points this binding knows (all declared in oasis_hip.h)."""
+    return ["oasis_last_error"] + list(SIGNATURES)
+
+
+def call(name, *args):
+    """Call an int-returning entry point and raise OasisError on a non-zero code."""
+    h = lib()
+    rc = getattr(h, name)(*args)
+    if rc != OASIS_OK:
+        raise OasisError(name, rc, h.oasis_last_error().decode(errors="replace"))
+    return rc
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(stream=None):
+    """hipStream_t of a torch stream (default: the current stream)."""
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)

@@ -1,0 +1,297 @@
+// Attention kernels for gfx950.
+//
+// flash_kernel: flash-style multi-head attention on v_mfma_f32_16x16x32_bf16 with an
+//   online softmax. A workgroup of NW waves serves one (frame, head) and NW blocks of
+//   16 queries; K and V^T for 64-key chunks are staged in LDS and shared by the waves.
+//   The scores are computed transposed (S^T = K Q^T) so that every lane's scores all
+//   belong to one query (lane & 15): the running max/sum and the rescale of the output
+//   accumulators need only lane-group reductions, and the probabilities feed the
+//   P V product (as O^T = V^T P^T) straight from registers without an LDS round trip.
+//   Used for spatial attention (144 tokens per frame), the VAE (576 tokens) and the
+//   reference's sdpa / sdpa_causal surface (optional additive bias, causal mask).
+//
+// temporal_kernel: causal attention over the T frames of one (stream, position, head)
+//   group. At T=2 each group is 2 queries x 2 keys, far below an MFMA tile, so it is a
+//   VALU kernel: 16 lanes per group, 4 head dims per lane, dot products by 16-lane
+//   butterfly reductions and an online softmax over the causal keys.
+#include "oasis_common.h"
+
+namespace {
+
+constexpr int KC = 64;       // keys per LDS chunk
+constexpr int KPITCH = 64 + 8;
+constexpr int VPITCH = KC + 8;
+constexpr float LOG2E = 1.4426950408889634f;
+
+template <typename T>
+__device__ __forceinline__ bf16x8 load8_bf16(const T* p);
+template <>
+__device__ __forceinline__ bf16x8 load8_bf16<bf16>(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+template <>
+__device__ __forceinline__ bf16x8 load8_bf16<float>(const float* p) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return pack8(v);
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d);
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, float a, float b, float c, float d) {
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{f2bf(a), f2bf(b), f2bf(c), f2bf(d)};
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+
+struct AttnArgs {
+  int Lq, Lk;
+  int64_t q_bh, kv_bh;      // element stride between (frame, head) blocks of Q and K/V
+  float scale_log2;         // softmax scale * log2(e)
+  const float* bias;        // [Lq, Lk] or nullptr
+  int causal;
+  int H;                    // heads per frame (output addressing)
+  int64_t o_sf, o_sh, o_si; // out offset = (bh/H)*o_sf + (bh%H)*o_sh + i*o_si + d
+};
+
+template <int NW, typename T>
+__global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                                                        const T* __restrict__ V, T* __restrict__ O, AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 Ks[KC * KPITCH];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.y;
+  const int q0 = (blockIdx.x * NW + wave) * 16;
+  const int lr = lane & 15, g = lane >> 4;
+  const T* Qb = Q + (int64_t)bh * a.q_bh;
+  const T* Kb = K + (int64_t)bh * a.kv_bh;
+  const T* Vb = V + (int64_t)bh * a.kv_bh;
+
+  // this lane's query row (B operand of S^T = K Q^T): 8 dims at 8g and 32 + 8g
+  const int qrow = min(q0 + lr, a.Lq - 1);
+  const bf16x8 qf0 = load8_bf16<T>(Qb + (int64_t)qrow * 64 + g * 8);
+  const bf16x8 qf1 = load8_bf16<T>(Qb + (int64_t)qrow * 64 + 32 + g * 8);
+  const int my_q = q0 + lr;
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kc0 = 0; kc0 < a.Lk; kc0 += KC) {
+    __syncthreads();
+    for (int c = tid; c < KC * 8; c += NW * 64) {
+      const int key = c >> 3, d0 = (c & 7) * 8;
+      const int gk = kc0 + key;
+      bf16x8 kv, vv;
+      if (gk < a.Lk) {
+        kv = load8_bf16<T>(Kb + (int64_t)gk * 64 + d0);
+        vv = load8_bf16<T>(Vb + (int64_t)gk * 64 + d0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          kv[j] = f2bf(0.f);
+          vv[j] = f2bf(0.f);
+        }
+      }
+      *reinterpret_cast<bf16x8*>(Ks + key * KPITCH + d0) = kv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VPITCH + key] = vv[j];
+    }
+    __syncthreads();
+    if (q0 >= a.Lq) continue;
+
+    // S^T for 4 key tiles of 16: s[kt][i] = score(key kc0 + kt*16 + 4g + i, query my_q)
+    float s[4][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const bf16* kp = Ks + (kt * 16 + lr) * KPITCH + g * 8;
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc = mfma16(*reinterpret_cast<const bf16x8*>(kp), qf0, acc);
+      acc = mfma16(*reinterpret_cast<const bf16x8*>(kp + 32), qf1, acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kc0 + kt * 16 + 4 * g + i;
+        float x = acc[i] * a.scale_log2;
+        if (a.bias && key < a.Lk && my_q < a.Lq) x += a.bias[(int64_t)my_q * a.Lk + key] * LOG2E;
+        if (key >= a.Lk || (a.causal && key > my_q)) x = -INFINITY;
+        s[kt][i] = x;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - m_use);
+    float ps = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[kt][i] = exp2f(s[kt][i] - m_use);
+        ps += s[kt][i];
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * alpha + ps;
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
+
+    // O^T += V^T P^T over 2 sub-chunks of 32 keys; k-slot j of lane group g maps to
+    // key 32kc + 4g + j (j < 4) and 32kc + 16 + 4g + (j - 4) (j >= 4).
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      bf16x8 pb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pb[i] = f2bf(s[2 * kc][i]);
+        pb[4 + i] = f2bf(s[2 * kc + 1][i]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const bf16* vp = Vt + (dt * 16 + lr) * VPITCH + kc * 32 + 4 * g;
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vp);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vp + 16);
+        const bf16x8 va = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[dt] = mfma16(va, pb, o[dt]);
+      }
+    }
+  }
+  if (q0 >= a.Lq || my_q >= a.Lq) return;
+  const float inv = 1.0f / lsum;
+  const int f = bh / a.H, h = bh - f * a.H;
+  T* op = O + f * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const int d = dt * 16 + 4 * g;
+    store4<T>(op + d, o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+  }
+}
+
+template <typename T>
+int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
+  OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
+  OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
+  if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
+    hipLaunchKernelGGL((flash_kernel<3, T>), dim3((unsigned)(a.Lq / 48), (unsigned)n_bh), dim3(192), 0, s, q, k,
+                       v, o, a);
+  } else {
+    hipLaunchKernelGGL((flash_kernel<4, T>), dim3((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh), dim3(256), 0, s,
+                       q, k, v, o, a);
+  }
+  return oasis::check_launch("attention");
+}
+
+// q,k,v: [B][P][H][T][64] bf16; out: token-major [(b*T + t)*P + p][h*64 + d]
+__global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                       const bf16* __restrict__ v, bf16* __restrict__ out,
+                                                       int64_t G, int T, int P, int H, float scale_log2) {
+  const int64_t grp = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int j = threadIdx.x & 15;
+  if (grp >= G) return;  // whole 16-lane groups exit together; no cross-group shuffles
+  const int h = (int)(grp % H);
+  const int64_t bp = grp / H;
+  const int p = (int)(bp % P);
+  const int64_t b = bp / P;
+  const int64_t base = grp * T * 64 + j * 4;
+  for (int t = 0; t < T; ++t) {
+    const bf16x4 qv4 = *reinterpret_cast<const bf16x4*>(q + base + t * 64);
+    float qv[4] = {bf2f(qv4[0]), bf2f(qv4[1]), bf2f(qv4[2]), bf2f(qv4[3])};
+    float m = -INFINITY, l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s <= t; ++s) {
+      const bf16x4 kv4 = *reinterpret_cast<const bf16x4*>(k + base + s * 64);
+      float dot = qv[0] * bf2f(kv4[0]) + qv[1] * bf2f(kv4[1]) + qv[2] * bf2f(kv4[2]) + qv[3] * bf2f(kv4[3]);
+      dot += __shfl_xor(dot, 1, 16);
+      dot += __shfl_xor(dot, 2, 16);
+      dot += __shfl_xor(dot, 4, 16);
+      dot += __shfl_xor(dot, 8, 16);
+      const float x = dot * scale_log2;
+      const float m_new = fmaxf(m, x);
+      const float alpha = exp2f(m - m_new);
+      const float pexp = exp2f(x - m_new);
+      const bf16x4 vv4 = *reinterpret_cast<const bf16x4*>(v + base + s * 64);
+      l = l * alpha + pexp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = acc[i] * alpha + pexp * bf2f(vv4[i]);
+      m = m_new;
+    }
+    const float inv = 1.0f / l;
+    bf16* dst = out + ((b * T + t) * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
+    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(acc[0] * inv), f2bf(acc[1] * inv), f2bf(acc[2] * inv),
+                                              f2bf(acc[3] * inv)};
+  }
+}
+
+}  // namespace
+
+extern "C" int oasis_attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
+                               int64_t n_heads, float scale, oasis_stream_t stream) {
+  OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "attention: null pointer");
+  OASIS_REQUIRE(n_frames > 0 && L > 0 && n_heads > 0 && L < (1 << 30), OASIS_ERR_SHAPE, "attention: bad shape");
+  AttnArgs a;
+  a.Lq = a.Lk = (int)L;
+  a.q_bh = a.kv_bh = L * 64;
+  a.scale_log2 = scale * LOG2E;
+  a.bias = nullptr;
+  a.causal = 0;
+  a.H = (int)n_heads;
+  a.o_sf = L * n_heads * 64;
+  a.o_sh = 64;
+  a.o_si = n_heads * 64;
+  return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                            static_cast<bf16*>(out), n_frames * n_heads, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out, int64_t n_heads_total, int64_t sq,
+                          int64_t skv, int64_t head_dim, float scale, const float* bias, int causal, int dtype,
+                          oasis_stream_t stream) {
+  OASIS_REQUIRE(Q && K && V && out, OASIS_ERR_NULL, "sdpa: null pointer");
+  OASIS_REQUIRE(head_dim == 64, OASIS_ERR_SHAPE, "sdpa: head_dim must be 64");
+  OASIS_REQUIRE(sq > 0 && skv > 0 && sq < (1 << 30) && skv < (1 << 30), OASIS_ERR_SHAPE, "sdpa: bad shape");
+  AttnArgs a;
+  a.Lq = (int)sq;
+  a.Lk = (int)skv;
+  a.q_bh = sq * 64;
+  a.kv_bh = skv * 64;
+  a.scale_log2 = scale * LOG2E;
+  a.bias = bias;
+  a.causal = causal;
+  a.H = 1;
+  a.o_sf = sq * 64;
+  a.o_sh = 0;
+  a.o_si = 64;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OASIS_BF16)
+    return flash_launch<bf16>(static_cast<const bf16*>(Q), static_cast<const bf16*>(K), static_cast<const bf16*>(V),
+                              static_cast<bf16*>(out), n_heads_total, a, s);
+  if (dtype == OASIS_F32)
+    return flash_launch<float>(static_cast<const float*>(Q), static_cast<const float*>(K),
+                               static_cast<const float*>(V), static_cast<float*>(out), n_heads_total, a, s);
+  oasis::set_error("sdpa: unsupported dtype %d", dtype);
+  return OASIS_ERR_DTYPE;
+}
+
+extern "C" int oasis_temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T,
+                                        int64_t P, int64_t n_heads, float scale, oasis_stream_t stream) {
+  OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
+  OASIS_REQUIRE(B > 0 && T > 0 && P > 0 && n_heads > 0 && T <= 4096, OASIS_ERR_SHAPE,
+                "temporal_attention: bad shape");
+  const int64_t G = B * P * n_heads;
+  hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                     static_cast<const bf16*>(v), static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads,
+                     scale * LOG2E);
+  return oasis::check_launch("temporal_attention");
+}

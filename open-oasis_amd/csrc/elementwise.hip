@@ -1,0 +1,296 @@
+// Elementwise and small utility kernels: the reference's elementwise surface
+// (silu, adaln_modulate, gated_residual), the DDIM update, the DiT->VAE bridge,
+// VAE unpatchify, the timestep embedding, small-K fp32 projections, the reference
+// adaln_matmul_expand and the standalone RoPE + head-split kernel.
+//
+// All of these are HBM-bound; they use grid-stride loops with one element (or one
+// 8-element group) per thread step and coalesced accesses.
+#include "oasis_common.h"
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float ld<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float ld<bf16>(const bf16* p, int64_t i) { return bf2f(p[i]); }
+
+template <typename T>
+__device__ __forceinline__ void st(T* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void st<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <>
+__device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) { p[i] = f2bf(v); }
+
+enum { EW_SILU = 0, EW_MODULATE = 1, EW_GATED = 2, EW_BIAS_GATED = 3 };
+
+template <typename T, int OP>
+__global__ void ew_kernel(const T* a, const T* b, const T* c, const T* d, T* out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float r;
+    if (OP == EW_SILU) {
+      r = silu(ld<T>(a, i));
+    } else if (OP == EW_MODULATE) {  // x * (scale + 1) + shift ; a=x b=shift c=scale
+      r = ld<T>(a, i) * (ld<T>(c, i) + 1.0f) + ld<T>(b, i);
+    } else if (OP == EW_GATED) {  // residual + x * gate ; a=res b=x c=gate
+      r = ld<T>(a, i) + ld<T>(b, i) * ld<T>(c, i);
+    } else {  // residual + (x + bias) * gate ; a=res b=x c=bias d=gate
+      r = ld<T>(a, i) + (ld<T>(b, i) + ld<T>(c, i)) * ld<T>(d, i);
+    }
+    st<T>(out, i, r);
+  }
+}
+
+unsigned ew_grid(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  return (unsigned)(g > 8192 ? 8192 : (g < 1 ? 1 : g));
+}
+
+template <int OP>
+int ew_launch(const void* a, const void* b, const void* c, const void* d, void* out, int64_t n, int dtype,
+              oasis_stream_t stream, const char* what) {
+  OASIS_REQUIRE(n >= 0, OASIS_ERR_SHAPE, "%s: negative n", what);
+  if (n == 0) return OASIS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OASIS_F32) {
+    hipLaunchKernelGGL((ew_kernel<float, OP>), dim3(ew_grid(n)), dim3(256), 0, s, (const float*)a,
+                       (const float*)b, (const float*)c, (const float*)d, (float*)out, n);
+  } else if (dtype == OASIS_BF16) {
+    hipLaunchKernelGGL((ew_kernel<bf16, OP>), dim3(ew_grid(n)), dim3(256), 0, s, (const bf16*)a,
+                       (const bf16*)b, (const bf16*)c, (const bf16*)d, (bf16*)out, n);
+  } else {
+    oasis::set_error("%s: unsupported dtype %d", what, dtype);
+    return OASIS_ERR_DTYPE;
+  }
+  return oasis::check_launch(what);
+}
+
+__global__ void ddim_kernel(float* chunk, const float* v, int64_t n, float c0, float c1, float c2, float c3,
+                            float c4, float c5) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float x = chunk[i];
+    const float x0 = c0 * x - c1 * v[i];
+    const float eps = (c2 * x - x0) * c3;
+    chunk[i] = c4 * x0 + c5 * eps;
+  }
+}
+
+// latent row r = (h*2+p)*(2gw) + (w*2+q), col c  <-  chunk row h*gw+w, col (p*2+q)*C + c
+__global__ void bridge_kernel(const float* chunk, float* lat, int gh, int gw, int C, int out_cols, float inv) {
+  const int64_t n = (int64_t)gh * 2 * gw * 2 * out_cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int col = (int)(i % out_cols);
+    const int64_t r = i / out_cols;
+    float val = 0.f;
+    if (col < C) {
+      const int wq = (int)(r % (2 * gw)), hp = (int)(r / (2 * gw));
+      const int h = hp >> 1, p = hp & 1, w = wq >> 1, q = wq & 1;
+      val = chunk[((int64_t)h * gw + w) * (4 * C) + (p * 2 + q) * C + col] * inv;
+    }
+    lat[i] = val;
+  }
+}
+
+// frame[c][hh*ps+pp][ww*ps+qq] = clamp(patches[hh*gw+ww][(c*ps+pp)*ps+qq])
+__global__ void unpatchify_kernel(const float* patches, float* frame, int gh, int gw, int ps) {
+  const int64_t H = (int64_t)gh * ps, W = (int64_t)gw * ps, n = 3 * H * W;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t x = i % W, y = (i / W) % H, c = i / (W * H);
+    const int64_t hh = y / ps, pp = y % ps, ww = x / ps, qq = x % ps;
+    const float v = patches[(hh * gw + ww) * (3 * ps * ps) + (c * ps + pp) * ps + qq];
+    frame[i] = fminf(fmaxf(v, -1.0f), 1.0f);
+  }
+}
+
+__global__ void temb_kernel(const float* t, int64_t R, int half, float* out) {
+  const int64_t n = R * half;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / half;
+    const int k = (int)(i % half);
+    const float f = expf(-9.210340371976184f * (float)k / (float)half);  // ln(10000)
+    const float a = t[r] * f;
+    out[r * 2 * half + k] = cosf(a);
+    out[r * 2 * half + half + k] = sinf(a);
+  }
+}
+
+// out[m, n] = b[n] + sum_k x[m, k] W[n, k]; block = one row m, threads over n.
+__global__ __launch_bounds__(256) void small_linear_kernel(const float* x, int64_t ldx, int K, const bf16* W,
+                                                           int N, const float* b, float* out, int64_t ld_out) {
+  __shared__ float xs[256];
+  const int64_t m = blockIdx.y;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) xs[k] = x[m * ldx + k];
+  __syncthreads();
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const bf16* w = W + (int64_t)n * K;
+  float acc = b ? b[n] : 0.f;
+  for (int k = 0; k < K; k += 8) {
+    float wv[8];
+    unpack8(*reinterpret_cast<const bf16x8*>(w + k), wv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += xs[k + j] * wv[j];
+  }
+  out[m * ld_out + n] = acc;
+}
+
+// reference surface: out[r, n] = sum_k c[k] w[k, n] + b[n] (w is [K, N]), rows r < out_rows.
+__global__ void adaln_expand_kernel(const float* c, const bf16* w, const float* b, float* out, int K, int N,
+                                    int64_t rows) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float acc = b ? b[n] : 0.f;
+  for (int k = 0; k < K; ++k) acc += c[k] * bf2f(w[(int64_t)k * N + n]);
+  for (int64_t r = 0; r < rows; ++r) out[r * N + n] = acc;
+}
+
+// Standalone RoPE + head split: one thread per 8 consecutive dims of one (row, q|k|v, head).
+template <typename T>
+__global__ void rope_layout_kernel(const T* qkv, int64_t ldq, const float* cs, const float* sn, int64_t tab_ld,
+                                   int64_t tab_hs, int64_t pos_div, int64_t pos_mod, T* qo, T* ko, T* vo,
+                                   int64_t rows, int64_t seq, int H, int mode) {
+  const int D = H * 64;
+  const int64_t n = rows * 3 * (D / 8);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / (3 * (D / 8));
+    const int rem = (int)(i % (3 * (D / 8)));
+    const int which = rem / (D / 8), c8 = (rem % (D / 8)) * 8;
+    const int h = c8 >> 6, d0 = c8 & 63;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ld<T>(qkv, row * ldq + which * D + c8 + j);
+    if (which < 2) {
+      const int64_t pos = (row / pos_div) % pos_mod;
+      const float* c = cs + pos * tab_ld + h * tab_hs + d0;
+      const float* s = sn + pos * tab_ld + h * tab_hs + d0;
+      float r[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * s[j];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = r[j];
+    }
+    T* dst = which == 0 ? qo : (which == 1 ? ko : vo);
+    int64_t off;
+    if (mode == 0) {
+      const int64_t f = row / seq, p = row % seq;
+      off = ((f * H + h) * seq + p) * 64 + d0;
+    } else {
+      off = row * D + c8;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st<T>(dst, off + j, v[j]);
+  }
+}
+
+}  // namespace
+
+extern "C" int oasis_silu(const void* x, void* out, int64_t n, int dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && out, OASIS_ERR_NULL, "silu: null pointer");
+  return ew_launch<EW_SILU>(x, nullptr, nullptr, nullptr, out, n, dtype, stream, "silu");
+}
+
+extern "C" int oasis_adaln_modulate(const void* x, const void* shift, const void* scale, void* out, int64_t n,
+                                    int dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && shift && scale && out, OASIS_ERR_NULL, "adaln_modulate: null pointer");
+  return ew_launch<EW_MODULATE>(x, shift, scale, nullptr, out, n, dtype, stream, "adaln_modulate");
+}
+
+extern "C" int oasis_gated_residual(const void* residual, const void* x, const void* gate, void* out, int64_t n,
+                                    int dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(residual && x && gate && out, OASIS_ERR_NULL, "gated_residual: null pointer");
+  return ew_launch<EW_GATED>(residual, x, gate, nullptr, out, n, dtype, stream, "gated_residual");
+}
+
+extern "C" int oasis_bias_gated_residual(const void* residual, const void* x, const void* bias, const void* gate,
+                                         void* out, int64_t n, int dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(residual && x && bias && gate && out, OASIS_ERR_NULL, "bias_gated_residual: null pointer");
+  return ew_launch<EW_BIAS_GATED>(residual, x, bias, gate, out, n, dtype, stream, "bias_gated_residual");
+}
+
+extern "C" int oasis_ddim_update(float* chunk, const float* v, int64_t n, float c0, float c1, float c2, float c3,
+                                 float c4, float c5, oasis_stream_t stream) {
+  OASIS_REQUIRE(chunk && v, OASIS_ERR_NULL, "ddim_update: null pointer");
+  OASIS_REQUIRE(n >= 0, OASIS_ERR_SHAPE, "ddim_update: negative n");
+  if (n == 0) return OASIS_OK;
+  hipLaunchKernelGGL(ddim_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), chunk, v, n,
+                     c0, c1, c2, c3, c4, c5);
+  return oasis::check_launch("ddim_update");
+}
+
+extern "C" int oasis_bridge(const float* chunk, float* latent, int64_t gh, int64_t gw, int64_t C, int64_t out_cols,
+                            float inv_scale, oasis_stream_t stream) {
+  OASIS_REQUIRE(chunk && latent, OASIS_ERR_NULL, "bridge: null pointer");
+  OASIS_REQUIRE(gh > 0 && gw > 0 && C > 0 && out_cols >= C, OASIS_ERR_SHAPE, "bridge: bad shape");
+  const int64_t n = gh * 2 * gw * 2 * out_cols;
+  hipLaunchKernelGGL(bridge_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), chunk, latent,
+                     (int)gh, (int)gw, (int)C, (int)out_cols, inv_scale);
+  return oasis::check_launch("bridge");
+}
+
+extern "C" int oasis_vae_unpatchify(const float* patches, float* frame, int64_t gh, int64_t gw, int64_t ps,
+                                    oasis_stream_t stream) {
+  OASIS_REQUIRE(patches && frame, OASIS_ERR_NULL, "vae_unpatchify: null pointer");
+  OASIS_REQUIRE(gh > 0 && gw > 0 && ps > 0, OASIS_ERR_SHAPE, "vae_unpatchify: bad shape");
+  const int64_t n = 3 * gh * ps * gw * ps;
+  hipLaunchKernelGGL(unpatchify_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), patches,
+                     frame, (int)gh, (int)gw, (int)ps);
+  return oasis::check_launch("vae_unpatchify");
+}
+
+extern "C" int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, float* out, oasis_stream_t stream) {
+  OASIS_REQUIRE(t && out, OASIS_ERR_NULL, "timestep_embedding: null pointer");
+  OASIS_REQUIRE(R > 0 && dim > 0 && dim % 2 == 0, OASIS_ERR_SHAPE, "timestep_embedding: bad shape");
+  hipLaunchKernelGGL(temb_kernel, dim3(ew_grid(R * dim / 2)), dim3(256), 0, static_cast<hipStream_t>(stream), t, R,
+                     (int)(dim / 2), out);
+  return oasis::check_launch("timestep_embedding");
+}
+
+extern "C" int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W, int64_t N,
+                                  const float* b, float* out, int64_t ld_out, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "small_linear: null pointer");
+  OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K <= 256 && K % 8 == 0 && ldx >= K && ld_out >= N, OASIS_ERR_SHAPE,
+                "small_linear: need 0 < K <= 256, K % 8 == 0");
+  OASIS_REQUIRE(M <= 65535, OASIS_ERR_SHAPE, "small_linear: M too large");
+  hipLaunchKernelGGL(small_linear_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, ldx, (int)K, static_cast<const bf16*>(W), (int)N, b, out,
+                     ld_out);
+  return oasis::check_launch("small_linear");
+}
+
+extern "C" int oasis_adaln_matmul_expand(const float* silu_cond, const void* w, const float* b, float* out,
+                                         int64_t K, int64_t N, int64_t out_rows, oasis_stream_t stream) {
+  OASIS_REQUIRE(silu_cond && w && out, OASIS_ERR_NULL, "adaln_matmul_expand: null pointer");
+  OASIS_REQUIRE(K > 0 && N > 0 && out_rows > 0, OASIS_ERR_SHAPE, "adaln_matmul_expand: bad shape");
+  hipLaunchKernelGGL(adaln_expand_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), silu_cond, static_cast<const bf16*>(w), b, out, (int)K, (int)N,
+                     out_rows);
+  return oasis::check_launch("adaln_matmul_expand");
+}
+
+extern "C" int oasis_rope_layout(const void* qkv, int64_t ld_qkv, const float* cos, const float* sinp, int64_t tab_ld,
+                                 int64_t tab_head_stride, int64_t pos_div, int64_t pos_mod, void* q_out, void* k_out,
+                                 void* v_out, int64_t rows, int64_t seq, int64_t n_heads, int64_t head_dim, int mode,
+                                 int dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(qkv && cos && sinp && q_out && k_out && v_out, OASIS_ERR_NULL, "rope_layout: null pointer");
+  OASIS_REQUIRE(head_dim == 64, OASIS_ERR_SHAPE, "rope_layout: head_dim must be 64");
+  OASIS_REQUIRE(rows > 0 && seq > 0 && n_heads > 0 && ld_qkv >= 3 * n_heads * 64 && pos_div > 0 && pos_mod > 0,
+                OASIS_ERR_SHAPE, "rope_layout: bad shape");
+  OASIS_REQUIRE(mode == 0 || mode == 1, OASIS_ERR_ARG, "rope_layout: mode must be 0 or 1");
+  OASIS_REQUIRE(mode == 1 || rows % seq == 0, OASIS_ERR_SHAPE, "rope_layout: rows must be a multiple of seq");
+  const int64_t n = rows * 3 * n_heads * 8;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == OASIS_F32) {
+    hipLaunchKernelGGL((rope_layout_kernel<float>), dim3(ew_grid(n)), dim3(256), 0, s, (const float*)qkv, ld_qkv,
+                       cos, sinp, tab_ld, tab_head_stride, pos_div, pos_mod, (float*)q_out, (float*)k_out,
+                       (float*)v_out, rows, seq, (int)n_heads, mode);
+  } else if (dtype == OASIS_BF16) {
+    hipLaunchKernelGGL((rope_layout_kernel<bf16>), dim3(ew_grid(n)), dim3(256), 0, s, (const bf16*)qkv, ld_qkv, cos,
+                       sinp, tab_ld, tab_head_stride, pos_div, pos_mod, (bf16*)q_out, (bf16*)k_out, (bf16*)v_out,
+                       rows, seq, (int)n_heads, mode);
+  } else {
+    oasis::set_error("rope_layout: unsupported dtype %d", dtype);
+    return OASIS_ERR_DTYPE;
+  }
+  return oasis::check_launch("rope_layout");
+}

@@ -1,0 +1,452 @@
+// bf16 MFMA GEMM for gfx950 with fused epilogues.
+//
+//   acc[M,N] = A[M,K] @ B[N,K]^T, A = activations (bf16, row-major), B = weights in
+//   the nn.Linear layout [out, in] (bf16), fp32 accumulation, then one epilogue
+//   (bias, tanh/erf GELU, gated residual into the fp32 stream, RoPE + head split,
+//   VAE unpatchify) applied on the way out.
+//
+// Tiling: a 256-thread workgroup (4 waves of 64) owns a BM x BN output tile and walks
+// K in BK=64 steps. A and B tiles go global -> registers -> LDS with a double-buffered
+// LDS ring (the next tile's global loads are in flight while the current tile feeds
+// v_mfma_f32_16x16x32_bf16). Each wave owns a (BM/WM) x (BN/WN) sub-tile. After the
+// K loop the fp32 tile is staged through LDS so each thread handles 8 consecutive
+// columns of one row: coalesced 16/32-byte stores and in-register RoPE pair swaps.
+//
+// Workgroup -> tile order is XCD-aware: MI355X dispatches workgroup i to XCD i % 8,
+// so ids are remapped such that every M tile of one weight column block lands on the
+// same XCD; the weight block is then fetched from HBM once into that XCD's L2.
+#include <string.h>
+
+#include "oasis_common.h"
+
+namespace {
+
+constexpr int BK = 64;
+constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row (16 B pad: conflict-free b128 reads)
+constexpr int NUM_XCD = 8;
+
+struct Epi {
+  int kind;
+  int n_heads;
+  const float* bias;
+  float* out_f32;
+  bf16* out_bf16;
+  int64_t ld_out;
+  const float* gate;
+  int64_t gate_fstride;
+  int64_t rows_per_frame;
+  int64_t frames_per_stream;
+  bf16* q;
+  bf16* k;
+  bf16* v;
+  const float* rope_cos;
+  const float* rope_sinp;
+  int rope_by_frame;
+  int unpatch_grid_w;
+  int64_t s_b, s_t, s_p, s_h;
+  int unpatch_patch;
+  int unpatch_channels;
+};
+
+__device__ __forceinline__ int xcd_remap(int pid, int G) {
+  const int q = G / NUM_XCD, r = G % NUM_XCD;
+  const int xcd = pid % NUM_XCD, local = pid / NUM_XCD;
+  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+__device__ __forceinline__ void store8_bf16(bf16* dst, const float* v) {
+  *reinterpret_cast<bf16x8*>(dst) = pack8(v);
+}
+
+// Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N).
+__device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float* v) {
+  if (e.bias) {
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(e.bias + n0);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(e.bias + n0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] += b0[j];
+      v[j + 4] += b1[j];
+    }
+  }
+  switch (e.kind) {
+    case OASIS_EPI_STORE_F32: {
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      break;
+    }
+    case OASIS_EPI_STORE_BF16:
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    case OASIS_EPI_GELU_TANH: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_tanh(v[j]);
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    }
+    case OASIS_EPI_GELU_ERF: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    }
+    case OASIS_EPI_GATED_RES: {
+      const int64_t f = m / e.rows_per_frame;
+      const float* g = e.gate + f * e.gate_fstride + n0;
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g), g1 = *reinterpret_cast<const f32x4*>(g + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x0[j] += g0[j] * v[j];
+        x1[j] += g1[j] * v[j + 4];
+      }
+      *reinterpret_cast<f32x4*>(d) = x0;
+      *reinterpret_cast<f32x4*>(d + 4) = x1;
+      break;
+    }
+    case OASIS_EPI_RESIDUAL: {
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x0[j] += v[j];
+        x1[j] += v[j + 4];
+      }
+      *reinterpret_cast<f32x4*>(d) = x0;
+      *reinterpret_cast<f32x4*>(d + 4) = x1;
+      break;
+    }
+    case OASIS_EPI_QKV_ROPE: {
+      const int D = e.n_heads * 64;
+      const int which = n0 / D;          // 0 q, 1 k, 2 v
+      const int nn = n0 - which * D;
+      const int h = nn >> 6, d0 = nn & 63;
+      const int64_t f = m / e.rows_per_frame, p = m - f * e.rows_per_frame;
+      const int64_t b = f / e.frames_per_stream, t = f - b * e.frames_per_stream;
+      if (which < 2) {
+        const int64_t pos = e.rope_by_frame ? t : p;
+        const float* c = e.rope_cos + pos * 64 + d0;
+        const float* s = e.rope_sinp + pos * 64 + d0;
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * s[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = r[j];
+      }
+      bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
+      store8_bf16(base + b * e.s_b + t * e.s_t + p * e.s_p + h * e.s_h + d0, v);
+      break;
+    }
+    case OASIS_EPI_UNPATCHIFY: {
+      // m = hh*gw + ww; n = (c*ps + pp)*ps + qq -> frame[c][hh*ps + pp][ww*ps + qq]
+      const int ps = e.unpatch_patch, gw = e.unpatch_grid_w;
+      const int64_t hh = m / gw, ww = m - hh * gw;
+      const int64_t W = (int64_t)gw * ps;
+      const int64_t H = e.rows_per_frame / gw * ps;  // rows_per_frame = gh*gw
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = n0 + j;
+        const int c = n / (ps * ps), rem = n - c * ps * ps;
+        const int pp = rem / ps, qq = rem - pp * ps;
+        const float val = fminf(fmaxf(v[j], -1.0f), 1.0f);
+        e.out_f32[(c * H + hh * ps + pp) * W + ww * ps + qq] = val;
+      }
+      break;
+    }
+    default:
+      break;
+  }
+}
+
+// BKN = false: B is [N, K] (weights as stored by this library); true: B is [K, N]
+// (the reference's transposed weight layout, used by the linear_k32 surface only).
+template <int BM, int BN, int WM, int WN, bool BKN>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__ A, int64_t lda,
+                                                        const bf16* __restrict__ B, int64_t ldb,
+                                                        int M, int N, int K, Epi e) {
+  static_assert(WM * WN == 4, "4 waves");
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
+  constexpr int A_CHUNKS = BM * (BK / 8);  // 16-byte chunks per A tile
+  constexpr int B_CHUNKS = BN * (BK / 8);
+  constexpr int A_PER = (A_CHUNKS + 255) / 256;
+  constexpr int B_PER = (B_CHUNKS + 255) / 256;
+  constexpr int AB_BYTES = 2 * (BM + BN) * LDS_PITCH * 2;
+  constexpr int C_PITCH = BN + 4;
+  constexpr int C_BYTES = BM * C_PITCH * 4;
+  constexpr int SMEM = AB_BYTES > C_BYTES ? AB_BYTES : C_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  bf16* As = reinterpret_cast<bf16*>(smem);                    // [2][BM][LDS_PITCH]
+  bf16* Bs = As + 2 * BM * LDS_PITCH;                          // [2][BN][LDS_PITCH]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt);
+  const int nt = pid / Mt, mt = pid - nt * Mt;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  // global chunk coordinates (fixed across K)
+  const bf16* a_src[A_PER];
+  int a_dst[A_PER];
+  bool a_ok[A_PER];
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int c = tid + i * 256;
+    const int row = c >> 3, col = (c & 7) * 8;
+    a_ok[i] = c < A_CHUNKS;
+    const int gr = min(m0 + row, M - 1);
+    a_src[i] = A + (int64_t)gr * lda + col;
+    a_dst[i] = row * LDS_PITCH + col;
+  }
+  const bf16* b_src[B_PER];
+  int b_dst[B_PER];
+  bool b_ok[B_PER];
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) {
+    const int c = tid + i * 256;
+    b_ok[i] = c < B_CHUNKS;
+    if (!BKN) {
+      const int row = c >> 3, col = (c & 7) * 8;
+      const int gr = min(n0 + row, N - 1);
+      b_src[i] = B + (int64_t)gr * ldb + col;
+      b_dst[i] = row * LDS_PITCH + col;
+    } else {  // chunk = 8 consecutive n of one k row; stored transposed into [n][k]
+      const int krow = c / (BN / 8), nc = (c % (BN / 8)) * 8;
+      const int gn = min(n0 + nc, N - 8);
+      b_src[i] = B + (int64_t)krow * ldb + gn;
+      b_dst[i] = nc * LDS_PITCH + krow;
+    }
+  }
+
+  i32x4 ra[A_PER], rb[B_PER];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i)
+      if (a_ok[i]) ra[i] = *reinterpret_cast<const i32x4*>(a_src[i] + k0);
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i)
+      if (b_ok[i]) rb[i] = *reinterpret_cast<const i32x4*>(b_src[i] + (BKN ? (int64_t)k0 * ldb : (int64_t)k0));
+  };
+  auto lstore = [&](int buf) {
+    bf16* as = As + buf * BM * LDS_PITCH;
+    bf16* bs = Bs + buf * BN * LDS_PITCH;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i)
+      if (a_ok[i]) *reinterpret_cast<i32x4*>(as + a_dst[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      if (!b_ok[i]) continue;
+      if (!BKN) {
+        *reinterpret_cast<i32x4*>(bs + b_dst[i]) = rb[i];
+      } else {
+        const bf16x8 t = __builtin_bit_cast(bf16x8, rb[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bs[b_dst[i] + j * LDS_PITCH] = t[j];
+      }
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  const int lr = lane & 15, lk = (lane >> 4) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+    const bf16* as = As + cur * BM * LDS_PITCH + (wm * TM + lr) * LDS_PITCH + lk;
+    const bf16* bs = Bs + cur * BN * LDS_PITCH + (wn * TN + lr) * LDS_PITCH + lk;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(as + i * 16 * LDS_PITCH + ks * 32);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(bs + j * 16 * LDS_PITCH + ks * 32);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // stage the fp32 tile through LDS (the A/B ring is free after the last barrier)
+  float* Cs = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        Cs[(wm * TM + i * 16 + (lane >> 4) * 4 + r) * C_PITCH + wn * TN + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+
+  constexpr int UNITS = BM * (BN / 8);
+  for (int u = tid; u < UNITS; u += 256) {
+    const int r = u / (BN / 8), c8 = (u % (BN / 8)) * 8;
+    const int gm = m0 + r, gn = n0 + c8;
+    if (gm >= M || gn >= N) continue;
+    float v[8];
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = c0[j];
+      v[j + 4] = c1[j];
+    }
+    epilogue8(e, gm, gn, v);
+  }
+}
+
+template <int BM, int BN, int WM, int WN, bool BKN = false>
+hipError_t launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K,
+                      const Epi& e, hipStream_t s) {
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, BKN>), dim3(Mt * Nt), dim3(256), 0, s, A, lda, B,
+                     ldb, M, N, K, e);
+  return hipGetLastError();
+}
+
+Epi to_epi(const oasis_epilogue_t& x) {
+  Epi e;
+  e.kind = x.kind;
+  e.n_heads = x.n_heads;
+  e.bias = x.bias;
+  e.out_f32 = x.out_f32;
+  e.out_bf16 = static_cast<bf16*>(x.out_bf16);
+  e.ld_out = x.ld_out;
+  e.gate = x.gate;
+  e.gate_fstride = x.gate_fstride;
+  e.rows_per_frame = x.rows_per_frame > 0 ? x.rows_per_frame : 1;
+  e.frames_per_stream = x.frames_per_stream > 0 ? x.frames_per_stream : 1;
+  e.q = static_cast<bf16*>(x.q);
+  e.k = static_cast<bf16*>(x.k);
+  e.v = static_cast<bf16*>(x.v);
+  e.rope_cos = x.rope_cos;
+  e.rope_sinp = x.rope_sinp;
+  e.rope_by_frame = x.rope_by_frame;
+  e.unpatch_grid_w = x.unpatch_grid_w;
+  e.s_b = x.s_b;
+  e.s_t = x.s_t;
+  e.s_p = x.s_p;
+  e.s_h = x.s_h;
+  e.unpatch_patch = x.unpatch_patch;
+  e.unpatch_channels = x.unpatch_channels;
+  return e;
+}
+
+}  // namespace
+
+namespace oasis {
+
+// Tile choice per shape. M is small (288 / 576 tokens) and the weights are streamed
+// once, so the tiles trade L2 re-reads of A and B against enough workgroups to keep
+// all 256 CUs issuing HBM loads.
+int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N,
+                int64_t K, const oasis_epilogue_t& ex, hipStream_t s) {
+  OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm: null operand");
+  OASIS_REQUIRE(M > 0 && N > 0 && K > 0, OASIS_ERR_SHAPE, "gemm: empty shape M=%lld N=%lld K=%lld",
+                (long long)M, (long long)N, (long long)K);
+  OASIS_REQUIRE(K % BK == 0, OASIS_ERR_SHAPE, "gemm: K=%lld must be a multiple of 64", (long long)K);
+  OASIS_REQUIRE(N % 8 == 0, OASIS_ERR_SHAPE, "gemm: N=%lld must be a multiple of 8", (long long)N);
+  OASIS_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K, OASIS_ERR_SHAPE,
+                "gemm: lda/ldb must be >= K and multiples of 8");
+  OASIS_REQUIRE(M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE, "gemm: M/N too large");
+  const Epi e = to_epi(ex);
+  switch (e.kind) {
+    case OASIS_EPI_STORE_F32:
+    case OASIS_EPI_GATED_RES:
+    case OASIS_EPI_RESIDUAL:
+      OASIS_REQUIRE(e.out_f32 && e.ld_out >= N && e.ld_out % 4 == 0, OASIS_ERR_ARG,
+                    "gemm: fp32 epilogue needs out_f32 and ld_out >= N (multiple of 4)");
+      OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES || e.gate, OASIS_ERR_NULL, "gemm: gate is NULL");
+      break;
+    case OASIS_EPI_STORE_BF16:
+    case OASIS_EPI_GELU_TANH:
+    case OASIS_EPI_GELU_ERF:
+      OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 8 == 0, OASIS_ERR_ARG,
+                    "gemm: bf16 epilogue needs out_bf16 and ld_out >= N (multiple of 8)");
+      break;
+    case OASIS_EPI_QKV_ROPE:
+      OASIS_REQUIRE(e.q && e.k && e.v && e.rope_cos && e.rope_sinp, OASIS_ERR_NULL,
+                    "gemm: QKV_ROPE needs q/k/v and rope tables");
+      OASIS_REQUIRE(e.n_heads > 0 && N == 3LL * e.n_heads * 64, OASIS_ERR_SHAPE,
+                    "gemm: QKV_ROPE needs N == 3*n_heads*64");
+      break;
+    case OASIS_EPI_UNPATCHIFY:
+      OASIS_REQUIRE(e.out_f32 && e.unpatch_patch > 0 && e.unpatch_grid_w > 0, OASIS_ERR_ARG,
+                    "gemm: UNPATCHIFY needs out_f32, patch and grid_w");
+      OASIS_REQUIRE(N == 3LL * e.unpatch_patch * e.unpatch_patch && e.rows_per_frame == M &&
+                        M % e.unpatch_grid_w == 0,
+                    OASIS_ERR_SHAPE, "gemm: UNPATCHIFY shape mismatch");
+      break;
+    default:
+      OASIS_REQUIRE(false, OASIS_ERR_ARG, "gemm: unknown epilogue kind %d", e.kind);
+  }
+  const int m = (int)M, n = (int)N, k = (int)K;
+  hipError_t err;
+  if (M <= 64) {
+    err = launch_cfg<32, 64, 1, 4>(A, lda, B, ldb, m, n, k, e, s);
+  } else if (N <= 1216) {
+    err = launch_cfg<32, 64, 1, 4>(A, lda, B, ldb, m, n, k, e, s);
+  } else {
+    err = launch_cfg<64, 64, 2, 2>(A, lda, B, ldb, m, n, k, e, s);
+  }
+  if (err != hipSuccess) {
+    set_error("gemm launch failed: %s", hipGetErrorString(err));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
+}  // namespace oasis
+
+extern "C" int oasis_linear(const void* x, const void* w, void* out, int64_t M, int64_t K, int64_t N,
+                            int w_layout, int out_dtype, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && w && out, OASIS_ERR_NULL, "linear: null pointer");
+  OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K % BK == 0 && N % 8 == 0 && M < (1ll << 31) && N < (1ll << 31),
+                OASIS_ERR_SHAPE, "linear: need K %% 64 == 0 and N %% 8 == 0");
+  OASIS_REQUIRE(w_layout == 0 || w_layout == 1, OASIS_ERR_ARG, "linear: w_layout must be 0 ([K,N]) or 1 ([N,K])");
+  OASIS_REQUIRE(out_dtype == OASIS_F32 || out_dtype == OASIS_BF16, OASIS_ERR_DTYPE, "linear: bad out dtype %d",
+                out_dtype);
+  oasis_epilogue_t ex;
+  memset(&ex, 0, sizeof(ex));
+  ex.kind = out_dtype == OASIS_F32 ? OASIS_EPI_STORE_F32 : OASIS_EPI_STORE_BF16;
+  ex.out_f32 = static_cast<float*>(out);
+  ex.out_bf16 = out;
+  ex.ld_out = N;
+  if (w_layout == 1)
+    return oasis::gemm_launch(static_cast<const bf16*>(x), K, static_cast<const bf16*>(w), K, M, N, K, ex,
+                              static_cast<hipStream_t>(stream));
+  const Epi e = to_epi(ex);
+  const hipError_t err = launch_cfg<32, 64, 1, 4, true>(static_cast<const bf16*>(x), K, static_cast<const bf16*>(w), N,
+                                                        (int)M, (int)N, (int)K, e, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    oasis::set_error("linear launch failed: %s", hipGetErrorString(err));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
+extern "C" int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                               int64_t N, int64_t K, const oasis_epilogue_t* epi,
+                               oasis_stream_t stream) {
+  OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm: null epilogue");
+  return oasis::gemm_launch(static_cast<const bf16*>(A), lda, static_cast<const bf16*>(B), ldb, M, N,
+                            K, *epi, static_cast<hipStream_t>(stream));
+}

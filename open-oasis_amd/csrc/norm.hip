@@ -1,0 +1,155 @@
+// Single-pass LayerNorm kernels: one 64-lane wave per row, the row held in registers
+// (D/64 floats per lane, 16 B vector loads), mean and variance by two wave reductions
+// over the registers (exact two-pass arithmetic, one HBM read), then the modulation or
+// affine transform fused into the store.
+//
+//   ln_modulate:  y_bf16 = LN(x) * scale_p1[frame] + shift[frame]   (DiT, no affine)
+//   ln_affine:    y_bf16 = LN(x) * w + b                            (VAE)
+//   layernorm:    reference surface, fp32/bf16 in and out, w/b optionally row-expanded
+#include "oasis_common.h"
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load4<float>(const float* p, float* v) {
+  const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+  v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+}
+template <>
+__device__ __forceinline__ void load4<bf16>(const bf16* p, float* v) {
+  const bf16x4 t = *reinterpret_cast<const bf16x4*>(p);
+  v[0] = bf2f(t[0]); v[1] = bf2f(t[1]); v[2] = bf2f(t[2]); v[3] = bf2f(t[3]);
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store4<float>(float* p, const float* v) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+}
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, const float* v) {
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{f2bf(v[0]), f2bf(v[1]), f2bf(v[2]), f2bf(v[3])};
+}
+
+// mode 0: modulate with per-frame (shift, scale_p1); mode 1: affine (w, b) with row stride.
+template <int NC, typename TIn, typename TOut, int MODE>
+__global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int64_t M, float eps,
+                                                 const float* __restrict__ p0, const float* __restrict__ p1,
+                                                 int64_t pstride, int64_t rows_per_frame,
+                                                 TOut* __restrict__ y) {
+  constexpr int D = NC * 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const TIn* xr = x + row * D;
+  float v[NC][4];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    load4<TIn>(xr + c * 256 + lane * 4, v[c]);
+    s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
+  }
+  const float mean = wave_sum(s) * (1.0f / D);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[c][j] -= mean;
+      q += v[c][j] * v[c][j];
+    }
+  const float rstd = rsqrtf(wave_sum(q) * (1.0f / D) + eps);
+  const float* a;
+  const float* b;
+  if (MODE == 0) {
+    const int64_t f = row / rows_per_frame;
+    a = p1 + f * pstride;  // scale_p1
+    b = p0 + f * pstride;  // shift
+  } else {
+    a = p0 + row * pstride;  // w
+    b = p1 + row * pstride;  // b
+  }
+  TOut* yr = y + row * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 256 + lane * 4;
+    const f32x4 av = *reinterpret_cast<const f32x4*>(a + k);
+    const f32x4 bv = *reinterpret_cast<const f32x4*>(b + k);
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[c][j] * rstd * av[j] + bv[j];
+    store4<TOut>(yr + k, o);
+  }
+}
+
+template <typename TIn, typename TOut, int MODE>
+hipError_t ln_dispatch(const TIn* x, int64_t M, int64_t D, float eps, const float* p0,
+                       const float* p1, int64_t pstride, int64_t rpf, TOut* y, hipStream_t s) {
+  const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  switch (D) {
+    case 256: hipLaunchKernelGGL((ln_kernel<1, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 512: hipLaunchKernelGGL((ln_kernel<2, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 1024: hipLaunchKernelGGL((ln_kernel<4, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 2048: hipLaunchKernelGGL((ln_kernel<8, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 4096: hipLaunchKernelGGL((ln_kernel<16, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int finish(hipError_t e, const char* what) {
+  if (e == hipErrorInvalidValue) {
+    oasis::set_error("%s: D must be one of 256, 512, 1024, 2048, 4096", what);
+    return OASIS_ERR_SHAPE;
+  }
+  if (e != hipSuccess) {
+    oasis::set_error("%s launch failed: %s", what, hipGetErrorString(e));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
+}  // namespace
+
+extern "C" int oasis_ln_modulate(const float* x, int64_t M, int64_t D, const float* shift,
+                                 const float* scale_p1, int64_t ada_fstride, int64_t rows_per_frame,
+                                 void* y_bf16, float eps, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && shift && scale_p1 && y_bf16, OASIS_ERR_NULL, "ln_modulate: null pointer");
+  OASIS_REQUIRE(M > 0 && rows_per_frame > 0, OASIS_ERR_SHAPE, "ln_modulate: bad M/rows_per_frame");
+  return finish(ln_dispatch<float, bf16, 0>(x, M, D, eps, shift, scale_p1, ada_fstride, rows_per_frame,
+                                            static_cast<bf16*>(y_bf16), static_cast<hipStream_t>(stream)),
+                "ln_modulate");
+}
+
+extern "C" int oasis_ln_affine(const float* x, int64_t M, int64_t D, const float* w, const float* b,
+                               void* y_bf16, float eps, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && w && b && y_bf16, OASIS_ERR_NULL, "ln_affine: null pointer");
+  OASIS_REQUIRE(M > 0, OASIS_ERR_SHAPE, "ln_affine: bad M");
+  return finish(ln_dispatch<float, bf16, 1>(x, M, D, eps, w, b, 0, 1, static_cast<bf16*>(y_bf16),
+                                            static_cast<hipStream_t>(stream)),
+                "ln_affine");
+}
+
+extern "C" int oasis_layernorm(const void* x, const void* weight, const void* bias, int64_t wb_ld,
+                               void* out, int64_t rows, int64_t cols, float eps, int dtype,
+                               oasis_stream_t stream) {
+  OASIS_REQUIRE(x && weight && bias && out, OASIS_ERR_NULL, "layernorm: null pointer");
+  OASIS_REQUIRE(rows > 0 && wb_ld >= 0, OASIS_ERR_SHAPE, "layernorm: bad rows/wb_ld");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // weight/bias are fp32 for both dtypes (the Python surface upcasts them once).
+  if (dtype == OASIS_F32)
+    return finish(ln_dispatch<float, float, 1>(static_cast<const float*>(x), rows, cols, eps,
+                                               static_cast<const float*>(weight), static_cast<const float*>(bias),
+                                               wb_ld, 1, static_cast<float*>(out), s),
+                  "layernorm");
+  if (dtype == OASIS_BF16)
+    return finish(ln_dispatch<bf16, bf16, 1>(static_cast<const bf16*>(x), rows, cols, eps,
+                                             static_cast<const float*>(weight), static_cast<const float*>(bias),
+                                             wb_ld, 1, static_cast<bf16*>(out), s),
+                  "layernorm");
+  oasis::set_error("layernorm: unsupported dtype %d", dtype);
+  return OASIS_ERR_DTYPE;
+}

@@ -1,0 +1,84 @@
+// Shared device helpers for the Oasis gfx950 kernels.
+//
+// Storage types: activations that feed MFMA are bf16; the residual stream,
+// adaLN parameters, biases, RoPE tables and all accumulators are fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "oasis_hip.h"
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+
+#define OASIS_DEV static __device__ __forceinline__
+
+// ---- error reporting (host) -------------------------------------------------
+namespace oasis {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+// acc = A[M,K] @ B[N,K]^T with the given epilogue (gemm.hip).
+int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                const oasis_epilogue_t& epi, hipStream_t s);
+}  // namespace oasis
+
+#define OASIS_REQUIRE(cond, code, ...)          \
+  do {                                          \
+    if (!(cond)) {                              \
+      oasis::set_error(__VA_ARGS__);            \
+      return (code);                            \
+    }                                           \
+  } while (0)
+
+// ---- conversions ------------------------------------------------------------
+OASIS_DEV float bf2f(bf16 v) { return (float)v; }
+OASIS_DEV bf16 f2bf(float v) { return (bf16)v; }  // round-to-nearest-even
+
+OASIS_DEV bf16x8 pack8(const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = f2bf(v[i]);
+  return r;
+}
+
+OASIS_DEV void unpack8(bf16x8 p, float* v) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = bf2f(p[i]);
+}
+
+// ---- wave reductions (64 lanes) ---------------------------------------------
+OASIS_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+OASIS_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---- activations ------------------------------------------------------------
+// tanh-GELU written as x * sigmoid(2u): 0.5 x (1 + tanh(u)) == x / (1 + exp(-2u)),
+// u = sqrt(2/pi) (x + 0.044715 x^3).
+OASIS_DEV float gelu_tanh(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  return x / (1.0f + __expf(-2.0f * u));
+}
+
+OASIS_DEV float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
+
+OASIS_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// ---- MFMA -------------------------------------------------------------------
+// v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8*(l/16)+j] and
+// B[8*(l/16)+j][l%16] (j=0..7) and receives D[4*(l/16)+i][l%16] (i=0..3).
+OASIS_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}

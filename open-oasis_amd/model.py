@@ -1,0 +1,436 @@
+"""Device-resident Oasis DiT, ViT VAE decoder and the DDIM frame pipeline.
+
+Host side of the hot path: it lays the weights out in HBM once, owns the activation
+workspaces (allocated up front, so nothing allocates inside a step or a captured
+graph), fills the C structs of include/oasis_hip.h and calls the composite entry
+points of liboasis_hip.so on a torch-ROCm stream.
+
+HBM layout (bf16 weights in the nn.Linear [out, in] layout, fp32 biases/tables):
+  - ``ada_w``: every sub-block's adaLN projection stacked, then the final layer's:
+    [n_sub*6D + 2D, D] (406 MB at Oasis-500M). One skinny-GEMM pass over it produces
+    the adaLN rows of all 33 consumers for every conditioning row at once.
+  - per sub-block: qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
+    contiguous (37.7 MB of the 1.21 GB weight set per sub-block incl. adaLN).
+  - small: final_w [64, D], patch-embed [D, 64] in (p, q, c) column order, conditioning
+    MLP and action projection (zero-padded to 64 inputs), RoPE cos/sin tables.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib as L
+
+HEAD_DIM = 64
+
+
+def _count(w, pattern):
+    n = 0
+    while (pattern % n) in w:
+        n += 1
+    return n
+
+
+def _axial_angles(freqs, gh, gw):
+    """Axial 2D RoPE angles [gh*gw, 4F]: dims [0,2F) row position, [2F,4F) column
+    position, positions linspace(-1, 1), each frequency repeated for its pair
+    (precompute_spatial_rope_freqs, oasis_inference.py:344-362)."""
+    hp = torch.linspace(-1, 1, gh, dtype=torch.float64)
+    wp = torch.linspace(-1, 1, gw, dtype=torch.float64)
+    f = freqs.double()
+    ha = (hp[:, None] * f[None]).repeat_interleave(2, dim=1)   # [gh, 2F]
+    wa = (wp[:, None] * f[None]).repeat_interleave(2, dim=1)   # [gw, 2F]
+    a = torch.cat([ha[:, None, :].expand(gh, gw, -1), wa[None, :, :].expand(gh, gw, -1)], dim=-1)
+    return a.reshape(gh * gw, -1)
+
+
+def rope_tables(angles, head_dim=HEAD_DIM):
+    """cos and sign-baked sin ([-sin, +sin] per pair) over a full head; identity past
+    the rotated dims (build_*_rope_device_tables, oasis_inference.py:390-403,464-473)."""
+    n, rot = angles.shape
+    cos = torch.ones(n, head_dim, dtype=torch.float64)
+    sin = torch.zeros(n, head_dim, dtype=torch.float64)
+    cos[:, :rot] = torch.cos(angles)
+    sin[:, :rot] = torch.sin(angles)
+    sin[:, 0:rot:2] *= -1
+    return cos.float(), sin.float()
+
+
+def temporal_angles(freqs, t_max):
+    """1D angles [t_max, 2F] at positions arange (oasis_inference.py:364-373)."""
+    pos = torch.arange(t_max, dtype=torch.float64)
+    return (pos[:, None] * freqs.double()[None]).repeat_interleave(2, dim=1)
+
+
+class DiT:
+    """Oasis DiT weights resident on one GPU."""
+
+    def __init__(self, w, device="cuda", grid=(9, 16), t_max=32):
+        self.device = torch.device(device)
+        dev = self.device
+        self.d = d = w["t_emb.w2"].shape[0]
+        assert d % HEAD_DIM == 0
+        self.n_heads = d // HEAD_DIM
+        self.n_blocks = _count(w, "blocks.%d.s.ada_w")
+        self.n_sub = 2 * self.n_blocks
+        assert 0 < self.n_sub <= L.MAX_SUB
+        self.d_mlp = w["blocks.0.s.fc1_w"].shape[0]
+        self.grid = grid
+        self.P = grid[0] * grid[1]
+        self.in_ch = w["x_emb.w"].shape[1]
+        self.patch_dim = w["final.w"].shape[0]
+        self.freq_dim = w["t_emb.w0"].shape[1]
+        self.ext_dim = w["ext.w"].shape[1]
+        self.ext_pad = 64 * ((self.ext_dim + 63) // 64)
+        self.t_max = t_max
+        bf = torch.bfloat16
+        keep = []
+
+        def put(t, dtype):
+            x = t.to(device=dev, dtype=dtype).contiguous()
+            keep.append(x)
+            return x
+
+        # adaLN projections of all sub-blocks + the final layer, +1 folded into each scale chunk
+        ws, bs = [], []
+        for i in range(self.n_blocks):
+            for kind in "st":
+                ws.append(w["blocks.%d.%s.ada_w" % (i, kind)])
+                b = w["blocks.%d.%s.ada_b" % (i, kind)].float().clone()
+                b[d:2 * d] += 1.0
+                b[4 * d:5 * d] += 1.0
+                bs.append(b)
+        ws.append(w["final.ada_w"])
+        fb = w["final.ada_b"].float().clone()
+        fb[d:2 * d] += 1.0
+        bs.append(fb)
+        self.ada_width = self.n_sub * 6 * d + 2 * d
+        self.ada_w = put(torch.cat([x.to(bf) for x in ws], 0), bf)
+        self.ada_b = put(torch.cat(bs, 0), torch.float32)
+        del ws, bs
+
+        S = L.DiTWeights()
+        S.n_sub, S.d_model, S.n_heads, S.d_mlp = self.n_sub, d, self.n_heads, self.d_mlp
+        S.grid_h, S.grid_w, S.patch_dim = grid[0], grid[1], self.patch_dim
+        S.freq_dim, S.ext_dim_pad = self.freq_dim, self.ext_pad
+        S.ada_w, S.ada_b = self.ada_w.data_ptr(), self.ada_b.data_ptr()
+        for j in range(self.n_sub):
+            p = "blocks.%d.%s." % (j // 2, "st"[j % 2])
+            S.qkv_w[j] = put(w[p + "qkv_w"], bf).data_ptr()
+            S.out_w[j] = put(w[p + "out_w"], bf).data_ptr()
+            S.out_b[j] = put(w[p + "out_b"], torch.float32).data_ptr()
+            S.fc1_w[j] = put(w[p + "fc1_w"], bf).data_ptr()
+            S.fc1_b[j] = put(w[p + "fc1_b"], torch.float32).data_ptr()
+            S.fc2_w[j] = put(w[p + "fc2_w"], bf).data_ptr()
+            S.fc2_b[j] = put(w[p + "fc2_b"], torch.float32).data_ptr()
+        S.final_w = put(w["final.w"], bf).data_ptr()
+        S.final_b = put(w["final.b"], torch.float32).data_ptr()
+        # patch embed: conv [D, C, 2, 2] -> [D, (p, q, c)] (W_rt of oasis_inference.py:1821-1826)
+        cw = w["x_emb.w"]
+        S.xemb_w = put(cw.permute(0, 2, 3, 1).reshape(d, -1), bf).data_ptr()
+        S.xemb_b = put(w["x_emb.b"], torch.float32).data_ptr()
+        S.temb_w0 = put(w["t_emb.w0"], bf).data_ptr()
+        S.temb_b0 = put(w["t_emb.b0"], torch.float32).data_ptr()
+        S.temb_w2 = put(w["t_emb.w2"], bf).data_ptr()
+        S.temb_b2 = put(w["t_emb.b2"], torch.float32).data_ptr()
+        ext = torch.zeros(d, self.ext_pad, dtype=bf)
+        ext[:, :self.ext_dim] = w["ext.w"].to(bf)
+        S.ext_w = put(ext, bf).data_ptr()
+        S.ext_b = put(w["ext.b"], torch.float32).data_ptr()
+        sc, ss = rope_tables(_axial_angles(w["rope.spatial_freqs"].float(), *grid))
+        tc, ts = rope_tables(temporal_angles(w["rope.temporal_freqs"].float(), t_max))
+        self.s_cos, self.s_sinp = put(sc, torch.float32), put(ss, torch.float32)
+        self.t_cos, self.t_sinp = put(tc, torch.float32), put(ts, torch.float32)
+        S.s_cos, S.s_sinp = self.s_cos.data_ptr(), self.s_sinp.data_ptr()
+        S.t_cos, S.t_sinp = self.t_cos.data_ptr(), self.t_sinp.data_ptr()
+        S.t_max = t_max
+        self.struct = S
+        self._keep = keep
+
+    @property
+    def weight_bytes(self):
+        return sum(t.numel() * t.element_size() for t in self._keep)
+
+    def workspace(self, max_rows, max_cond=16):
+        return DiTWorkspace(self, max_rows, max_cond)
+
+    # -- building blocks ---------------------------------------------------------------
+    def conditioning(self, t, actions, ws, stream=None):
+        """ada rows [R, ada_width] for R frames: cond = MLP(temb(t)) + ext(action), then
+        silu + every adaLN projection. t: [R] fp32, actions: [R, ext_dim] fp32 (device)."""
+        R = t.shape[0]
+        assert R <= ws.max_cond
+        ws.t[:R].copy_(t.reshape(-1))
+        ws.act[:R, :self.ext_dim].copy_(actions.reshape(R, -1))
+        ws.act[:R, self.ext_dim:].zero_()
+        self.conditioning_inplace(R, ws, stream)
+        return ws.ada[:R]
+
+    def conditioning_inplace(self, R, ws, stream=None):
+        """Conditioning from ws.t[:R] / ws.act[:R] into ws.cond / ws.ada (no host work)."""
+        s = L.stream_handle(stream)
+        for r0 in range(0, R, 16):
+            n = min(16, R - r0)
+            L.call("oasis_dit_conditioning", ctypes.byref(self.struct), L.ptr(ws.t[r0:]),
+                   L.ptr(ws.act[r0:]), n, L.ptr(ws.tfreq[r0:]), L.ptr(ws.hid[r0:]),
+                   L.ptr(ws.cond[r0:]), L.ptr(ws.ada[r0:]), s)
+
+    def adaln_from_cond(self, cond, ws, stream=None):
+        """ada rows from given (pre-SiLU) cond vectors [R, D] (the reference passes cond
+        computed on the host, oasis_inference.py:1406-1427)."""
+        R = cond.shape[0]
+        ws.cond[:R].copy_(cond)
+        s = L.stream_handle(stream)
+        for r0 in range(0, R, 16):
+            n = min(16, R - r0)
+            L.call("oasis_gemv_bf16", L.ptr(ws.cond[r0:]), self.d, n, L.ptr(self.ada_w),
+                   self.ada_width, self.d, L.ptr(self.ada_b), L.ptr(ws.ada[r0:]), self.ada_width,
+                   L.ACT_SILU, L.ACT_NONE, 0, s)
+        return ws.ada[:R]
+
+    def patch_embed(self, patches, out, stream=None):
+        """out[M, D] = patches[M, 64] @ W_rt + b (patches in (p, q, c) column order)."""
+        M = patches.shape[0]
+        L.call("oasis_small_linear", L.ptr(patches), self.patch_dim, M, self.patch_dim,
+               ctypes.c_void_p(self.struct.xemb_w), self.d, ctypes.c_void_p(self.struct.xemb_b),
+               L.ptr(out), self.d, L.stream_handle(stream))
+
+    def sub_blocks_inplace(self, ws, B, T, ada, ada_fstride, j0, j1, stream=None):
+        """Sub-blocks [j0, j1) on ws.x[:B*T*P] in place (run_sub_block, oasis_inference.py:995)."""
+        L.call("oasis_dit_sub_blocks", ctypes.byref(self.struct), ctypes.byref(ws.struct), B, T,
+               L.ptr(ada), ada_fstride, j0, j1, L.stream_handle(stream))
+
+    def forward_inplace(self, ws, B, T, ada, ada_fstride, v_out, stream=None):
+        """Blocks + final layer on ws.x[:B*T*P] (in place); v_out [B*T*P, 64] fp32."""
+        L.call("oasis_dit_forward", ctypes.byref(self.struct), ctypes.byref(ws.struct), B, T,
+               L.ptr(ada), ada_fstride, L.ptr(v_out), L.stream_handle(stream))
+
+
+class DiTWorkspace:
+    """Activation buffers for up to max_rows tokens and max_cond conditioning rows."""
+
+    def __init__(self, dit, max_rows, max_cond=16):
+        dev, d, bf = dit.device, dit.d, torch.bfloat16
+        self.max_rows, self.max_cond = max_rows, max_cond
+        self.x = torch.zeros(max_rows, d, device=dev)
+        self.h = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.q = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.k = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.v = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.attn = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.mlp = torch.zeros(max_rows, dit.d_mlp, device=dev, dtype=bf)
+        self.v_out = torch.zeros(max_rows, dit.patch_dim, device=dev)
+        self.t = torch.zeros(max_cond, device=dev)
+        self.act = torch.zeros(max_cond, dit.ext_pad, device=dev)
+        self.tfreq = torch.zeros(max_cond, dit.freq_dim, device=dev)
+        self.hid = torch.zeros(max_cond, d, device=dev)
+        self.cond = torch.zeros(max_cond, d, device=dev)
+        self.ada = torch.zeros(max_cond, dit.ada_width, device=dev)
+        S = L.DiTBuffers()
+        S.max_rows = max_rows
+        for name in ("x", "h", "q", "k", "v", "attn", "mlp"):
+            setattr(S, name, getattr(self, name).data_ptr())
+        self.struct = S
+
+
+class VAE:
+    """ViT VAE decoder weights resident on one GPU."""
+
+    def __init__(self, vw, device="cuda", grid=(18, 32), patch=20):
+        dev = self.device = torch.device(device)
+        self.d = d = vw["pq_w"].shape[0]
+        self.n_heads = d // HEAD_DIM
+        self.depth = _count(vw, "dec.%d.qkv_w")
+        assert 0 < self.depth <= L.MAX_SUB
+        self.d_mlp = vw["dec.0.fc1_w"].shape[0]
+        self.latent_dim = vw["pq_w"].shape[1]
+        self.grid, self.patch = grid, patch
+        self.L = grid[0] * grid[1]
+        bf, f32 = torch.bfloat16, torch.float32
+        keep = []
+
+        def put(t, dtype):
+            x = t.to(device=dev, dtype=dtype).contiguous()
+            keep.append(x)
+            return x.data_ptr()
+
+        S = L.VAEWeights()
+        S.depth, S.d_model, S.n_heads, S.d_mlp = self.depth, d, self.n_heads, self.d_mlp
+        S.latent_dim, S.grid_h, S.grid_w, S.patch = self.latent_dim, grid[0], grid[1], patch
+        S.pq_w, S.pq_b = put(vw["pq_w"], bf), put(vw["pq_b"], f32)
+        for i in range(self.depth):
+            p = "dec.%d." % i
+            S.n1_w[i], S.n1_b[i] = put(vw[p + "n1_w"], f32), put(vw[p + "n1_b"], f32)
+            S.qkv_w[i], S.qkv_b[i] = put(vw[p + "qkv_w"], bf), put(vw[p + "qkv_b"], f32)
+            S.proj_w[i], S.proj_b[i] = put(vw[p + "proj_w"], bf), put(vw[p + "proj_b"], f32)
+            S.n2_w[i], S.n2_b[i] = put(vw[p + "n2_w"], f32), put(vw[p + "n2_b"], f32)
+            S.fc1_w[i], S.fc1_b[i] = put(vw[p + "fc1_w"], bf), put(vw[p + "fc1_b"], f32)
+            S.fc2_w[i], S.fc2_b[i] = put(vw[p + "fc2_w"], bf), put(vw[p + "fc2_b"], f32)
+        S.norm_w, S.norm_b = put(vw["norm_w"], f32), put(vw["norm_b"], f32)
+        S.pred_w, S.pred_b = put(vw["pred_w"], bf), put(vw["pred_b"], f32)
+        c, s = rope_tables(_axial_angles(vw["rope.vae_freqs"].float(), *grid))
+        S.rope_cos, S.rope_sinp = put(c, f32), put(s, f32)
+        self.struct = S
+        self._keep = keep
+        self.frame_shape = (3, grid[0] * patch, grid[1] * patch)
+
+    @property
+    def weight_bytes(self):
+        return sum(t.numel() * t.element_size() for t in self._keep)
+
+    def workspace(self):
+        return VAEWorkspace(self)
+
+    def decode_inplace(self, latent, frame, ws, stream=None):
+        L.call("oasis_vae_decode", ctypes.byref(self.struct), ctypes.byref(ws.struct),
+               L.ptr(latent), L.ptr(frame), L.stream_handle(stream))
+
+
+class VAEWorkspace:
+    def __init__(self, vae):
+        dev, d, n, bf = vae.device, vae.d, vae.L, torch.bfloat16
+        self.x = torch.zeros(n, d, device=dev)
+        self.h = torch.zeros(n, d, device=dev, dtype=bf)
+        self.q = torch.zeros(n, d, device=dev, dtype=bf)
+        self.k = torch.zeros(n, d, device=dev, dtype=bf)
+        self.v = torch.zeros(n, d, device=dev, dtype=bf)
+        self.attn = torch.zeros(n, d, device=dev, dtype=bf)
+        self.mlp = torch.zeros(n, vae.d_mlp, device=dev, dtype=bf)
+        self.latent = torch.zeros(n, vae.latent_dim, device=dev)
+        self.frame = torch.zeros(*vae.frame_shape, device=dev)
+        S = L.VAEBuffers()
+        for name in ("x", "h", "q", "k", "v", "attn", "mlp"):
+            setattr(S, name, getattr(self, name).data_ptr())
+        self.struct = S
+
+
+class Graph:
+    """A hipGraph captured from a sequence of liboasis_hip calls on one stream
+    (ttnn begin/end_trace_capture + execute_trace, oasis_inference.py:2133-2146,2224)."""
+
+    def __init__(self, fn, stream):
+        self.stream = stream
+        self.exec = ctypes.c_void_p()
+        torch.cuda.synchronize()
+        h = L.stream_handle(stream)
+        L.call("oasis_graph_begin", h)
+        try:
+            fn()
+        except BaseException:
+            g = ctypes.c_void_p()
+            L.lib().oasis_graph_end(h, ctypes.byref(g))
+            if g.value:
+                L.lib().oasis_graph_destroy(g)
+            raise
+        L.call("oasis_graph_end", h, ctypes.byref(self.exec))
+
+    def launch(self):
+        L.call("oasis_graph_launch", self.exec, L.stream_handle(self.stream))
+
+    def __del__(self):
+        if getattr(self, "exec", None) is not None and self.exec.value:
+            L.lib().oasis_graph_destroy(self.exec)
+            self.exec = None
+
+
+class DiTStep:
+    """One full DiT denoising step for B streams of T frames, on fixed device buffers:
+    conditioning (timestep MLP + action projection + every adaLN projection), patch embed
+    of the patch-space latent, 16 x (spatial, temporal) sub-blocks and the final layer.
+    Inputs: self.patches [B*T*P, 64], self.ws.t [B*T], self.ws.act [B*T, :25]."""
+
+    def __init__(self, dit, B=1, T=2, stream=None):
+        self.dit, self.B, self.T = dit, B, T
+        self.M = B * T * dit.P
+        self.ws = dit.workspace(self.M, max_cond=max(16, B * T))
+        self.patches = torch.zeros(self.M, dit.patch_dim, device=dit.device)
+        self.stream = stream if stream is not None else torch.cuda.Stream(device=dit.device)
+        self.graph = None
+
+    def set_inputs(self, patches, t, actions):
+        R = self.B * self.T
+        self.patches.copy_(patches.reshape(self.M, -1))
+        self.ws.t[:R].copy_(t.reshape(-1))
+        self.ws.act[:R].zero_()
+        self.ws.act[:R, :self.dit.ext_dim].copy_(actions.reshape(R, -1))
+        torch.cuda.synchronize(self.dit.device)
+
+    def enqueue(self):
+        d, ws = self.dit, self.ws
+        d.conditioning_inplace(self.B * self.T, ws, self.stream)
+        d.patch_embed(self.patches, ws.x, self.stream)
+        d.forward_inplace(ws, self.B, self.T, ws.ada, d.ada_width, ws.v_out, self.stream)
+
+    def capture(self):
+        self.graph = Graph(self.enqueue, self.stream)
+        return self.graph
+
+    def run(self):
+        """Enqueue one step on self.stream; the caller's current stream waits for it."""
+        if self.graph is not None:
+            self.graph.launch()
+        else:
+            self.enqueue()
+        torch.cuda.current_stream(self.dit.device).wait_stream(self.stream)
+        return self.ws.v_out[:self.M]
+
+
+class FramePipeline:
+    """One generated frame (reference traced frame, oasis_inference.py:2131-2148):
+    conditioning for the context row and the n_steps generated rows, context patch
+    embed, n_steps T=2 DDIM v-prediction steps, bridge, VAE decode and unpatchify.
+    Inputs: self.chunk [P, 64] noise (patch space), self.ctx_patches [P, 64],
+    self.ws.t / self.ws.act rows [0] context and [1+i] generated frame at step i."""
+
+    def __init__(self, dit, vae, steps, alphas_cumprod, stream=None):
+        from .schedule import ddim_coefficients
+        self.dit, self.vae = dit, vae
+        self.steps = list(steps)
+        self.n = len(self.steps)
+        P, dev = dit.P, dit.device
+        self.ws = dit.workspace(2 * P, max_cond=max(16, 1 + self.n))
+        self.vws = vae.workspace()
+        self.chunk = torch.zeros(P, dit.patch_dim, device=dev)
+        self.ctx_patches = torch.zeros(P, dit.patch_dim, device=dev)
+        self.ctx_z = torch.zeros(P, dit.d, device=dev)
+        self.coeffs = (ctypes.c_float * (6 * self.n))(*ddim_coefficients(alphas_cumprod, self.steps))
+        self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
+        self.graph = None
+
+    def set_inputs(self, noise_patches, ctx_patches, ctx_t, ctx_action, gen_action):
+        R = 1 + self.n
+        self.chunk.copy_(noise_patches)
+        self.ctx_patches.copy_(ctx_patches)
+        t = torch.tensor([float(ctx_t)] + [float(t) for t, _ in self.steps])
+        self.ws.t[:R].copy_(t)
+        self.ws.act[:R].zero_()
+        e = self.dit.ext_dim
+        self.ws.act[0, :e].copy_(ctx_action)
+        self.ws.act[1:R, :e].copy_(gen_action.reshape(1, -1).expand(self.n, -1))
+        torch.cuda.synchronize(self.dit.device)
+
+    def enqueue(self):
+        d, ws, s = self.dit, self.ws, self.stream
+        d.conditioning_inplace(1 + self.n, ws, s)
+        d.patch_embed(self.ctx_patches, self.ctx_z, s)
+        L.call("oasis_ddim_frame", ctypes.byref(d.struct), ctypes.byref(ws.struct),
+               ctypes.byref(self.vae.struct), ctypes.byref(self.vws.struct), L.ptr(self.chunk),
+               L.ptr(self.ctx_z), L.ptr(ws.ada), self.n, ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.v_out),
+               L.ptr(self.vws.latent), L.ptr(self.vws.frame), L.stream_handle(s))
+
+    def capture(self):
+        self.graph = Graph(self.enqueue, self.stream)
+        return self.graph
+
+    def run(self):
+        """Enqueue one frame on self.stream; the caller's current stream waits for it."""
+        if self.graph is not None:
+            self.graph.launch()
+        else:
+            self.enqueue()
+        torch.cuda.current_stream(self.dit.device).wait_stream(self.stream)
+        return self.vws.frame
+
+
+def attention_scale(head_dim=HEAD_DIM):
+    return 1.0 / math.sqrt(head_dim)

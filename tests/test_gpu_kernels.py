@@ -1,0 +1,400 @@
+"""Per-kernel parity on the GPU through the C ABI against fp32 CPU references.
+
+Inputs are seeded; GEMM-type references use the same bf16-rounded operands the kernel
+sees, so the only differences are accumulation order and the bf16 rounding of outputs.
+"""
+import ctypes
+import math
+
+import pytest
+import torch
+
+import oracle
+from helpers import L, assert_close, bf, cuda, stream, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+_ALIVE = []  # device tensors whose raw pointers were handed to C (freed at test end)
+
+
+@pytest.fixture(autouse=True)
+def _release_device_temporaries():
+    yield
+    _ALIVE.clear()
+
+
+def dev(t):
+    """Device copy kept alive until the test ends (a bare temporary could be freed and its
+    memory reused before the kernel reading it has run)."""
+    d = cuda(t)
+    _ALIVE.append(d)
+    return d
+
+
+def _epi(**kw):
+    e = L.Epilogue()
+    for k, v in kw.items():
+        if isinstance(v, torch.Tensor):
+            _ALIVE.append(v)
+            v = v.data_ptr()
+        setattr(e, k, v)
+    return e
+
+
+def _gemm(A, B, M, N, K, epi, lda=None, ldb=None):
+    L.call("oasis_gemm_bf16", L.ptr(A), lda or K, L.ptr(B), ldb or K, M, N, K, ctypes.byref(epi), stream())
+
+
+# ---------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("M,N,K", [(288, 3072, 1024), (288, 1024, 4096), (576, 1200, 1024), (13, 64, 64),
+                                   (1, 8, 128), (100, 520, 192)])
+def test_gemm_store_f32(M, N, K):
+    g = _gen(M + N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g)
+    out = torch.zeros(M, N, device="cuda")
+    _gemm(dev(A), dev(B), M, N, K, _epi(kind=L.EPI_STORE_F32, bias=dev(bias), out_f32=out, ld_out=N))
+    sync()
+    ref = A.float() @ B.float().t() + bias
+    assert_close(out, ref, 0.999999, 1e-4, "gemm %dx%dx%d" % (M, N, K))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "gelu_tanh", "gelu_erf"])
+def test_gemm_bf16_epilogues(kind):
+    M, N, K = 288, 4096, 1024
+    g = _gen(3)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.03).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    out = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+    k = {"bf16": L.EPI_STORE_BF16, "gelu_tanh": L.EPI_GELU_TANH, "gelu_erf": L.EPI_GELU_ERF}[kind]
+    _gemm(dev(A), dev(B), M, N, K, _epi(kind=k, bias=dev(bias), out_bf16=out, ld_out=N))
+    sync()
+    ref = A.float() @ B.float().t() + bias
+    ref = {"bf16": ref, "gelu_tanh": oracle.gelu_tanh(ref), "gelu_erf": oracle.gelu_erf(ref)}[kind]
+    assert_close(out, ref, 0.99999, 1e-2, "gemm epilogue " + kind)
+
+
+def test_gemm_gated_and_plain_residual():
+    M, N, K, P = 288, 1024, 4096, 144
+    g = _gen(4)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g)
+    x0 = torch.randn(M, N, generator=g)
+    fstride = 3 * N
+    ada = torch.randn(2, fstride, generator=g)
+    gate = ada[:, N:2 * N]
+    x = dev(x0)
+    ada_d = dev(ada)
+    _gemm(dev(A), dev(B), M, N, K, _epi(kind=L.EPI_GATED_RES, bias=dev(bias), out_f32=x, ld_out=N,
+                                          gate=ada_d[0, N:], gate_fstride=fstride, rows_per_frame=P))
+    sync()
+    y = A.float() @ B.float().t() + bias
+    ref = x0 + torch.cat([gate[0].expand(P, N), gate[1].expand(P, N)]) * y
+    assert_close(x, ref, 0.999999, 1e-5, "gated residual")
+    _gemm(dev(A), dev(B), M, N, K, _epi(kind=L.EPI_RESIDUAL, bias=dev(bias), out_f32=x, ld_out=N))
+    sync()
+    assert_close(x, ref + y, 0.999999, 1e-5, "residual")
+
+
+@pytest.mark.parametrize("layout", ["spatial", "temporal", "vae"])
+def test_gemm_qkv_rope(layout):
+    H, D = 4, 256
+    if layout == "vae":
+        B_, T, P, K = 1, 1, 576, 256
+    else:
+        B_, T, P, K = 2, 2, 144, 256
+    M, N = B_ * T * P, 3 * D
+    g = _gen(5)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    if layout == "spatial":
+        ang = oracle.spatial_rope_angles(torch.rand(16, generator=g) * 2, 9, 16)
+    elif layout == "temporal":
+        ang = oracle.temporal_rope_angles(torch.rand(32, generator=g), T)
+    else:
+        ang = oracle.vae_rope_angles(torch.rand(8, generator=g) * 2, 18, 32)
+    cos, sinp = oracle.rope_cos_sinperm(ang, 64)
+    q, k, v = (torch.zeros(M * D, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+    if layout == "temporal":
+        s_b, s_t, s_p, s_h = P * H * T * 64, 64, H * T * 64, T * 64
+    else:
+        s_b, s_t, s_p, s_h = T * H * P * 64, H * P * 64, 64, P * 64
+    e = _epi(kind=L.EPI_QKV_ROPE, n_heads=H, bias=dev(bias), q=q, k=k, v=v, rope_cos=dev(cos),
+             rope_sinp=dev(sinp), rope_by_frame=int(layout == "temporal"), rows_per_frame=P,
+             frames_per_stream=T, s_b=s_b, s_t=s_t, s_p=s_p, s_h=s_h)
+    _gemm(dev(A), dev(W), M, N, K, e)
+    sync()
+    y = (A.float() @ W.float().t() + bias).reshape(B_, T, P, 3, H, 64)
+    pos_c = cos[torch.arange(T)] if layout == "temporal" else cos
+    pos_s = sinp[torch.arange(T)] if layout == "temporal" else sinp
+    if layout == "temporal":
+        c4, s4 = pos_c[None, :, None, None, :], pos_s[None, :, None, None, :]
+    else:
+        c4, s4 = pos_c[None, None, :, None, :], pos_s[None, None, :, None, :]
+    rq = oracle.apply_rope_swap(y[:, :, :, 0], c4, s4)     # [B,T,P,H,64]
+    rk = oracle.apply_rope_swap(y[:, :, :, 1], c4, s4)
+    rv = y[:, :, :, 2]
+    perm = (0, 2, 3, 1, 4) if layout == "temporal" else (0, 1, 3, 2, 4)
+    for name, got, ref in (("q", q, rq), ("k", k, rk), ("v", v, rv)):
+        assert_close(got, ref.permute(*perm).contiguous(), 0.99999, 1e-2, "qkv_rope %s %s" % (layout, name))
+
+
+def test_gemm_unpatchify():
+    gh, gw, ps, D = 18, 32, 20, 256
+    M, N = gh * gw, 3 * ps * ps
+    g = _gen(6)
+    A = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, D, generator=g) * 0.1).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    frame = torch.zeros(3, gh * ps, gw * ps, device="cuda")
+    _gemm(dev(A), dev(W), M, N, D, _epi(kind=L.EPI_UNPATCHIFY, bias=dev(bias), out_f32=frame, rows_per_frame=M,
+                                          unpatch_grid_w=gw, unpatch_patch=ps, unpatch_channels=3))
+    sync()
+    ref = oracle.vae_unpatchify(A.float() @ W.float().t() + bias, gh, gw, ps)
+    assert_close(frame, ref, 0.999999, 1e-4, "unpatchify epilogue")
+
+
+def test_gemm_rejects_bad_shapes():
+    A = torch.zeros(4, 96, device="cuda", dtype=torch.bfloat16)
+    out = torch.zeros(4, 8, device="cuda")
+    with pytest.raises(L.OasisError, match="multiple of 64"):
+        _gemm(A, A, 4, 8, 96, _epi(kind=L.EPI_STORE_F32, out_f32=out, ld_out=8))
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_linear_surface(layout):
+    M, K, N = 160, 1024, 320
+    g = _gen(7)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(K, N, generator=g) * 0.05).to(torch.bfloat16)
+    wd = dev(w) if layout == 0 else dev(w.t().contiguous())
+    out = torch.zeros(M, N, device="cuda")
+    L.call("oasis_linear", L.ptr(dev(x)), L.ptr(wd), L.ptr(out), M, K, N, layout, L.F32, stream())
+    sync()
+    assert_close(out, x.float() @ w.float(), 0.999999, 1e-4, "linear layout %d" % layout)
+
+
+# ---------------------------------------------------------------- norms
+def test_ln_modulate():
+    M, D, P = 288, 1024, 144
+    g = _gen(8)
+    x = torch.randn(M, D, generator=g) * 3 + 1
+    ada = torch.randn(2, 4 * D, generator=g) * 0.2
+    shift, scale_p1 = ada[:, :D], ada[:, D:2 * D] + 1
+    ada[:, D:2 * D] += 1
+    out = torch.zeros(M, D, device="cuda", dtype=torch.bfloat16)
+    ad = dev(ada)
+    L.call("oasis_ln_modulate", L.ptr(dev(x)), M, D, L.ptr(ad[0, :]), L.ptr(ad[0, D:]), 4 * D, P, L.ptr(out),
+           1e-6, stream())
+    sync()
+    f = torch.arange(M) // P
+    ref = oracle.layer_norm(x) * scale_p1[f] + shift[f]
+    assert_close(out, ref, 0.99999, 1e-2, "ln_modulate")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layernorm_surface(dtype):
+    rows, cols = 160, 1024
+    g = _gen(9)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(dtype)
+    w = torch.randn(cols, generator=g)
+    b = torch.randn(cols, generator=g)
+    out = torch.zeros(rows, cols, device="cuda", dtype=dtype)
+    L.call("oasis_layernorm", L.ptr(dev(x)), L.ptr(dev(w)), L.ptr(dev(b)), 0, L.ptr(out), rows, cols, 1e-6,
+           L.F32 if dtype == torch.float32 else L.BF16, stream())
+    sync()
+    ref = oracle.layer_norm(x.float(), w, b)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_close(out, ref, 0.9999, tol, "layernorm %s" % dtype)
+
+
+def test_ln_affine():
+    M, D = 576, 1024
+    g = _gen(10)
+    x = torch.randn(M, D, generator=g)
+    w = torch.randn(D, generator=g)
+    b = torch.randn(D, generator=g)
+    out = torch.zeros(M, D, device="cuda", dtype=torch.bfloat16)
+    L.call("oasis_ln_affine", L.ptr(dev(x)), M, D, L.ptr(dev(w)), L.ptr(dev(b)), L.ptr(out), 1e-6, stream())
+    sync()
+    assert_close(out, oracle.layer_norm(x, w, b), 0.99999, 1e-2, "ln_affine")
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("L_", [144, 576, 37])
+def test_attention_heads_first(L_):
+    F_, H = 2, 4
+    g = _gen(11 + L_)
+    q, k, v = (torch.randn(F_ * H, L_, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    out = torch.zeros(F_ * L_, H * 64, device="cuda", dtype=torch.bfloat16)
+    L.call("oasis_attention", L.ptr(dev(q)), L.ptr(dev(k)), L.ptr(dev(v)), L.ptr(out), F_, L_, H, 0.125, stream())
+    sync()
+    ref = oracle.attention(q.float(), k.float(), v.float())          # [F*H, L, 64]
+    ref = ref.reshape(F_, H, L_, 64).permute(0, 2, 1, 3).reshape(F_ * L_, H * 64)
+    assert_close(out, ref, 0.9999, 1e-2, "attention L=%d" % L_)
+
+
+@pytest.mark.parametrize("dtype,causal,bias", [(torch.float32, False, False), (torch.bfloat16, True, False),
+                                               (torch.float32, False, True)])
+def test_sdpa_surface(dtype, causal, bias):
+    nh, sq, skv = 6, 32, 32
+    g = _gen(12)
+    Q, K, V = (torch.randn(nh * sq, 64, generator=g).to(dtype) for _ in range(3))
+    bmask = None
+    if bias:  # the reference's block-diagonal causal bias (oasis_inference.py:843-857), T=2 pairs
+        bmask = torch.zeros(sq, skv)
+        for i in range(sq):
+            for j in range(skv):
+                if i // 2 != j // 2 or j % 2 > i % 2:
+                    bmask[i, j] = -1e4
+    out = torch.zeros(nh * sq, 64, device="cuda", dtype=dtype)
+    L.call("oasis_sdpa", L.ptr(dev(Q)), L.ptr(dev(K)), L.ptr(dev(V)), L.ptr(out), nh, sq, skv, 64, 0.125,
+           L.ptr(None if bmask is None else dev(bmask)), int(causal), L.F32 if dtype == torch.float32 else L.BF16,
+           stream())
+    sync()
+    q4, k4, v4 = (t.float().reshape(nh, sq, 64) for t in (Q, K, V))
+    if bias:
+        s = q4 @ k4.transpose(1, 2) * 0.125 + bmask
+        ref = torch.softmax(s, -1) @ v4
+    else:
+        ref = oracle.attention(bf(q4), bf(k4), bf(v4), causal=causal)
+    assert_close(out, ref.reshape(nh * sq, 64), 0.9999, 2e-2, "sdpa %s causal=%s bias=%s" % (dtype, causal, bias))
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 32])
+def test_temporal_attention(T):
+    B_, P, H = 1, 144, 4
+    g = _gen(13 + T)
+    q, k, v = (torch.randn(B_, P, H, T, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    out = torch.zeros(B_ * T * P, H * 64, device="cuda", dtype=torch.bfloat16)
+    L.call("oasis_temporal_attention", L.ptr(dev(q)), L.ptr(dev(k)), L.ptr(dev(v)), L.ptr(out), B_, T, P, H,
+           0.125, stream())
+    sync()
+    ref = oracle.attention(q.float(), k.float(), v.float(), causal=True)   # [B,P,H,T,64]
+    ref = ref.permute(0, 3, 1, 2, 4).reshape(B_ * T * P, H * 64)
+    assert_close(out, ref, 0.9999, 1e-2, "temporal T=%d" % T)
+    if T == 1:  # a single causal key: out == v exactly (bf16 round trip)
+        assert torch.equal(out.cpu(), v.permute(0, 3, 1, 2, 4).reshape(B_ * T * P, H * 64))
+
+
+# ---------------------------------------------------------------- skinny GEMM
+@pytest.mark.parametrize("R,K,N,act_in,act_out,acc", [(2, 1024, 6144 * 2 + 2048, 1, 0, 0), (5, 256, 1024, 0, 1, 0),
+                                                       (16, 1024, 1024, 0, 0, 1), (1, 64, 1024, 0, 0, 0)])
+def test_gemv(R, K, N, act_in, act_out, acc):
+    g = _gen(14 + R)
+    x = torch.randn(R, K, generator=g)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g)
+    out0 = torch.randn(R, N, generator=g)
+    out = dev(out0)
+    L.call("oasis_gemv_bf16", L.ptr(dev(x)), K, R, L.ptr(dev(W)), N, K, L.ptr(dev(b)), L.ptr(out), N, act_in,
+           act_out, acc, stream())
+    sync()
+    xi = oracle.silu(x) if act_in else x
+    ref = xi.double() @ W.double().t() + b.double()
+    if act_out:
+        ref = oracle.silu(ref)
+    if acc:
+        ref = ref + out0.double()
+    # x is split into bf16 hi+lo, so the result keeps ~fp32 accuracy
+    assert_close(out, ref, 0.9999999, 1e-4, "gemv R=%d K=%d N=%d" % (R, K, N))
+
+
+# ---------------------------------------------------------------- small ops
+def test_timestep_embedding():
+    t = torch.tensor([0.0, 14.0, 249.0, 999.0, 517.0])
+    out = torch.zeros(5, 256, device="cuda")
+    L.call("oasis_timestep_embedding", L.ptr(dev(t)), 5, 256, L.ptr(out), stream())
+    sync()
+    assert_close(out, oracle.timestep_embedding(t), 0.9999999, 2e-4, "timestep embedding")
+
+
+def test_small_linear_and_ddim_and_bridge():
+    g = _gen(15)
+    x = torch.randn(144, 64, generator=g)
+    W = (torch.randn(1024, 64, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(1024, generator=g)
+    out = torch.zeros(144, 1024, device="cuda")
+    L.call("oasis_small_linear", L.ptr(dev(x)), 64, 144, 64, L.ptr(dev(W)), 1024, L.ptr(dev(b)), L.ptr(out),
+           1024, stream())
+    sync()
+    assert_close(out, x @ W.float().t() + b, 0.9999999, 1e-5, "small_linear")
+
+    ac = oracle.cosine_alphas_cumprod()
+    v = torch.randn(144, 64, generator=g)
+    chunk = dev(x)
+    c = oracle.ddim_coeffs(ac, 749, 499, last=False)
+    L.call("oasis_ddim_update", L.ptr(chunk), L.ptr(dev(v)), chunk.numel(), *[ctypes.c_float(z) for z in c],
+           stream())
+    sync()
+    assert_close(chunk, oracle.ddim_update(x, v, c), 0.9999999, 1e-5, "ddim update")
+
+    lat = torch.zeros(576, 32, device="cuda")
+    L.call("oasis_bridge", L.ptr(dev(x)), L.ptr(lat), 9, 16, 16, 32, 1.0 / oracle.SCALING_FACTOR, stream())
+    sync()
+    assert torch.allclose(lat.cpu(), oracle.bridge(x), rtol=1e-6, atol=1e-6)
+
+    patches = torch.randn(576, 1200, generator=g) * 2
+    frame = torch.zeros(3, 360, 640, device="cuda")
+    L.call("oasis_vae_unpatchify", L.ptr(dev(patches)), L.ptr(frame), 18, 32, 20, stream())
+    sync()
+    assert torch.equal(frame.cpu(), oracle.vae_unpatchify(patches))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_elementwise_surface(dtype):
+    n = 160 * 1024 + 3
+    g = _gen(16)
+    a, b, c, d = (torch.randn(n, generator=g).to(dtype) for _ in range(4))
+    code = L.F32 if dtype == torch.float32 else L.BF16
+    out = torch.zeros(n, device="cuda", dtype=dtype)
+    A, Bd, C, Dd = dev(a), dev(b), dev(c), dev(d)
+    af, bf_, cf, df = a.float(), b.float(), c.float(), d.float()
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    L.call("oasis_silu", L.ptr(A), L.ptr(out), n, code, stream())
+    sync()
+    assert_close(out, oracle.silu(af), 0.99999, tol, "silu")
+    L.call("oasis_adaln_modulate", L.ptr(A), L.ptr(Bd), L.ptr(C), L.ptr(out), n, code, stream())
+    sync()
+    assert_close(out, oracle.modulate(af, bf_, cf), 0.99999, tol, "modulate")
+    L.call("oasis_gated_residual", L.ptr(A), L.ptr(Bd), L.ptr(C), L.ptr(out), n, code, stream())
+    sync()
+    assert_close(out, af + bf_ * cf, 0.99999, tol, "gated_residual")
+    L.call("oasis_bias_gated_residual", L.ptr(A), L.ptr(Bd), L.ptr(C), L.ptr(Dd), L.ptr(out), n, code, stream())
+    sync()
+    assert_close(out, af + (bf_ + cf) * df, 0.99999, tol, "bias_gated_residual")
+
+
+def test_rope_layout_surface():
+    """Reference-layout inputs: qkv_full [SEQ, 5D] with swap columns and [SEQ, D] tables."""
+    T, S, H = 2, 160, 4
+    D = H * 64
+    g = _gen(17)
+    qkv = torch.randn(T * S, 5 * D, generator=g)
+    ang = oracle.spatial_rope_angles(torch.rand(16, generator=g), 9, 16)
+    cos, sinp = oracle.rope_cos_sinperm(ang, 64)
+    ctab = torch.zeros(T * S, D)
+    stab = torch.zeros(T * S, D)
+    for t in range(T):
+        ctab[t * S:t * S + 144] = cos.repeat(1, H)
+        stab[t * S:t * S + 144] = sinp.repeat(1, H)
+    qo, ko, vo = (torch.zeros(T * H * S, 64, device="cuda") for _ in range(3))
+    L.call("oasis_rope_layout", L.ptr(dev(qkv)), 5 * D, L.ptr(dev(ctab)), L.ptr(dev(stab)), D, 64, 1, T * S,
+           L.ptr(qo), L.ptr(ko), L.ptr(vo), T * S, S, H, 64, 0, L.F32, stream())
+    sync()
+    x = qkv.reshape(T, S, 5, H, 64)
+    c4 = ctab.reshape(T, S, H, 64)
+    s4 = stab.reshape(T, S, H, 64)
+    for i, (name, got) in enumerate((("q", qo), ("k", ko))):
+        ref = oracle.apply_rope_swap(x[:, :, i], c4, s4).permute(0, 2, 1, 3).reshape(-1, 64)
+        assert_close(got, ref, 0.999999, 1e-5, "rope_layout " + name)
+    assert torch.equal(vo.cpu(), x[:, :, 2].permute(0, 2, 1, 3).reshape(-1, 64))

@@ -1,0 +1,167 @@
+"""Model-level parity on the GPU: sub-blocks (configs 0 and 2), the full DiT step
+(config 1), the VAE decoder and the 4-step DDIM frame (config 3), graph replay and the
+context-frame invariance property. References are the fp32 CPU oracle run on the same
+bf16-valued weights the GPU holds.
+"""
+import pytest
+import torch
+
+import oracle
+from helpers import COS_STEP, COS_SUB, REL_SUB, assert_close, cuda, metrics, pkg
+
+pytestmark = pytest.mark.gpu
+
+synth = pkg.synth
+
+
+def _bf16_weights(w):
+    return {k: (v.to(torch.bfloat16) if v.dtype == torch.float32 and k != "rope.spatial_freqs"
+                and k != "rope.temporal_freqs" else v) for k, v in w.items()}
+
+
+def _single_block_dit(sub_w, kind, d=1024, d_mlp=4096, spatial_freqs=None, temporal_freqs=None):
+    """A one-block DiT whose `kind` sub-block carries `sub_w` (the other one is zeros)."""
+    dr = synth.Draw(99)
+    w = synth.dit_weights(dr, n_blocks=1, d=d, n_heads=d // 64, d_mlp=d_mlp)
+    for k, v in sub_w.items():
+        w["blocks.0.%s.%s" % (kind, k)] = v.to(torch.bfloat16)
+    if spatial_freqs is not None:
+        w["rope.spatial_freqs"] = spatial_freqs
+    if temporal_freqs is not None:
+        w["rope.temporal_freqs"] = temporal_freqs
+    return w
+
+
+def _check_sub_block(x, cond, w, kind, T, what):
+    dit = pkg.DiT(w, "cuda", t_max=max(T, 2))
+    ws = dit.workspace(T * dit.P, max_cond=max(16, T))
+    ada = dit.adaln_from_cond(cuda(cond), ws)
+    ws.x[:T * dit.P].copy_(cuda(x.reshape(T * dit.P, -1)))
+    j = 0 if kind == "s" else 1
+    dit.sub_blocks_inplace(ws, 1, T, ada, dit.ada_width, j, j + 1)
+    torch.cuda.synchronize()
+    got = ws.x[:T * dit.P].cpu().reshape(T, dit.P, -1)
+    blk = {k[len("blocks.0.%s." % kind):]: v for k, v in w.items() if k.startswith("blocks.0.%s." % kind)}
+    if kind == "s":
+        cs, ss = oracle.rope_cos_sinperm(oracle.spatial_rope_angles(w["rope.spatial_freqs"].float()), 64)
+    else:
+        cs, ss = oracle.rope_cos_sinperm(oracle.temporal_rope_angles(w["rope.temporal_freqs"].float(), T), 64)
+    ref = oracle.sub_block(x.reshape(T, dit.P, -1).float(), oracle.silu(cond.float()), blk, kind, cs, ss)
+    assert_close(got, ref, COS_SUB, REL_SUB, what + " output")
+    # the residual update alone is the stricter check (the output is dominated by x)
+    assert_close(got - x.reshape(T, dit.P, -1), ref - x.reshape(T, dit.P, -1), COS_SUB, REL_SUB, what + " update")
+
+
+def test_spatial_sub_block_config0():
+    c = synth.config0()
+    w = _single_block_dit(c["w"], "s", spatial_freqs=c["spatial_freqs"], temporal_freqs=c["temporal_freqs"])
+    _check_sub_block(c["x"][0], c["cond"][0], w, "s", 2, "config0 spatial sub-block")
+
+
+def test_temporal_sub_block_config2():
+    c = synth.config2()
+    w = _single_block_dit(c["w"], "t", temporal_freqs=c["temporal_freqs"])
+    _check_sub_block(c["x"][0], c["cond"][0], w, "t", 32, "config2 temporal sub-block T=32")
+
+
+@pytest.fixture(scope="module")
+def c1():
+    c = synth.config1()
+    dit = pkg.DiT(c["w"], "cuda")
+    return c, dit
+
+
+def _c1_reference(c, latent=None):
+    lat = c["latent"][0] if latent is None else latent
+    z = oracle.patch_embed(lat, c["w"])
+    cond = oracle.conditioning(c["t"], c["actions"], c["w"])
+    return oracle.dit_forward(z, cond, c["w"]).reshape(-1, 64)
+
+
+def test_dit_step_config1(c1):
+    c, dit = c1
+    step = pkg.DiTStep(dit, B=1, T=2)
+    patches = oracle.patchify_to_output_space(c["latent"][0]).reshape(-1, 64)
+    step.set_inputs(cuda(patches), cuda(c["t"]), cuda(c["actions"]))
+    v = step.run()
+    torch.cuda.synchronize()
+    ref = _c1_reference(c)
+    cos, rel = metrics(v, ref)
+    print("config1 DiT step: cos=%.6f max_rel=%.3e" % (cos, rel), flush=True)
+    assert cos >= COS_STEP, cos
+
+
+def test_dit_step_graph_replay_and_context_invariance(c1):
+    c, dit = c1
+    step = pkg.DiTStep(dit, B=1, T=2)
+    patches = oracle.patchify_to_output_space(c["latent"][0]).reshape(-1, 64)
+    step.set_inputs(cuda(patches), cuda(c["t"]), cuda(c["actions"]))
+    eager = step.run().clone()
+    torch.cuda.synchronize()
+    step.capture()
+    for i in range(3):
+        v = step.run()
+        torch.cuda.synchronize()
+        assert torch.equal(v, eager), "graph replay %d differs from eager" % i
+        torch.randn(1000, device="cuda").sum().item()  # unrelated eager work between replays
+    # causal temporal attention + per-frame ops: frame-0 rows never see frame 1
+    P = dit.P
+    patches2 = patches.clone()
+    patches2[P:] = torch.randn(P, 64, generator=torch.Generator().manual_seed(5))
+    step.set_inputs(cuda(patches2), cuda(c["t"]), cuda(c["actions"]))
+    v2 = step.run()
+    torch.cuda.synchronize()
+    assert torch.equal(v2[:P], eager[:P]), "context rows changed with the generated frame"
+    assert not torch.equal(v2[P:], eager[P:])
+
+
+def test_dit_forward_surface_reduced():
+    dr = synth.Draw(21)
+    w = synth.dit_weights(dr, n_blocks=2, d=256, n_heads=4, d_mlp=1024)
+    z = dr.normal(2, 144, 256)
+    cond = dr.normal(2, 256)
+    dit = pkg.DiT(w, "cuda")
+    v = pkg.kernels.dit_forward_device(cuda(z.reshape(-1, 256)), [cuda(cond[0]), cuda(cond[1])], dit)
+    torch.cuda.synchronize()
+    ref = oracle.dit_forward(z, cond, w).reshape(-1, 64)
+    assert_close(v, ref, COS_SUB, REL_SUB, "dit_forward surface (2 blocks, D=256)")
+
+
+@pytest.fixture(scope="module")
+def c3():
+    c = synth.config3()
+    dit = pkg.DiT(c["w"], "cuda")
+    vae = pkg.VAE(c["vw"], "cuda")
+    return c, dit, vae
+
+
+def test_vae_decode_config3(c3):
+    c, _, vae = c3
+    frame = pkg.kernels.vae_decode(cuda(c["vae_latent"]), vae)
+    torch.cuda.synchronize()
+    ref = oracle.vae_unpatchify(oracle.vae_decode(c["vae_latent"], c["vw"]))
+    cos, rel = metrics(frame, ref)
+    print("config3 VAE decode: cos=%.6f max_rel=%.3e" % (cos, rel), flush=True)
+    assert cos >= COS_STEP and rel <= 5e-2, (cos, rel)
+
+
+def test_ddim_frame_config3(c3):
+    c, dit, vae = c3
+    ac = pkg.schedule.cosine_alphas_cumprod()
+    fp = pkg.FramePipeline(dit, vae, c["steps"], ac)
+    noise = oracle.patchify_to_output_space(c["x_T"])[0]
+    ctx = oracle.patchify_to_output_space(c["ctx_latent"])[0]
+    fp.set_inputs(cuda(noise), cuda(ctx), c["ctx_t"], cuda(c["ctx_action"]), cuda(c["gen_action"]))
+    fp.capture()
+    frame = fp.run()
+    torch.cuda.synchronize()
+    chunk = fp.chunk.cpu()
+    w = c["w"]
+    ctx_z = oracle.patch_embed(c["ctx_latent"], w)[0]
+    ctx_cond = oracle.conditioning(torch.tensor([c["ctx_t"]]), c["ctx_action"][None], w)[0]
+    gen_conds = [oracle.conditioning(torch.tensor([float(t)]), c["gen_action"][None], w)[0] for t, _ in c["steps"]]
+    ref_chunk, ref_frame = oracle.ddim_frame(noise, ctx_z, ctx_cond, gen_conds, w, c["vw"], ac, c["steps"])
+    cc, rc = metrics(chunk, ref_chunk)
+    cf, rf = metrics(frame, ref_frame)
+    print("config3 frame: chunk cos=%.6f rel=%.3e | frame cos=%.6f rel=%.3e" % (cc, rc, cf, rf), flush=True)
+    assert cc >= COS_STEP and cf >= COS_STEP, (cc, cf)
