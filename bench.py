@@ -1,0 +1,180 @@
+"""Benchmark: ms per Oasis-500M DiT denoising step (config 1: T=2, bf16, 16 blocks) and FPS of
+the 4-step DDIM + VAE frame (config 3) on one MI355X, with synthetic seeded inputs and
+random-init weights.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames F] [--no-cpu-baseline]
+
+A step is one replay of the captured hipGraph of the full DiT step: on-device
+conditioning (timestep MLP, action projection and all 33 adaLN projections), patch
+embed of the two frames, 16 x (spatial, temporal) sub-blocks and the final layer.
+Inputs are resident in HBM before the timed region. Prints one JSON line.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _event_ms(fn, stream, n):
+    """Average duration of fn() over n launches, HIP events on `stream`."""
+    import torch
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        fn()
+        s.record(stream)
+        for _ in range(n):
+            fn()
+        e.record(stream)
+    e.synchronize()
+    return s.elapsed_time(e) / n
+
+
+def cpu_baseline(cfg, oracle, seconds=15.0):
+    """The fp32 oracle's DiT step (same weights and inputs) on this host's cores."""
+    import torch
+    torch.set_num_threads(os.cpu_count() or 1)
+    w = cfg["w"]
+    z = oracle.patch_embed(cfg["latent"][0], w)
+    times = []
+    with torch.inference_mode():
+        for i in range(2):  # warm-up
+            oracle.dit_forward(z, oracle.conditioning(cfg["t"], cfg["actions"], w), w)
+        t_end = time.perf_counter() + seconds
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            zz = oracle.patch_embed(cfg["latent"][0], w)
+            oracle.dit_forward(zz, oracle.conditioning(cfg["t"], cfg["actions"], w), w)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return {"value": round(1e3 * times[len(times) // 2], 2), "unit": "ms/DiT step",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "median of %d full config-1 DiT steps (T=2, 16 blocks) of the fp32 CPU oracle "
+                      "after 2 warm-ups" % len(times)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--frames", type=int, default=100)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-frame", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build targets one MI355X; multi-GPU runs are not part of it "
+              "(the path would shard by independent streams, one per GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    import oracle
+    synth, L = pkg.synth, pkg._lib
+
+    # ---------------- config 1: the DiT step ----------------
+    c1 = synth.config1()
+    dit = pkg.DiT(c1["w"], "cuda")
+    step = pkg.DiTStep(dit, B=1, T=2)
+    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
+    step.capture()
+    for _ in range(args.warmup):
+        step.graph.launch()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(step.stream)
+    for _ in range(args.steps):
+        step.graph.launch()
+    ev1.record(step.stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = 1e3 * (t1 - t0) / args.steps
+    ms_step_gpu = ev0.elapsed_time(ev1) / args.steps
+
+    # dominant kernel: the skinny adaLN GEMM streaming every sub-block's adaLN weights
+    # (406 MB bf16) once per step; HIP events on the step stream, same buffers as the step.
+    ws = step.ws
+    R = 2
+    def ada_gemv():
+        L.call("oasis_gemv_bf16", L.ptr(ws.cond), dit.d, R, L.ptr(dit.ada_w), dit.ada_width, dit.d,
+               L.ptr(dit.ada_b), L.ptr(ws.ada), dit.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
+               L.stream_handle(step.stream))
+    ada_ms = _event_ms(ada_gemv, step.stream, 50)
+    ada_bytes = dit.ada_width * dit.d * 2 + R * dit.d * 4 + R * dit.ada_width * 4 + dit.ada_width * 4
+    ada_gbs = ada_bytes / (ada_ms * 1e-3) / 1e9
+
+    # whole-step roofline: 1.2124 GB of weights must stream from HBM each step
+    step_bytes = sum(t.numel() * t.element_size() for t in dit._keep)
+
+    out = {
+        "metric": "ms/DiT step (T=2 bf16) + FPS for 4-step DDIM+VAE frame on 1 MI355X",
+        "value": round(ms_step, 4), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "config1: Oasis-500M DiT denoising step, latent [1,2,16,18,32], "
+                               "16 blocks, D=1024, 16 heads, T=2 (288 tokens), bf16 weights, fp32 residual",
+                   "global_batch": 1, "seq_len": 288, "parallelism": "none (1 GPU)"},
+        "ms_per_step_gpu_events": round(ms_step_gpu, 4),
+        "step_weight_bytes": step_bytes,
+        "step_hbm_floor_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
+        "roofline": {"kernel": "gemv_kernel (adaLN projections of all 33 consumers, R=2)",
+                     "bound": "hbm", "achieved": round(ada_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ada_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_ms": round(ada_ms, 4), "algorithmic_bytes": ada_bytes},
+    }
+
+    # ---------------- config 3: the DDIM + VAE frame ----------------
+    if not args.no_frame:
+        del step
+        c3 = synth.config3()
+        dit3 = pkg.DiT(c3["w"], "cuda")
+        vae3 = pkg.VAE(c3["vw"], "cuda")
+        fp = pkg.FramePipeline(dit3, vae3, c3["steps"], pkg.schedule.cosine_alphas_cumprod())
+        noise = oracle.patchify_to_output_space(c3["x_T"])[0]
+        ctx = oracle.patchify_to_output_space(c3["ctx_latent"])[0]
+        fp.set_inputs(noise.cuda(), ctx.cuda(), c3["ctx_t"], c3["ctx_action"].cuda(), c3["gen_action"].cuda())
+        fp.capture()
+        for _ in range(max(3, args.warmup // 4)):
+            fp.graph.launch()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.frames):
+            fp.graph.launch()
+        torch.cuda.synchronize()
+        ms_frame = 1e3 * (time.perf_counter() - t0) / args.frames
+        # per-frame host inputs (noise chunk, context patches, conditioning rows) over PCIe
+        noise_h = noise.pin_memory()
+        ctx_h = ctx.pin_memory()
+        t0 = time.perf_counter()
+        for _ in range(args.frames):
+            fp.chunk.copy_(noise_h, non_blocking=True)
+            fp.ctx_patches.copy_(ctx_h, non_blocking=True)
+            fp.stream.wait_stream(torch.cuda.current_stream())
+            fp.graph.launch()
+            torch.cuda.current_stream().wait_stream(fp.stream)
+        torch.cuda.synchronize()
+        ms_frame_h2d = 1e3 * (time.perf_counter() - t0) / args.frames
+        out["frame_ms"] = round(ms_frame, 4)
+        out["frame_fps"] = round(1e3 / ms_frame, 1)
+        out["frame_fps_with_h2d"] = round(1e3 / ms_frame_h2d, 1)
+        out["frame_workload"] = ("config3: 4 DDIM v-prediction steps (t=999,749,499,249, cosine alphas) "
+                                 "over the T=2 DiT + bridge + 12-block ViT VAE decode + unpatchify to "
+                                 "[3,360,640], one hipGraph")
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(c1, oracle)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
