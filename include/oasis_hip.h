@@ -136,7 +136,9 @@ enum {
   OASIS_EPI_GATED_RES = 4,    /* out_f32[m, n] += gate[f(m), n] * (acc + bias)     */
   OASIS_EPI_RESIDUAL = 5,     /* out_f32[m, n] += acc + bias                       */
   OASIS_EPI_QKV_ROPE = 6,     /* RoPE on Q,K + head split into q/k/v (bf16)         */
-  OASIS_EPI_UNPATCHIFY = 7    /* VAE predictor -> clamp(-1,1) CHW frame (fp32)      */
+  OASIS_EPI_UNPATCHIFY = 7,   /* VAE predictor -> clamp(-1,1) CHW frame (fp32)      */
+  OASIS_EPI_PARTIAL_F32 = 8   /* split-K slice s: out_f32[s*split_stride + m*ld_out + n] = acc
+                                 (no bias; summed by oasis_residual_ln)                */
 };
 
 /* Row m is token p of frame f = m / rows_per_frame (p = m % rows_per_frame);
@@ -164,12 +166,20 @@ typedef struct {
   int64_t s_b, s_t, s_p, s_h;
   int unpatch_patch;        /* UNPATCHIFY: patch edge (20)                         */
   int unpatch_channels;     /* UNPATCHIFY: channels (3)                            */
+  int64_t split_stride;     /* PARTIAL_F32: elements between split-K slices         */
 } oasis_epilogue_t;
 
 /* acc[M,N] = A[M,K] @ B[N,K]^T (bf16 in, fp32 accumulate) followed by the epilogue.
  * K % 64 == 0, N % 8 == 0. */
 int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                     int64_t N, int64_t K, const oasis_epilogue_t* epi, oasis_stream_t stream);
+
+/* Same with an explicit tile configuration (0..9, see gemm.hip; -1 = default) and
+ * split-K count (splits divides K/64; splits > 1 requires OASIS_EPI_PARTIAL_F32).
+ * No counterpart in the reference: it exposes the tiling for tuning and benchmarks. */
+int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                           int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
+                           oasis_stream_t stream);
 
 /* y_bf16[m, :] = LN(x[m, :]) * scale_p1[f(m), :] + shift[f(m), :], f(m) = m / rows_per_frame,
  * frame rows of shift/scale_p1 at + f*ada_fstride.  scale_p1 already holds (1 + scale).
@@ -178,6 +188,21 @@ int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int6
 int oasis_ln_modulate(const float* x, int64_t M, int64_t D, const float* shift,
                       const float* scale_p1, int64_t ada_fstride, int64_t rows_per_frame,
                       void* y_bf16, float eps, oasis_stream_t stream);
+
+/* Residual update fused with the next LayerNorm, one pass over each row:
+ *   if n_partials > 0: x[m, :] += g(m) * (sum_s partial[s*partial_stride + m*D + :] + bias)
+ *       g(m) = gate[f(m)*gate_fstride + :] (gate != NULL) or 1; f(m) = m / rows_per_frame;
+ *   if y_bf16 != NULL: y_bf16[m, :] = LN(x[m, :]) * ln_a[f(m)*ln_fstride + :] + ln_b[...]
+ *       (modulation: ln_a = scale_p1 and ln_b = shift rows; affine: ln_fstride = 0).
+ * n_partials in {0..4, 8}; D in {256, 512, 1024, 2048}. The partials are the split-K
+ * slices of an OASIS_EPI_PARTIAL_F32 GEMM. (O / FC2 bias + gated residual + the next
+ * LN + modulate, oasis_inference.py:1153-1171,1191-1201,1053-1056; VAE residual + LN,
+ * oasis_inference.py:1584-1611.) */
+int oasis_residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials,
+                      int64_t partial_stride, const float* bias, const float* gate,
+                      int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
+                      const float* ln_b, int64_t ln_fstride, void* y_bf16, float eps,
+                      oasis_stream_t stream);
 
 /* y_bf16 = LN(x) * w + b (affine LayerNorm of the VAE, oasis_inference.py:1559,1592,1611). */
 int oasis_ln_affine(const float* x, int64_t M, int64_t D, const float* w, const float* b,
@@ -289,6 +314,8 @@ typedef struct {
   void* v;
   void* attn;      /* [max_rows, D] bf16                                          */
   void* mlp;       /* [max_rows, Dm] bf16                                         */
+  float* partial;  /* [max_splits, max_rows, D] fp32 split-K slices               */
+  int64_t max_splits;
 } oasis_dit_buffers_t;
 
 /* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action), then
@@ -319,6 +346,17 @@ int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf
 int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                       int64_t B, int64_t T, const float* ada, int64_t ada_fstride,
                       float* v_out, oasis_stream_t stream);
+
+/* One full DiT denoising step for B streams of T frames (B*T <= 16): conditioning MLP
+ * (t fp32 [B*T], action fp32 [B*T, ext_dim_pad]), patch embed of patches fp32 [B*T*P, 64]
+ * into buf->x, every sub-block and the final layer; v_out fp32 [B*T*P, 64].
+ * tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The
+ * adaLN projections run on a library-owned side stream, overlapped with the sub-blocks.
+ * (dit_forward_device with compute_cond_for_frame, oasis_inference.py:1406-1526.) */
+int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
+                   int64_t T, const float* t, const float* action, const float* patches,
+                   float* tfreq, float* hid, float* cond, float* ada, float* v_out,
+                   oasis_stream_t stream);
 
 typedef struct {
   int depth;                 /* 12                                                 */
@@ -358,6 +396,8 @@ typedef struct {
   void* v;
   void* attn;      /* [L, D] bf16   */
   void* mlp;       /* [L, Dm] bf16  */
+  float* partial;  /* [max_splits, L, D] fp32 split-K slices */
+  int64_t max_splits;
 } oasis_vae_buffers_t;
 
 /* latent fp32 [L, latent_dim] -> frame fp32 [3, grid_h*patch, grid_w*patch] in [-1, 1].
@@ -365,19 +405,24 @@ typedef struct {
 int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf,
                      const float* latent, float* frame, oasis_stream_t stream);
 
-/* One generated frame at T=2: n_steps DDIM v-prediction steps, then bridge + VAE decode.
+/* One generated frame at T=2: conditioning, n_steps DDIM v-prediction steps, then bridge +
+ * VAE decode.
  *   chunk: fp32 [P, 64] noise in, denoised latent patches out;
- *   ctx_z: fp32 [P, D] embedded context frame;
- *   ada: fp32 rows [1 + n_steps, n_sub*6D + 2D]: row 0 the context frame, row 1+i the
- *        generated frame at step i (see oasis_dit_conditioning);
+ *   ctx_patches: fp32 [P, 64] context frame in patch space (embedded on device into ctx_z);
+ *   t, action: fp32 [1 + n_steps] timesteps and [1 + n_steps, ext_dim_pad] actions; row 0 is
+ *        the context frame, row 1 + i the generated frame at step i;
  *   coeffs: HOST array of n_steps x 6 DDIM coefficients (oasis_ddim_update order);
- *   v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae latent_dim] scratch;
- *   frame: fp32 [3, H, W] output.
+ *   tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (1 + n_steps rows);
+ *   ctx_z: fp32 [P, D] scratch; v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae
+ *   latent_dim] scratch; frame: fp32 [3, H, W] output. n_steps <= 15.
+ * The adaLN projections of all conditioning rows run on a library-owned side stream,
+ * overlapped with the first step (each sub-block waits only for its own rows).
  * (ddim_step_fn and the traced frame, oasis_inference.py:1909-1932,2131-2148.) */
 int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                      const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
-                     float* chunk, const float* ctx_z, const float* ada, int64_t n_steps,
-                     const float* coeffs, float* v_out, float* latent, float* frame,
+                     float* chunk, const float* ctx_patches, const float* t, const float* action,
+                     int64_t n_steps, const float* coeffs, float* tfreq, float* hid, float* cond,
+                     float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
                      oasis_stream_t stream);
 
 /* ---- hipGraph capture of any sequence of the calls above on one stream ---------

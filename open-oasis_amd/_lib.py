@@ -15,6 +15,7 @@ MAX_SUB = 64
 
 EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
+EPI_PARTIAL_F32 = 8
 ACT_NONE, ACT_SILU = 0, 1
 
 
@@ -39,7 +40,7 @@ class Epilogue(ctypes.Structure):
         ("frames_per_stream", c_i64), ("q", c_p), ("k", c_p), ("v", c_p), ("rope_cos", c_p),
         ("rope_sinp", c_p), ("rope_by_frame", c_i), ("unpatch_grid_w", c_i),
         ("s_b", c_i64), ("s_t", c_i64), ("s_p", c_i64), ("s_h", c_i64),
-        ("unpatch_patch", c_i), ("unpatch_channels", c_i),
+        ("unpatch_patch", c_i), ("unpatch_channels", c_i), ("split_stride", c_i64),
     ]
 
 
@@ -60,7 +61,7 @@ class DiTWeights(ctypes.Structure):
 
 class DiTBuffers(ctypes.Structure):
     _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p),
-                ("attn", c_p), ("mlp", c_p)]
+                ("attn", c_p), ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64)]
 
 
 class VAEWeights(ctypes.Structure):
@@ -79,7 +80,7 @@ class VAEWeights(ctypes.Structure):
 
 class VAEBuffers(ctypes.Structure):
     _fields_ = [("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p), ("attn", c_p),
-                ("mlp", c_p)]
+                ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64)]
 
 
 P = ctypes.POINTER
@@ -97,8 +98,11 @@ SIGNATURES = {
                           c_i64, c_i64, c_i64, c_i64, c_i, c_i, c_p],
     "oasis_sdpa": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_i, c_i, c_p],
     "oasis_gemm_bf16": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_p],
+    "oasis_gemm_bf16_config": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_ln_modulate": [c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_f, c_p],
     "oasis_ln_affine": [c_p, c_i64, c_i64, c_p, c_p, c_p, c_f, c_p],
+    "oasis_residual_ln": [c_p, c_i64, c_i64, c_p, c_i, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_p,
+                          c_f, c_p],
     "oasis_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_temporal_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_gemv_bf16": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
@@ -112,8 +116,10 @@ SIGNATURES = {
     "oasis_dit_sub_blocks": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
-    "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), c_p, c_p,
-                         c_p, c_i64, c_p, c_p, c_p, c_p, c_p],
+    "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
+                       c_p],
+    "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p, c_p,
+                         c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_graph_begin": [c_p],
     "oasis_graph_end": [c_p, P(c_p)],
     "oasis_graph_launch": [c_p, c_p],

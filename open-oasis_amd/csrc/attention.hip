@@ -18,9 +18,7 @@
 
 namespace {
 
-constexpr int KC = 64;       // keys per LDS chunk
 constexpr int KPITCH = 64 + 8;
-constexpr int VPITCH = KC + 8;
 constexpr float LOG2E = 1.4426950408889634f;
 
 template <typename T>
@@ -58,9 +56,13 @@ struct AttnArgs {
   int64_t o_sf, o_sh, o_si; // out offset = (bh/H)*o_sf + (bh%H)*o_sh + i*o_si + d
 };
 
-template <int NW, typename T>
+// KC keys per LDS chunk (KC = 192 stages a whole 144-token frame in one shot).
+template <int NW, int KC, typename T>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                         const T* __restrict__ V, T* __restrict__ O, AttnArgs a) {
+  constexpr int VPITCH = KC + 8;
+  constexpr int KT = KC / 16;   // 16-key tiles per chunk
+  constexpr int NL = 4;         // K/V chunk loads in flight per thread
   __shared__ __attribute__((aligned(16))) bf16 Ks[KC * KPITCH];
   __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -84,31 +86,42 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
 
   for (int kc0 = 0; kc0 < a.Lk; kc0 += KC) {
     __syncthreads();
-    for (int c = tid; c < KC * 8; c += NW * 64) {
-      const int key = c >> 3, d0 = (c & 7) * 8;
-      const int gk = kc0 + key;
-      bf16x8 kv, vv;
-      if (gk < a.Lk) {
-        kv = load8_bf16<T>(Kb + (int64_t)gk * 64 + d0);
-        vv = load8_bf16<T>(Vb + (int64_t)gk * 64 + d0);
-      } else {
+    // K rows and V^T columns of this chunk into LDS, NL loads in flight per thread
+    for (int c0 = tid; c0 < KC * 8; c0 += NW * 64 * NL) {
+      bf16x8 kv[NL], vv[NL];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          kv[j] = f2bf(0.f);
-          vv[j] = f2bf(0.f);
+      for (int u = 0; u < NL; ++u) {
+        const int c = c0 + u * NW * 64;
+        const int gk = kc0 + (c >> 3), d0 = (c & 7) * 8;
+        if (c < KC * 8 && gk < a.Lk) {
+          kv[u] = load8_bf16<T>(Kb + (int64_t)gk * 64 + d0);
+          vv[u] = load8_bf16<T>(Vb + (int64_t)gk * 64 + d0);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            kv[u][j] = f2bf(0.f);
+            vv[u][j] = f2bf(0.f);
+          }
         }
       }
-      *reinterpret_cast<bf16x8*>(Ks + key * KPITCH + d0) = kv;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VPITCH + key] = vv[j];
+      for (int u = 0; u < NL; ++u) {
+        const int c = c0 + u * NW * 64;
+        if (c < KC * 8) {
+          const int key = c >> 3, d0 = (c & 7) * 8;
+          *reinterpret_cast<bf16x8*>(Ks + key * KPITCH + d0) = kv[u];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VPITCH + key] = vv[u][j];
+        }
+      }
     }
     __syncthreads();
     if (q0 >= a.Lq) continue;
 
-    // S^T for 4 key tiles of 16: s[kt][i] = score(key kc0 + kt*16 + 4g + i, query my_q)
-    float s[4][4];
+    // S^T for KT key tiles of 16: s[kt][i] = score(key kc0 + kt*16 + 4g + i, query my_q)
+    float s[KT][4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
       const bf16* kp = Ks + (kt * 16 + lr) * KPITCH + g * 8;
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
       acc = mfma16(*reinterpret_cast<const bf16x8*>(kp), qf0, acc);
@@ -124,7 +137,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -134,7 +147,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
     const float alpha = exp2f(m - m_use);
     float ps = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         s[kt][i] = exp2f(s[kt][i] - m_use);
@@ -149,10 +162,10 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[dt][i] *= alpha;
 
-    // O^T += V^T P^T over 2 sub-chunks of 32 keys; k-slot j of lane group g maps to
+    // O^T += V^T P^T over KT/2 sub-chunks of 32 keys; k-slot j of lane group g maps to
     // key 32kc + 4g + j (j < 4) and 32kc + 16 + 4g + (j - 4) (j >= 4).
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
+    for (int kc = 0; kc < KT / 2; ++kc) {
       bf16x8 pb;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -184,12 +197,19 @@ template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
+  const bool one_chunk = a.Lk <= 192;  // a whole 144-token frame: stage all keys at once
   if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
-    hipLaunchKernelGGL((flash_kernel<3, T>), dim3((unsigned)(a.Lq / 48), (unsigned)n_bh), dim3(192), 0, s, q, k,
-                       v, o, a);
+    const dim3 g((unsigned)(a.Lq / 48), (unsigned)n_bh);
+    if (one_chunk)
+      hipLaunchKernelGGL((flash_kernel<3, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
+    else
+      hipLaunchKernelGGL((flash_kernel<3, 64, T>), g, dim3(192), 0, s, q, k, v, o, a);
   } else {
-    hipLaunchKernelGGL((flash_kernel<4, T>), dim3((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh), dim3(256), 0, s,
-                       q, k, v, o, a);
+    const dim3 g((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh);
+    if (one_chunk)
+      hipLaunchKernelGGL((flash_kernel<4, 192, T>), g, dim3(256), 0, s, q, k, v, o, a);
+    else
+      hipLaunchKernelGGL((flash_kernel<4, 64, T>), g, dim3(256), 0, s, q, k, v, o, a);
   }
   return oasis::check_launch("attention");
 }
@@ -206,6 +226,35 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
   const int p = (int)(bp % P);
   const int64_t b = bp / P;
   const int64_t base = grp * T * 64 + j * 4;
+  if (T == 2) {  // the DiT's 2-frame window: one round trip for all six rows
+    const bf16x4 q0 = *reinterpret_cast<const bf16x4*>(q + base), q1 = *reinterpret_cast<const bf16x4*>(q + base + 64);
+    const bf16x4 k0 = *reinterpret_cast<const bf16x4*>(k + base), k1 = *reinterpret_cast<const bf16x4*>(k + base + 64);
+    const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(v + base), v1 = *reinterpret_cast<const bf16x4*>(v + base + 64);
+    // query 0 sees one causal key (softmax weight exactly 1): out_0 = v_0
+    float d10 = 0.f, d11 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d10 += bf2f(q1[i]) * bf2f(k0[i]);
+      d11 += bf2f(q1[i]) * bf2f(k1[i]);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      d10 += __shfl_xor(d10, o, 16);
+      d11 += __shfl_xor(d11, o, 16);
+    }
+    (void)q0;
+    const float x0 = d10 * scale_log2, x1 = d11 * scale_log2;
+    const float mx = fmaxf(x0, x1);
+    const float p0 = exp2f(x0 - mx), p1 = exp2f(x1 - mx);
+    const float inv = 1.0f / (p0 + p1);
+    bf16* dst0 = out + (b * T * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
+    bf16* dst1 = dst0 + (int64_t)P * H * 64;
+    *reinterpret_cast<bf16x4*>(dst0) = v0;
+    *reinterpret_cast<bf16x4*>(dst1) =
+        bf16x4{f2bf((p0 * bf2f(v0[0]) + p1 * bf2f(v1[0])) * inv), f2bf((p0 * bf2f(v0[1]) + p1 * bf2f(v1[1])) * inv),
+               f2bf((p0 * bf2f(v0[2]) + p1 * bf2f(v1[2])) * inv), f2bf((p0 * bf2f(v0[3]) + p1 * bf2f(v1[3])) * inv)};
+    return;
+  }
   for (int t = 0; t < T; ++t) {
     const bf16x4 qv4 = *reinterpret_cast<const bf16x4*>(q + base + t * 64);
     float qv[4] = {bf2f(qv4[0]), bf2f(qv4[1]), bf2f(qv4[2]), bf2f(qv4[3])};

@@ -21,8 +21,7 @@
 
 namespace {
 
-constexpr int BK = 64;
-constexpr int LDS_PITCH = BK + 8;  // bf16 elements per LDS row (16 B pad: conflict-free b128 reads)
+constexpr int BK = 64;            // K granularity every configuration supports
 constexpr int NUM_XCD = 8;
 
 struct Epi {
@@ -46,6 +45,7 @@ struct Epi {
   int64_t s_b, s_t, s_p, s_h;
   int unpatch_patch;
   int unpatch_channels;
+  int64_t split_stride;
 };
 
 __device__ __forceinline__ int xcd_remap(int pid, int G) {
@@ -162,18 +162,27 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
 
 // BKN = false: B is [N, K] (weights as stored by this library); true: B is [K, N]
 // (the reference's transposed weight layout, used by the linear_k32 surface only).
-template <int BM, int BN, int WM, int WN, bool BKN>
+// STAGES K-tiles are in flight per workgroup: a register ring of STAGES global-load
+// slots feeds a double-buffered LDS tile pair. With `splits` > 1 the K range is cut
+// into equal slices, one per workgroup, and the epilogue must be PARTIAL_F32.
+template <int BM, int BN, int WM, int WN, int STAGES, bool BKN, int BKT>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__ A, int64_t lda,
                                                         const bf16* __restrict__ B, int64_t ldb,
-                                                        int M, int N, int K, Epi e) {
+                                                        int M, int N, int K, int splits, Epi e) {
   static_assert(WM * WN == 4, "4 waves");
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
   static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
-  constexpr int A_CHUNKS = BM * (BK / 8);  // 16-byte chunks per A tile
-  constexpr int B_CHUNKS = BN * (BK / 8);
-  constexpr int A_PER = (A_CHUNKS + 255) / 256;
-  constexpr int B_PER = (B_CHUNKS + 255) / 256;
+  constexpr int BK = BKT;                  // K per pipeline step
+  constexpr int LDS_PITCH = BK + 8;        // bf16 per LDS row (16 B pad: conflict-free b128 reads)
+  constexpr int CPR = BK / 8;              // 16-byte chunks per tile row
+  constexpr int A_CHUNKS = BM * CPR;       // 16-byte chunks per A tile
+  constexpr int B_CHUNKS = BN * CPR;
+  // every thread loads whole chunks: no per-thread guards, so the compiler can keep
+  // STAGES tiles of loads in flight (a divergent guard forces a full vmcnt(0) wait)
+  static_assert(A_CHUNKS % 256 == 0 && B_CHUNKS % 256 == 0, "BM and BN must be multiples of 32");
+  constexpr int A_PER = A_CHUNKS / 256;
+  constexpr int B_PER = B_CHUNKS / 256;
   constexpr int AB_BYTES = 2 * (BM + BN) * LDS_PITCH * 2;
   constexpr int C_PITCH = BN + 4;
   constexpr int C_BYTES = BM * C_PITCH * 4;
@@ -185,65 +194,63 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  const int pid = xcd_remap(blockIdx.x, Mt * Nt);
-  const int nt = pid / Mt, mt = pid - nt * Mt;
+  // (n tile, split, m tile) with m fastest: consecutive ids share one weight slice
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
+  const int mt = pid % Mt;
+  const int rest = pid / Mt;
+  const int split = rest % splits, nt = rest / splits;
   const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = K / BK / splits;  // the host guarantees nk % STAGES == 0
+  const int kb = split * nk * BK;
 
-  // global chunk coordinates (fixed across K)
   const bf16* a_src[A_PER];
   int a_dst[A_PER];
-  bool a_ok[A_PER];
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
     const int c = tid + i * 256;
-    const int row = c >> 3, col = (c & 7) * 8;
-    a_ok[i] = c < A_CHUNKS;
+    const int row = c / CPR, col = (c % CPR) * 8;
     const int gr = min(m0 + row, M - 1);
-    a_src[i] = A + (int64_t)gr * lda + col;
+    a_src[i] = A + (int64_t)gr * lda + kb + col;
     a_dst[i] = row * LDS_PITCH + col;
   }
   const bf16* b_src[B_PER];
   int b_dst[B_PER];
-  bool b_ok[B_PER];
 #pragma unroll
   for (int i = 0; i < B_PER; ++i) {
     const int c = tid + i * 256;
-    b_ok[i] = c < B_CHUNKS;
     if (!BKN) {
-      const int row = c >> 3, col = (c & 7) * 8;
+      const int row = c / CPR, col = (c % CPR) * 8;
       const int gr = min(n0 + row, N - 1);
-      b_src[i] = B + (int64_t)gr * ldb + col;
+      b_src[i] = B + (int64_t)gr * ldb + kb + col;
       b_dst[i] = row * LDS_PITCH + col;
     } else {  // chunk = 8 consecutive n of one k row; stored transposed into [n][k]
       const int krow = c / (BN / 8), nc = (c % (BN / 8)) * 8;
       const int gn = min(n0 + nc, N - 8);
-      b_src[i] = B + (int64_t)krow * ldb + gn;
+      b_src[i] = B + (int64_t)(kb + krow) * ldb + gn;
       b_dst[i] = nc * LDS_PITCH + krow;
     }
   }
 
-  i32x4 ra[A_PER], rb[B_PER];
-  auto gload = [&](int k0) {
+  i32x4 ra[STAGES][A_PER], rb[STAGES][B_PER];
+  auto gload = [&](int slot, int kt) {
+    const int64_t ka = (int64_t)kt * BK;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      if (a_ok[i]) ra[i] = *reinterpret_cast<const i32x4*>(a_src[i] + k0);
+    for (int i = 0; i < A_PER; ++i) ra[slot][i] = *reinterpret_cast<const i32x4*>(a_src[i] + ka);
 #pragma unroll
     for (int i = 0; i < B_PER; ++i)
-      if (b_ok[i]) rb[i] = *reinterpret_cast<const i32x4*>(b_src[i] + (BKN ? (int64_t)k0 * ldb : (int64_t)k0));
+      rb[slot][i] = *reinterpret_cast<const i32x4*>(b_src[i] + (BKN ? ka * ldb : ka));
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int slot, int buf) {
     bf16* as = As + buf * BM * LDS_PITCH;
     bf16* bs = Bs + buf * BN * LDS_PITCH;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      if (a_ok[i]) *reinterpret_cast<i32x4*>(as + a_dst[i]) = ra[i];
+    for (int i = 0; i < A_PER; ++i) *reinterpret_cast<i32x4*>(as + a_dst[i]) = ra[slot][i];
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
-      if (!b_ok[i]) continue;
       if (!BKN) {
-        *reinterpret_cast<i32x4*>(bs + b_dst[i]) = rb[i];
+        *reinterpret_cast<i32x4*>(bs + b_dst[i]) = rb[slot][i];
       } else {
-        const bf16x8 t = __builtin_bit_cast(bf16x8, rb[i]);
+        const bf16x8 t = __builtin_bit_cast(bf16x8, rb[slot][i]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) bs[b_dst[i] + j * LDS_PITCH] = t[j];
       }
@@ -256,17 +263,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = K / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
   const int lr = lane & 15, lk = (lane >> 4) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
-    const bf16* as = As + cur * BM * LDS_PITCH + (wm * TM + lr) * LDS_PITCH + lk;
-    const bf16* bs = Bs + cur * BN * LDS_PITCH + (wn * TN + lr) * LDS_PITCH + lk;
+  auto compute = [&](int buf) {
+    const bf16* as = As + buf * BM * LDS_PITCH + (wm * TM + lr) * LDS_PITCH + lk;
+    const bf16* bs = Bs + buf * BN * LDS_PITCH + (wn * TN + lr) * LDS_PITCH + lk;
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
       bf16x8 af[FM], bfr[FN];
@@ -281,8 +281,25 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);
-    __syncthreads();
+  };
+
+  // Prologue: tiles 0..STAGES-1 in flight, tile 0 in LDS. Tile indices past the end are
+  // clamped to the last tile (a redundant L2 hit) instead of branched around, so the
+  // loop body is straight-line and the waits before each LDS store count only the
+  // STAGES-1 younger tiles.
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s) gload(s, min(s, nk - 1));
+  lstore(0, 0);
+  __syncthreads();
+  for (int k0 = 0; k0 < nk; k0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      const int k = k0 + s;
+      gload(s, min(k + STAGES, nk - 1));     // slot s held tile k, already in LDS
+      compute(k & 1);
+      lstore((s + 1) % STAGES, (k + 1) & 1);  // tile k+1 (a copy of the last tile at the end)
+      __syncthreads();
+    }
   }
 
   // stage the fp32 tile through LDS (the A/B ring is free after the last barrier)
@@ -309,18 +326,61 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
       v[j] = c0[j];
       v[j + 4] = c1[j];
     }
-    epilogue8(e, gm, gn, v);
+    if (e.kind == OASIS_EPI_PARTIAL_F32) {
+      float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+      *reinterpret_cast<f32x4*>(d) = c0;
+      *reinterpret_cast<f32x4*>(d + 4) = c1;
+    } else {
+      epilogue8(e, gm, gn, v);
+    }
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool BKN = false>
+template <int BM, int BN, int WM, int WN, int STAGES, bool BKN = false, int BKT = 64>
 hipError_t launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K,
-                      const Epi& e, hipStream_t s) {
+                      int splits, const Epi& e, hipStream_t s) {
+  if ((K / splits) % BKT != 0) return hipErrorInvalidConfiguration;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, BKN>), dim3(Mt * Nt), dim3(256), 0, s, A, lda, B,
-                     ldb, M, N, K, e);
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, STAGES, BKN, BKT>), dim3(Mt * Nt * splits), dim3(256), 0, s,
+                     A, lda, B, ldb, M, N, K, splits, e);
   return hipGetLastError();
 }
+
+// Tile configurations (id -> BM x BN, wave grid, prefetch depth).
+typedef hipError_t (*launch_fn)(const bf16*, int64_t, const bf16*, int64_t, int, int, int, int, const Epi&,
+                                hipStream_t);
+struct TileCfg {
+  int bm, bn, stages, bk;
+  launch_fn fn;         // STAGES-deep prefetch ring (K tiles per split divisible by stages)
+  launch_fn fn_single;  // one tile in flight, any K
+};
+const TileCfg kTiles[] = {
+    {32, 64, 4, 64, launch_cfg<32, 64, 1, 4, 4>, launch_cfg<32, 64, 1, 4, 1>},      // 0
+    {64, 64, 4, 64, launch_cfg<64, 64, 2, 2, 4>, launch_cfg<64, 64, 2, 2, 1>},      // 1
+    {32, 128, 4, 64, launch_cfg<32, 128, 1, 4, 4>, launch_cfg<32, 128, 1, 4, 1>},   // 2
+    {64, 128, 2, 64, launch_cfg<64, 128, 2, 2, 2>, launch_cfg<64, 128, 2, 2, 1>},   // 3
+    {96, 64, 2, 64, launch_cfg<96, 64, 2, 2, 2>, launch_cfg<96, 64, 2, 2, 1>},      // 4
+    {32, 32, 8, 64, launch_cfg<32, 32, 2, 2, 8>, launch_cfg<32, 32, 2, 2, 1>},      // 5
+    {128, 64, 2, 64, launch_cfg<128, 64, 2, 2, 2>, launch_cfg<128, 64, 2, 2, 1>},   // 6
+    {32, 64, 2, 64, launch_cfg<32, 64, 1, 4, 2>, launch_cfg<32, 64, 1, 4, 1>},      // 7
+    {32, 64, 8, 64, launch_cfg<32, 64, 1, 4, 8>, launch_cfg<32, 64, 1, 4, 1>},      // 8
+    {64, 32, 4, 64, launch_cfg<64, 32, 2, 2, 4>, launch_cfg<64, 32, 2, 2, 1>},      // 9
+    {96, 64, 4, 64, launch_cfg<96, 64, 2, 2, 4>, launch_cfg<96, 64, 2, 2, 1>},      // 10
+    {96, 32, 8, 64, launch_cfg<96, 32, 2, 2, 8>, launch_cfg<96, 32, 2, 2, 1>},      // 11
+    {128, 64, 4, 64, launch_cfg<128, 64, 2, 2, 4>, launch_cfg<128, 64, 2, 2, 1>},   // 12
+    {96, 128, 2, 64, launch_cfg<96, 128, 2, 2, 2>, launch_cfg<96, 128, 2, 2, 1>},   // 13
+    {64, 64, 8, 64, launch_cfg<64, 64, 2, 2, 8>, launch_cfg<64, 64, 2, 2, 1>},      // 14
+    {96, 64, 8, 64, launch_cfg<96, 64, 2, 2, 8>, launch_cfg<96, 64, 2, 2, 1>},      // 15
+    {128, 32, 8, 64, launch_cfg<128, 32, 2, 2, 8>, launch_cfg<128, 32, 2, 2, 1>},   // 16
+    {64, 128, 4, 64, launch_cfg<64, 128, 2, 2, 4>, launch_cfg<64, 128, 2, 2, 1>},   // 17
+    // 128-wide K steps: half the pipeline iterations (and barriers) per tile
+    {32, 64, 2, 128, launch_cfg<32, 64, 1, 4, 2, false, 128>, launch_cfg<32, 64, 1, 4, 1>},     // 18
+    {96, 64, 2, 128, launch_cfg<96, 64, 2, 2, 2, false, 128>, launch_cfg<96, 64, 2, 2, 1>},     // 19
+    {64, 64, 2, 128, launch_cfg<64, 64, 2, 2, 2, false, 128>, launch_cfg<64, 64, 2, 2, 1>},     // 20
+    {32, 128, 2, 128, launch_cfg<32, 128, 1, 4, 2, false, 128>, launch_cfg<32, 128, 1, 4, 1>},  // 21
+    {32, 64, 4, 128, launch_cfg<32, 64, 1, 4, 4, false, 128>, launch_cfg<32, 64, 1, 4, 1>},     // 22
+};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 Epi to_epi(const oasis_epilogue_t& x) {
   Epi e;
@@ -347,6 +407,7 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.s_h = x.s_h;
   e.unpatch_patch = x.unpatch_patch;
   e.unpatch_channels = x.unpatch_channels;
+  e.split_stride = x.split_stride;
   return e;
 }
 
@@ -357,8 +418,19 @@ namespace oasis {
 // Tile choice per shape. M is small (288 / 576 tokens) and the weights are streamed
 // once, so the tiles trade L2 re-reads of A and B against enough workgroups to keep
 // all 256 CUs issuing HBM loads.
-int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N,
-                int64_t K, const oasis_epilogue_t& ex, hipStream_t s) {
+// Default tile per shape, from sweeps of the DiT / VAE projections on MI355X (M = 288 and
+// 576 tokens, weights streamed from HBM): 32 x 64 tiles with a 2-deep ring for the QKV-
+// and O-sized products, 96 x 64 tiles with a 4-deep ring for the 4096-wide MLP products.
+int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
+  bool wide = false;
+  if (kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF) wide = N >= 2048;
+  if (kind == OASIS_EPI_PARTIAL_F32) wide = Kslice >= 1024;
+  if (wide && M >= 192) return 10;
+  return 7;
+}
+
+int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                    const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
   OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm: null operand");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0, OASIS_ERR_SHAPE, "gemm: empty shape M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
@@ -367,14 +439,21 @@ int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t 
   OASIS_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K, OASIS_ERR_SHAPE,
                 "gemm: lda/ldb must be >= K and multiples of 8");
   OASIS_REQUIRE(M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE, "gemm: M/N too large");
+  OASIS_REQUIRE(splits >= 1 && (K / BK) % splits == 0, OASIS_ERR_SHAPE,
+                "gemm: splits=%d must divide K/64=%lld", splits, (long long)(K / BK));
   const Epi e = to_epi(ex);
+  OASIS_REQUIRE(splits == 1 || e.kind == OASIS_EPI_PARTIAL_F32, OASIS_ERR_ARG,
+                "gemm: split-K needs the PARTIAL_F32 epilogue");
   switch (e.kind) {
     case OASIS_EPI_STORE_F32:
     case OASIS_EPI_GATED_RES:
     case OASIS_EPI_RESIDUAL:
+    case OASIS_EPI_PARTIAL_F32:
       OASIS_REQUIRE(e.out_f32 && e.ld_out >= N && e.ld_out % 4 == 0, OASIS_ERR_ARG,
                     "gemm: fp32 epilogue needs out_f32 and ld_out >= N (multiple of 4)");
       OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES || e.gate, OASIS_ERR_NULL, "gemm: gate is NULL");
+      OASIS_REQUIRE(e.kind != OASIS_EPI_PARTIAL_F32 || splits == 1 || e.split_stride >= M * e.ld_out,
+                    OASIS_ERR_ARG, "gemm: split_stride must be >= M * ld_out");
       break;
     case OASIS_EPI_STORE_BF16:
     case OASIS_EPI_GELU_TANH:
@@ -398,20 +477,27 @@ int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t 
     default:
       OASIS_REQUIRE(false, OASIS_ERR_ARG, "gemm: unknown epilogue kind %d", e.kind);
   }
-  const int m = (int)M, n = (int)N, k = (int)K;
-  hipError_t err;
-  if (M <= 64) {
-    err = launch_cfg<32, 64, 1, 4>(A, lda, B, ldb, m, n, k, e, s);
-  } else if (N <= 1216) {
-    err = launch_cfg<32, 64, 1, 4>(A, lda, B, ldb, m, n, k, e, s);
-  } else {
-    err = launch_cfg<64, 64, 2, 2>(A, lda, B, ldb, m, n, k, e, s);
-  }
+  if (tile < 0) tile = auto_tile(M, N, K / splits, e.kind);
+  OASIS_REQUIRE(tile < kNumTiles, OASIS_ERR_ARG, "gemm: tile config %d out of range", tile);
+  const TileCfg& t = kTiles[tile];
+  // the prefetch ring needs (K steps per split) % stages == 0; 128-wide configs also need
+  // K % 128 per split, else their one-stage 64-wide twin runs
+  const int64_t ks = K / splits / t.bk;
+  const bool ring = (K / splits) % t.bk == 0 && ks % t.stages == 0;
+  const hipError_t err = (ring ? t.fn : t.fn_single)(A, lda, B, ldb, (int)M, (int)N, (int)K, splits, e, s);
   if (err != hipSuccess) {
     set_error("gemm launch failed: %s", hipGetErrorString(err));
     return OASIS_ERR_LAUNCH;
   }
   return OASIS_OK;
+}
+
+// Default tile choice. M is small (288 / 576 tokens) and the weights are streamed once,
+// so the tiles trade L2 re-reads of A and B against enough workgroups (and K-tiles in
+// flight per workgroup) to keep all 256 CUs issuing HBM loads.
+int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                const oasis_epilogue_t& ex, hipStream_t s) {
+  return gemm_launch_cfg(A, lda, B, ldb, M, N, K, ex, -1, 1, s);
 }
 
 }  // namespace oasis
@@ -434,13 +520,22 @@ extern "C" int oasis_linear(const void* x, const void* w, void* out, int64_t M, 
     return oasis::gemm_launch(static_cast<const bf16*>(x), K, static_cast<const bf16*>(w), K, M, N, K, ex,
                               static_cast<hipStream_t>(stream));
   const Epi e = to_epi(ex);
-  const hipError_t err = launch_cfg<32, 64, 1, 4, true>(static_cast<const bf16*>(x), K, static_cast<const bf16*>(w), N,
-                                                        (int)M, (int)N, (int)K, e, static_cast<hipStream_t>(stream));
+  const hipError_t err = launch_cfg<32, 64, 1, 4, 1, true>(static_cast<const bf16*>(x), K, static_cast<const bf16*>(w),
+                                                           N, (int)M, (int)N, (int)K, 1, e,
+                                                           static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     oasis::set_error("linear launch failed: %s", hipGetErrorString(err));
     return OASIS_ERR_LAUNCH;
   }
   return OASIS_OK;
+}
+
+extern "C" int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                                      int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
+                                      oasis_stream_t stream) {
+  OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm: null epilogue");
+  return oasis::gemm_launch_cfg(static_cast<const bf16*>(A), lda, static_cast<const bf16*>(B), ldb, M, N, K,
+                                *epi, tile, splits, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,

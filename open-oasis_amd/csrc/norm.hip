@@ -85,6 +85,127 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
   }
 }
 
+// Residual update fused with the next LayerNorm. One 256-thread workgroup per row
+// (VPT = D/256 floats per thread), every load issued up front so a row costs one memory
+// round trip; mean and variance by two block reductions:
+//   x[m] += g * (sum_s partial[s][m] + bias)          (NP > 0; g = gate[f(m)] or 1)
+//   y[m]  = LN(x[m]) * a + b                           (a, b: modulate rows or affine)
+template <int VPT, int NP>
+__global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
+                                                          int64_t pstride, const float* __restrict__ bias,
+                                                          const float* __restrict__ gate, int64_t gate_fs,
+                                                          int64_t rpf, const float* __restrict__ la,
+                                                          const float* __restrict__ lb, int64_t ln_fs,
+                                                          bf16* __restrict__ y, float eps) {
+  constexpr int D = VPT * 256;
+  constexpr int NC = VPT / 4 > 0 ? VPT / 4 : 1;   // 4-float groups per thread
+  constexpr int W = VPT < 4 ? VPT : 4;            // floats per group
+  __shared__ float red[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t f = row / rpf;
+  float* xr = x + row * D;
+  float v[NC][4], pv[NP > 0 ? NP : 1][NC][4], bv[NC][4], gv[NC][4], av[NC][4], cv[NC][4];
+  auto ld = [&](const float* p, float* o) {
+    if (W == 4) {
+      load4<float>(p, o);
+    } else {
+#pragma unroll
+      for (int j = 0; j < W; ++j) o[j] = p[j];
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 1024 + tid * W;  // W == 4: groups of 1024; W < 4: one group of 256*W
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[c][j] = 0.f;
+    ld(xr + k, v[c]);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) ld(part + p * pstride + row * D + k, pv[p][c]);
+    if (NP > 0) {
+      if (bias) ld(bias + k, bv[c]); else bv[c][0] = bv[c][1] = bv[c][2] = bv[c][3] = 0.f;
+      if (gate) ld(gate + f * gate_fs + k, gv[c]); else gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 1.f;
+    }
+    if (y) {
+      ld(la + f * ln_fs + k, av[c]);
+      ld(lb + f * ln_fs + k, cv[c]);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 1024 + tid * W;
+    if (NP > 0) {
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        float acc = bv[c][j];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc += pv[p][c][j];
+        v[c][j] += gv[c][j] * acc;
+      }
+      if (W == 4) {
+        store4<float>(xr + k, v[c]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j) xr[k + j] = v[c][j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) s += v[c][j];
+  }
+  if (!y) return;
+  s = wave_sum(s);
+  if (lane == 0) red[0][wave] = s;
+  __syncthreads();
+  const float mean = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) * (1.0f / D);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      v[c][j] -= mean;
+      q += v[c][j] * v[c][j];
+    }
+  q = wave_sum(q);
+  if (lane == 0) red[1][wave] = q;
+  __syncthreads();
+  const float rstd = rsqrtf((red[1][0] + red[1][1] + red[1][2] + red[1][3]) * (1.0f / D) + eps);
+  bf16* yr = y + row * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 1024 + tid * W;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < W; ++j) o[j] = v[c][j] * rstd * av[c][j] + cv[c][j];
+    if (W == 4) {
+      store4<bf16>(yr + k, o);
+    } else {
+#pragma unroll
+      for (int j = 0; j < W; ++j) yr[k + j] = f2bf(o[j]);
+    }
+  }
+}
+
+template <int VPT>
+hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
+                          const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
+                          bf16* y, float eps, hipStream_t s) {
+  const dim3 grid((unsigned)M), block(256);
+#define OASIS_RLN(NPV) \
+  hipLaunchKernelGGL((residual_ln_kernel<VPT, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, lb, lfs, y, eps)
+  switch (np) {
+    case 0: OASIS_RLN(0); break;
+    case 1: OASIS_RLN(1); break;
+    case 2: OASIS_RLN(2); break;
+    case 3: OASIS_RLN(3); break;
+    case 4: OASIS_RLN(4); break;
+    case 8: OASIS_RLN(8); break;
+    default: return hipErrorInvalidConfiguration;
+  }
+#undef OASIS_RLN
+  return hipGetLastError();
+}
+
 template <typename TIn, typename TOut, int MODE>
 hipError_t ln_dispatch(const TIn* x, int64_t M, int64_t D, float eps, const float* p0,
                        const float* p1, int64_t pstride, int64_t rpf, TOut* y, hipStream_t s) {
@@ -152,4 +273,36 @@ extern "C" int oasis_layernorm(const void* x, const void* weight, const void* bi
                   "layernorm");
   oasis::set_error("layernorm: unsupported dtype %d", dtype);
   return OASIS_ERR_DTYPE;
+}
+
+extern "C" int oasis_residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials,
+                                 int64_t partial_stride, const float* bias, const float* gate, int64_t gate_fstride,
+                                 int64_t rows_per_frame, const float* ln_a, const float* ln_b, int64_t ln_fstride,
+                                 void* y_bf16, float eps, oasis_stream_t stream) {
+  OASIS_REQUIRE(x, OASIS_ERR_NULL, "residual_ln: null x");
+  OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "residual_ln: bad M/rows_per_frame");
+  OASIS_REQUIRE(n_partials == 0 || partial, OASIS_ERR_NULL, "residual_ln: null partials");
+  OASIS_REQUIRE(n_partials <= 1 || partial_stride >= M * D, OASIS_ERR_ARG, "residual_ln: partial_stride too small");
+  OASIS_REQUIRE(!y_bf16 || (ln_a && ln_b), OASIS_ERR_NULL, "residual_ln: LN output needs ln_a and ln_b");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  bf16* y = static_cast<bf16*>(y_bf16);
+  hipError_t e;
+  switch (D) {
+    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
+    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
+    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
+    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
+    default:
+      oasis::set_error("residual_ln: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
+      return OASIS_ERR_SHAPE;
+  }
+  if (e == hipErrorInvalidConfiguration) {
+    oasis::set_error("residual_ln: n_partials=%d must be one of 0-4 or 8", n_partials);
+    return OASIS_ERR_ARG;
+  }
+  if (e != hipSuccess) {
+    oasis::set_error("residual_ln launch failed: %s", hipGetErrorString(e));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
 }

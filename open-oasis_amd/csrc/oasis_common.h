@@ -25,6 +25,9 @@ int check_launch(const char* what);
 // acc = A[M,K] @ B[N,K]^T with the given epilogue (gemm.hip).
 int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                 const oasis_epilogue_t& epi, hipStream_t s);
+// explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
+int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                    const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
 }  // namespace oasis
 
 #define OASIS_REQUIRE(cond, code, ...)          \

@@ -5,6 +5,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "oasis_common.h"
 
 namespace oasis {
@@ -28,6 +30,98 @@ int check_launch(const char* what) {
 }
 
 }  // namespace oasis
+
+#include <stdlib.h>
+
+#include <mutex>
+#include <string>
+
+namespace {
+
+// Per-device side stream + events used to overlap the adaLN projections (pure weight
+// streaming, independent of the token path) with the sub-blocks that consume them.
+// Created on first use, kept for the process lifetime; default stream priority.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t ev[OASIS_MAX_SUB + 1] = {};
+};
+
+int side_stream(SideStream** out) {
+  static std::mutex mu;
+  static SideStream table[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    oasis::set_error("side stream: no current device");
+    return OASIS_ERR_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& t = table[dev];
+  if (!t.s) {
+    if (hipStreamCreateWithFlags(&t.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&t.fork, hipEventDisableTiming) != hipSuccess) {
+      oasis::set_error("side stream: creation failed");
+      return OASIS_ERR_LAUNCH;
+    }
+    for (auto& e : t.ev)
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        oasis::set_error("side stream: event creation failed");
+        return OASIS_ERR_LAUNCH;
+      }
+  }
+  *out = &t;
+  return OASIS_OK;
+}
+
+// GEMM plan per projection role: tile configuration (-1 = gemm.hip's default for the
+// shape) and split-K count (0 = chosen from the shape). Tuning override, read once:
+//   OASIS_GEMM_PLAN="qkv:7,o:7:4,fc1:0,fc2:0:4,vqkv:7,vo:7:2,vfc1:0,vfc2:0:2"
+//   OASIS_ADALN_OVERLAP=1 streams the adaLN projections on a side stream, overlapped with
+//   the sub-blocks (off by default: the cross-stream graph edges cost more than they
+//   hide on MI355X, 2.09 vs 1.90 ms per config-1 step).
+enum { ROLE_QKV, ROLE_O, ROLE_FC1, ROLE_FC2, ROLE_VQKV, ROLE_VO, ROLE_VFC1, ROLE_VFC2, ROLE_N };
+struct Plan {
+  int tile[ROLE_N];
+  int splits[ROLE_N];
+  bool overlap;
+};
+
+const Plan& plan() {
+  static Plan p = [] {
+    Plan q;
+    for (int i = 0; i < ROLE_N; ++i) {
+      q.tile[i] = -1;
+      q.splits[i] = 0;
+    }
+    q.overlap = false;
+    static const char* names[ROLE_N] = {"qkv", "o", "fc1", "fc2", "vqkv", "vo", "vfc1", "vfc2"};
+    if (const char* env = getenv("OASIS_GEMM_PLAN")) {
+      std::string str(env);
+      size_t pos = 0;
+      while (pos < str.size()) {
+        size_t end = str.find(',', pos);
+        if (end == std::string::npos) end = str.size();
+        const std::string item = str.substr(pos, end - pos);
+        pos = end + 1;
+        const size_t c1 = item.find(':');
+        if (c1 == std::string::npos) continue;
+        const std::string name = item.substr(0, c1);
+        int tile = -1, splits = 0;
+        if (sscanf(item.c_str() + c1 + 1, "%d:%d", &tile, &splits) < 1) continue;
+        for (int i = 0; i < ROLE_N; ++i)
+          if (name == names[i]) {
+            q.tile[i] = tile;
+            q.splits[i] = splits;
+          }
+      }
+    }
+    if (const char* env = getenv("OASIS_ADALN_OVERLAP")) q.overlap = atoi(env) != 0;
+    return q;
+  }();
+  return p;
+}
+
+}  // namespace
 
 #define OASIS_TRY(call)          \
   do {                           \
@@ -89,22 +183,55 @@ extern "C" int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float*
   return oasis_gemv_bf16(cond, D, R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, stream);
 }
 
-extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
-                                    int64_t T, const float* ada, int64_t ada_fstride, int64_t j0, int64_t j1,
-                                    oasis_stream_t stream) {
-  OASIS_TRY(check_dit(w));
-  OASIS_REQUIRE(buf && buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp, OASIS_ERR_NULL,
-                "dit: missing buffer");
-  OASIS_REQUIRE(ada, OASIS_ERR_NULL, "dit: null ada");
-  OASIS_REQUIRE(B > 0 && T > 0 && T <= w->t_max, OASIS_ERR_SHAPE, "dit: need B > 0, 0 < T <= t_max (%d)", w->t_max);
-  OASIS_REQUIRE(0 <= j0 && j0 <= j1 && j1 <= w->n_sub, OASIS_ERR_ARG, "dit: sub-block range [%lld, %lld) invalid",
-                (long long)j0, (long long)j1);
+namespace {
+
+// Split-K count for an O / FC2 GEMM (tile 0: 32 x 64): enough workgroups to cover the
+// 256 CUs, each split still a multiple of the 4-deep prefetch ring.
+int choose_splits(int64_t M, int64_t N, int64_t K, int64_t max_splits) {
+  const int64_t tiles = ((M + 31) / 32) * ((N + 63) / 64);
+  const int64_t nk = K / 64;
+  int s = 1;
+  while (2 * s <= max_splits && 2 * s <= 8 && tiles * s < 512 && nk % (2 * s) == 0 && (nk / (2 * s)) % 4 == 0) s *= 2;
+  return s;
+}
+
+// A residual that has been computed as split-K partials but not yet added to x.
+struct Pending {
+  const float* bias = nullptr;
+  const float* gate = nullptr;
+  int n = 0;
+};
+
+oasis_epilogue_t partial_epi(float* part, int64_t M, int64_t N) {
+  oasis_epilogue_t e = epi_zero();
+  e.kind = OASIS_EPI_PARTIAL_F32;
+  e.out_f32 = part;
+  e.ld_out = N;
+  e.split_stride = M * N;
+  return e;
+}
+
+int check_dit_buf(const oasis_dit_buffers_t* buf) {
+  OASIS_REQUIRE(buf && buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp && buf->partial,
+                OASIS_ERR_NULL, "dit: missing buffer");
+  OASIS_REQUIRE(buf->max_splits >= 1, OASIS_ERR_ARG, "dit: max_splits must be >= 1");
+  return OASIS_OK;
+}
+
+// run_sub_block (oasis_inference.py:995-1215) for sub-blocks [j0, j1); sub-block j is
+// spatial for even j. The FC2 residual of the last sub-block is left pending.
+int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T, const float* ada,
+               int64_t fs, int64_t j0, int64_t j1, Pending* pend, oasis_stream_t stream,
+               const hipEvent_t* ada_ready = nullptr) {
   const int64_t D = w->d_model, H = w->n_heads, Dm = w->d_mlp;
   const int64_t P = (int64_t)w->grid_h * w->grid_w;
   const int64_t M = B * T * P;
-  OASIS_REQUIRE(M <= buf->max_rows, OASIS_ERR_SHAPE, "dit: %lld rows exceed the workspace (%lld)", (long long)M,
-                (long long)buf->max_rows);
   hipStream_t s = (hipStream_t)stream;
+  const Plan& pl = plan();
+  const int so = pl.splits[ROLE_O] > 0 ? std::min<int>(pl.splits[ROLE_O], buf->max_splits)
+                                       : choose_splits(M, D, D, buf->max_splits);
+  const int sf = pl.splits[ROLE_FC2] > 0 ? std::min<int>(pl.splits[ROLE_FC2], buf->max_splits)
+                                         : choose_splits(M, D, Dm, buf->max_splits);
 
   oasis_epilogue_t qkv = epi_zero();
   qkv.kind = OASIS_EPI_QKV_ROPE;
@@ -114,24 +241,20 @@ extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_di
   qkv.v = buf->v;
   qkv.rows_per_frame = P;
   qkv.frames_per_stream = T;
-
-  oasis_epilogue_t gres = epi_zero();
-  gres.kind = OASIS_EPI_GATED_RES;
-  gres.out_f32 = buf->x;
-  gres.ld_out = D;
-  gres.gate_fstride = ada_fstride;
-  gres.rows_per_frame = P;
-
   oasis_epilogue_t gelu = epi_zero();
   gelu.kind = OASIS_EPI_GELU_TANH;
   gelu.out_bf16 = buf->mlp;
   gelu.ld_out = Dm;
+  const oasis_epilogue_t part = partial_epi(buf->partial, M, D);
 
-  // run_sub_block (oasis_inference.py:995-1215): sub-block j is spatial for even j
   for (int64_t j = j0; j < j1; ++j) {
     const bool spatial = (j % 2) == 0;
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
-    OASIS_TRY(oasis_ln_modulate(buf->x, M, D, a, a + D, ada_fstride, P, buf->h, kLnEps, stream));
+    if (ada_ready && hipStreamWaitEvent(s, ada_ready[j], 0) != hipSuccess)
+      return oasis::check_launch("wait for adaLN rows");
+    // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
+    OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
+                                fs, buf->h, kLnEps, stream));
     if (spatial) {  // heads-first per frame: [(b*T + t)*H + h][p][64]
       qkv.s_b = T * H * P * 64;
       qkv.s_t = H * P * 64;
@@ -149,33 +272,50 @@ extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_di
       qkv.rope_sinp = w->t_sinp;
       qkv.rope_by_frame = 1;
     }
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->qkv_w[j], D, M, 3 * D, D, qkv, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[j], D, M, 3 * D, D, qkv,
+                                     pl.tile[ROLE_QKV], 1, s));
     if (spatial)
       OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
     else
       OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
-    gres.bias = w->out_b[j];
-    gres.gate = a + 2 * D;
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->attn, D, (const bf16*)w->out_w[j], D, M, D, D, gres, s));
-    OASIS_TRY(oasis_ln_modulate(buf->x, M, D, a + 3 * D, a + 4 * D, ada_fstride, P, buf->h, kLnEps, stream));
+    // O projection as split-K partials; bias + gated residual + LN + modulate fused after
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->out_w[j], D, M, D, D, part,
+                                     pl.tile[ROLE_O], so, s));
+    OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, so, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
+                                a + 3 * D, fs, buf->h, kLnEps, stream));
     gelu.bias = w->fc1_b[j];
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->fc1_w[j], D, M, Dm, D, gelu, s));
-    gres.bias = w->fc2_b[j];
-    gres.gate = a + 5 * D;
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[j], Dm, M, D, Dm, gres, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->fc1_w[j], D, M, Dm, D, gelu,
+                                     pl.tile[ROLE_FC1], 1, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[j], Dm, M, D, Dm, part,
+                                     pl.tile[ROLE_FC2], sf, s));
+    pend->bias = w->fc2_b[j];
+    pend->gate = a + 5 * D;
+    pend->n = sf;
   }
   return OASIS_OK;
 }
 
-extern "C" int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M,
-                               const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream) {
+int dit_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T, const float* ada) {
   OASIS_TRY(check_dit(w));
-  OASIS_REQUIRE(buf && buf->x && buf->h && ada && v_out, OASIS_ERR_NULL, "dit_final: null pointer");
-  OASIS_REQUIRE(M > 0 && M <= buf->max_rows, OASIS_ERR_SHAPE, "dit_final: bad row count");
+  OASIS_TRY(check_dit_buf(buf));
+  OASIS_REQUIRE(ada, OASIS_ERR_NULL, "dit: null ada");
+  OASIS_REQUIRE(B > 0 && T > 0 && T <= w->t_max, OASIS_ERR_SHAPE, "dit: need B > 0, 0 < T <= t_max (%d)", w->t_max);
+  const int64_t M = B * T * (int64_t)w->grid_h * w->grid_w;
+  OASIS_REQUIRE(M <= buf->max_rows, OASIS_ERR_SHAPE, "dit: %lld rows exceed the workspace (%lld)", (long long)M,
+                (long long)buf->max_rows);
+  return OASIS_OK;
+}
+
+// final layer (oasis_inference.py:1497-1521): adaLN(2 chunks) + LN + modulate + linear,
+// with any pending FC2 residual folded into the LN pass
+int dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M, const float* ada, int64_t fs,
+              const Pending& pend, float* v_out, oasis_stream_t stream, hipEvent_t ada_ready = nullptr) {
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w;
-  // final layer (oasis_inference.py:1497-1521): adaLN(2 chunks) + LN + modulate + linear
+  if (ada_ready && hipStreamWaitEvent((hipStream_t)stream, ada_ready, 0) != hipSuccess)
+    return oasis::check_launch("wait for adaLN rows");
   const float* fa = ada + (int64_t)w->n_sub * 6 * D;
-  OASIS_TRY(oasis_ln_modulate(buf->x, M, D, fa, fa + D, ada_fstride, P, buf->h, kLnEps, stream));
+  OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, pend.n, M * D, pend.bias, pend.gate, fs, P, fa + D, fa, fs,
+                              buf->h, kLnEps, stream));
   oasis_epilogue_t fin = epi_zero();
   fin.kind = OASIS_EPI_STORE_F32;
   fin.bias = w->final_b;
@@ -185,11 +325,100 @@ extern "C" int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buf
                             (hipStream_t)stream);
 }
 
+}  // namespace
+
+namespace {
+
+// conditioning MLP for R rows: cond = W2 silu(W0 temb(t) + b0) + b2 + Wext action + bext
+int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, int64_t R, float* tfreq, float* hid,
+             float* cond, oasis_stream_t stream) {
+  OASIS_REQUIRE(t && action && tfreq && hid && cond, OASIS_ERR_NULL, "conditioning: null buffer");
+  OASIS_REQUIRE(w->temb_w0 && w->temb_b0 && w->temb_w2 && w->temb_b2 && w->ext_w && w->ext_b, OASIS_ERR_NULL,
+                "conditioning: missing conditioning weights");
+  const int64_t D = w->d_model, F = w->freq_dim, E = w->ext_dim_pad;
+  OASIS_TRY(oasis_timestep_embedding(t, R, F, tfreq, stream));
+  OASIS_TRY(oasis_gemv_bf16(tfreq, F, R, w->temb_w0, D, F, w->temb_b0, hid, D, OASIS_ACT_NONE, OASIS_ACT_SILU, 0,
+                            stream));
+  OASIS_TRY(oasis_gemv_bf16(action, E, R, w->ext_w, D, E, w->ext_b, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 0,
+                            stream));
+  return oasis_gemv_bf16(hid, D, R, w->temb_w2, D, D, w->temb_b2, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 1, stream);
+}
+
+// ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b on the side stream, one event per consumer
+// (sub-block j -> ev[j], final layer -> ev[n_sub]); returns the side-stream table.
+int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, oasis_stream_t stream,
+               SideStream** out) {
+  SideStream* ss = nullptr;
+  OASIS_TRY(side_stream(&ss));
+  const int64_t D = w->d_model, NA = ada_width(w);
+  if (!plan().overlap) {  // all projections in one pass on the caller's stream; no waits needed
+    OASIS_TRY(oasis_gemv_bf16(cond, D, R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
+                              stream));
+    *out = nullptr;
+    return OASIS_OK;
+  }
+  if (hipEventRecord(ss->fork, (hipStream_t)stream) != hipSuccess || hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
+    return oasis::check_launch("adaLN fork");
+  for (int j = 0; j <= w->n_sub; ++j) {
+    const int64_t r0 = (int64_t)j * 6 * D, n = j < w->n_sub ? 6 * D : 2 * D;
+    OASIS_TRY(oasis_gemv_bf16(cond, D, R, static_cast<const bf16*>(w->ada_w) + r0 * D, n, D, w->ada_b + r0, ada + r0,
+                              NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, ss->s));
+    if (hipEventRecord(ss->ev[j], ss->s) != hipSuccess) return oasis::check_launch("adaLN event");
+  }
+  *out = ss;
+  return OASIS_OK;
+}
+
+}  // namespace
+
+extern "C" int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T,
+                              const float* t, const float* action, const float* patches, float* tfreq, float* hid,
+                              float* cond, float* ada, float* v_out, oasis_stream_t stream) {
+  OASIS_TRY(dit_args(w, buf, B, T, ada));
+  OASIS_REQUIRE(patches && v_out, OASIS_ERR_NULL, "dit_step: null patches/v_out");
+  OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "dit_step: missing patch-embed weights");
+  const int64_t R = B * T, D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
+  OASIS_REQUIRE(R <= 16, OASIS_ERR_SHAPE, "dit_step: at most 16 frames per call (got %lld)", (long long)R);
+  OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
+  SideStream* ss = nullptr;
+  OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
+  OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x, D,
+                               stream));
+  Pending pend;
+  OASIS_TRY(dit_blocks(w, buf, B, T, ada, NA, 0, w->n_sub, &pend, stream, ss ? ss->ev : nullptr));
+  return dit_final(w, buf, B * T * P, ada, NA, pend, v_out, stream, ss ? ss->ev[w->n_sub] : nullptr);
+}
+
+extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
+                                    int64_t T, const float* ada, int64_t ada_fstride, int64_t j0, int64_t j1,
+                                    oasis_stream_t stream) {
+  OASIS_TRY(dit_args(w, buf, B, T, ada));
+  OASIS_REQUIRE(0 <= j0 && j0 <= j1 && j1 <= w->n_sub, OASIS_ERR_ARG, "dit: sub-block range [%lld, %lld) invalid",
+                (long long)j0, (long long)j1);
+  Pending pend;
+  OASIS_TRY(dit_blocks(w, buf, B, T, ada, ada_fstride, j0, j1, &pend, stream));
+  if (pend.n == 0) return OASIS_OK;
+  const int64_t M = B * T * (int64_t)w->grid_h * w->grid_w;
+  return oasis_residual_ln(buf->x, M, w->d_model, buf->partial, pend.n, M * w->d_model, pend.bias, pend.gate,
+                           ada_fstride, (int64_t)w->grid_h * w->grid_w, nullptr, nullptr, 0, nullptr, kLnEps, stream);
+}
+
+extern "C" int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M,
+                               const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream) {
+  OASIS_TRY(check_dit(w));
+  OASIS_TRY(check_dit_buf(buf));
+  OASIS_REQUIRE(ada && v_out, OASIS_ERR_NULL, "dit_final: null pointer");
+  OASIS_REQUIRE(M > 0 && M <= buf->max_rows, OASIS_ERR_SHAPE, "dit_final: bad row count");
+  return dit_final(w, buf, M, ada, ada_fstride, Pending(), v_out, stream);
+}
+
 extern "C" int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T,
                                  const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream) {
-  OASIS_REQUIRE(w, OASIS_ERR_NULL, "dit_forward: null weights");
-  OASIS_TRY(oasis_dit_sub_blocks(w, buf, B, T, ada, ada_fstride, 0, w->n_sub, stream));
-  return oasis_dit_final(w, buf, B * T * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, v_out, stream);
+  OASIS_TRY(dit_args(w, buf, B, T, ada));
+  OASIS_REQUIRE(v_out, OASIS_ERR_NULL, "dit_forward: null v_out");
+  Pending pend;
+  OASIS_TRY(dit_blocks(w, buf, B, T, ada, ada_fstride, 0, w->n_sub, &pend, stream));
+  return dit_final(w, buf, B * T * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, pend, v_out, stream);
 }
 
 extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, const float* latent,
@@ -197,14 +426,20 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
   OASIS_REQUIRE(w && buf && latent && frame, OASIS_ERR_NULL, "vae_decode: null pointer");
   OASIS_REQUIRE(w->depth > 0 && w->depth <= OASIS_MAX_SUB && w->n_heads > 0 && w->d_model == w->n_heads * 64,
                 OASIS_ERR_SHAPE, "vae_decode: bad depth/heads/d_model");
-  OASIS_REQUIRE(buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp, OASIS_ERR_NULL,
-                "vae_decode: missing buffer");
+  OASIS_REQUIRE(buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp && buf->partial,
+                OASIS_ERR_NULL, "vae_decode: missing buffer");
+  OASIS_REQUIRE(buf->max_splits >= 1, OASIS_ERR_ARG, "vae_decode: max_splits must be >= 1");
   OASIS_REQUIRE(w->pq_w && w->pq_b && w->norm_w && w->norm_b && w->pred_w && w->pred_b && w->rope_cos &&
                     w->rope_sinp,
                 OASIS_ERR_NULL, "vae_decode: missing weight pointer");
   const int64_t D = w->d_model, H = w->n_heads, Dm = w->d_mlp;
   const int64_t L = (int64_t)w->grid_h * w->grid_w;
   hipStream_t s = (hipStream_t)stream;
+  const Plan& pl = plan();
+  const int sp = pl.splits[ROLE_VO] > 0 ? std::min<int>(pl.splits[ROLE_VO], buf->max_splits)
+                                        : choose_splits(L, D, D, buf->max_splits);
+  const int sf = pl.splits[ROLE_VFC2] > 0 ? std::min<int>(pl.splits[ROLE_VFC2], buf->max_splits)
+                                          : choose_splits(L, D, Dm, buf->max_splits);
   OASIS_TRY(oasis_small_linear(latent, w->latent_dim, L, w->latent_dim, w->pq_w, D, w->pq_b, buf->x, D, stream));
 
   oasis_epilogue_t qkv = epi_zero();
@@ -220,32 +455,38 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
   qkv.s_p = 64;
   qkv.rope_cos = w->rope_cos;
   qkv.rope_sinp = w->rope_sinp;
-  oasis_epilogue_t res = epi_zero();
-  res.kind = OASIS_EPI_RESIDUAL;
-  res.out_f32 = buf->x;
-  res.ld_out = D;
   oasis_epilogue_t gelu = epi_zero();
   gelu.kind = OASIS_EPI_GELU_ERF;
   gelu.out_bf16 = buf->mlp;
   gelu.ld_out = Dm;
+  const oasis_epilogue_t part = partial_epi(buf->partial, L, D);
 
+  Pending pend;
   for (int i = 0; i < w->depth; ++i) {
     OASIS_REQUIRE(w->n1_w[i] && w->n1_b[i] && w->qkv_w[i] && w->qkv_b[i] && w->proj_w[i] && w->proj_b[i] &&
                       w->n2_w[i] && w->n2_b[i] && w->fc1_w[i] && w->fc1_b[i] && w->fc2_w[i] && w->fc2_b[i],
                   OASIS_ERR_NULL, "vae_decode: missing weights of block %d", i);
-    OASIS_TRY(oasis_ln_affine(buf->x, L, D, w->n1_w[i], w->n1_b[i], buf->h, kLnEps, stream));
+    // x + attn(LN(x)); x + MLP(LN(x)) (oasis_inference.py:1557-1608)
+    OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->n1_w[i],
+                                w->n1_b[i], 0, buf->h, kLnEps, stream));
     qkv.bias = w->qkv_b[i];
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->qkv_w[i], D, L, 3 * D, D, qkv, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[i], D, L, 3 * D, D, qkv,
+                                     pl.tile[ROLE_VQKV], 1, s));
     OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, 1, L, H, kAttnScale, stream));
-    res.bias = w->proj_b[i];
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, res, s));
-    OASIS_TRY(oasis_ln_affine(buf->x, L, D, w->n2_w[i], w->n2_b[i], buf->h, kLnEps, stream));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, part,
+                                     pl.tile[ROLE_VO], sp, s));
+    OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, sp, L * D, w->proj_b[i], nullptr, 0, L, w->n2_w[i],
+                                w->n2_b[i], 0, buf->h, kLnEps, stream));
     gelu.bias = w->fc1_b[i];
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->fc1_w[i], D, L, Dm, D, gelu, s));
-    res.bias = w->fc2_b[i];
-    OASIS_TRY(oasis::gemm_launch((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[i], Dm, L, D, Dm, res, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->fc1_w[i], D, L, Dm, D, gelu,
+                                     pl.tile[ROLE_VFC1], 1, s));
+    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[i], Dm, L, D, Dm, part,
+                                     pl.tile[ROLE_VFC2], sf, s));
+    pend.bias = w->fc2_b[i];
+    pend.n = sf;
   }
-  OASIS_TRY(oasis_ln_affine(buf->x, L, D, w->norm_w, w->norm_b, buf->h, kLnEps, stream));
+  OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->norm_w, w->norm_b,
+                              0, buf->h, kLnEps, stream));
   oasis_epilogue_t pred = epi_zero();
   pred.kind = OASIS_EPI_UNPATCHIFY;
   pred.bias = w->pred_b;
@@ -254,31 +495,45 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
   pred.unpatch_grid_w = w->grid_w;
   pred.unpatch_patch = w->patch;
   pred.unpatch_channels = 3;
-  return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->pred_w, D, L,
-                            3LL * w->patch * w->patch, D, pred, s);
+  return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->pred_w, D, L, 3LL * w->patch * w->patch, D, pred,
+                            s);
 }
 
 extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                                 const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf, float* chunk,
-                                const float* ctx_z, const float* ada, int64_t n_steps, const float* coeffs,
+                                const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
+                                const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
                                 float* v_out, float* latent, float* frame, oasis_stream_t stream) {
   OASIS_TRY(check_dit(w));
-  OASIS_REQUIRE(buf && vw && vbuf && chunk && ctx_z && ada && coeffs && v_out && latent && frame, OASIS_ERR_NULL,
-                "ddim_frame: null pointer");
-  OASIS_REQUIRE(n_steps > 0 && n_steps <= 1000, OASIS_ERR_ARG, "ddim_frame: bad step count");
+  OASIS_TRY(check_dit_buf(buf));
+  OASIS_REQUIRE(vw && vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
+                OASIS_ERR_NULL, "ddim_frame: null pointer");
+  OASIS_REQUIRE(n_steps > 0 && n_steps <= 15, OASIS_ERR_ARG, "ddim_frame: n_steps must be in [1, 15]");
   OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "ddim_frame: missing patch-embed weights");
+  OASIS_REQUIRE(w->t_max >= 2, OASIS_ERR_SHAPE, "ddim_frame: temporal RoPE table needs >= 2 frames");
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
   OASIS_REQUIRE(2 * P <= buf->max_rows, OASIS_ERR_SHAPE, "ddim_frame: workspace too small for T=2");
   OASIS_REQUIRE((int64_t)vw->grid_h * vw->grid_w == 4 * P && vw->latent_dim >= C, OASIS_ERR_SHAPE,
                 "ddim_frame: VAE grid must be the 2x-upsampled DiT grid");
-  const int64_t NA = ada_width(w);
+  const int64_t NA = ada_width(w), R = 1 + n_steps;
   hipStream_t s = (hipStream_t)stream;
+  // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; the adaLN
+  // projections of all rows stream on the side stream while step 0 runs
+  OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
+  SideStream* ss = nullptr;
+  OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
+  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
   for (int64_t i = 0; i < n_steps; ++i) {
+    // z = [context frame; patch-embedded chunk] (oasis_inference.py:1911-1913)
     if (hipMemcpyAsync(buf->x, ctx_z, P * D * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess)
       return oasis::check_launch("ddim_frame context copy");
     OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x + P * D, D,
                                  stream));
-    OASIS_TRY(oasis_dit_forward(w, buf, 1, 2, ada, (1 + i) * NA, v_out, stream));
+    const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
+    Pending pend;
+    const bool wait = ss && i == 0;
+    OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, wait ? ss->ev : nullptr));
+    OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream, wait ? ss->ev[w->n_sub] : nullptr));
     const float* c = coeffs + 6 * i;
     OASIS_TRY(oasis_ddim_update(chunk, v_out + P * w->patch_dim, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5],
                                 stream));

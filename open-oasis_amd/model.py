@@ -151,8 +151,8 @@ class DiT:
     def weight_bytes(self):
         return sum(t.numel() * t.element_size() for t in self._keep)
 
-    def workspace(self, max_rows, max_cond=16):
-        return DiTWorkspace(self, max_rows, max_cond)
+    def workspace(self, max_rows, max_cond=16, max_splits=None):
+        return DiTWorkspace(self, max_rows, max_cond, max_splits)
 
     # -- building blocks ---------------------------------------------------------------
     def conditioning(self, t, actions, ws, stream=None):
@@ -209,8 +209,11 @@ class DiT:
 class DiTWorkspace:
     """Activation buffers for up to max_rows tokens and max_cond conditioning rows."""
 
-    def __init__(self, dit, max_rows, max_cond=16):
+    def __init__(self, dit, max_rows, max_cond=16, max_splits=None):
         dev, d, bf = dit.device, dit.d, torch.bfloat16
+        # split-K slices for the O / FC2 projections; small token counts need more splits
+        if max_splits is None:
+            max_splits = 8 if max_rows <= 640 else (2 if max_rows <= 2048 else 1)
         self.max_rows, self.max_cond = max_rows, max_cond
         self.x = torch.zeros(max_rows, d, device=dev)
         self.h = torch.zeros(max_rows, d, device=dev, dtype=bf)
@@ -219,6 +222,8 @@ class DiTWorkspace:
         self.v = torch.zeros(max_rows, d, device=dev, dtype=bf)
         self.attn = torch.zeros(max_rows, d, device=dev, dtype=bf)
         self.mlp = torch.zeros(max_rows, dit.d_mlp, device=dev, dtype=bf)
+        self.max_splits = max_splits
+        self.partial = torch.zeros(max_splits, max_rows, d, device=dev)
         self.v_out = torch.zeros(max_rows, dit.patch_dim, device=dev)
         self.t = torch.zeros(max_cond, device=dev)
         self.act = torch.zeros(max_cond, dit.ext_pad, device=dev)
@@ -228,8 +233,9 @@ class DiTWorkspace:
         self.ada = torch.zeros(max_cond, dit.ada_width, device=dev)
         S = L.DiTBuffers()
         S.max_rows = max_rows
-        for name in ("x", "h", "q", "k", "v", "attn", "mlp"):
+        for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
             setattr(S, name, getattr(self, name).data_ptr())
+        S.max_splits = max_splits
         self.struct = S
 
 
@@ -296,11 +302,14 @@ class VAEWorkspace:
         self.v = torch.zeros(n, d, device=dev, dtype=bf)
         self.attn = torch.zeros(n, d, device=dev, dtype=bf)
         self.mlp = torch.zeros(n, vae.d_mlp, device=dev, dtype=bf)
+        self.max_splits = 4
+        self.partial = torch.zeros(self.max_splits, n, d, device=dev)
         self.latent = torch.zeros(n, vae.latent_dim, device=dev)
         self.frame = torch.zeros(*vae.frame_shape, device=dev)
         S = L.VAEBuffers()
-        for name in ("x", "h", "q", "k", "v", "attn", "mlp"):
+        for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
             setattr(S, name, getattr(self, name).data_ptr())
+        S.max_splits = self.max_splits
         self.struct = S
 
 
@@ -342,7 +351,8 @@ class DiTStep:
     def __init__(self, dit, B=1, T=2, stream=None):
         self.dit, self.B, self.T = dit, B, T
         self.M = B * T * dit.P
-        self.ws = dit.workspace(self.M, max_cond=max(16, B * T))
+        assert B * T <= 16, "one step conditions at most 16 frames"
+        self.ws = dit.workspace(self.M, max_cond=16)
         self.patches = torch.zeros(self.M, dit.patch_dim, device=dit.device)
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dit.device)
         self.graph = None
@@ -357,9 +367,9 @@ class DiTStep:
 
     def enqueue(self):
         d, ws = self.dit, self.ws
-        d.conditioning_inplace(self.B * self.T, ws, self.stream)
-        d.patch_embed(self.patches, ws.x, self.stream)
-        d.forward_inplace(ws, self.B, self.T, ws.ada, d.ada_width, ws.v_out, self.stream)
+        L.call("oasis_dit_step", ctypes.byref(d.struct), ctypes.byref(ws.struct), self.B, self.T, L.ptr(ws.t),
+               L.ptr(ws.act), L.ptr(self.patches), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada),
+               L.ptr(ws.v_out), L.stream_handle(self.stream))
 
     def capture(self):
         self.graph = Graph(self.enqueue, self.stream)
@@ -410,13 +420,13 @@ class FramePipeline:
         torch.cuda.synchronize(self.dit.device)
 
     def enqueue(self):
-        d, ws, s = self.dit, self.ws, self.stream
-        d.conditioning_inplace(1 + self.n, ws, s)
-        d.patch_embed(self.ctx_patches, self.ctx_z, s)
+        d, ws = self.dit, self.ws
         L.call("oasis_ddim_frame", ctypes.byref(d.struct), ctypes.byref(ws.struct),
                ctypes.byref(self.vae.struct), ctypes.byref(self.vws.struct), L.ptr(self.chunk),
-               L.ptr(self.ctx_z), L.ptr(ws.ada), self.n, ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.v_out),
-               L.ptr(self.vws.latent), L.ptr(self.vws.frame), L.stream_handle(s))
+               L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
+               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
+               L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent), L.ptr(self.vws.frame),
+               L.stream_handle(self.stream))
 
     def capture(self):
         self.graph = Graph(self.enqueue, self.stream)

@@ -398,3 +398,67 @@ def test_rope_layout_surface():
         ref = oracle.apply_rope_swap(x[:, :, i], c4, s4).permute(0, 2, 1, 3).reshape(-1, 64)
         assert_close(got, ref, 0.999999, 1e-5, "rope_layout " + name)
     assert torch.equal(vo.cpu(), x[:, :, 2].permute(0, 2, 1, 3).reshape(-1, 64))
+
+
+# ---------------------------------------------------------------- tile configs, split-K, fused LN
+@pytest.mark.parametrize("tile", list(range(23)))
+def test_gemm_tile_configs(tile):
+    M, N, K = 288, 1024, 1024
+    g = _gen(30 + tile)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    out = torch.zeros(M, N, device="cuda")
+    e = _epi(kind=L.EPI_STORE_F32, out_f32=out, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    sync()
+    assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4, 8])
+def test_gemm_split_k_partials(splits):
+    M, N, K = 288, 1024, 4096
+    g = _gen(40 + splits)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    part = torch.zeros(splits, M, N, device="cuda")
+    e = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(e), 0, splits,
+           stream())
+    sync()
+    ref = A.float() @ B.float().t()
+    assert_close(part.sum(0), ref, 0.999999, 1e-4, "split-K %d" % splits)
+    kk = K // splits  # each slice is the product over its own K range
+    assert_close(part[-1], A[:, -kk:].float() @ B[:, -kk:].float().t(), 0.999999, 1e-4, "last slice")
+
+
+@pytest.mark.parametrize("np_,mode", [(0, "mod"), (4, "mod"), (2, "affine"), (3, "residual_only")])
+def test_residual_ln(np_, mode):
+    M, D, P = 288, 1024, 144
+    g = _gen(50 + np_)
+    x0 = torch.randn(M, D, generator=g) * 2
+    part = torch.randn(max(np_, 1), M, D, generator=g)
+    bias = torch.randn(D, generator=g)
+    fs = 6 * D
+    ada = torch.randn(2, fs, generator=g) * 0.3
+    x = dev(x0)
+    y = torch.zeros(M, D, device="cuda", dtype=torch.bfloat16)
+    ada_d = dev(ada)
+    f = torch.arange(M) // P
+    if mode == "affine":
+        w_aff, b_aff = torch.randn(D, generator=g), torch.randn(D, generator=g)
+        la, lb, lfs, gate, gfs = dev(w_aff), dev(b_aff), 0, None, 0
+    else:
+        la, lb, lfs, gate, gfs = ada_d[0, D:], ada_d[0, :], fs, ada_d[0, 2 * D:], fs
+    yp = None if mode == "residual_only" else y
+    L.call("oasis_residual_ln", L.ptr(x), M, D, L.ptr(dev(part)), np_, M * D, L.ptr(dev(bias)), L.ptr(gate), gfs, P,
+           L.ptr(la), L.ptr(lb), lfs, L.ptr(yp), 1e-6, stream())
+    sync()
+    xr = x0.clone()
+    if np_ > 0:
+        upd = part[:np_].sum(0) + bias
+        xr = xr + (upd if mode == "affine" else ada[f, 2 * D:3 * D] * upd)
+    assert_close(x, xr, 0.9999999, 1e-5, "residual (%s, %d partials)" % (mode, np_))
+    if mode == "mod":
+        assert_close(y, oracle.layer_norm(xr) * ada[f, D:2 * D] + ada[f, :D], 0.99999, 1e-2, "ln modulate")
+    elif mode == "affine":
+        assert_close(y, oracle.layer_norm(xr, w_aff, b_aff), 0.99999, 1e-2, "ln affine")
