@@ -41,6 +41,11 @@ typedef void* oasis_stream_t;
 const char* oasis_last_error(void);
 int oasis_abi_version(void);
 
+/* sizeof of the ABI structs, for bindings to check their mirrors: which = 0 epilogue,
+ * 1 DiT weights, 2 DiT buffers, 3 VAE weights, 4 VAE buffers; -1 for anything else.
+ * No counterpart in the reference (its kernels take ttnn tensors). */
+int64_t oasis_abi_struct_size(int which);
+
 /* ======================================================================
  * Reference kernel surface (destination passing: inputs first, outputs last).
  * Elementwise kernels take flat tensors of n elements, all of one dtype.

@@ -139,17 +139,32 @@ def lib():
         h = ctypes.CDLL(LIB_PATH)
         h.oasis_last_error.restype = ctypes.c_char_p
         h.oasis_last_error.argtypes = []
+        h.oasis_abi_struct_size.restype = c_i64
+        h.oasis_abi_struct_size.argtypes = [c_i]
         for name, argt in SIGNATURES.items():
             f = getattr(h, name)
             f.argtypes = argt
             f.restype = c_i
         _LIB = h
+        check_struct_layouts()
     return _LIB
 
 
 def exported_names():
     """Names of the C entry points this binding knows (all declared in oasis_hip.h)."""
-    return ["oasis_last_error"] + list(SIGNATURES)
+    return ["oasis_last_error", "oasis_abi_struct_size"] + list(SIGNATURES)
+
+
+STRUCTS = (Epilogue, DiTWeights, DiTBuffers, VAEWeights, VAEBuffers)
+
+
+def check_struct_layouts():
+    """Raise if a ctypes mirror's size differs from the C struct's."""
+    h = lib()
+    for i, st in enumerate(STRUCTS):
+        c = h.oasis_abi_struct_size(i)
+        if c != ctypes.sizeof(st):
+            raise ImportError("ABI mismatch: %s is %d bytes in C, %d in ctypes" % (st.__name__, c, ctypes.sizeof(st)))
 
 
 def call(name, *args):

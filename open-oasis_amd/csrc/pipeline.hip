@@ -132,6 +132,17 @@ const Plan& plan() {
 extern "C" const char* oasis_last_error(void) { return oasis::g_err; }
 extern "C" int oasis_abi_version(void) { return OASIS_ABI_VERSION; }
 
+extern "C" int64_t oasis_abi_struct_size(int which) {
+  switch (which) {
+    case 0: return sizeof(oasis_epilogue_t);
+    case 1: return sizeof(oasis_dit_weights_t);
+    case 2: return sizeof(oasis_dit_buffers_t);
+    case 3: return sizeof(oasis_vae_weights_t);
+    case 4: return sizeof(oasis_vae_buffers_t);
+    default: return -1;
+  }
+}
+
 namespace {
 
 constexpr float kLnEps = 1e-6f;

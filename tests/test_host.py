@@ -1,0 +1,114 @@
+"""Host-side logic on the CPU: schedules and DDIM coefficients, the RoPE tables and the
+weight packing the device kernels consume (laid out on device='cpu' here), and the
+determinism of the synthetic inputs."""
+import torch
+
+import oracle
+from helpers import pkg
+
+M = pkg.model
+S = pkg.schedule
+synth = pkg.synth
+
+
+def test_schedules_match_the_oracle():
+    assert torch.equal(S.sigmoid_alphas_cumprod(), oracle.sigmoid_alphas_cumprod())
+    assert torch.equal(S.cosine_alphas_cumprod(), oracle.cosine_alphas_cumprod())
+    for n in (1, 4, 10, 50):
+        assert S.ddim_steps(n) == oracle.ddim_timesteps(n)
+
+
+def test_ddim_coefficients_match_the_oracle():
+    ac = S.cosine_alphas_cumprod()
+    steps = S.ddim_steps(4)
+    flat = S.ddim_coefficients(ac, steps)
+    assert len(flat) == 24
+    for i, (t, tn) in enumerate(steps):
+        ref = oracle.ddim_coeffs(ac, t, tn, i == len(steps) - 1)
+        for a, b in zip(flat[6 * i:6 * i + 6], ref):
+            assert abs(a - b) <= 1e-6 * max(1.0, abs(b))
+
+
+def test_rope_tables_match_the_oracle():
+    f = synth.theta_freqs(16, 32)
+    cos, sinp = M.rope_tables(M._axial_angles(f, 9, 16))
+    rc, rs = oracle.rope_cos_sinperm(oracle.spatial_rope_angles(f, 9, 16), 64)
+    assert torch.allclose(cos, rc, atol=1e-6) and torch.allclose(sinp, rs, atol=1e-6)
+    ft = synth.theta_freqs(32, 64)
+    cos, sinp = M.rope_tables(M.temporal_angles(ft, 32))
+    rc, rs = oracle.rope_cos_sinperm(oracle.temporal_rope_angles(ft, 32), 64)
+    assert torch.allclose(cos, rc, atol=1e-6) and torch.allclose(sinp, rs, atol=1e-6)
+    # VAE: 32 of the 64 head dims rotate; the rest is the identity
+    fv = synth.theta_freqs(8, 16)
+    cos, sinp = M.rope_tables(M._axial_angles(fv, 18, 32))
+    assert cos.shape == (576, 64)
+    assert torch.equal(cos[:, 32:], torch.ones(576, 32)) and torch.equal(sinp[:, 32:], torch.zeros(576, 32))
+    x = torch.randn(576, 64, generator=torch.Generator().manual_seed(0))
+    ref = oracle.apply_rotary_emb(oracle.vae_rope_angles(fv, 18, 32), x)
+    assert torch.allclose(oracle.apply_rope_swap(x, cos, sinp), ref, atol=1e-5)
+
+
+def _small_dit(seed=3):
+    dr = synth.Draw(seed)
+    return synth.dit_weights(dr, n_blocks=2, d=128, n_heads=2, d_mlp=256)
+
+
+def test_dit_packing_adaln_rows():
+    w = _small_dit()
+    dit = M.DiT(w, "cpu")
+    assert dit.ada_width == 4 * 6 * 128 + 2 * 128 and dit.ada_w.shape == (dit.ada_width, 128)
+    cond = torch.randn(3, 128, generator=torch.Generator().manual_seed(1))
+    rows = oracle.silu(cond) @ dit.ada_w.float().t() + dit.ada_b
+    for j in range(4):  # sub-block j: blocks.(j//2).(s|t), chunks shift, scale+1, gate, shift, scale+1, gate
+        p = "blocks.%d.%s." % (j // 2, "st"[j % 2])
+        ref = oracle.silu(cond) @ w[p + "ada_w"].float().t() + w[p + "ada_b"]
+        got = rows[:, j * 768:(j + 1) * 768]
+        for c in range(6):
+            add = 1.0 if c in (1, 4) else 0.0
+            assert torch.allclose(got[:, c * 128:(c + 1) * 128], ref[:, c * 128:(c + 1) * 128] + add, atol=1e-4)
+    ref = oracle.silu(cond) @ w["final.ada_w"].float().t() + w["final.ada_b"]
+    fin = rows[:, 4 * 768:]
+    assert torch.allclose(fin[:, :128], ref[:, :128], atol=1e-4)
+    assert torch.allclose(fin[:, 128:], ref[:, 128:] + 1.0, atol=1e-4)
+
+
+def test_dit_packing_patch_embed_and_action_pad():
+    w = _small_dit()
+    dit = M.DiT(w, "cpu")
+    lat = torch.randn(2, 16, 18, 32, generator=torch.Generator().manual_seed(2))
+    patches = oracle.patchify_to_output_space(lat)                  # [2, 144, 64], (p, q, c) columns
+    xw = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.xemb_w)]
+    got = patches @ xw.float().t() + w["x_emb.b"]
+    ref = oracle.patch_embed(lat, {k: v.float() for k, v in w.items()})
+    assert torch.allclose(got, ref, atol=2e-2 * ref.abs().max().item())
+    ext = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.ext_w)]
+    assert ext.shape == (128, 64) and torch.equal(ext[:, 25:], torch.zeros(128, 39, dtype=ext.dtype))
+    assert dit.struct.n_sub == 4 and dit.struct.d_model == 128 and dit.struct.t_max == 32
+
+
+def test_vae_packing():
+    dr = synth.Draw(4)
+    vw = synth.vae_weights(dr, depth=2, d=128, n_heads=2, d_mlp=256)
+    vae = M.VAE(vw, "cpu")
+    assert vae.depth == 2 and vae.frame_shape == (3, 360, 640)
+    assert vae.struct.depth == 2 and vae.struct.latent_dim == 32 and vae.struct.patch == 20
+    ws = vae.workspace()
+    assert ws.struct.max_splits == ws.partial.shape[0]
+
+
+def test_synthetic_inputs_are_deterministic():
+    a, b = synth.config0(), synth.config0()
+    for k in ("x", "cond"):
+        assert torch.equal(a[k], b[k])
+    for k in a["w"]:
+        assert torch.equal(a["w"][k], b["w"][k])
+    acts = synth.one_hot_actions(synth.Draw(5), 7)
+    assert acts.shape == (7, 25) and torch.equal(acts.sum(-1), torch.ones(7))
+
+
+def test_workspace_split_sizing():
+    dit = M.DiT(_small_dit(), "cpu")
+    assert dit.workspace(288).max_splits == 8
+    assert dit.workspace(2048).max_splits == 2
+    ws = dit.workspace(4608)
+    assert ws.max_splits == 1 and ws.struct.max_rows == 4608

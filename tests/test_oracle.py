@@ -1,0 +1,383 @@
+"""Pins the fp32 CPU oracle (CPU only).
+
+The reference ships no golden vectors and its own tests need Tenstorrent hardware, so
+each oracle function is checked against something independent of its own formula:
+torch.nn.functional, closed forms evaluated in fp64 with ``math``, invariants the
+mathematics fixes, or fp64 brute-force loops written from the reference's semantics.
+Each check is chosen so that a plausible mistake (dropped term, wrong sign, wrong index,
+transposed operand) fails it.
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+torch.set_default_dtype(torch.float32)
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _close(a, b, tol):
+    a, b = a.double(), b.double()
+    err = (a - b).abs().max().item() / max(b.abs().max().item(), 1e-30)
+    assert err <= tol, err
+
+
+# ----------------------------------------------------------------- elementwise
+def test_activations_against_torch_and_scalars():
+    x = torch.linspace(-8, 8, 2001)
+    _close(oracle.silu(x), F.silu(x), 1e-6)
+    _close(oracle.gelu_tanh(x), F.gelu(x, approximate="tanh"), 1e-6)
+    _close(oracle.gelu_erf(x), F.gelu(x), 1e-6)
+    for v in (-3.7, -0.5, 0.0, 0.25, 2.0, 6.5):  # fp64 closed forms
+        t = torch.tensor([v])
+        ref = 0.5 * v * (1 + math.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3)))
+        assert abs(oracle.gelu_tanh(t).item() - ref) < 1e-6
+        assert abs(oracle.gelu_erf(t).item() - 0.5 * v * (1 + math.erf(v / math.sqrt(2)))) < 1e-6
+        assert abs(oracle.silu(t).item() - v / (1 + math.exp(-v))) < 1e-6
+
+
+def test_layer_norm_and_modulate():
+    g = _g(1)
+    x = torch.randn(7, 1024, generator=g) * 3 + 2
+    w, b = torch.randn(1024, generator=g), torch.randn(1024, generator=g)
+    _close(oracle.layer_norm(x), F.layer_norm(x, (1024,), eps=1e-6), 1e-5)
+    _close(oracle.layer_norm(x, w, b), F.layer_norm(x, (1024,), w, b, eps=1e-6), 1e-5)
+    # eps matters for a constant row: (x - mean) = 0 -> output == b exactly
+    c = torch.full((1, 1024), 5.0)
+    assert torch.equal(oracle.layer_norm(c, w, b), b[None])
+    sh, sc = torch.randn(1024, generator=g), torch.randn(1024, generator=g)
+    _close(oracle.modulate(x, sh, sc), x + x * sc + sh, 1e-6)
+
+
+# ----------------------------------------------------------------- conditioning, schedules
+def test_timestep_embedding_closed_form():
+    t = torch.tensor([0.0, 1.0, 14.0, 999.0])
+    e = oracle.timestep_embedding(t, 256)
+    assert e.shape == (4, 256)
+    for r, tv in enumerate(t.tolist()):
+        for i in (0, 1, 37, 127):
+            f = math.exp(-math.log(10000) * i / 128)
+            assert abs(e[r, i].item() - math.cos(tv * f)) < 2e-4
+            assert abs(e[r, 128 + i].item() - math.sin(tv * f)) < 2e-4
+    assert torch.equal(e[0, :128], torch.ones(128)) and torch.equal(e[0, 128:], torch.zeros(128))
+
+
+def test_sigmoid_schedule_closed_form():
+    ac = oracle.sigmoid_alphas_cumprod(1000)
+    assert ac.shape == (1000,) and bool((ac[1:] < ac[:-1]).all())
+    sig = lambda z: 1 / (1 + math.exp(-z))  # noqa: E731
+
+    def f(k):  # normalised alpha-bar before clipping, oasis_inference.py:313-321
+        u = k / 1000
+        return (sig(3) - sig(u * 6 - 3)) / (sig(3) - sig(-3))
+    for k in (1, 10, 250, 500, 750, 990):
+        # cumprod of (1 - beta_i) telescopes to f(k+1)/f(0) while no beta is clipped
+        assert abs(ac[k].item() - f(k + 1) / f(0)) < 1e-5
+
+
+def test_cosine_schedule_closed_form():
+    ac = oracle.cosine_alphas_cumprod(1000)
+    f = lambda k: math.cos((k / 1000 + 0.008) / 1.008 * math.pi / 2) ** 2  # noqa: E731
+    for k in (0, 249, 499, 749, 900):
+        assert abs(ac[k].item() - f(k + 1) / f(0)) < 1e-5
+
+
+def test_ddim_timesteps_follow_the_reference_linspace():
+    assert oracle.ddim_timesteps(4) == [(999, 749), (749, 499), (499, 249), (249, -1)]
+    steps = oracle.ddim_timesteps(12)
+    assert steps[0][0] == 999 and steps[-1] == (82, -1) and len(steps) == 12
+
+
+def test_conditioning_brute_force():
+    g = _g(2)
+    D, Fd = 32, 16
+    w = {"t_emb.w0": torch.randn(D, Fd, generator=g), "t_emb.b0": torch.randn(D, generator=g),
+         "t_emb.w2": torch.randn(D, D, generator=g), "t_emb.b2": torch.randn(D, generator=g),
+         "ext.w": torch.randn(D, 25, generator=g), "ext.b": torch.randn(D, generator=g)}
+    t = torch.tensor([3.0, 700.0])
+    a = torch.zeros(2, 25)
+    a[0, 11] = a[1, 15] = 1.0
+    got = oracle.conditioning(t, a, w)
+    for r in range(2):
+        half = Fd // 2
+        tf = [math.cos(t[r].item() * math.exp(-math.log(1e4) * i / half)) for i in range(half)] + \
+             [math.sin(t[r].item() * math.exp(-math.log(1e4) * i / half)) for i in range(half)]
+        h = [sum(w["t_emb.w0"][o, i].item() * tf[i] for i in range(Fd)) + w["t_emb.b0"][o].item() for o in range(D)]
+        h = [v / (1 + math.exp(-v)) for v in h]
+        for o in range(D):
+            c = sum(w["t_emb.w2"][o, i].item() * h[i] for i in range(D)) + w["t_emb.b2"][o].item()
+            c += sum(w["ext.w"][o, i].item() * a[r, i].item() for i in range(25)) + w["ext.b"][o].item()
+            assert abs(got[r, o].item() - c) < 1e-3 * max(1.0, abs(c))
+
+
+# ----------------------------------------------------------------- RoPE
+def test_rotate_half_and_swap_trick():
+    g = _g(3)
+    x = torch.randn(5, 64, generator=g)
+    assert torch.equal(oracle.rotate_half(oracle.rotate_half(x)), -x)
+    assert torch.equal(oracle.rotate_half(x)[:, 0], -x[:, 1]) and torch.equal(oracle.rotate_half(x)[:, 1], x[:, 0])
+    ang = torch.randn(5, 64, generator=g)
+    cos, sinp = oracle.rope_cos_sinperm(ang, 64)
+    # the reference's device formulation x*cos + swap(x)*sin_perm == apply_rotary_emb
+    _close(oracle.apply_rope_swap(x, cos, sinp), oracle.apply_rotary_emb(ang, x), 1e-6)
+    # ... which is also what the Q_swap weight columns produce (oasis_inference.py:375-403)
+    W = torch.randn(64, 64, generator=g)
+    Wswap = W.clone()
+    Wswap[:, 0::2], Wswap[:, 1::2] = W[:, 1::2], W[:, 0::2]
+    h = torch.randn(5, 64, generator=g)
+    _close((h @ W) * cos + (h @ Wswap) * sinp, oracle.apply_rotary_emb(ang, h @ W), 1e-5)
+
+
+def test_rope_invariants():
+    g = _g(4)
+    x = torch.randn(3, 64, generator=g)
+    ang = torch.randn(3, 64, generator=g).repeat_interleave(1, -1)
+    ang = ang[:, ::2].repeat_interleave(2, -1)  # one angle per pair
+    y = oracle.apply_rotary_emb(ang, x)
+    pn = lambda t: (t.reshape(3, 32, 2) ** 2).sum(-1)  # noqa: E731
+    _close(pn(y), pn(x), 1e-5)                          # rotations preserve each pair's norm
+    assert torch.equal(oracle.apply_rotary_emb(torch.zeros(3, 64), x), x)  # position 0 is the identity
+    # partial rotation (the VAE rotates 32 of 64 dims): the tail passes through unchanged
+    y2 = oracle.apply_rotary_emb(ang[:, :32], x)
+    assert torch.equal(y2[:, 32:], x[:, 32:])
+
+
+def test_axial_angles_match_broadcast_construction():
+    freqs = torch.rand(16, generator=_g(5))
+    a = oracle.spatial_rope_angles(freqs, 9, 16)
+    assert a.shape == (144, 64)
+    hpos = torch.linspace(-1, 1, 9)
+    wpos = torch.linspace(-1, 1, 16)
+    for p in (0, 17, 80, 143):
+        hh, ww = divmod(p, 16)
+        for d in range(64):  # dims 0-31 use the row position, 32-63 the column position
+            ref = (hpos[hh] if d < 32 else wpos[ww]).item() * freqs[(d % 32) // 2].item()
+            assert abs(a[p, d].item() - ref) < 1e-6
+    t = oracle.temporal_rope_angles(torch.rand(32, generator=_g(6)), 5)
+    assert torch.equal(t[0], torch.zeros(64)) and t.shape == (5, 64)
+
+
+# ----------------------------------------------------------------- attention
+def _attn_loops(q, k, v, causal):
+    Lq, Lk, d = q.shape[0], k.shape[0], q.shape[1]
+    out = torch.zeros(Lq, d, dtype=torch.float64)
+    for i in range(Lq):
+        keys = [j for j in range(Lk) if not causal or j <= i]
+        s = [sum(q[i, c].item() * k[j, c].item() for c in range(d)) / math.sqrt(d) for j in keys]
+        m = max(s)
+        e = [math.exp(x - m) for x in s]
+        z = sum(e)
+        for j, ej in zip(keys, e):
+            out[i] += (ej / z) * v[j].double()
+    return out
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_brute_force(causal):
+    g = _g(7)
+    q, k, v = (torch.randn(5, 8, generator=g) for _ in range(3))
+    _close(oracle.attention(q, k, v, causal=causal), _attn_loops(q, k, v, causal), 1e-5)
+
+
+def test_attention_invariants():
+    g = _g(8)
+    v = torch.randn(6, 16, generator=g)
+    k = torch.randn(6, 16, generator=g)
+    q = torch.zeros(6, 16)  # constant scores -> the mean of V
+    _close(oracle.attention(q, k, v), v.mean(0, keepdim=True).expand(6, 16), 1e-6)
+    q = torch.randn(1, 16, generator=g)  # one causal key -> V itself
+    _close(oracle.attention(q, k[:1], v[:1], causal=True), v[:1], 1e-6)
+    # the reference's additive causal bias (oasis_inference.py:843-857) == the causal flag
+    q = torch.randn(6, 16, generator=g)
+    bias = torch.zeros(6, 6).masked_fill(torch.ones(6, 6, dtype=torch.bool).triu(1), -1e4)
+    s = q @ k.t() / 4.0 + bias
+    _close(oracle.attention(q, k, v, causal=True), torch.softmax(s, -1) @ v, 1e-5)
+    # zero-padded keys as in tests/test_dit_block.py:548-554
+    qp, kp, vp = (F.pad(t, [0, 0, 0, 3]) for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qp[None], kp[None], vp[None])[0][:6]
+    _close(oracle.attention(q, k, v, pad_keys_to=9), ref, 1e-5)
+
+
+# ----------------------------------------------------------------- sub-block and step (fp64 loops)
+def _ln64(x):
+    m = x.mean(-1, keepdim=True)
+    return (x - m) / torch.sqrt(((x - m) ** 2).mean(-1, keepdim=True) + 1e-6)
+
+
+def _rope64(x, ang):  # x [..., 64], ang [..., 64] one angle per pair; rotates pairs (2k, 2k+1)
+    y = x.clone()
+    for kk in range(32):
+        a = ang[..., 2 * kk]
+        c, s = torch.cos(a), torch.sin(a)
+        y[..., 2 * kk] = x[..., 2 * kk] * c - x[..., 2 * kk + 1] * s
+        y[..., 2 * kk + 1] = x[..., 2 * kk + 1] * c + x[..., 2 * kk] * s
+    return y
+
+
+def _sub_block_loops(x, c, w, kind, ang):
+    """fp64 restatement of run_sub_block (oasis_inference.py:995-1215) with explicit loops
+    over frames, tokens and heads. x [T, P, D]; c [T, D] (pre-SiLU); ang: spatial [P, 64]
+    or temporal [T, 64]."""
+    T, P, D = x.shape
+    H = D // 64
+    W = {k: v.double() for k, v in w.items()}
+    x = x.double().clone()
+    sc = c.double() * torch.sigmoid(c.double())
+    ada = sc @ W["ada_w"].t() + W["ada_b"]
+    out = x.clone()
+    q = torch.zeros(T, P, D, dtype=torch.float64)
+    k = torch.zeros_like(q)
+    v = torch.zeros_like(q)
+    for t in range(T):
+        sh, s1 = ada[t, 0:D], ada[t, D:2 * D]
+        hmod = _ln64(x[t]) * (1 + s1) + sh
+        qkv = hmod @ W["qkv_w"].t()
+        q[t], k[t], v[t] = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    attn = torch.zeros_like(q)
+    for h in range(H):
+        sl = slice(64 * h, 64 * h + 64)
+        if kind == "s":
+            for t in range(T):
+                qq = _rope64(q[t, :, sl], ang)
+                kk = _rope64(k[t, :, sl], ang)
+                attn[t, :, sl] = _attn_loops(qq, kk, v[t, :, sl], False) if P <= 8 else \
+                    torch.softmax(qq @ kk.t() / 8.0, -1) @ v[t, :, sl]
+        else:
+            for p in range(P):
+                qq = _rope64(q[:, p, sl], ang[:T])
+                kk = _rope64(k[:, p, sl], ang[:T])
+                attn[:, p, sl] = _attn_loops(qq, kk, v[:, p, sl], True)
+    for t in range(T):
+        g_a, sh_m, s_m, g_m = ada[t, 2 * D:3 * D], ada[t, 3 * D:4 * D], ada[t, 4 * D:5 * D], ada[t, 5 * D:]
+        y = out[t] + g_a * (attn[t] @ W["out_w"].t() + W["out_b"])
+        hh = _ln64(y) * (1 + s_m) + sh_m
+        gg = hh @ W["fc1_w"].t() + W["fc1_b"]
+        gg = 0.5 * gg * (1 + torch.tanh(math.sqrt(2 / math.pi) * (gg + 0.044715 * gg ** 3)))
+        out[t] = y + g_m * (gg @ W["fc2_w"].t() + W["fc2_b"])
+    return out
+
+
+def _tiny_sub_w(g, D=128, Dm=256, bias=True):
+    r = lambda *s: torch.randn(*s, generator=g) * 0.1  # noqa: E731
+    return {"ada_w": r(6 * D, D), "ada_b": r(6 * D) if bias else torch.zeros(6 * D), "qkv_w": r(3 * D, D),
+            "out_w": r(D, D), "out_b": r(D), "fc1_w": r(Dm, D), "fc1_b": r(Dm), "fc2_w": r(D, Dm), "fc2_b": r(D)}
+
+
+@pytest.mark.parametrize("kind", ["s", "t"])
+def test_sub_block_against_loops(kind):
+    g = _g(9 if kind == "s" else 10)
+    T, P, D = (2, 6, 128) if kind == "s" else (3, 4, 128)
+    w = _tiny_sub_w(g, D)
+    x = torch.randn(T, P, D, generator=g)
+    c = torch.randn(T, D, generator=g)
+    if kind == "s":
+        ang = oracle.spatial_rope_angles(torch.rand(16, generator=g) * 3, 2, 3)
+    else:
+        ang = oracle.temporal_rope_angles(torch.rand(32, generator=g), T)
+    cs, sp = oracle.rope_cos_sinperm(ang, 64)
+    got = oracle.sub_block(x, oracle.silu(c), w, kind, cs, sp)
+    _close(got, _sub_block_loops(x, c, w, kind, ang), 1e-4)
+
+
+def test_dit_forward_context_rows_do_not_see_the_generated_frame():
+    """KV-invariance (docs/kv_cache_plan.md:15-39): frame-0 rows depend on frame 0 only."""
+    g = _g(11)
+    D = 128
+    w = {"rope.spatial_freqs": torch.rand(16, generator=g), "rope.temporal_freqs": torch.rand(32, generator=g),
+         "final.ada_w": torch.randn(2 * D, D, generator=g) * 0.1, "final.ada_b": torch.randn(2 * D, generator=g),
+         "final.w": torch.randn(64, D, generator=g) * 0.1, "final.b": torch.randn(64, generator=g)}
+    for i in range(2):
+        for kind in "st":
+            for k, v in _tiny_sub_w(g, D).items():
+                w["blocks.%d.%s.%s" % (i, kind, k)] = v
+    z = torch.randn(2, 6, D, generator=g)
+    c = torch.randn(2, D, generator=g)
+    v1 = oracle.dit_forward(z, c, w, grid=(2, 3))
+    z2, c2 = z.clone(), c.clone()
+    z2[1] += torch.randn(6, D, generator=g)
+    c2[1] += 1.0
+    v2 = oracle.dit_forward(z2, c2, w, grid=(2, 3))
+    assert torch.equal(v1[0], v2[0]) and not torch.allclose(v1[1], v2[1])
+
+
+# ----------------------------------------------------------------- DDIM, patches, bridge
+def test_ddim_exact_v_recovers_x0_and_eps():
+    g = _g(12)
+    ac = oracle.cosine_alphas_cumprod()
+    x0, eps = torch.randn(144, 64, generator=g).double(), torch.randn(144, 64, generator=g).double()
+    for (t, tn), last in ((((749, 499)), False), ((249, -1), True)):
+        a = ac[t].double()
+        xt = a.sqrt() * x0 + (1 - a).sqrt() * eps
+        v = a.sqrt() * eps - (1 - a).sqrt() * x0          # v-parametrisation target
+        c = oracle.ddim_coeffs(ac, t, tn, last)
+        an = 1.0 if last else ac[tn].item()
+        _close(oracle.ddim_update(xt, v, c), an ** 0.5 * x0 + (1 - an) ** 0.5 * eps, 1e-6)
+    assert oracle.ddim_coeffs(ac, 249, -1, True)[4:] == (1.0, 0.0)  # last step returns x0
+
+
+def test_patchify_unpatchify_and_embed():
+    g = _g(13)
+    img = torch.randn(2, 16, 18, 32, generator=g)
+    p = oracle.patchify_to_output_space(img)
+    assert p.shape == (2, 144, 64)
+    assert torch.equal(oracle.unpatchify(p), img)
+    # column (p, q, c) of row (h, w) is pixel (c, 2h+p, 2w+q)
+    assert p[1, 5 * 16 + 7, (1 * 2 + 0) * 16 + 3].item() == img[1, 3, 11, 14].item()
+    w = {"x_emb.w": torch.randn(64, 16, 2, 2, generator=g), "x_emb.b": torch.randn(64, generator=g)}
+    _close(oracle.patch_embed(img, w), p @ oracle.patch_embed_roundtrip_weight(w) + w["x_emb.b"], 1e-5)
+
+
+def test_bridge_is_the_pixel_grid_of_the_latent():
+    g = _g(14)
+    img = torch.randn(1, 16, 18, 32, generator=g)
+    lat = oracle.bridge(oracle.patchify_to_output_space(img)[0])
+    # VAE row r = y*32 + x holds the 16 latent channels of pixel (y, x), scaled
+    _close(lat[:, :16], img[0].permute(1, 2, 0).reshape(576, 16) / oracle.SCALING_FACTOR, 1e-6)
+    assert torch.equal(lat[:, 16:], torch.zeros(576, 16))
+
+
+def test_vae_unpatchify_pixels():
+    g = _g(15)
+    patches = torch.randn(576, 1200, generator=g) * 2
+    fr = oracle.vae_unpatchify(patches)
+    assert fr.shape == (3, 360, 640) and fr.abs().max().item() <= 1.0
+    for c, y, x in ((0, 0, 0), (2, 359, 639), (1, 123, 457)):
+        v = patches[(y // 20) * 32 + x // 20, c * 400 + (y % 20) * 20 + x % 20].clamp(-1, 1)
+        assert fr[c, y, x].item() == v.item()
+
+
+def test_vae_decode_against_loops():
+    g = _g(16)
+    D, L_ = 128, 4 * 4
+    r = lambda *s: torch.randn(*s, generator=g) * 0.1  # noqa: E731
+    w = {"pq_w": r(D, 8), "pq_b": r(D), "dec.0.n1_w": 1 + r(D), "dec.0.n1_b": r(D), "dec.0.qkv_w": r(3 * D, D),
+         "dec.0.qkv_b": r(3 * D), "dec.0.proj_w": r(D, D), "dec.0.proj_b": r(D), "dec.0.n2_w": 1 + r(D),
+         "dec.0.n2_b": r(D), "dec.0.fc1_w": r(2 * D, D), "dec.0.fc1_b": r(2 * D), "dec.0.fc2_w": r(D, 2 * D),
+         "dec.0.fc2_b": r(D), "norm_w": 1 + r(D), "norm_b": r(D), "pred_w": r(12, D), "pred_b": r(12),
+         "rope.vae_freqs": torch.rand(8, generator=g)}
+    lat = torch.randn(L_, 8, generator=g)
+    got = oracle.vae_decode(lat, w, grid=(4, 4))
+    W = {k: v.double() for k, v in w.items()}
+    x = lat.double() @ W["pq_w"].t() + W["pq_b"]
+    ang = oracle.vae_rope_angles(w["rope.vae_freqs"], 4, 4).double()   # [16, 32]
+    h = _ln64(x) * W["dec.0.n1_w"] + W["dec.0.n1_b"]
+    qkv = h @ W["dec.0.qkv_w"].t() + W["dec.0.qkv_b"]
+    att = torch.zeros(L_, D, dtype=torch.float64)
+    for hd in range(2):
+        sl = slice(64 * hd, 64 * hd + 64)
+        q, k, v = qkv[:, sl], qkv[:, D:][:, sl], qkv[:, 2 * D:][:, sl]
+        full = torch.cat([ang, torch.zeros(L_, 32, dtype=torch.float64)], -1)  # dims >= 32 unrotated
+        att[:, sl] = _attn_loops(_rope64(q, full), _rope64(k, full), v, False)
+    x = x + att @ W["dec.0.proj_w"].t() + W["dec.0.proj_b"]
+    hh = _ln64(x) * W["dec.0.n2_w"] + W["dec.0.n2_b"]
+    gg = hh @ W["dec.0.fc1_w"].t() + W["dec.0.fc1_b"]
+    gg = 0.5 * gg * (1 + torch.erf(gg / math.sqrt(2)))
+    x = x + gg @ W["dec.0.fc2_w"].t() + W["dec.0.fc2_b"]
+    ref = (_ln64(x) * W["norm_w"] + W["norm_b"]) @ W["pred_w"].t() + W["pred_b"]
+    _close(got, ref, 1e-4)
