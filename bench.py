@@ -37,10 +37,70 @@ def _event_ms(fn, stream, n):
     return s.elapsed_time(e) / n
 
 
+# HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
+# `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
+# scaled by what the same counter reads for a plain device copy of known size.
+TRAFFIC = {"fc1": 15625025, "gemv": 409840236}
+
+
+def _fc1_timing(pkg, dit, ws, stream, n=100):
+    """One FC1 projection of the step (sub-block 0, same buffers, same tile choice),
+    timed alone with HIP events on the step stream."""
+    L = pkg._lib
+    M, D, Dm = 288, dit.d, dit.d_mlp
+    e = L.Epilogue()
+    e.kind, e.bias, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, dit.struct.fc1_b[0], ws.mlp.data_ptr(), Dm
+    A, B = L.ptr(ws.h), ctypes.c_void_p(dit.struct.fc1_w[0])
+
+    def fc1():
+        L.call("oasis_gemm_bf16", A, D, B, D, M, Dm, D, ctypes.byref(e), L.stream_handle(stream))
+    ms = _event_ms(fc1, stream, n)
+    flop = 2 * M * D * Dm
+    nbytes = M * D * 2 + Dm * D * 2 + Dm * 4 + M * Dm * 2   # A, W, bias, out (bf16)
+    return ms, flop, nbytes
+
+
+def _gemv_timing(pkg, dit, ws, stream, R=2, n=50):
+    """The adaLN skinny GEMM over every sub-block's adaLN weights (406 MB bf16)."""
+    L = pkg._lib
+
+    def gemv():
+        L.call("oasis_gemv_bf16", L.ptr(ws.cond), dit.d, R, L.ptr(dit.ada_w), dit.ada_width, dit.d,
+               L.ptr(dit.ada_b), L.ptr(ws.ada), dit.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
+               L.stream_handle(stream))
+    ms = _event_ms(gemv, stream, n)
+    nbytes = dit.ada_width * dit.d * 2 + R * dit.d * 4 + R * dit.ada_width * 4 + dit.ada_width * 4
+    return ms, nbytes
+
+
+def probe(pkg, n=10):
+    """Short run for hardware-counter passes: n launches each of the FC1 GEMM and the
+    adaLN GEMV on config-1 buffers, and n plain 256 MiB device copies (the calibration
+    kernel, 268435456 bytes read and written per launch)."""
+    import torch
+    c1 = pkg.synth.config1()
+    dit = pkg.DiT(c1["w"], "cuda")
+    step = pkg.DiTStep(dit, B=1, T=2)
+    import oracle
+    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
+    step.run()
+    torch.cuda.synchronize()
+    _fc1_timing(pkg, dit, step.ws, step.stream, n)
+    _gemv_timing(pkg, dit, step.ws, step.stream, n=n)
+    src = torch.ones(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "fc1 gemm x%d, adaLN gemv x%d, 256 MiB copy x%d" % (n + 1, n + 1, n)}), flush=True)
+
+
 def cpu_baseline(cfg, oracle, seconds=15.0):
     """The fp32 oracle's DiT step (same weights and inputs) on this host's cores."""
     import torch
-    torch.set_num_threads(os.cpu_count() or 1)
+    # the host cores this job may use (the GPU box exports its CPU share as OMP_NUM_THREADS)
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1)
     w = cfg["w"]
     z = oracle.patch_embed(cfg["latent"][0], w)
     times = []
@@ -68,6 +128,7 @@ def main():
     ap.add_argument("--frames", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-frame", action="store_true")
+    ap.add_argument("--probe", action="store_true", help="short run of the roofline kernels for counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build targets one MI355X; multi-GPU runs are not part of it "
@@ -77,8 +138,11 @@ def main():
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    if args.probe:
+        probe(pkg)
+        return
     import oracle
-    synth, L = pkg.synth, pkg._lib
+    synth = pkg.synth
 
     # ---------------- config 1: the DiT step ----------------
     c1 = synth.config1()
@@ -101,20 +165,15 @@ def main():
     ms_step = 1e3 * (t1 - t0) / args.steps
     ms_step_gpu = ev0.elapsed_time(ev1) / args.steps
 
-    # dominant kernel: the skinny adaLN GEMM streaming every sub-block's adaLN weights
-    # (406 MB bf16) once per step; HIP events on the step stream, same buffers as the step.
     ws = step.ws
-    R = 2
-    def ada_gemv():
-        L.call("oasis_gemv_bf16", L.ptr(ws.cond), dit.d, R, L.ptr(dit.ada_w), dit.ada_width, dit.d,
-               L.ptr(dit.ada_b), L.ptr(ws.ada), dit.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
-               L.stream_handle(step.stream))
-    ada_ms = _event_ms(ada_gemv, step.stream, 50)
-    ada_bytes = dit.ada_width * dit.d * 2 + R * dit.d * 4 + R * dit.ada_width * 4 + dit.ada_width * 4
+    fc1_ms, fc1_flop, fc1_bytes = _fc1_timing(pkg, dit, ws, step.stream)
+    ada_ms, ada_bytes = _gemv_timing(pkg, dit, ws, step.stream)
+    fc1_tflops = fc1_flop / (fc1_ms * 1e-3) / 1e12
     ada_gbs = ada_bytes / (ada_ms * 1e-3) / 1e9
 
-    # whole-step roofline: 1.2124 GB of weights must stream from HBM each step
-    step_bytes = sum(t.numel() * t.element_size() for t in dit._keep)
+    # whole-step floor: every weight (1.21 GB) must stream from HBM once per step
+    step_bytes = dit.weight_bytes
+    step_floor_ms = step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
 
     out = {
         "metric": "ms/DiT step (T=2 bf16) + FPS for 4-step DDIM+VAE frame on 1 MI355X",
@@ -126,11 +185,18 @@ def main():
                    "global_batch": 1, "seq_len": 288, "parallelism": "none (1 GPU)"},
         "ms_per_step_gpu_events": round(ms_step_gpu, 4),
         "step_weight_bytes": step_bytes,
-        "step_hbm_floor_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
-        "roofline": {"kernel": "gemv_kernel (adaLN projections of all 33 consumers, R=2)",
-                     "bound": "hbm", "achieved": round(ada_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ada_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_ms": round(ada_ms, 4), "algorithmic_bytes": ada_bytes},
+        "step_hbm_floor_ms": round(step_floor_ms, 4),
+        "step_roofline_frac": round(step_floor_ms / ms_step, 4),
+        "roofline": {"kernel": "gemm_bf16_kernel, FC1 projection + bias + tanh-GELU (M=288, N=4096, K=1024), "
+                               "the largest of the step's 128 GEMM launches",
+                     "bound": "mfma", "achieved": round(fc1_tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(fc1_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": TRAFFIC.get("fc1"), "avg_launch_ms": round(fc1_ms, 5),
+                     "algorithmic_flop": fc1_flop, "algorithmic_bytes": fc1_bytes},
+        "roofline_hbm": {"kernel": "gemv_kernel, adaLN projections of all 33 consumers (R=2 rows)",
+                         "bound": "hbm", "achieved": round(ada_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ada_gbs / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get("gemv"),
+                         "avg_launch_ms": round(ada_ms, 5), "algorithmic_bytes": ada_bytes},
     }
 
     # ---------------- config 3: the DDIM + VAE frame ----------------
@@ -164,8 +230,11 @@ def main():
             torch.cuda.current_stream().wait_stream(fp.stream)
         torch.cuda.synchronize()
         ms_frame_h2d = 1e3 * (time.perf_counter() - t0) / args.frames
+        frame_floor_ms = (len(c3["steps"]) * dit3.weight_bytes + vae3.weight_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
         out["frame_ms"] = round(ms_frame, 4)
         out["frame_fps"] = round(1e3 / ms_frame, 1)
+        out["frame_hbm_floor_ms"] = round(frame_floor_ms, 4)
+        out["frame_roofline_frac"] = round(frame_floor_ms / ms_frame, 4)
         out["frame_fps_with_h2d"] = round(1e3 / ms_frame_h2d, 1)
         out["frame_workload"] = ("config3: 4 DDIM v-prediction steps (t=999,749,499,249, cosine alphas) "
                                  "over the T=2 DiT + bridge + 12-block ViT VAE decode + unpatchify to "

@@ -179,7 +179,7 @@ typedef struct {
 int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                     int64_t N, int64_t K, const oasis_epilogue_t* epi, oasis_stream_t stream);
 
-/* Same with an explicit tile configuration (0..9, see gemm.hip; -1 = default) and
+/* Same with an explicit tile configuration (0..22, the kTiles table of gemm.hip; -1 = default) and
  * split-K count (splits divides K/64; splits > 1 requires OASIS_EPI_PARTIAL_F32).
  * No counterpart in the reference: it exposes the tiling for tuning and benchmarks. */
 int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
@@ -356,7 +356,9 @@ int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* b
  * (t fp32 [B*T], action fp32 [B*T, ext_dim_pad]), patch embed of patches fp32 [B*T*P, 64]
  * into buf->x, every sub-block and the final layer; v_out fp32 [B*T*P, 64].
  * tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The
- * adaLN projections run on a library-owned side stream, overlapped with the sub-blocks.
+ * adaLN projections of all sub-blocks run as one pass over the stacked adaLN weights before
+ * the first sub-block (with OASIS_ADALN_OVERLAP=1 in the environment: on a library-owned
+ * side stream, each sub-block waiting only for its own rows).
  * (dit_forward_device with compute_cond_for_frame, oasis_inference.py:1406-1526.) */
 int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
                    int64_t T, const float* t, const float* action, const float* patches,
@@ -420,8 +422,8 @@ int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* bu
  *   tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (1 + n_steps rows);
  *   ctx_z: fp32 [P, D] scratch; v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae
  *   latent_dim] scratch; frame: fp32 [3, H, W] output. n_steps <= 15.
- * The adaLN projections of all conditioning rows run on a library-owned side stream,
- * overlapped with the first step (each sub-block waits only for its own rows).
+ * The adaLN projections of all conditioning rows run as one pass before the first step
+ * (OASIS_ADALN_OVERLAP=1: on a library-owned side stream, overlapped with the first step).
  * (ddim_step_fn and the traced frame, oasis_inference.py:1909-1932,2131-2148.) */
 int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                      const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,

@@ -359,8 +359,6 @@ int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, 
 // (sub-block j -> ev[j], final layer -> ev[n_sub]); returns the side-stream table.
 int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, oasis_stream_t stream,
                SideStream** out) {
-  SideStream* ss = nullptr;
-  OASIS_TRY(side_stream(&ss));
   const int64_t D = w->d_model, NA = ada_width(w);
   if (!plan().overlap) {  // all projections in one pass on the caller's stream; no waits needed
     OASIS_TRY(oasis_gemv_bf16(cond, D, R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
@@ -368,6 +366,8 @@ int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float
     *out = nullptr;
     return OASIS_OK;
   }
+  SideStream* ss = nullptr;
+  OASIS_TRY(side_stream(&ss));
   if (hipEventRecord(ss->fork, (hipStream_t)stream) != hipSuccess || hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
     return oasis::check_launch("adaLN fork");
   for (int j = 0; j <= w->n_sub; ++j) {
@@ -528,8 +528,8 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
                 "ddim_frame: VAE grid must be the 2x-upsampled DiT grid");
   const int64_t NA = ada_width(w), R = 1 + n_steps;
   hipStream_t s = (hipStream_t)stream;
-  // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; the adaLN
-  // projections of all rows stream on the side stream while step 0 runs
+  // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
+  // covers all rows (with the overlap option it streams on the side stream during step 0)
   OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
   SideStream* ss = nullptr;
   OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));

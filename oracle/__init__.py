@@ -18,12 +18,18 @@ Pinning (what each function is checked against, in ``tests/test_oracle.py``):
     and the axial broadcast construction of tests/test_rope.py:32-45.
   - attention: fp64 brute-force softmax loops on tiny inputs, T=1 causal == V,
     constant-score == mean(V), causal bias mask == is_causal.
-  - sub-blocks and the DiT step: fp64 loop-level restatement at tiny dims
-    (D=16, H=2, 2x3 grid) in tests, and the KV-invariance property
-    (context-frame rows do not depend on the generated frame).
+  - conditioning: fp64 scalar loops over the timestep MLP and action projection.
+  - schedules: the telescoped closed forms of the sigmoid and cosine alpha-bar.
+  - sub-blocks and the DiT step: fp64 loop-level restatement over frames, tokens
+    and heads at small dims (D=128, 2 heads, 2x3 grid / T=3), and the
+    KV-invariance property (context-frame rows do not depend on the generated
+    frame).
   - DDIM: exact v-target recovers x0 and eps; last step returns x0.
   - bridge / patchify / unpatchify: permutation round trips.
-  - VAE decoder: composition of the pinned pieces; fp64 tiny-dim restatement.
+  - VAE decoder: fp64 restatement of one block at D=128 on a 4x4 grid.
+  - tests/golden/ holds known-answer vectors generated from this oracle (the
+    reference ships none); tests/test_golden.py checks the oracle still
+    reproduces them.
     Parity unpinned for what only the absent upstream vae.py fixes (its RoPE
     frequencies and GELU flavour): those are synthesised from the build's
     stated configuration, not from the real model.
