@@ -35,6 +35,7 @@ enum {
 };
 
 enum { OASIS_F32 = 0, OASIS_BF16 = 1 };
+enum { OASIS_WEIGHTS_BF16 = 0, OASIS_WEIGHTS_FP8 = 1 };
 
 typedef void* oasis_stream_t;
 
@@ -186,6 +187,23 @@ int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ld
                            int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
                            oasis_stream_t stream);
 
+/* fp8 weight GEMM: acc[M,N] = A[M,K] @ (Bq[N,K] * w_scale[N])^T, then the epilogue.
+ * A bf16 (quantized per 32-wide K block to e4m3 with a power-of-two scale inside the kernel),
+ * Bq OCP fp8 e4m3 bytes, w_scale fp32 per output channel. K % 128 == 0, N % 8 == 0,
+ * lda % 8 == 0, ldb % 16 == 0. tile: 0..4 (gemm_fp8.hip's kTiles8), -1 = default;
+ * splits divides K/128 (> 1 requires OASIS_EPI_PARTIAL_F32).
+ * No counterpart in the reference: it has no sub-fp32 weight path (the config-4 serving
+ * case of the build's benchmark plan). */
+int oasis_gemm_fp8(const void* A, int64_t lda, const void* Bq, int64_t ldb, const float* w_scale, int64_t M,
+                   int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
+                   oasis_stream_t stream);
+
+/* Per-output-channel e4m3 quantization of a bf16 weight W[N,K] (K % 8 == 0):
+ * scale[n] = max_k |W[n,k]| / 448 (1 for an all-zero row), q[n,k] = round_e4m3(W[n,k] / scale[n]),
+ * round to nearest even. No counterpart in the reference (see oasis_gemm_fp8). */
+int oasis_quantize_fp8_rows(const void* W, int64_t N, int64_t K, void* q, float* scale,
+                            oasis_stream_t stream);
+
 /* y_bf16[m, :] = LN(x[m, :]) * scale_p1[f(m), :] + shift[f(m), :], f(m) = m / rows_per_frame,
  * frame rows of shift/scale_p1 at + f*ada_fstride.  scale_p1 already holds (1 + scale).
  * LN has no affine, eps as given.  (ttnn.layer_norm + addcmul,
@@ -228,7 +246,8 @@ int oasis_temporal_attention(const void* q, const void* k, const void* v, void* 
 
 enum { OASIS_ACT_NONE = 0, OASIS_ACT_SILU = 1 };
 
-/* Skinny GEMM for R <= 16 rows: out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]).
+/* Skinny GEMM for R <= 1024 rows (one pass over W per 16 rows):
+ * out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]).
  * x fp32 [R, ldx], W bf16 [N, K] (K % 64 == 0), b fp32 [N] or NULL, out fp32 [R, ld_out].
  * x is split into bf16 hi + lo parts, so the product keeps ~16 mantissa bits of x.
  * accumulate != 0 adds into out. (adaLN GEMMs, oasis_inference.py:983-993, and the
@@ -307,6 +326,14 @@ typedef struct {
   const float* t_cos;        /* [t_max, 64] temporal RoPE                          */
   const float* t_sinp;
   int t_max;
+  /* OASIS_WEIGHTS_BF16: qkv_w/out_w/fc1_w/fc2_w are bf16. OASIS_WEIGHTS_FP8: they are e4m3
+   * bytes ([out, in], from oasis_quantize_fp8_rows) with fp32 per-output-channel scales in
+   * qkv_s/out_s/fc1_s/fc2_s, and the four projections run on oasis_gemm_fp8. */
+  int weight_format;
+  const float* qkv_s[OASIS_MAX_SUB];
+  const float* out_s[OASIS_MAX_SUB];
+  const float* fc1_s[OASIS_MAX_SUB];
+  const float* fc2_s[OASIS_MAX_SUB];
 } oasis_dit_weights_t;
 
 /* Activation workspace for up to max_rows = B*T*P tokens (caller-allocated). */
@@ -326,7 +353,7 @@ typedef struct {
 /* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action), then
  * ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b for every sub-block and the final layer.
  *   t: fp32 [R]; action: fp32 [R, ext_dim_pad]; tfreq: fp32 [R, freq_dim] scratch;
- *   hid: fp32 [R, D] scratch; cond: fp32 [R, D]; ada: fp32 [R, n_sub*6D + 2D].  R <= 16.
+ *   hid: fp32 [R, D] scratch; cond: fp32 [R, D]; ada: fp32 [R, n_sub*6D + 2D].  R <= 1024.
  * (compute_cond_for_frame, oasis_inference.py:1406-1427; build_per_frame_adaln,
  * oasis_inference.py:971-993; silu_kernel call, oasis_inference.py:1459-1463.) */
 int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action,
@@ -352,7 +379,7 @@ int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* b
                       int64_t B, int64_t T, const float* ada, int64_t ada_fstride,
                       float* v_out, oasis_stream_t stream);
 
-/* One full DiT denoising step for B streams of T frames (B*T <= 16): conditioning MLP
+/* One full DiT denoising step for B streams of T frames (B*T <= 1024): conditioning MLP
  * (t fp32 [B*T], action fp32 [B*T, ext_dim_pad]), patch embed of patches fp32 [B*T*P, 64]
  * into buf->x, every sub-block and the final layer; v_out fp32 [B*T*P, 64].
  * tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The

@@ -17,6 +17,7 @@ EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32 = 8
 ACT_NONE, ACT_SILU = 0, 1
+WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
 class OasisError(RuntimeError):
@@ -56,6 +57,8 @@ class DiTWeights(ctypes.Structure):
         ("temb_w0", c_p), ("temb_b0", c_p), ("temb_w2", c_p), ("temb_b2", c_p),
         ("ext_w", c_p), ("ext_b", c_p),
         ("s_cos", c_p), ("s_sinp", c_p), ("t_cos", c_p), ("t_sinp", c_p), ("t_max", c_i),
+        ("weight_format", c_i), ("qkv_s", c_p * MAX_SUB), ("out_s", c_p * MAX_SUB), ("fc1_s", c_p * MAX_SUB),
+        ("fc2_s", c_p * MAX_SUB),
     ]
 
 
@@ -99,6 +102,8 @@ SIGNATURES = {
     "oasis_sdpa": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_i, c_i, c_p],
     "oasis_gemm_bf16": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_p],
     "oasis_gemm_bf16_config": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
+    "oasis_gemm_fp8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
+    "oasis_quantize_fp8_rows": [c_p, c_i64, c_i64, c_p, c_p, c_p],
     "oasis_ln_modulate": [c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_f, c_p],
     "oasis_ln_affine": [c_p, c_i64, c_i64, c_p, c_p, c_p, c_f, c_p],
     "oasis_residual_ln": [c_p, c_i64, c_i64, c_p, c_i, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_p,

@@ -1,0 +1,217 @@
+// Epilogue of the projection GEMMs (bf16 and fp8 kernels share it): the device-side
+// copy of oasis_epilogue_t, the XCD-aware workgroup order and the 8-column epilogue.
+#pragma once
+
+#include "oasis_common.h"
+
+namespace {
+
+constexpr int NUM_XCD = 8;
+
+
+struct Epi {
+  int kind;
+  int n_heads;
+  const float* bias;
+  float* out_f32;
+  bf16* out_bf16;
+  int64_t ld_out;
+  const float* gate;
+  int64_t gate_fstride;
+  int64_t rows_per_frame;
+  int64_t frames_per_stream;
+  bf16* q;
+  bf16* k;
+  bf16* v;
+  const float* rope_cos;
+  const float* rope_sinp;
+  int rope_by_frame;
+  int unpatch_grid_w;
+  int64_t s_b, s_t, s_p, s_h;
+  int unpatch_patch;
+  int unpatch_channels;
+  int64_t split_stride;
+};
+
+__device__ __forceinline__ int xcd_remap(int pid, int G) {
+  const int q = G / NUM_XCD, r = G % NUM_XCD;
+  const int xcd = pid % NUM_XCD, local = pid / NUM_XCD;
+  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+__device__ __forceinline__ void store8_bf16(bf16* dst, const float* v) {
+  *reinterpret_cast<bf16x8*>(dst) = pack8(v);
+}
+
+// Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N).
+__device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float* v) {
+  if (e.bias) {
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(e.bias + n0);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(e.bias + n0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] += b0[j];
+      v[j + 4] += b1[j];
+    }
+  }
+  switch (e.kind) {
+    case OASIS_EPI_STORE_F32: {
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      break;
+    }
+    case OASIS_EPI_STORE_BF16:
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    case OASIS_EPI_GELU_TANH: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_tanh(v[j]);
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    }
+    case OASIS_EPI_GELU_ERF: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_erf(v[j]);
+      store8_bf16(e.out_bf16 + m * e.ld_out + n0, v);
+      break;
+    }
+    case OASIS_EPI_GATED_RES: {
+      const int64_t f = m / e.rows_per_frame;
+      const float* g = e.gate + f * e.gate_fstride + n0;
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(g), g1 = *reinterpret_cast<const f32x4*>(g + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x0[j] += g0[j] * v[j];
+        x1[j] += g1[j] * v[j + 4];
+      }
+      *reinterpret_cast<f32x4*>(d) = x0;
+      *reinterpret_cast<f32x4*>(d + 4) = x1;
+      break;
+    }
+    case OASIS_EPI_RESIDUAL: {
+      float* d = e.out_f32 + m * e.ld_out + n0;
+      f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x0[j] += v[j];
+        x1[j] += v[j + 4];
+      }
+      *reinterpret_cast<f32x4*>(d) = x0;
+      *reinterpret_cast<f32x4*>(d + 4) = x1;
+      break;
+    }
+    case OASIS_EPI_QKV_ROPE: {
+      const int D = e.n_heads * 64;
+      const int which = n0 / D;          // 0 q, 1 k, 2 v
+      const int nn = n0 - which * D;
+      const int h = nn >> 6, d0 = nn & 63;
+      const int64_t f = m / e.rows_per_frame, p = m - f * e.rows_per_frame;
+      const int64_t b = f / e.frames_per_stream, t = f - b * e.frames_per_stream;
+      if (which < 2) {
+        const int64_t pos = e.rope_by_frame ? t : p;
+        const float* c = e.rope_cos + pos * 64 + d0;
+        const float* s = e.rope_sinp + pos * 64 + d0;
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * s[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = r[j];
+      }
+      bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
+      store8_bf16(base + b * e.s_b + t * e.s_t + p * e.s_p + h * e.s_h + d0, v);
+      break;
+    }
+    case OASIS_EPI_UNPATCHIFY: {
+      // m = hh*gw + ww; n = (c*ps + pp)*ps + qq -> frame[c][hh*ps + pp][ww*ps + qq]
+      const int ps = e.unpatch_patch, gw = e.unpatch_grid_w;
+      const int64_t hh = m / gw, ww = m - hh * gw;
+      const int64_t W = (int64_t)gw * ps;
+      const int64_t H = e.rows_per_frame / gw * ps;  // rows_per_frame = gh*gw
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = n0 + j;
+        const int c = n / (ps * ps), rem = n - c * ps * ps;
+        const int pp = rem / ps, qq = rem - pp * ps;
+        const float val = fminf(fmaxf(v[j], -1.0f), 1.0f);
+        e.out_f32[(c * H + hh * ps + pp) * W + ww * ps + qq] = val;
+      }
+      break;
+    }
+    default:
+      break;
+  }
+}
+
+Epi to_epi(const oasis_epilogue_t& x) {
+  Epi e;
+  e.kind = x.kind;
+  e.n_heads = x.n_heads;
+  e.bias = x.bias;
+  e.out_f32 = x.out_f32;
+  e.out_bf16 = static_cast<bf16*>(x.out_bf16);
+  e.ld_out = x.ld_out;
+  e.gate = x.gate;
+  e.gate_fstride = x.gate_fstride;
+  e.rows_per_frame = x.rows_per_frame > 0 ? x.rows_per_frame : 1;
+  e.frames_per_stream = x.frames_per_stream > 0 ? x.frames_per_stream : 1;
+  e.q = static_cast<bf16*>(x.q);
+  e.k = static_cast<bf16*>(x.k);
+  e.v = static_cast<bf16*>(x.v);
+  e.rope_cos = x.rope_cos;
+  e.rope_sinp = x.rope_sinp;
+  e.rope_by_frame = x.rope_by_frame;
+  e.unpatch_grid_w = x.unpatch_grid_w;
+  e.s_b = x.s_b;
+  e.s_t = x.s_t;
+  e.s_p = x.s_p;
+  e.s_h = x.s_h;
+  e.unpatch_patch = x.unpatch_patch;
+  e.unpatch_channels = x.unpatch_channels;
+  e.split_stride = x.split_stride;
+  return e;
+}
+
+// Checks the epilogue against the GEMM shape; returns OASIS_OK or an error code (message set).
+int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
+  OASIS_REQUIRE(splits == 1 || e.kind == OASIS_EPI_PARTIAL_F32, OASIS_ERR_ARG,
+                "gemm: split-K needs the PARTIAL_F32 epilogue");
+  switch (e.kind) {
+    case OASIS_EPI_STORE_F32:
+    case OASIS_EPI_GATED_RES:
+    case OASIS_EPI_RESIDUAL:
+    case OASIS_EPI_PARTIAL_F32:
+      OASIS_REQUIRE(e.out_f32 && e.ld_out >= N && e.ld_out % 4 == 0, OASIS_ERR_ARG,
+                    "gemm: fp32 epilogue needs out_f32 and ld_out >= N (multiple of 4)");
+      OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES || e.gate, OASIS_ERR_NULL, "gemm: gate is NULL");
+      OASIS_REQUIRE(e.kind != OASIS_EPI_PARTIAL_F32 || splits == 1 || e.split_stride >= M * e.ld_out,
+                    OASIS_ERR_ARG, "gemm: split_stride must be >= M * ld_out");
+      break;
+    case OASIS_EPI_STORE_BF16:
+    case OASIS_EPI_GELU_TANH:
+    case OASIS_EPI_GELU_ERF:
+      OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 8 == 0, OASIS_ERR_ARG,
+                    "gemm: bf16 epilogue needs out_bf16 and ld_out >= N (multiple of 8)");
+      break;
+    case OASIS_EPI_QKV_ROPE:
+      OASIS_REQUIRE(e.q && e.k && e.v && e.rope_cos && e.rope_sinp, OASIS_ERR_NULL,
+                    "gemm: QKV_ROPE needs q/k/v and rope tables");
+      OASIS_REQUIRE(e.n_heads > 0 && N == 3LL * e.n_heads * 64, OASIS_ERR_SHAPE,
+                    "gemm: QKV_ROPE needs N == 3*n_heads*64");
+      break;
+    case OASIS_EPI_UNPATCHIFY:
+      OASIS_REQUIRE(e.out_f32 && e.unpatch_patch > 0 && e.unpatch_grid_w > 0, OASIS_ERR_ARG,
+                    "gemm: UNPATCHIFY needs out_f32, patch and grid_w");
+      OASIS_REQUIRE(N == 3LL * e.unpatch_patch * e.unpatch_patch && e.rows_per_frame == M &&
+                        M % e.unpatch_grid_w == 0,
+                    OASIS_ERR_SHAPE, "gemm: UNPATCHIFY shape mismatch");
+      break;
+    default:
+      OASIS_REQUIRE(false, OASIS_ERR_ARG, "gemm: unknown epilogue kind %d", e.kind);
+  }
+  return OASIS_OK;
+}
+
+}  // namespace

@@ -1,0 +1,319 @@
+// fp8 weight GEMM for gfx950: bf16 activations x OCP e4m3 weights on the block-scaled
+// MFMA v_mfma_scale_f32_16x16x128_f8f6f4, with the same fused epilogues as the bf16 GEMM.
+//
+//   acc[m, n] = sum_k A[m, k] * Wq[n, k] * w_scale[n]
+//
+// Weights: Wq = round_e4m3(W / w_scale[n]), w_scale[n] = max_k |W[n, k]| / 448, one fp32
+// scale per output channel, stored [N, K] bytes (oasis_quantize_fp8_rows makes them).
+// Activations stay bf16 in HBM. Each workgroup quantizes its A tile on the way into LDS:
+// every 32-wide K block of a row gets a power-of-two (e8m0) scale 2^e with the block's
+// max |a| / 2^e in [128, 256), and the MFMA applies that scale in hardware. The per-channel
+// weight scale multiplies the fp32 accumulator before the epilogue.
+//
+// MFMA operand layout (16x16x128, verified on MI355X against a host reference): lane l
+// supplies row l%16 of A (column l%16 of B) with the 32 bytes k = 16g..16g+15 and
+// 64+16g..64+16g+15, g = l/16; its scale byte covers row l%16 and K block [32g, 32g+32).
+// Accumulator element r of lane l is D[4*(l/16) + r][l%16].
+#include "gemm_epilogue.h"
+
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int BK8 = 128;          // K per MFMA step and per pipeline step
+constexpr int P8 = BK8 + 16;      // LDS row pitch in bytes (16 B pad)
+constexpr int kScaleOne = 127;    // e8m0 encoding of 1.0
+
+// Quantizes 8 consecutive bf16 of one row whose 32-wide K block is shared with the
+// threads tid^1, tid^2 (same wave): returns the 8 e4m3 bytes and the block's e8m0 scale.
+__device__ __forceinline__ uint2 quant8(i32x4 raw, int* sbyte) {
+  const bf16x8 h = __builtin_bit_cast(bf16x8, raw);
+  float v[8];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[j] = (float)h[j];
+    amax = fmaxf(amax, fabsf(v[j]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  // amax = m * 2^(E-127), m in [1, 2): scale 2^(E-134) maps amax into [128, 256)
+  const int E = (__float_as_int(amax) >> 23) & 0xff;
+  const int sb = E > 7 ? E - 7 : 0;                       // e8m0 byte of the scale 2^(sb-127)
+  const float inv = __int_as_float((254 - sb) << 23);     // 2^(127-sb), exact
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+  *sbyte = sb;
+  return make_uint2((unsigned)lo, (unsigned)hi);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ A, int64_t lda,
+                                                       const uint8_t* __restrict__ B, int64_t ldb,
+                                                       const float* __restrict__ wscale, int M, int N, int K,
+                                                       int splits, Epi e) {
+  static_assert(WM * WN == 4, "4 waves");
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
+  constexpr int A_CHUNKS = BM * (BK8 / 8);   // 16-byte chunks of 8 bf16
+  constexpr int B_CHUNKS = BN * (BK8 / 16);  // 16-byte chunks of 16 fp8
+  static_assert(A_CHUNKS % 256 == 0 && B_CHUNKS % 256 == 0, "BM multiple of 16, BN multiple of 32");
+  constexpr int A_PER = A_CHUNKS / 256;
+  constexpr int B_PER = B_CHUNKS / 256;
+  constexpr int A_BYTES = BM * P8, B_BYTES = BN * P8, S_BYTES = BM * 4;
+  constexpr int RING = 2 * (A_BYTES + B_BYTES + S_BYTES);
+  constexpr int C_PITCH = BN + 4;
+  constexpr int C_BYTES = BM * C_PITCH * 4;
+  constexpr int SMEM = RING > C_BYTES ? RING : C_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  uint8_t* As = reinterpret_cast<uint8_t*>(smem);   // [2][BM][P8]
+  uint8_t* Bs = As + 2 * A_BYTES;                   // [2][BN][P8]
+  uint8_t* Ss = Bs + 2 * B_BYTES;                   // [2][BM][4] e8m0 scales of A
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
+  const int mt = pid % Mt;
+  const int rest = pid / Mt;
+  const int split = rest % splits, nt = rest / splits;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = K / BK8 / splits;  // the host guarantees nk % STAGES == 0
+  const int kb = split * nk * BK8;
+
+  const bf16* a_src[A_PER];
+  int a_dst[A_PER], s_dst[A_PER];
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / (BK8 / 8), col = (c % (BK8 / 8)) * 8;
+    a_src[i] = A + (int64_t)min(m0 + row, M - 1) * lda + kb + col;
+    a_dst[i] = row * P8 + col;
+    s_dst[i] = (col & 31) == 0 ? row * 4 + col / 32 : -1;
+  }
+  const uint8_t* b_src[B_PER];
+  int b_dst[B_PER];
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / (BK8 / 16), col = (c % (BK8 / 16)) * 16;
+    b_src[i] = B + (int64_t)min(n0 + row, N - 1) * ldb + kb + col;
+    b_dst[i] = row * P8 + col;
+  }
+
+  i32x4 ra[STAGES][A_PER], rb[STAGES][B_PER];
+  auto gload = [&](int slot, int kt) {
+    const int64_t ka = (int64_t)kt * BK8;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) ra[slot][i] = *reinterpret_cast<const i32x4*>(a_src[i] + ka);
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) rb[slot][i] = *reinterpret_cast<const i32x4*>(b_src[i] + ka);
+  };
+  auto lstore = [&](int slot, int buf) {
+    uint8_t* as = As + buf * A_BYTES;
+    uint8_t* bs = Bs + buf * B_BYTES;
+    uint8_t* ss = Ss + buf * S_BYTES;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      int sb;
+      *reinterpret_cast<uint2*>(as + a_dst[i]) = quant8(ra[slot][i], &sb);
+      if (s_dst[i] >= 0) ss[s_dst[i]] = (uint8_t)sb;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) *reinterpret_cast<i32x4*>(bs + b_dst[i]) = rb[slot][i];
+  };
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, g = lane >> 4;
+  auto compute = [&](int buf) {
+    const uint8_t* as = As + buf * A_BYTES + (wm * TM + lr) * P8 + 16 * g;
+    const uint8_t* bs = Bs + buf * B_BYTES + (wn * TN + lr) * P8 + 16 * g;
+    const uint8_t* ss = Ss + buf * S_BYTES + (wm * TM + lr) * 4 + g;
+    i32x8 af[FM], bfr[FN];
+    int sa[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const i32x4 x0 = *reinterpret_cast<const i32x4*>(as + i * 16 * P8);
+      const i32x4 x1 = *reinterpret_cast<const i32x4*>(as + i * 16 * P8 + 64);
+      af[i] = i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      sa[i] = ss[i * 16 * 4];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const i32x4 x0 = *reinterpret_cast<const i32x4*>(bs + j * 16 * P8);
+      const i32x4 x1 = *reinterpret_cast<const i32x4*>(bs + j * 16 * P8 + 64);
+      bfr[j] = i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bfr[j], acc[i][j], 0, 0, 0, sa[i], 0,
+                                                                      kScaleOne);
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s) gload(s, min(s, nk - 1));
+  lstore(0, 0);
+  __syncthreads();
+  for (int k0 = 0; k0 < nk; k0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      const int k = k0 + s;
+      gload(s, min(k + STAGES, nk - 1));
+      compute(k & 1);
+      lstore((s + 1) % STAGES, (k + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  float* Cs = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        Cs[(wm * TM + i * 16 + g * 4 + r) * C_PITCH + wn * TN + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+
+  constexpr int UNITS = BM * (BN / 8);
+  for (int u = tid; u < UNITS; u += 256) {
+    const int r = u / (BN / 8), c8 = (u % (BN / 8)) * 8;
+    const int gm = m0 + r, gn = n0 + c8;
+    if (gm >= M || gn >= N) continue;
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8 + 4);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(wscale + gn);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(wscale + gn + 4);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = c0[j] * s0[j];
+      v[j + 4] = c1[j] * s1[j];
+    }
+    if (e.kind == OASIS_EPI_PARTIAL_F32) {
+      float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+      *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+      epilogue8(e, gm, gn, v);
+    }
+  }
+}
+
+typedef hipError_t (*launch8_fn)(const bf16*, int64_t, const uint8_t*, int64_t, const float*, int, int, int, int,
+                                 const Epi&, hipStream_t);
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+hipError_t launch8(const bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* ws, int M, int N, int K,
+                   int splits, const Epi& e, hipStream_t s) {
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, WM, WN, STAGES>), dim3(Mt * Nt * splits), dim3(256), 0, s, A, lda, B,
+                     ldb, ws, M, N, K, splits, e);
+  return hipGetLastError();
+}
+
+struct Tile8 {
+  int bm, bn, stages;
+  launch8_fn fn, fn_single;
+};
+const Tile8 kTiles8[] = {
+    {128, 128, 2, launch8<128, 128, 2, 2, 2>, launch8<128, 128, 2, 2, 1>},  // 0
+    {128, 64, 2, launch8<128, 64, 2, 2, 2>, launch8<128, 64, 2, 2, 1>},     // 1
+    {64, 128, 2, launch8<64, 128, 2, 2, 2>, launch8<64, 128, 2, 2, 1>},     // 2
+    {64, 64, 2, launch8<64, 64, 2, 2, 2>, launch8<64, 64, 2, 2, 1>},        // 3
+    {32, 64, 2, launch8<32, 64, 1, 4, 2>, launch8<32, 64, 1, 4, 1>},        // 4
+};
+constexpr int kNumTiles8 = sizeof(kTiles8) / sizeof(kTiles8[0]);
+
+int auto_tile8(int64_t M, int64_t N) {
+  if (M >= 2048) return N >= 2048 ? 0 : 1;
+  if (M >= 256) return 3;
+  return 4;
+}
+
+// Per-row quantization of a bf16 [N, K] weight: scale[n] = max|W[n, :]| / 448,
+// q[n, k] = round_e4m3(W[n, k] / scale[n]) (round to nearest even). One wave per row.
+__global__ __launch_bounds__(256) void quant_rows_kernel(const bf16* __restrict__ W, int64_t N, int64_t K,
+                                                         uint8_t* __restrict__ q, float* __restrict__ scale) {
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const bf16* w = W + n * K;
+  float amax = 0.f;
+  for (int64_t k = lane * 8; k < K; k += 512) {
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(w + k);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf((float)h[j]));
+  }
+  amax = wave_max(amax);
+  const float s = amax > 0.f ? amax / 448.0f : 1.0f;
+  if (lane == 0) scale[n] = s;
+  for (int64_t k = lane * 8; k < K; k += 512) {
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(w + k);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32((float)h[0] / s, (float)h[1] / s, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32((float)h[2] / s, (float)h[3] / s, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32((float)h[4] / s, (float)h[5] / s, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32((float)h[6] / s, (float)h[7] / s, hi, true);
+    *reinterpret_cast<uint2*>(q + n * K + k) = make_uint2((unsigned)lo, (unsigned)hi);
+  }
+}
+
+}  // namespace
+
+namespace oasis {
+
+int gemm_fp8_launch(const bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* w_scale, int64_t M,
+                    int64_t N, int64_t K, const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
+  OASIS_REQUIRE(A && B && w_scale, OASIS_ERR_NULL, "gemm_fp8: null operand");
+  OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE,
+                "gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  OASIS_REQUIRE(K % BK8 == 0, OASIS_ERR_SHAPE, "gemm_fp8: K=%lld must be a multiple of 128", (long long)K);
+  OASIS_REQUIRE(N % 8 == 0, OASIS_ERR_SHAPE, "gemm_fp8: N=%lld must be a multiple of 8", (long long)N);
+  OASIS_REQUIRE(lda % 8 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K, OASIS_ERR_SHAPE,
+                "gemm_fp8: need lda %% 8 == 0, ldb %% 16 == 0, both >= K");
+  OASIS_REQUIRE(splits >= 1 && (K / BK8) % splits == 0, OASIS_ERR_SHAPE, "gemm_fp8: splits=%d must divide K/128",
+                splits);
+  const Epi e = to_epi(ex);
+  if (const int rc = check_epilogue(e, M, N, splits)) return rc;
+  if (tile < 0) tile = auto_tile8(M, N);
+  OASIS_REQUIRE(tile < kNumTiles8, OASIS_ERR_ARG, "gemm_fp8: tile config %d out of range", tile);
+  const Tile8& t = kTiles8[tile];
+  const bool ring = (K / BK8 / splits) % t.stages == 0;
+  const hipError_t err = (ring ? t.fn : t.fn_single)(A, lda, B, ldb, w_scale, (int)M, (int)N, (int)K, splits, e, s);
+  if (err != hipSuccess) {
+    set_error("gemm_fp8 launch failed: %s", hipGetErrorString(err));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
+}  // namespace oasis
+
+extern "C" int oasis_gemm_fp8(const void* A, int64_t lda, const void* B, int64_t ldb, const float* w_scale, int64_t M,
+                              int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
+                              oasis_stream_t stream) {
+  OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm_fp8: null epilogue");
+  return oasis::gemm_fp8_launch(static_cast<const bf16*>(A), lda, static_cast<const uint8_t*>(B), ldb, w_scale, M, N,
+                                K, *epi, tile, splits, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_quantize_fp8_rows(const void* W, int64_t N, int64_t K, void* q, float* scale,
+                                       oasis_stream_t stream) {
+  OASIS_REQUIRE(W && q && scale, OASIS_ERR_NULL, "quantize_fp8_rows: null pointer");
+  OASIS_REQUIRE(N > 0 && K > 0 && K % 8 == 0 && N <= (1ll << 30), OASIS_ERR_SHAPE,
+                "quantize_fp8_rows: need N > 0 and K a positive multiple of 8");
+  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16*>(W), N, K, static_cast<uint8_t*>(q), scale);
+  return oasis::check_launch("quantize_fp8_rows");
+}

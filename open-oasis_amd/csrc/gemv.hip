@@ -99,7 +99,7 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
                                const float* b, float* out, int64_t ld_out, int act_in, int act_out, int accumulate,
                                oasis_stream_t stream) {
   OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "gemv: null pointer");
-  OASIS_REQUIRE(R > 0 && R <= 16, OASIS_ERR_SHAPE, "gemv: R=%lld must be in [1, 16]", (long long)R);
+  OASIS_REQUIRE(R > 0 && R <= 1024, OASIS_ERR_SHAPE, "gemv: R=%lld must be in [1, 1024]", (long long)R);
   OASIS_REQUIRE(K > 0 && K % KSTEP == 0 && K <= 2048, OASIS_ERR_SHAPE, "gemv: K=%lld must be a multiple of 64, <= 2048",
                 (long long)K);
   OASIS_REQUIRE(N > 0 && N % 16 == 0 && N < (1ll << 31), OASIS_ERR_SHAPE, "gemv: N=%lld must be a multiple of 16",
@@ -108,6 +108,13 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   OASIS_REQUIRE((act_in == OASIS_ACT_NONE || act_in == OASIS_ACT_SILU) &&
                     (act_out == OASIS_ACT_NONE || act_out == OASIS_ACT_SILU),
                 OASIS_ERR_ARG, "gemv: bad activation");
+  // one pass over W per 16 rows
+  for (int64_t r0 = 16; r0 < R; r0 += 16) {
+    const int rc = oasis_gemv_bf16(x + r0 * ldx, ldx, R - r0 < 16 ? R - r0 : 16, W, N, K, b, out + r0 * ld_out, ld_out,
+                                   act_in, act_out, accumulate, stream);
+    if (rc != OASIS_OK) return rc;
+  }
+  if (R > 16) R = 16;
   const int tiles = (int)(N / 16);
   int blocks = (tiles + 3) / 4;
   if (blocks > 2048) blocks = 2048;

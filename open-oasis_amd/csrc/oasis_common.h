@@ -28,6 +28,9 @@ int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int6
 // explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
 int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                     const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
+// acc = A[M,K] (bf16) @ (Bq[N,K] (e4m3) * w_scale[N])^T with the given epilogue (gemm_fp8.hip).
+int gemm_fp8_launch(const __bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* w_scale, int64_t M,
+                    int64_t N, int64_t K, const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
 }  // namespace oasis
 
 #define OASIS_REQUIRE(cond, code, ...)          \

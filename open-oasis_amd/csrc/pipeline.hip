@@ -169,7 +169,30 @@ int check_dit(const oasis_dit_weights_t* w) {
     OASIS_REQUIRE(w->qkv_w[j] && w->out_w[j] && w->out_b[j] && w->fc1_w[j] && w->fc1_b[j] && w->fc2_w[j] &&
                       w->fc2_b[j],
                   OASIS_ERR_NULL, "dit: missing weights of sub-block %d", j);
+  OASIS_REQUIRE(w->weight_format == OASIS_WEIGHTS_BF16 || w->weight_format == OASIS_WEIGHTS_FP8, OASIS_ERR_ARG,
+                "dit: unknown weight_format %d", w->weight_format);
+  if (w->weight_format == OASIS_WEIGHTS_FP8) {
+    OASIS_REQUIRE(w->d_model % 128 == 0 && w->d_mlp % 128 == 0, OASIS_ERR_SHAPE,
+                  "dit: fp8 weights need d_model and d_mlp multiples of 128");
+    for (int j = 0; j < w->n_sub; ++j)
+      OASIS_REQUIRE(w->qkv_s[j] && w->out_s[j] && w->fc1_s[j] && w->fc2_s[j], OASIS_ERR_NULL,
+                    "dit: missing fp8 scales of sub-block %d", j);
+  }
   return OASIS_OK;
+}
+
+// One projection of sub-block j (role QKV/O/FC1/FC2): the bf16 GEMM, or the fp8 GEMM
+// when the projection weights are e4m3 with per-channel scales.
+int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64_t lda, int64_t M, int64_t N,
+         int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s) {
+  const void* W = role == ROLE_QKV ? w->qkv_w[j] : role == ROLE_O ? w->out_w[j] : role == ROLE_FC1 ? w->fc1_w[j]
+                                                                                                   : w->fc2_w[j];
+  if (w->weight_format == OASIS_WEIGHTS_FP8) {
+    const float* sc = role == ROLE_QKV ? w->qkv_s[j] : role == ROLE_O ? w->out_s[j] : role == ROLE_FC1 ? w->fc1_s[j]
+                                                                                                       : w->fc2_s[j];
+    return oasis::gemm_fp8_launch((const bf16*)A, lda, (const uint8_t*)W, K, sc, M, N, K, e, -1, splits, s);
+  }
+  return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s);
 }
 
 int64_t ada_width(const oasis_dit_weights_t* w) { return (int64_t)w->n_sub * 6 * w->d_model + 2 * w->d_model; }
@@ -283,22 +306,18 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       qkv.rope_sinp = w->t_sinp;
       qkv.rope_by_frame = 1;
     }
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[j], D, M, 3 * D, D, qkv,
-                                     pl.tile[ROLE_QKV], 1, s));
+    OASIS_TRY(proj(w, ROLE_QKV, j, buf->h, D, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1, s));
     if (spatial)
       OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
     else
       OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
     // O projection as split-K partials; bias + gated residual + LN + modulate fused after
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->out_w[j], D, M, D, D, part,
-                                     pl.tile[ROLE_O], so, s));
+    OASIS_TRY(proj(w, ROLE_O, j, buf->attn, D, M, D, D, part, pl.tile[ROLE_O], so, s));
     OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, so, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
                                 a + 3 * D, fs, buf->h, kLnEps, stream));
     gelu.bias = w->fc1_b[j];
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->fc1_w[j], D, M, Dm, D, gelu,
-                                     pl.tile[ROLE_FC1], 1, s));
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[j], Dm, M, D, Dm, part,
-                                     pl.tile[ROLE_FC2], sf, s));
+    OASIS_TRY(proj(w, ROLE_FC1, j, buf->h, D, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+    OASIS_TRY(proj(w, ROLE_FC2, j, buf->mlp, Dm, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
     pend->bias = w->fc2_b[j];
     pend->gate = a + 5 * D;
     pend->n = sf;
@@ -389,7 +408,7 @@ extern "C" int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buff
   OASIS_REQUIRE(patches && v_out, OASIS_ERR_NULL, "dit_step: null patches/v_out");
   OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "dit_step: missing patch-embed weights");
   const int64_t R = B * T, D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
-  OASIS_REQUIRE(R <= 16, OASIS_ERR_SHAPE, "dit_step: at most 16 frames per call (got %lld)", (long long)R);
+  OASIS_REQUIRE(R <= 1024, OASIS_ERR_SHAPE, "dit_step: at most 1024 frames per call (got %lld)", (long long)R);
   OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
   SideStream* ss = nullptr;
   OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));

@@ -63,9 +63,17 @@ def temporal_angles(freqs, t_max):
 
 
 class DiT:
-    """Oasis DiT weights resident on one GPU."""
+    """Oasis DiT weights resident on one GPU.
 
-    def __init__(self, w, device="cuda", grid=(9, 16), t_max=32):
+    weights="bf16" keeps the projection weights in bf16. weights="fp8" stores the QKV, O,
+    FC1 and FC2 weights as OCP e4m3 with one fp32 scale per output channel (quantized on
+    the device by oasis_quantize_fp8_rows) and runs those projections on the fp8 GEMM;
+    adaLN, conditioning, patch embed and the final layer stay bf16."""
+
+    def __init__(self, w, device="cuda", grid=(9, 16), t_max=32, weights="bf16"):
+        if weights not in ("bf16", "fp8"):
+            raise ValueError("weights must be 'bf16' or 'fp8'")
+        self.weights = weights
         self.device = torch.device(device)
         dev = self.device
         self.d = d = w["t_emb.w2"].shape[0]
@@ -114,15 +122,35 @@ class DiT:
         S.grid_h, S.grid_w, S.patch_dim = grid[0], grid[1], self.patch_dim
         S.freq_dim, S.ext_dim_pad = self.freq_dim, self.ext_pad
         S.ada_w, S.ada_b = self.ada_w.data_ptr(), self.ada_b.data_ptr()
+        fp8 = weights == "fp8"
+        if fp8 and self.device.type != "cuda":
+            raise ValueError("fp8 weights are quantized on the GPU")
+
+        def proj(t):
+            """(weight pointer, scale pointer or None) of one projection weight."""
+            x = put(t, bf)
+            if not fp8:
+                return x.data_ptr(), None
+            n, k = x.shape
+            q = torch.empty(n, k, dtype=torch.uint8, device=dev)
+            sc = torch.empty(n, dtype=torch.float32, device=dev)
+            L.call("oasis_quantize_fp8_rows", L.ptr(x), n, k, L.ptr(q), L.ptr(sc), L.stream_handle())
+            keep.pop()            # the bf16 copy is dropped once quantized
+            keep.extend([q, sc])
+            return q.data_ptr(), sc.data_ptr()
+
+        S.weight_format = L.WEIGHTS_FP8 if fp8 else L.WEIGHTS_BF16
         for j in range(self.n_sub):
             p = "blocks.%d.%s." % (j // 2, "st"[j % 2])
-            S.qkv_w[j] = put(w[p + "qkv_w"], bf).data_ptr()
-            S.out_w[j] = put(w[p + "out_w"], bf).data_ptr()
+            S.qkv_w[j], S.qkv_s[j] = proj(w[p + "qkv_w"])
+            S.out_w[j], S.out_s[j] = proj(w[p + "out_w"])
             S.out_b[j] = put(w[p + "out_b"], torch.float32).data_ptr()
-            S.fc1_w[j] = put(w[p + "fc1_w"], bf).data_ptr()
+            S.fc1_w[j], S.fc1_s[j] = proj(w[p + "fc1_w"])
             S.fc1_b[j] = put(w[p + "fc1_b"], torch.float32).data_ptr()
-            S.fc2_w[j] = put(w[p + "fc2_w"], bf).data_ptr()
+            S.fc2_w[j], S.fc2_s[j] = proj(w[p + "fc2_w"])
             S.fc2_b[j] = put(w[p + "fc2_b"], torch.float32).data_ptr()
+        if fp8:
+            torch.cuda.synchronize(dev)
         S.final_w = put(w["final.w"], bf).data_ptr()
         S.final_b = put(w["final.b"], torch.float32).data_ptr()
         # patch embed: conv [D, C, 2, 2] -> [D, (p, q, c)] (W_rt of oasis_inference.py:1821-1826)
@@ -168,24 +196,17 @@ class DiT:
 
     def conditioning_inplace(self, R, ws, stream=None):
         """Conditioning from ws.t[:R] / ws.act[:R] into ws.cond / ws.ada (no host work)."""
-        s = L.stream_handle(stream)
-        for r0 in range(0, R, 16):
-            n = min(16, R - r0)
-            L.call("oasis_dit_conditioning", ctypes.byref(self.struct), L.ptr(ws.t[r0:]),
-                   L.ptr(ws.act[r0:]), n, L.ptr(ws.tfreq[r0:]), L.ptr(ws.hid[r0:]),
-                   L.ptr(ws.cond[r0:]), L.ptr(ws.ada[r0:]), s)
+        L.call("oasis_dit_conditioning", ctypes.byref(self.struct), L.ptr(ws.t), L.ptr(ws.act), R,
+               L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada), L.stream_handle(stream))
 
     def adaln_from_cond(self, cond, ws, stream=None):
         """ada rows from given (pre-SiLU) cond vectors [R, D] (the reference passes cond
         computed on the host, oasis_inference.py:1406-1427)."""
         R = cond.shape[0]
         ws.cond[:R].copy_(cond)
-        s = L.stream_handle(stream)
-        for r0 in range(0, R, 16):
-            n = min(16, R - r0)
-            L.call("oasis_gemv_bf16", L.ptr(ws.cond[r0:]), self.d, n, L.ptr(self.ada_w),
-                   self.ada_width, self.d, L.ptr(self.ada_b), L.ptr(ws.ada[r0:]), self.ada_width,
-                   L.ACT_SILU, L.ACT_NONE, 0, s)
+        L.call("oasis_gemv_bf16", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), self.ada_width, self.d,
+               L.ptr(self.ada_b), L.ptr(ws.ada), self.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
+               L.stream_handle(stream))
         return ws.ada[:R]
 
     def patch_embed(self, patches, out, stream=None):
@@ -351,8 +372,7 @@ class DiTStep:
     def __init__(self, dit, B=1, T=2, stream=None):
         self.dit, self.B, self.T = dit, B, T
         self.M = B * T * dit.P
-        assert B * T <= 16, "one step conditions at most 16 frames"
-        self.ws = dit.workspace(self.M, max_cond=16)
+        self.ws = dit.workspace(self.M, max_cond=max(16, B * T))
         self.patches = torch.zeros(self.M, dit.patch_dim, device=dit.device)
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dit.device)
         self.graph = None

@@ -108,7 +108,7 @@ def one_hot_actions(dr, n, dim=25):
 
 
 # ---------------------------------------------------------------------------
-# configurations (BASELINE.json configs[0..4])
+# configurations (the benchmark plan's configs 0..4)
 # ---------------------------------------------------------------------------
 
 def config0(seed=0, dtype=torch.float32):
@@ -152,3 +152,14 @@ def config3(seed=3, n_blocks=16, vae_depth=12):
     return {"x_T": x_T, "ctx_latent": ctx_latent, "ctx_t": 14.0, "ctx_action": torch.zeros(25),
             "gen_action": gen_action, "vae_latent": vae_latent, "w": w, "vw": vw,
             "steps": [(999, 749), (749, 499), (499, 249), (249, -1)]}
+
+
+def config4(seed=4, B=8, T=4, n_blocks=16, d=1024, n_heads=16, d_mlp=4096):
+    """Batched serving: B independent streams of T frames, latent [B,T,16,18,32], t per
+    frame ~ U[0,1000), one-hot actions; the weights are quantized to e4m3 by the model."""
+    dr = Draw(seed)
+    latent = dr.normal(B, T, 16, 18, 32)
+    t = dr.randint(0, 1000, (B, T)).float()
+    actions = one_hot_actions(dr, B * T).reshape(B, T, -1)
+    w = dit_weights(dr, n_blocks=n_blocks, d=d, n_heads=n_heads, d_mlp=d_mlp)
+    return {"latent": latent, "t": t, "actions": actions, "w": w}

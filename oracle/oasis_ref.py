@@ -30,6 +30,7 @@ __all__ = [
     "conditioning", "dit_forward", "patch_embed", "patchify_to_output_space",
     "unpatchify", "patch_embed_roundtrip_weight", "ddim_coeffs", "ddim_update",
     "bridge", "vae_decode", "vae_unpatchify", "ddim_frame",
+    "E4M3_MAX", "quantize_e4m3_rows", "quantize_act_blocks", "fp8_weights",
 ]
 
 # ---- model constants (oasis_inference.py:90-163) ----
@@ -562,3 +563,46 @@ def ddim_frame(x_noise, ctx_z, ctx_cond, gen_conds, w, vae_w, alphas_cumprod, st
     lat = bridge(chunk, gh, gw)
     pred = vae_decode(lat, vae_w, grid=vae_grid)
     return chunk, vae_unpatchify(pred, *vae_grid)
+
+
+# ---------------------------------------------------------------------------
+# fp8 weight path (config 4). The reference has no sub-fp32 path, so these restate the
+# build's own scheme: OCP e4m3 (max 448), round to nearest even.
+# ---------------------------------------------------------------------------
+E4M3_MAX = 448.0
+
+
+def quantize_e4m3_rows(w):
+    """Per-output-channel e4m3 weights: s_n = max_k |W[n, k]| / 448 (1 for a zero row),
+    q = round_e4m3(W / s_n). Returns (q as fp32 values on the e4m3 grid, s [N])."""
+    w = _f(w)
+    amax = w.abs().amax(dim=1)
+    s = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+    q = (w / s[:, None]).to(torch.float8_e4m3fn).float()
+    return q, s
+
+
+def quantize_act_blocks(x, block=32):
+    """Activations as the fp8 GEMM sees them: each `block`-wide run of a row gets a
+    power-of-two scale 2^e with max |x| / 2^e in [128, 256) (e >= -127), then
+    round_e4m3(x / 2^e) * 2^e."""
+    x = _f(x)
+    M, K = x.shape
+    xb = x.reshape(M, K // block, block)
+    amax = xb.abs().amax(dim=-1, keepdim=True)
+    _, ex = torch.frexp(amax)               # amax = m * 2^ex, m in [0.5, 1)
+    e = torch.clamp(ex - 8, min=-127).float()
+    scale = torch.pow(2.0, e)
+    q = (xb / scale).to(torch.float8_e4m3fn).float() * scale
+    return q.reshape(M, K)
+
+
+def fp8_weights(w):
+    """A copy of a DiT weight dict whose QKV / O / FC1 / FC2 weights are replaced by
+    their per-channel e4m3 dequantized values (what the fp8 path multiplies by)."""
+    out = dict(w)
+    for k, v in w.items():
+        if k.startswith("blocks.") and k.rsplit(".", 1)[1] in ("qkv_w", "out_w", "fc1_w", "fc2_w"):
+            q, s = quantize_e4m3_rows(v)
+            out[k] = q * s[:, None]
+    return out

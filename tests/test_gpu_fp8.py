@@ -1,0 +1,170 @@
+"""The fp8 weight path on the GPU (config 4): the e4m3 weight quantizer, the block-scaled
+fp8 GEMM against the oracle's quantized operands, the fp8 DiT step against the oracle with
+dequantized weights, and the full config-4 batch (8 streams x T=4) against the bf16 path."""
+import ctypes
+
+import pytest
+import torch
+
+import oracle
+from helpers import COS_SUB, REL_SUB, L, assert_close, cuda, metrics, pkg, stream, sync
+
+pytestmark = pytest.mark.gpu
+
+_ALIVE = []
+
+
+def dev(t):
+    t = cuda(t)
+    _ALIVE.append(t)
+    return t
+
+
+@pytest.fixture(autouse=True)
+def _release():
+    yield
+    torch.cuda.synchronize()
+    _ALIVE.clear()
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _quantize(W):
+    """Device quantizer on a bf16 [N, K] weight -> (q uint8 [N, K], scale [N]) on the GPU."""
+    N, K = W.shape
+    q = torch.empty(N, K, dtype=torch.uint8, device="cuda")
+    s = torch.empty(N, device="cuda")
+    Wd = dev(W)
+    L.call("oasis_quantize_fp8_rows", L.ptr(Wd), N, K, L.ptr(q), L.ptr(s), stream())
+    sync()
+    return q, s
+
+
+def test_quantize_rows_matches_torch_e4m3():
+    W = (torch.randn(384, 1024, generator=_gen(1)) * 0.02).to(torch.bfloat16)
+    W[5] = 0
+    q, s = _quantize(W)
+    ref_q, ref_s = oracle.quantize_e4m3_rows(W)
+    assert torch.equal(s.cpu(), ref_s)
+    got = q.cpu().view(torch.float8_e4m3fn).float()
+    assert torch.equal(got, ref_q), (got - ref_q).abs().max()
+
+
+def _epi(**kw):
+    e = L.Epilogue()
+    for k, v in kw.items():
+        if isinstance(v, torch.Tensor):
+            _ALIVE.append(v)
+            v = v.data_ptr()
+        setattr(e, k, v)
+    return e
+
+
+def _ref(A, W):
+    """fp64 product of the operands exactly as the fp8 GEMM quantizes them."""
+    q, s = oracle.quantize_e4m3_rows(W)
+    return oracle.quantize_act_blocks(A).double() @ (q.double() * s.double()[:, None]).t()
+
+
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 512), (4608, 1024, 1024), (33, 64, 256)])
+def test_gemm_fp8_store_f32(tile, M, N, K):
+    if M > 1000 and tile not in (-1, 0, 1):
+        pytest.skip("large shape covered by the wide tiles")
+    g = _gen(M + N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    A[:, :32] *= 100.0  # blocks of very different magnitude
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g)
+    q, s = _quantize(W)
+    out = torch.zeros(M, N, device="cuda")
+    L.call("oasis_gemm_fp8", L.ptr(dev(A)), K, L.ptr(q), K, L.ptr(s), M, N, K,
+           ctypes.byref(_epi(kind=L.EPI_STORE_F32, bias=dev(bias), out_f32=out, ld_out=N)), tile, 1, stream())
+    sync()
+    ref = _ref(A, W) + bias.double()
+    cos, rel = metrics(out, ref)
+    print("fp8 gemm %dx%dx%d tile %d: cos=%.7f rel=%.2e" % (M, N, K, tile, cos, rel), flush=True)
+    assert rel <= 1e-4, rel  # fp32 accumulation against the fp64 reference
+
+
+def test_gemm_fp8_gelu_and_split_k():
+    M, N, K = 288, 512, 1024
+    g = _gen(7)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    q, s = _quantize(W)
+    out = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+    L.call("oasis_gemm_fp8", L.ptr(dev(A)), K, L.ptr(q), K, L.ptr(s), M, N, K,
+           ctypes.byref(_epi(kind=L.EPI_GELU_TANH, bias=dev(bias), out_bf16=out, ld_out=N)), -1, 1, stream())
+    part = torch.zeros(4, M, N, device="cuda")
+    L.call("oasis_gemm_fp8", L.ptr(dev(A)), K, L.ptr(q), K, L.ptr(s), M, N, K,
+           ctypes.byref(_epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)), 3, 4, stream())
+    sync()
+    ref = _ref(A, W)
+    assert_close(out, oracle.gelu_tanh((ref + bias.double()).float()), 0.99999, 1e-2, "fp8 gemm gelu")
+    assert_close(part.sum(0), ref, 0.9999999, 1e-4, "fp8 gemm split-K x4")
+
+
+def test_gemm_fp8_rejects_bad_shapes():
+    e = _epi(kind=L.EPI_STORE_F32, out_f32=torch.zeros(1, device="cuda"), ld_out=64)
+    fake = ctypes.c_void_p(16)
+    with pytest.raises(L.OasisError, match="multiple of 128"):
+        L.call("oasis_gemm_fp8", fake, 64, fake, 64, fake, 16, 64, 64, ctypes.byref(e), -1, 1, stream())
+
+
+def _step(dit, c, B, T):
+    P = dit.P
+    step = pkg.DiTStep(dit, B=B, T=T)
+    patches = oracle.patchify_to_output_space(c["latent"].reshape(B * T, 16, 18, 32)).reshape(-1, 64)
+    step.set_inputs(cuda(patches), cuda(c["t"].reshape(-1)), cuda(c["actions"].reshape(B * T, -1)))
+    v = step.run().clone()
+    torch.cuda.synchronize()
+    return v.cpu().reshape(B, T * P, 64), step
+
+
+def test_fp8_dit_step_reduced_vs_oracle():
+    """2 blocks at the full width, B=2 streams x T=4: the fp8 path against the fp32 oracle
+    run on the dequantized e4m3 weights (the remaining gap is the activation quantization)."""
+    c = pkg.synth.config4(seed=41, B=2, T=4, n_blocks=2)
+    dit = pkg.DiT(c["w"], "cuda", weights="fp8")
+    v, _ = _step(dit, c, 2, 4)
+    w8 = oracle.fp8_weights(c["w"])
+    for b in range(2):
+        z = oracle.patch_embed(c["latent"][b], w8)
+        cond = oracle.conditioning(c["t"][b], c["actions"][b], w8)
+        ref = oracle.dit_forward(z, cond, w8).reshape(-1, 64)
+        cos, rel = metrics(v[b], ref)
+        print("fp8 reduced step stream %d vs oracle(e4m3 weights): cos=%.6f rel=%.3e" % (b, cos, rel), flush=True)
+        assert cos >= 0.995, cos
+
+
+def test_config4_fp8_vs_bf16():
+    """Config 4 at full size: 8 streams x T=4 (4608 tokens), 16 blocks; the fp8 weight
+    path must hold cosine >= 0.99 against the bf16 path on the same inputs."""
+    c = pkg.synth.config4()
+    v16, s16 = _step(pkg.DiT(c["w"], "cuda"), c, 8, 4)
+    del s16
+    torch.cuda.empty_cache()
+    v8, _ = _step(pkg.DiT(c["w"], "cuda", weights="fp8"), c, 8, 4)
+    worst = 1.0
+    for b in range(8):
+        cos, rel = metrics(v8[b], v16[b])
+        worst = min(worst, cos)
+    cos, rel = metrics(v8, v16)
+    print("config4 fp8 vs bf16: cos=%.6f (worst stream %.6f) rel=%.3e" % (cos, worst, rel), flush=True)
+    assert worst >= 0.99, worst
+
+
+def test_config4_bf16_stream_matches_oracle():
+    """One stream of the batched bf16 step equals the single-stream oracle (batch rows
+    are independent): 2 blocks, B=8, T=4."""
+    c = pkg.synth.config4(seed=42, n_blocks=2)
+    v, _ = _step(pkg.DiT(c["w"], "cuda"), c, 8, 4)
+    for b in (0, 5):
+        z = oracle.patch_embed(c["latent"][b], c["w"])
+        cond = oracle.conditioning(c["t"][b], c["actions"][b], c["w"])
+        ref = oracle.dit_forward(z, cond, c["w"]).reshape(-1, 64)
+        assert_close(v[b], ref, COS_SUB, REL_SUB, "config4 bf16 stream %d (2 blocks)" % b)

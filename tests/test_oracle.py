@@ -381,3 +381,67 @@ def test_vae_decode_against_loops():
     x = x + gg @ W["dec.0.fc2_w"].t() + W["dec.0.fc2_b"]
     ref = (_ln64(x) * W["norm_w"] + W["norm_b"]) @ W["pred_w"].t() + W["pred_b"]
     _close(got, ref, 1e-4)
+
+
+# ----------------------------------------------------------------- fp8 (config 4)
+def _e4m3_decode(c):
+    s, e, m = c >> 7, (c >> 3) & 15, c & 7
+    if e == 15 and m == 7:
+        return float("nan")
+    v = (m / 8) * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+    return -v if s else v
+
+
+_GRID = sorted({(_e4m3_decode(c), c) for c in range(128) if _e4m3_decode(c) == _e4m3_decode(c)})
+
+
+def _nearest_e4m3(x):
+    """Round-to-nearest-even onto the e4m3 grid by brute force (|x| <= 448)."""
+    a = abs(x)
+    best = min(_GRID, key=lambda vc: (abs(vc[0] - a), vc[1] & 1))
+    return math.copysign(best[0], x) if best[0] != 0 else 0.0
+
+
+def test_e4m3_grid():
+    assert _GRID[-1][0] == 448.0 and len(_GRID) == 127  # 0 .. 448, NaN excluded
+    assert _GRID[1][0] == 2.0 ** -9                      # smallest subnormal
+
+
+def test_quantize_e4m3_rows_is_nearest_on_the_grid():
+    g = _g(17)
+    w = torch.randn(8, 96, generator=g) * 0.02
+    w[3] = 0.0
+    q, s = oracle.quantize_e4m3_rows(w)
+    assert s[3].item() == 1.0 and torch.equal(q[3], torch.zeros(96))
+    for n in (0, 5, 7):
+        assert abs(s[n].item() - w[n].abs().max().item() / 448.0) <= 1e-9
+        assert q[n].abs().max().item() == 448.0        # the row maximum lands on the top code
+        for k in range(0, 96, 7):
+            x = w[n, k].item() / s[n].item()
+            assert q[n, k].item() == _nearest_e4m3(x), (n, k)
+
+
+def test_quantize_act_blocks():
+    g = _g(18)
+    x = torch.randn(4, 128, generator=g) * torch.tensor([1e-3, 1.0, 30.0, 0.0]).repeat_interleave(32)
+    xq = oracle.quantize_act_blocks(x)
+    assert torch.equal(xq[:, 96:], torch.zeros(4, 32))
+    for r in range(4):
+        for b in range(3):
+            blk, qb = x[r, 32 * b:32 * b + 32], xq[r, 32 * b:32 * b + 32]
+            amax = blk.abs().max().item()
+            e = math.floor(math.log2(amax)) - 7          # power-of-two scale of the block
+            sc = 2.0 ** e
+            assert 128 <= amax / sc < 256
+            for k in range(0, 32, 5):
+                assert qb[k].item() == _nearest_e4m3(blk[k].item() / sc) * sc
+
+
+def test_fp8_weights_replace_only_the_projections():
+    g = _g(19)
+    w = {"blocks.0.s.qkv_w": torch.randn(6, 32, generator=g), "blocks.0.s.ada_w": torch.randn(6, 32, generator=g),
+         "final.w": torch.randn(4, 32, generator=g)}
+    w8 = oracle.fp8_weights(w)
+    assert w8["blocks.0.s.ada_w"] is w["blocks.0.s.ada_w"] and w8["final.w"] is w["final.w"]
+    q, s = oracle.quantize_e4m3_rows(w["blocks.0.s.qkv_w"])
+    assert torch.equal(w8["blocks.0.s.qkv_w"], q * s[:, None])
