@@ -21,6 +21,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 
 
 def _event_ms(fn, stream, n):
@@ -96,6 +97,66 @@ def probe(pkg, n=10):
     print(json.dumps({"probe": "fc1 gemm x%d, adaLN gemv x%d, 256 MiB copy x%d" % (n + 1, n + 1, n)}), flush=True)
 
 
+def _graph_step_ms(step, steps, warmup):
+    import torch
+    step.capture()
+    for _ in range(warmup):
+        step.graph.launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step.graph.launch()
+    torch.cuda.synchronize()
+    return 1e3 * (time.perf_counter() - t0) / steps
+
+
+def config4(pkg, oracle, steps, warmup):
+    """Config 4: 8 independent streams x T=4 frames (4608 tokens) per DiT step, QKV/O/FC1/FC2
+    on e4m3 weights, against the same batch on bf16 weights. A generated frame needs 4 DDIM
+    steps, so DiT frames/s = 8 streams / (4 x step time) (VAE decode not included)."""
+    import torch
+    c = pkg.synth.config4()
+    B, T = 8, 4
+    patches = oracle.patchify_to_output_space(c["latent"].reshape(B * T, 16, 18, 32)).reshape(-1, 64).cuda()
+    res = {"workload": "config4: 8 streams x T=4 (4608 tokens), 16 blocks, D=1024; QKV/O/FC1/FC2 weights "
+                       "e4m3 with per-channel fp32 scales, activations in e4m3 blocks of 32 with power-of-two "
+                       "scales (written by the LN / GELU producers) on the block-scaled fp8 MFMA; "
+                       "adaLN/conditioning/final layer bf16"}
+    for fmt in ("bf16", "fp8"):
+        dit = pkg.DiT(c["w"], "cuda", weights=fmt)
+        step = pkg.DiTStep(dit, B=B, T=T)
+        step.set_inputs(patches, c["t"].reshape(-1).cuda(), c["actions"].reshape(B * T, -1).cuda())
+        ms = _graph_step_ms(step, steps, warmup)
+        res["ms_per_step_" + fmt] = round(ms, 4)
+        res["dit_frames_per_s_" + fmt] = round(B * 1e3 / (4 * ms), 1)
+        # the FC1 projection of sub-block 0 alone (same buffers, same kernel choice)
+        M, D, Dm = B * T * dit.P, dit.d, dit.d_mlp
+        L = pkg._lib
+        e = L.Epilogue()
+        e.kind, e.bias, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, dit.struct.fc1_b[0], step.ws.mlp.data_ptr(), Dm
+        A, W = L.ptr(step.ws.h), ctypes.c_void_p(dit.struct.fc1_w[0])
+        if fmt == "fp8":  # as in the step: A in fp8 blocks (LN output), GELU output in fp8 blocks
+            S = ctypes.c_void_p(dit.struct.fc1_s[0])
+            A8, A8s = L.ptr(step.ws.act8), L.ptr(step.ws.act8_scale)
+            e.kind, e.out_fp8, e.out_scale, e.ld_scale = (L.EPI_GELU_TANH_FP8, step.ws.mlp8.data_ptr(),
+                                                          step.ws.mlp8_scale.data_ptr(), Dm // 32)
+            fn = lambda: L.call("oasis_gemm_fp8_a8", A8, D, A8s, D // 32, W, D, S, M, Dm, D,  # noqa: E731
+                                ctypes.byref(e), -1, 1, L.stream_handle(step.stream))
+            peak = FP8_PEAK_TFLOPS
+        else:
+            fn = lambda: L.call("oasis_gemm_bf16", A, D, W, D, M, Dm, D, ctypes.byref(e),  # noqa: E731
+                                L.stream_handle(step.stream))
+            peak = BF16_PEAK_TFLOPS
+        gms = _event_ms(fn, step.stream, 50)
+        tf = 2 * M * D * Dm / (gms * 1e-3) / 1e12
+        res["fc1_gemm_" + fmt] = {"avg_launch_ms": round(gms, 5), "achieved": round(tf, 1), "peak": peak,
+                                  "unit": "TFLOP/s", "frac": round(tf / peak, 4)}
+        del step, dit
+        torch.cuda.empty_cache()
+    res["speedup_fp8_vs_bf16"] = round(res["ms_per_step_bf16"] / res["ms_per_step_fp8"], 3)
+    return res
+
+
 def cpu_baseline(cfg, oracle, seconds=15.0):
     """The fp32 oracle's DiT step (same weights and inputs) on this host's cores."""
     import torch
@@ -128,6 +189,7 @@ def main():
     ap.add_argument("--frames", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-frame", action="store_true")
+    ap.add_argument("--no-c4", action="store_true", help="skip the config-4 (fp8, 8 streams x T=4) lines")
     ap.add_argument("--probe", action="store_true", help="short run of the roofline kernels for counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -239,6 +301,11 @@ def main():
         out["frame_workload"] = ("config3: 4 DDIM v-prediction steps (t=999,749,499,249, cosine alphas) "
                                  "over the T=2 DiT + bridge + 12-block ViT VAE decode + unpatchify to "
                                  "[3,360,640], one hipGraph")
+
+    if not args.no_c4:
+        fp = dit3 = vae3 = None  # release the config-3 model before loading config 4
+        torch.cuda.empty_cache()
+        out["config4"] = config4(pkg, oracle, max(10, args.steps // 4), max(3, args.warmup // 4))
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(c1, oracle)

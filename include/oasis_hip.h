@@ -143,8 +143,12 @@ enum {
   OASIS_EPI_RESIDUAL = 5,     /* out_f32[m, n] += acc + bias                       */
   OASIS_EPI_QKV_ROPE = 6,     /* RoPE on Q,K + head split into q/k/v (bf16)         */
   OASIS_EPI_UNPATCHIFY = 7,   /* VAE predictor -> clamp(-1,1) CHW frame (fp32)      */
-  OASIS_EPI_PARTIAL_F32 = 8   /* split-K slice s: out_f32[s*split_stride + m*ld_out + n] = acc
+  OASIS_EPI_PARTIAL_F32 = 8,  /* split-K slice s: out_f32[s*split_stride + m*ld_out + n] = acc
                                  (no bias; summed by oasis_residual_ln)                */
+  OASIS_EPI_GELU_TANH_FP8 = 9 /* g = gelu_tanh(acc + bias) as fp8 activation blocks:
+                                 out_fp8[m*ld_out + n] = e4m3(g / 2^e) and
+                                 out_scale[m*ld_scale + n/32] = e + 127 per 32 columns
+                                 (N % 32 == 0); the A operand of oasis_gemm_fp8_a8     */
 };
 
 /* Row m is token p of frame f = m / rows_per_frame (p = m % rows_per_frame);
@@ -173,6 +177,9 @@ typedef struct {
   int unpatch_patch;        /* UNPATCHIFY: patch edge (20)                         */
   int unpatch_channels;     /* UNPATCHIFY: channels (3)                            */
   int64_t split_stride;     /* PARTIAL_F32: elements between split-K slices         */
+  void* out_fp8;            /* GELU_TANH_FP8: e4m3 bytes, row stride ld_out         */
+  void* out_scale;          /* GELU_TANH_FP8: e8m0 block scales, row stride ld_scale */
+  int64_t ld_scale;
 } oasis_epilogue_t;
 
 /* acc[M,N] = A[M,K] @ B[N,K]^T (bf16 in, fp32 accumulate) followed by the epilogue.
@@ -197,6 +204,20 @@ int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ld
 int oasis_gemm_fp8(const void* A, int64_t lda, const void* Bq, int64_t ldb, const float* w_scale, int64_t M,
                    int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
                    oasis_stream_t stream);
+
+/* Same product with the A operand already in fp8 activation blocks: A8 e4m3 bytes [M, lda]
+ * (lda % 16 == 0) and A_scale e8m0 bytes [M, lds] (lds >= K/32, lds % 4 == 0), one scale per
+ * 32-wide K block (as oasis_quantize_act_fp8 and OASIS_EPI_GELU_TANH_FP8 write them).
+ * No counterpart in the reference (see oasis_gemm_fp8). */
+int oasis_gemm_fp8_a8(const void* A8, int64_t lda, const void* A_scale, int64_t lds, const void* Bq,
+                      int64_t ldb, const float* w_scale, int64_t M, int64_t N, int64_t K,
+                      const oasis_epilogue_t* epi, int tile, int splits, oasis_stream_t stream);
+
+/* bf16 activations x[M, K] (K % 32 == 0) -> fp8 blocks: for each 32-wide block of a row,
+ * e = floor(log2(max |x|)) - 7 (clamped at -127), q = e4m3(x / 2^e) (nearest even) and
+ * scale byte e + 127. No counterpart in the reference (see oasis_gemm_fp8). */
+int oasis_quantize_act_fp8(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
+                           void* scale, int64_t lds, oasis_stream_t stream);
 
 /* Per-output-channel e4m3 quantization of a bf16 weight W[N,K] (K % 8 == 0):
  * scale[n] = max_k |W[n,k]| / 448 (1 for an all-zero row), q[n,k] = round_e4m3(W[n,k] / scale[n]),
@@ -348,6 +369,12 @@ typedef struct {
   void* mlp;       /* [max_rows, Dm] bf16                                         */
   float* partial;  /* [max_splits, max_rows, D] fp32 split-K slices               */
   int64_t max_splits;
+  /* fp8 weights only (NULL otherwise): the projections' A operands as fp8 activation
+   * blocks (e4m3 bytes + one e8m0 scale per 32 columns) */
+  void* act8;        /* [max_rows, D] e4m3: LN outputs and the attention output     */
+  void* act8_scale;  /* [max_rows, D/32] e8m0                                       */
+  void* mlp8;        /* [max_rows, Dm] e4m3: GELU(FC1) output                       */
+  void* mlp8_scale;  /* [max_rows, Dm/32] e8m0                                      */
 } oasis_dit_buffers_t;
 
 /* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action), then

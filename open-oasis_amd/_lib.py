@@ -15,7 +15,7 @@ MAX_SUB = 64
 
 EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
-EPI_PARTIAL_F32 = 8
+EPI_PARTIAL_F32, EPI_GELU_TANH_FP8 = 8, 9
 ACT_NONE, ACT_SILU = 0, 1
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
@@ -42,6 +42,7 @@ class Epilogue(ctypes.Structure):
         ("rope_sinp", c_p), ("rope_by_frame", c_i), ("unpatch_grid_w", c_i),
         ("s_b", c_i64), ("s_t", c_i64), ("s_p", c_i64), ("s_h", c_i64),
         ("unpatch_patch", c_i), ("unpatch_channels", c_i), ("split_stride", c_i64),
+        ("out_fp8", c_p), ("out_scale", c_p), ("ld_scale", c_i64),
     ]
 
 
@@ -64,7 +65,8 @@ class DiTWeights(ctypes.Structure):
 
 class DiTBuffers(ctypes.Structure):
     _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p),
-                ("attn", c_p), ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64)]
+                ("attn", c_p), ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64),
+                ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p)]
 
 
 class VAEWeights(ctypes.Structure):
@@ -104,6 +106,9 @@ SIGNATURES = {
     "oasis_gemm_bf16_config": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_gemm_fp8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_quantize_fp8_rows": [c_p, c_i64, c_i64, c_p, c_p, c_p],
+    "oasis_gemm_fp8_a8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i,
+                          c_p],
+    "oasis_quantize_act_fp8": [c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p],
     "oasis_ln_modulate": [c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_f, c_p],
     "oasis_ln_affine": [c_p, c_i64, c_i64, c_p, c_p, c_p, c_f, c_p],
     "oasis_residual_ln": [c_p, c_i64, c_i64, c_p, c_i, c_i64, c_p, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_p,

@@ -254,8 +254,10 @@ namespace oasis {
 // all 256 CUs issuing HBM loads.
 // Default tile per shape, from sweeps of the DiT / VAE projections on MI355X (M = 288 and
 // 576 tokens, weights streamed from HBM): 32 x 64 tiles with a 2-deep ring for the QKV-
-// and O-sized products, 96 x 64 tiles with a 4-deep ring for the 4096-wide MLP products.
+// and O-sized products, 96 x 64 tiles with a 4-deep ring for the 4096-wide MLP products;
+// 96 x 128 tiles from 2048 tokens up.
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
+  if (M >= 2048) return 13;  // batched streams (thousands of tokens): 96 x 128 tiles
   bool wide = false;
   if (kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF) wide = N >= 2048;
   if (kind == OASIS_EPI_PARTIAL_F32) wide = Kslice >= 1024;

@@ -31,6 +31,9 @@ struct Epi {
   int unpatch_patch;
   int unpatch_channels;
   int64_t split_stride;
+  uint8_t* out_fp8;
+  uint8_t* out_scale;
+  int64_t ld_scale;
 };
 
 __device__ __forceinline__ int xcd_remap(int pid, int G) {
@@ -140,6 +143,24 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       }
       break;
     }
+    case OASIS_EPI_GELU_TANH_FP8: {
+      // the 4 threads of one 32-column block are lanes 4i..4i+3 of the caller's loop
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[j] = gelu_tanh(v[j]);
+        amax = fmaxf(amax, fabsf(v[j]));
+      }
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      const int sb = fp8_block_scale(amax);
+      const float inv = fp8_block_inv(sb);
+      *reinterpret_cast<uint2*>(e.out_fp8 + m * e.ld_out + n0) =
+          make_uint2(pack4_fp8(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
+                     pack4_fp8(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv));
+      if ((n0 & 31) == 0) e.out_scale[m * e.ld_scale + (n0 >> 5)] = (uint8_t)sb;
+      break;
+    }
     default:
       break;
   }
@@ -171,6 +192,9 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.unpatch_patch = x.unpatch_patch;
   e.unpatch_channels = x.unpatch_channels;
   e.split_stride = x.split_stride;
+  e.out_fp8 = static_cast<uint8_t*>(x.out_fp8);
+  e.out_scale = static_cast<uint8_t*>(x.out_scale);
+  e.ld_scale = x.ld_scale;
   return e;
 }
 
@@ -194,6 +218,12 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
     case OASIS_EPI_GELU_ERF:
       OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 8 == 0, OASIS_ERR_ARG,
                     "gemm: bf16 epilogue needs out_bf16 and ld_out >= N (multiple of 8)");
+      break;
+    case OASIS_EPI_GELU_TANH_FP8:
+      OASIS_REQUIRE(e.out_fp8 && e.out_scale && N % 32 == 0 && e.ld_out >= N && e.ld_out % 8 == 0 &&
+                        e.ld_scale >= N / 32,
+                    OASIS_ERR_ARG, "gemm: GELU_TANH_FP8 needs out_fp8/out_scale, N %% 32 == 0, ld_out >= N "
+                                   "(multiple of 8), ld_scale >= N/32");
       break;
     case OASIS_EPI_QKV_ROPE:
       OASIS_REQUIRE(e.q && e.k && e.v && e.rope_cos && e.rope_sinp, OASIS_ERR_NULL,

@@ -5,10 +5,13 @@
 //
 // Weights: Wq = round_e4m3(W / w_scale[n]), w_scale[n] = max_k |W[n, k]| / 448, one fp32
 // scale per output channel, stored [N, K] bytes (oasis_quantize_fp8_rows makes them).
-// Activations stay bf16 in HBM. Each workgroup quantizes its A tile on the way into LDS:
-// every 32-wide K block of a row gets a power-of-two (e8m0) scale 2^e with the block's
-// max |a| / 2^e in [128, 256), and the MFMA applies that scale in hardware. The per-channel
-// weight scale multiplies the fp32 accumulator before the epilogue.
+// Activations are fp8 blocks: every 32-wide K block of a row has a power-of-two (e8m0)
+// scale 2^e with the block's max |a| / 2^e in [128, 256), applied by the MFMA in hardware.
+// Two A forms: bf16 in HBM, quantized by each workgroup on the way into LDS (AQ = false,
+// oasis_gemm_fp8), or already quantized by the producer kernel (AQ = true,
+// oasis_gemm_fp8_a8: e4m3 bytes + one scale byte per block, half the A bytes and no
+// quantization work per N tile). The per-channel weight scale multiplies the fp32
+// accumulator before the epilogue.
 //
 // MFMA operand layout (16x16x128, verified on MI355X against a host reference): lane l
 // supplies row l%16 of A (column l%16 of B) with the 32 bytes k = 16g..16g+15 and
@@ -38,20 +41,16 @@ __device__ __forceinline__ uint2 quant8(i32x4 raw, int* sbyte) {
   }
   amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
   amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  // amax = m * 2^(E-127), m in [1, 2): scale 2^(E-134) maps amax into [128, 256)
-  const int E = (__float_as_int(amax) >> 23) & 0xff;
-  const int sb = E > 7 ? E - 7 : 0;                       // e8m0 byte of the scale 2^(sb-127)
-  const float inv = __int_as_float((254 - sb) << 23);     // 2^(127-sb), exact
-  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
-  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+  const int sb = fp8_block_scale(amax);
+  const float inv = fp8_block_inv(sb);
   *sbyte = sb;
-  return make_uint2((unsigned)lo, (unsigned)hi);
+  return make_uint2(pack4_fp8(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv),
+                    pack4_fp8(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv));
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
-__global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ A, int64_t lda,
+template <int BM, int BN, int WM, int WN, int STAGES, bool AQ>
+__global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ Av, int64_t lda,
+                                                       const uint8_t* __restrict__ Ascale, int64_t lds,
                                                        const uint8_t* __restrict__ B, int64_t ldb,
                                                        const float* __restrict__ wscale, int M, int N, int K,
                                                        int splits, Epi e) {
@@ -59,9 +58,11 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ 
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 16, FN = TN / 16;
   static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
-  constexpr int A_CHUNKS = BM * (BK8 / 8);   // 16-byte chunks of 8 bf16
+  constexpr int A_EPC = AQ ? 16 : 8;         // A elements per 16-byte chunk (fp8 or bf16)
+  constexpr int A_CHUNKS = BM * (BK8 / A_EPC);
   constexpr int B_CHUNKS = BN * (BK8 / 16);  // 16-byte chunks of 16 fp8
-  static_assert(A_CHUNKS % 256 == 0 && B_CHUNKS % 256 == 0, "BM multiple of 16, BN multiple of 32");
+  static_assert(A_CHUNKS % 256 == 0 && B_CHUNKS % 256 == 0, "BM multiple of 16 (32 for fp8 A), BN of 32");
+  static_assert(!AQ || BM <= 256, "one scale word per thread");
   constexpr int A_PER = A_CHUNKS / 256;
   constexpr int B_PER = B_CHUNKS / 256;
   constexpr int A_BYTES = BM * P8, B_BYTES = BN * P8, S_BYTES = BM * 4;
@@ -85,16 +86,18 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ 
   const int nk = K / BK8 / splits;  // the host guarantees nk % STAGES == 0
   const int kb = split * nk * BK8;
 
-  const bf16* a_src[A_PER];
+  const char* a_src[A_PER];
   int a_dst[A_PER], s_dst[A_PER];
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
     const int c = tid + i * 256;
-    const int row = c / (BK8 / 8), col = (c % (BK8 / 8)) * 8;
-    a_src[i] = A + (int64_t)min(m0 + row, M - 1) * lda + kb + col;
+    const int row = c / (BK8 / A_EPC), col = (c % (BK8 / A_EPC)) * A_EPC;
+    a_src[i] = static_cast<const char*>(Av) + ((int64_t)min(m0 + row, M - 1) * lda + kb + col) * (AQ ? 1 : 2);
     a_dst[i] = row * P8 + col;
     s_dst[i] = (col & 31) == 0 ? row * 4 + col / 32 : -1;
   }
+  // AQ: thread t < BM copies row t's 4 block scales of each K tile (one 32-bit word)
+  const uint8_t* sc_src = AQ ? Ascale + (int64_t)min(m0 + (tid % BM), M - 1) * lds + kb / 32 : nullptr;
   const uint8_t* b_src[B_PER];
   int b_dst[B_PER];
 #pragma unroll
@@ -106,22 +109,30 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ 
   }
 
   i32x4 ra[STAGES][A_PER], rb[STAGES][B_PER];
+  uint32_t rs[STAGES];
   auto gload = [&](int slot, int kt) {
     const int64_t ka = (int64_t)kt * BK8;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i) ra[slot][i] = *reinterpret_cast<const i32x4*>(a_src[i] + ka);
+    for (int i = 0; i < A_PER; ++i) ra[slot][i] = *reinterpret_cast<const i32x4*>(a_src[i] + ka * (AQ ? 1 : 2));
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) rb[slot][i] = *reinterpret_cast<const i32x4*>(b_src[i] + ka);
+    if (AQ) rs[slot] = *reinterpret_cast<const uint32_t*>(sc_src + ka / 32);
   };
   auto lstore = [&](int slot, int buf) {
     uint8_t* as = As + buf * A_BYTES;
     uint8_t* bs = Bs + buf * B_BYTES;
     uint8_t* ss = Ss + buf * S_BYTES;
+    if (AQ) {
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-      int sb;
-      *reinterpret_cast<uint2*>(as + a_dst[i]) = quant8(ra[slot][i], &sb);
-      if (s_dst[i] >= 0) ss[s_dst[i]] = (uint8_t)sb;
+      for (int i = 0; i < A_PER; ++i) *reinterpret_cast<i32x4*>(as + a_dst[i]) = ra[slot][i];
+      if (tid < BM) *reinterpret_cast<uint32_t*>(ss + tid * 4) = rs[slot];
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_PER; ++i) {
+        int sb;
+        *reinterpret_cast<uint2*>(as + a_dst[i]) = quant8(ra[slot][i], &sb);
+        if (s_dst[i] >= 0) ss[s_dst[i]] = (uint8_t)sb;
+      }
     }
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) *reinterpret_cast<i32x4*>(bs + b_dst[i]) = rb[slot][i];
@@ -211,33 +222,39 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const bf16* __restrict__ 
   }
 }
 
-typedef hipError_t (*launch8_fn)(const bf16*, int64_t, const uint8_t*, int64_t, const float*, int, int, int, int,
-                                 const Epi&, hipStream_t);
+typedef hipError_t (*launch8_fn)(const void*, int64_t, const uint8_t*, int64_t, const uint8_t*, int64_t,
+                                 const float*, int, int, int, int, const Epi&, hipStream_t);
 
-template <int BM, int BN, int WM, int WN, int STAGES>
-hipError_t launch8(const bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* ws, int M, int N, int K,
-                   int splits, const Epi& e, hipStream_t s) {
+template <int BM, int BN, int WM, int WN, int STAGES, bool AQ>
+hipError_t launch8(const void* A, int64_t lda, const uint8_t* As, int64_t lds, const uint8_t* B, int64_t ldb,
+                   const float* ws, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, WM, WN, STAGES>), dim3(Mt * Nt * splits), dim3(256), 0, s, A, lda, B,
-                     ldb, ws, M, N, K, splits, e);
+  hipLaunchKernelGGL((gemm_fp8_kernel<BM, BN, WM, WN, STAGES, AQ>), dim3(Mt * Nt * splits), dim3(256), 0, s, A,
+                     lda, As, lds, B, ldb, ws, M, N, K, splits, e);
   return hipGetLastError();
 }
 
 struct Tile8 {
   int bm, bn, stages;
-  launch8_fn fn, fn_single;
+  launch8_fn fn, fn_single;        // bf16 A
+  launch8_fn fn_q, fn_q_single;    // fp8 A blocks
 };
+#define OASIS_T8(BM, BN, WM, WN)                                                                       \
+  {BM, BN, 2, launch8<BM, BN, WM, WN, 2, false>, launch8<BM, BN, WM, WN, 1, false>,                   \
+   launch8<BM, BN, WM, WN, 2, true>, launch8<BM, BN, WM, WN, 1, true>}
 const Tile8 kTiles8[] = {
-    {128, 128, 2, launch8<128, 128, 2, 2, 2>, launch8<128, 128, 2, 2, 1>},  // 0
-    {128, 64, 2, launch8<128, 64, 2, 2, 2>, launch8<128, 64, 2, 2, 1>},     // 1
-    {64, 128, 2, launch8<64, 128, 2, 2, 2>, launch8<64, 128, 2, 2, 1>},     // 2
-    {64, 64, 2, launch8<64, 64, 2, 2, 2>, launch8<64, 64, 2, 2, 1>},        // 3
-    {32, 64, 2, launch8<32, 64, 1, 4, 2>, launch8<32, 64, 1, 4, 1>},        // 4
+    OASIS_T8(128, 128, 2, 2),  // 0
+    OASIS_T8(128, 64, 2, 2),   // 1
+    OASIS_T8(64, 128, 2, 2),   // 2
+    OASIS_T8(64, 64, 2, 2),    // 3
+    OASIS_T8(32, 64, 1, 4),    // 4
 };
+#undef OASIS_T8
 constexpr int kNumTiles8 = sizeof(kTiles8) / sizeof(kTiles8[0]);
 
-int auto_tile8(int64_t M, int64_t N) {
-  if (M >= 2048) return N >= 2048 ? 0 : 1;
+// Default tile per shape, from sweeps of the DiT projections at M = 4608 on MI355X.
+int auto_tile8(int64_t M, int64_t N, bool aq) {
+  if (M >= 2048) return aq ? (N >= 2048 ? 1 : 2) : 2;
   if (M >= 256) return 3;
   return 4;
 }
@@ -269,13 +286,38 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const bf16* __restrict_
   }
 }
 
+// bf16 [M, K] activations -> e4m3 blocks of 32 along K with e8m0 scales [M, K/32].
+// Each thread converts 8 consecutive values; lanes 4i..4i+3 share one block.
+__global__ __launch_bounds__(256) void quant_act_kernel(const bf16* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+                                                        uint8_t* __restrict__ q, int64_t ldq,
+                                                        uint8_t* __restrict__ sc, int64_t lds) {
+  const int64_t cpr = K / 8;  // 8-value chunks per row
+  const int64_t n = M * cpr;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;  // a multiple of 4: groups never straddle
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c - (threadIdx.x & 3) < n; c += step) {
+    const bool live = c < n;
+    const int64_t cc = live ? c : n - 1;
+    const int64_t m = cc / cpr, k = (cc - m * cpr) * 8;
+    int sb;
+    const uint2 v = quant8(*reinterpret_cast<const i32x4*>(x + m * ldx + k), &sb);
+    if (live) {
+      *reinterpret_cast<uint2*>(q + m * ldq + k) = v;
+      if ((k & 31) == 0) sc[m * lds + k / 32] = (uint8_t)sb;
+    }
+  }
+}
+
 }  // namespace
 
 namespace oasis {
 
-int gemm_fp8_launch(const bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* w_scale, int64_t M,
-                    int64_t N, int64_t K, const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
+int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t lds, const uint8_t* B, int64_t ldb,
+                    const float* w_scale, int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& ex, int tile,
+                    int splits, hipStream_t s) {
+  const bool aq = A_scale != nullptr;
   OASIS_REQUIRE(A && B && w_scale, OASIS_ERR_NULL, "gemm_fp8: null operand");
+  OASIS_REQUIRE(!aq || (lds >= K / 32 && lds % 4 == 0 && lda % 16 == 0), OASIS_ERR_SHAPE,
+                "gemm_fp8: fp8 A needs lda %% 16 == 0 and lds >= K/32, lds %% 4 == 0");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE,
                 "gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   OASIS_REQUIRE(K % BK8 == 0, OASIS_ERR_SHAPE, "gemm_fp8: K=%lld must be a multiple of 128", (long long)K);
@@ -286,11 +328,12 @@ int gemm_fp8_launch(const bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, c
                 splits);
   const Epi e = to_epi(ex);
   if (const int rc = check_epilogue(e, M, N, splits)) return rc;
-  if (tile < 0) tile = auto_tile8(M, N);
+  if (tile < 0) tile = auto_tile8(M, N, aq);
   OASIS_REQUIRE(tile < kNumTiles8, OASIS_ERR_ARG, "gemm_fp8: tile config %d out of range", tile);
   const Tile8& t = kTiles8[tile];
   const bool ring = (K / BK8 / splits) % t.stages == 0;
-  const hipError_t err = (ring ? t.fn : t.fn_single)(A, lda, B, ldb, w_scale, (int)M, (int)N, (int)K, splits, e, s);
+  const launch8_fn fn = aq ? (ring ? t.fn_q : t.fn_q_single) : (ring ? t.fn : t.fn_single);
+  const hipError_t err = fn(A, lda, A_scale, lds, B, ldb, w_scale, (int)M, (int)N, (int)K, splits, e, s);
   if (err != hipSuccess) {
     set_error("gemm_fp8 launch failed: %s", hipGetErrorString(err));
     return OASIS_ERR_LAUNCH;
@@ -304,8 +347,31 @@ extern "C" int oasis_gemm_fp8(const void* A, int64_t lda, const void* B, int64_t
                               int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
                               oasis_stream_t stream) {
   OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm_fp8: null epilogue");
-  return oasis::gemm_fp8_launch(static_cast<const bf16*>(A), lda, static_cast<const uint8_t*>(B), ldb, w_scale, M, N,
-                                K, *epi, tile, splits, static_cast<hipStream_t>(stream));
+  return oasis::gemm_fp8_launch(A, lda, nullptr, 0, static_cast<const uint8_t*>(B), ldb, w_scale, M, N, K, *epi, tile,
+                                splits, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_gemm_fp8_a8(const void* A8, int64_t lda, const void* A_scale, int64_t lds, const void* B,
+                                 int64_t ldb, const float* w_scale, int64_t M, int64_t N, int64_t K,
+                                 const oasis_epilogue_t* epi, int tile, int splits, oasis_stream_t stream) {
+  OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm_fp8_a8: null epilogue");
+  OASIS_REQUIRE(A_scale, OASIS_ERR_NULL, "gemm_fp8_a8: null A scales");
+  return oasis::gemm_fp8_launch(A8, lda, static_cast<const uint8_t*>(A_scale), lds, static_cast<const uint8_t*>(B),
+                                ldb, w_scale, M, N, K, *epi, tile, splits, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_quantize_act_fp8(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
+                                      void* scale, int64_t lds, oasis_stream_t stream) {
+  OASIS_REQUIRE(x && q && scale, OASIS_ERR_NULL, "quantize_act_fp8: null pointer");
+  OASIS_REQUIRE(M > 0 && K > 0 && K % 32 == 0 && ldx >= K && ldx % 8 == 0 && ldq >= K && ldq % 8 == 0 && lds >= K / 32,
+                OASIS_ERR_SHAPE, "quantize_act_fp8: need K %% 32 == 0, ldx/ldq >= K (multiples of 8), lds >= K/32");
+  const int64_t chunks = M * (K / 8);
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(quant_act_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16*>(x), ldx, M, K, static_cast<uint8_t*>(q), ldq,
+                     static_cast<uint8_t*>(scale), lds);
+  return oasis::check_launch("quantize_act_fp8");
 }
 
 extern "C" int oasis_quantize_fp8_rows(const void* W, int64_t N, int64_t K, void* q, float* scale,

@@ -90,13 +90,16 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
 // round trip; mean and variance by two block reductions:
 //   x[m] += g * (sum_s partial[s][m] + bias)          (NP > 0; g = gate[f(m)] or 1)
 //   y[m]  = LN(x[m]) * a + b                           (a, b: modulate rows or affine)
+// y is bf16, or (y8 != nullptr, D >= 1024) fp8 activation blocks: e4m3 bytes y8[m, :] and
+// one e8m0 scale per 32 columns in ys[m, :] (8 consecutive threads share a block).
 template <int VPT, int NP>
 __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
                                                           int64_t pstride, const float* __restrict__ bias,
                                                           const float* __restrict__ gate, int64_t gate_fs,
                                                           int64_t rpf, const float* __restrict__ la,
                                                           const float* __restrict__ lb, int64_t ln_fs,
-                                                          bf16* __restrict__ y, float eps) {
+                                                          bf16* __restrict__ y, uint8_t* __restrict__ y8,
+                                                          uint8_t* __restrict__ ys, float eps) {
   constexpr int D = VPT * 256;
   constexpr int NC = VPT / 4 > 0 ? VPT / 4 : 1;   // 4-float groups per thread
   constexpr int W = VPT < 4 ? VPT : 4;            // floats per group
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
       if (bias) ld(bias + k, bv[c]); else bv[c][0] = bv[c][1] = bv[c][2] = bv[c][3] = 0.f;
       if (gate) ld(gate + f * gate_fs + k, gv[c]); else gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 1.f;
     }
-    if (y) {
+    if (y || y8) {
       ld(la + f * ln_fs + k, av[c]);
       ld(lb + f * ln_fs + k, cv[c]);
     }
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
 #pragma unroll
     for (int j = 0; j < W; ++j) s += v[c][j];
   }
-  if (!y) return;
+  if (!y && !y8) return;
   s = wave_sum(s);
   if (lane == 0) red[0][wave] = s;
   __syncthreads();
@@ -177,7 +180,16 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
     float o[4];
 #pragma unroll
     for (int j = 0; j < W; ++j) o[j] = v[c][j] * rstd * av[c][j] + cv[c][j];
-    if (W == 4) {
+    if (W == 4 && y8) {
+      float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      const int sb = fp8_block_scale(amax);
+      const float inv = fp8_block_inv(sb);
+      *reinterpret_cast<uint32_t*>(y8 + row * D + k) = pack4_fp8(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+      if ((tid & 7) == 0) ys[row * (D / 32) + k / 32] = (uint8_t)sb;
+    } else if (W == 4) {
       store4<bf16>(yr + k, o);
     } else {
 #pragma unroll
@@ -189,10 +201,11 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
 template <int VPT>
 hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
-                          bf16* y, float eps, hipStream_t s) {
+                          bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s) {
   const dim3 grid((unsigned)M), block(256);
-#define OASIS_RLN(NPV) \
-  hipLaunchKernelGGL((residual_ln_kernel<VPT, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, lb, lfs, y, eps)
+#define OASIS_RLN(NPV)                                                                                        \
+  hipLaunchKernelGGL((residual_ln_kernel<VPT, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, lb, \
+                     lfs, y, y8, ys, eps)
   switch (np) {
     case 0: OASIS_RLN(0); break;
     case 1: OASIS_RLN(1); break;
@@ -275,34 +288,46 @@ extern "C" int oasis_layernorm(const void* x, const void* weight, const void* bi
   return OASIS_ERR_DTYPE;
 }
 
-extern "C" int oasis_residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials,
-                                 int64_t partial_stride, const float* bias, const float* gate, int64_t gate_fstride,
-                                 int64_t rows_per_frame, const float* ln_a, const float* ln_b, int64_t ln_fstride,
-                                 void* y_bf16, float eps, oasis_stream_t stream) {
+namespace oasis {
+
+int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
+                const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
+                const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
+                hipStream_t s) {
   OASIS_REQUIRE(x, OASIS_ERR_NULL, "residual_ln: null x");
   OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "residual_ln: bad M/rows_per_frame");
   OASIS_REQUIRE(n_partials == 0 || partial, OASIS_ERR_NULL, "residual_ln: null partials");
   OASIS_REQUIRE(n_partials <= 1 || partial_stride >= M * D, OASIS_ERR_ARG, "residual_ln: partial_stride too small");
-  OASIS_REQUIRE(!y_bf16 || (ln_a && ln_b), OASIS_ERR_NULL, "residual_ln: LN output needs ln_a and ln_b");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  OASIS_REQUIRE(!(y_bf16 || y8) || (ln_a && ln_b), OASIS_ERR_NULL, "residual_ln: LN output needs ln_a and ln_b");
+  OASIS_REQUIRE(!y8 || (y8_scale && D >= 1024), OASIS_ERR_ARG, "residual_ln: fp8 output needs scales and D >= 1024");
   bf16* y = static_cast<bf16*>(y_bf16);
   hipError_t e;
   switch (D) {
-    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
-    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
-    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
-    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, eps, s); break;
+    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
+    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
+    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
+    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
     default:
-      oasis::set_error("residual_ln: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
+      set_error("residual_ln: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
       return OASIS_ERR_SHAPE;
   }
   if (e == hipErrorInvalidConfiguration) {
-    oasis::set_error("residual_ln: n_partials=%d must be one of 0-4 or 8", n_partials);
+    set_error("residual_ln: n_partials=%d must be one of 0-4 or 8", n_partials);
     return OASIS_ERR_ARG;
   }
   if (e != hipSuccess) {
-    oasis::set_error("residual_ln launch failed: %s", hipGetErrorString(e));
+    set_error("residual_ln launch failed: %s", hipGetErrorString(e));
     return OASIS_ERR_LAUNCH;
   }
   return OASIS_OK;
+}
+
+}  // namespace oasis
+
+extern "C" int oasis_residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials,
+                                 int64_t partial_stride, const float* bias, const float* gate, int64_t gate_fstride,
+                                 int64_t rows_per_frame, const float* ln_a, const float* ln_b, int64_t ln_fstride,
+                                 void* y_bf16, float eps, oasis_stream_t stream) {
+  return oasis::residual_ln(x, M, D, partial, n_partials, partial_stride, bias, gate, gate_fstride, rows_per_frame,
+                            ln_a, ln_b, ln_fstride, y_bf16, nullptr, nullptr, eps, static_cast<hipStream_t>(stream));
 }

@@ -28,9 +28,17 @@ int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int6
 // explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
 int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                     const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
-// acc = A[M,K] (bf16) @ (Bq[N,K] (e4m3) * w_scale[N])^T with the given epilogue (gemm_fp8.hip).
-int gemm_fp8_launch(const __bf16* A, int64_t lda, const uint8_t* B, int64_t ldb, const float* w_scale, int64_t M,
-                    int64_t N, int64_t K, const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
+// acc = A[M,K] @ (Bq[N,K] (e4m3) * w_scale[N])^T with the given epilogue (gemm_fp8.hip).
+// A_scale == nullptr: A is bf16; else A is e4m3 blocks with e8m0 scales A_scale[M, lds].
+int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t lds, const uint8_t* B, int64_t ldb,
+                    const float* w_scale, int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& epi, int tile,
+                    int splits, hipStream_t s);
+// oasis_residual_ln with an optional fp8-block LN output (y8 e4m3 [M, D], y8_scale e8m0
+// [M, D/32]) in place of the bf16 one (norm.hip).
+int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
+                const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
+                const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
+                hipStream_t s);
 }  // namespace oasis
 
 #define OASIS_REQUIRE(cond, code, ...)          \
@@ -81,6 +89,22 @@ OASIS_DEV float gelu_tanh(float x) {
 OASIS_DEV float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
 
 OASIS_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// ---- fp8 (OCP e4m3) activation blocks -----------------------------------------
+// A block of values with max |v| = amax gets the power-of-two scale 2^(sb-127) (sb is the
+// e8m0 byte) that maps amax into [128, 256): amax = m 2^(E-127), m in [1, 2) -> sb = E - 7.
+OASIS_DEV int fp8_block_scale(float amax) {
+  const int E = (__float_as_int(amax) >> 23) & 0xff;
+  return E > 7 ? E - 7 : 0;
+}
+// 1 / 2^(sb-127), exact
+OASIS_DEV float fp8_block_inv(int sb) { return __int_as_float((254 - sb) << 23); }
+// four values -> four e4m3 bytes (round to nearest even), little-endian in a u32
+OASIS_DEV uint32_t pack4_fp8(float a, float b, float c, float d) {
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+  return (uint32_t)r;
+}
 
 // ---- MFMA -------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8*(l/16)+j] and

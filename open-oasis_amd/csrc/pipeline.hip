@@ -181,16 +181,17 @@ int check_dit(const oasis_dit_weights_t* w) {
   return OASIS_OK;
 }
 
-// One projection of sub-block j (role QKV/O/FC1/FC2): the bf16 GEMM, or the fp8 GEMM
-// when the projection weights are e4m3 with per-channel scales.
-int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64_t lda, int64_t M, int64_t N,
-         int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s) {
+// One projection of sub-block j (role QKV/O/FC1/FC2): the bf16 GEMM on a bf16 A, or,
+// with e4m3 weights, the fp8 GEMM on A given as fp8 blocks (A e4m3 bytes, A_scale e8m0).
+int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64_t lda, const void* A_scale,
+         int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s) {
   const void* W = role == ROLE_QKV ? w->qkv_w[j] : role == ROLE_O ? w->out_w[j] : role == ROLE_FC1 ? w->fc1_w[j]
                                                                                                    : w->fc2_w[j];
   if (w->weight_format == OASIS_WEIGHTS_FP8) {
     const float* sc = role == ROLE_QKV ? w->qkv_s[j] : role == ROLE_O ? w->out_s[j] : role == ROLE_FC1 ? w->fc1_s[j]
                                                                                                        : w->fc2_s[j];
-    return oasis::gemm_fp8_launch((const bf16*)A, lda, (const uint8_t*)W, K, sc, M, N, K, e, -1, splits, s);
+    return oasis::gemm_fp8_launch(A, lda, (const uint8_t*)A_scale, K / 32, (const uint8_t*)W, K, sc, M, N, K, e, -1,
+                                  splits, s);
   }
   return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s);
 }
@@ -245,10 +246,13 @@ oasis_epilogue_t partial_epi(float* part, int64_t M, int64_t N) {
   return e;
 }
 
-int check_dit_buf(const oasis_dit_buffers_t* buf) {
+int check_dit_buf(const oasis_dit_buffers_t* buf, const oasis_dit_weights_t* w) {
   OASIS_REQUIRE(buf && buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp && buf->partial,
                 OASIS_ERR_NULL, "dit: missing buffer");
   OASIS_REQUIRE(buf->max_splits >= 1, OASIS_ERR_ARG, "dit: max_splits must be >= 1");
+  OASIS_REQUIRE(w->weight_format != OASIS_WEIGHTS_FP8 ||
+                    (buf->act8 && buf->act8_scale && buf->mlp8 && buf->mlp8_scale),
+                OASIS_ERR_NULL, "dit: fp8 weights need the act8/mlp8 buffers");
   return OASIS_OK;
 }
 
@@ -275,11 +279,21 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   qkv.v = buf->v;
   qkv.rows_per_frame = P;
   qkv.frames_per_stream = T;
+  const bool fp8 = w->weight_format == OASIS_WEIGHTS_FP8;
   oasis_epilogue_t gelu = epi_zero();
-  gelu.kind = OASIS_EPI_GELU_TANH;
+  gelu.kind = fp8 ? OASIS_EPI_GELU_TANH_FP8 : OASIS_EPI_GELU_TANH;
   gelu.out_bf16 = buf->mlp;
+  gelu.out_fp8 = buf->mlp8;
+  gelu.out_scale = buf->mlp8_scale;
+  gelu.ld_scale = Dm / 32;
   gelu.ld_out = Dm;
   const oasis_epilogue_t part = partial_epi(buf->partial, M, D);
+  // A operands: bf16 (h, attn, mlp) or, with fp8 weights, fp8 blocks (act8, mlp8)
+  uint8_t* a8 = static_cast<uint8_t*>(buf->act8);
+  uint8_t* a8s = static_cast<uint8_t*>(buf->act8_scale);
+  const void* ln_out = fp8 ? nullptr : buf->h;
+  const void* mlp_in = fp8 ? buf->mlp8 : buf->mlp;
+  const void* mlp_sc = fp8 ? buf->mlp8_scale : nullptr;
 
   for (int64_t j = j0; j < j1; ++j) {
     const bool spatial = (j % 2) == 0;
@@ -287,8 +301,8 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     if (ada_ready && hipStreamWaitEvent(s, ada_ready[j], 0) != hipSuccess)
       return oasis::check_launch("wait for adaLN rows");
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
-    OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
-                                fs, buf->h, kLnEps, stream));
+    OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
+                                 fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
     if (spatial) {  // heads-first per frame: [(b*T + t)*H + h][p][64]
       qkv.s_b = T * H * P * 64;
       qkv.s_t = H * P * 64;
@@ -306,18 +320,20 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       qkv.rope_sinp = w->t_sinp;
       qkv.rope_by_frame = 1;
     }
-    OASIS_TRY(proj(w, ROLE_QKV, j, buf->h, D, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1, s));
+    OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
+                   s));
     if (spatial)
       OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
     else
       OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
+    if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     // O projection as split-K partials; bias + gated residual + LN + modulate fused after
-    OASIS_TRY(proj(w, ROLE_O, j, buf->attn, D, M, D, D, part, pl.tile[ROLE_O], so, s));
-    OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, so, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
-                                a + 3 * D, fs, buf->h, kLnEps, stream));
+    OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
+    OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
+                                 a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
     gelu.bias = w->fc1_b[j];
-    OASIS_TRY(proj(w, ROLE_FC1, j, buf->h, D, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
-    OASIS_TRY(proj(w, ROLE_FC2, j, buf->mlp, Dm, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
+    OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+    OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
     pend->bias = w->fc2_b[j];
     pend->gate = a + 5 * D;
     pend->n = sf;
@@ -327,7 +343,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
 
 int dit_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T, const float* ada) {
   OASIS_TRY(check_dit(w));
-  OASIS_TRY(check_dit_buf(buf));
+  OASIS_TRY(check_dit_buf(buf, w));
   OASIS_REQUIRE(ada, OASIS_ERR_NULL, "dit: null ada");
   OASIS_REQUIRE(B > 0 && T > 0 && T <= w->t_max, OASIS_ERR_SHAPE, "dit: need B > 0, 0 < T <= t_max (%d)", w->t_max);
   const int64_t M = B * T * (int64_t)w->grid_h * w->grid_w;
@@ -436,7 +452,7 @@ extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_di
 extern "C" int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M,
                                const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream) {
   OASIS_TRY(check_dit(w));
-  OASIS_TRY(check_dit_buf(buf));
+  OASIS_TRY(check_dit_buf(buf, w));
   OASIS_REQUIRE(ada && v_out, OASIS_ERR_NULL, "dit_final: null pointer");
   OASIS_REQUIRE(M > 0 && M <= buf->max_rows, OASIS_ERR_SHAPE, "dit_final: bad row count");
   return dit_final(w, buf, M, ada, ada_fstride, Pending(), v_out, stream);
@@ -535,7 +551,7 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
                                 const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
                                 float* v_out, float* latent, float* frame, oasis_stream_t stream) {
   OASIS_TRY(check_dit(w));
-  OASIS_TRY(check_dit_buf(buf));
+  OASIS_TRY(check_dit_buf(buf, w));
   OASIS_REQUIRE(vw && vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
                 OASIS_ERR_NULL, "ddim_frame: null pointer");
   OASIS_REQUIRE(n_steps > 0 && n_steps <= 15, OASIS_ERR_ARG, "ddim_frame: n_steps must be in [1, 15]");

@@ -257,6 +257,14 @@ class DiTWorkspace:
         for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
             setattr(S, name, getattr(self, name).data_ptr())
         S.max_splits = max_splits
+        if dit.weights == "fp8":  # fp8 activation blocks: e4m3 bytes + one e8m0 scale per 32 columns
+            u8 = torch.uint8
+            self.act8 = torch.zeros(max_rows, d, device=dev, dtype=u8)
+            self.act8_scale = torch.zeros(max_rows, d // 32, device=dev, dtype=u8)
+            self.mlp8 = torch.zeros(max_rows, dit.d_mlp, device=dev, dtype=u8)
+            self.mlp8_scale = torch.zeros(max_rows, dit.d_mlp // 32, device=dev, dtype=u8)
+            for name in ("act8", "act8_scale", "mlp8", "mlp8_scale"):
+                setattr(S, name, getattr(self, name).data_ptr())
         self.struct = S
 
 

@@ -168,3 +168,51 @@ def test_config4_bf16_stream_matches_oracle():
         cond = oracle.conditioning(c["t"][b], c["actions"][b], c["w"])
         ref = oracle.dit_forward(z, cond, c["w"]).reshape(-1, 64)
         assert_close(v[b], ref, COS_SUB, REL_SUB, "config4 bf16 stream %d (2 blocks)" % b)
+
+
+def test_quantize_act_fp8_matches_oracle():
+    M, K = 300, 1024
+    g = _gen(11)
+    x = (torch.randn(M, K, generator=g) * torch.logspace(-3, 2, K // 32).repeat_interleave(32)).to(torch.bfloat16)
+    x[7] = 0
+    q = torch.zeros(M, K, dtype=torch.uint8, device="cuda")
+    sc = torch.zeros(M, K // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_quantize_act_fp8", L.ptr(dev(x)), K, M, K, L.ptr(q), K, L.ptr(sc), K // 32, stream())
+    sync()
+    deq = q.cpu().view(torch.float8_e4m3fn).float() * torch.pow(2.0, sc.cpu().float() - 127).repeat_interleave(32, 1)
+    assert torch.equal(deq, oracle.quantize_act_blocks(x))
+
+
+def test_gemm_fp8_a8_equals_in_kernel_quantization():
+    """Pre-quantized A blocks give bit-identical results to quantizing A inside the GEMM,
+    and the fp8 GELU epilogue writes the blocks the next fp8 GEMM reads."""
+    M, N, K = 600, 1024, 1024
+    g = _gen(12)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    q, s = _quantize(W)
+    Ad = dev(A)
+    a8 = torch.zeros(M, K, dtype=torch.uint8, device="cuda")
+    a8s = torch.zeros(M, K // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_quantize_act_fp8", L.ptr(Ad), K, M, K, L.ptr(a8), K, L.ptr(a8s), K // 32, stream())
+    for tile in (0, 1, 2, 3, 4):
+        o1 = torch.zeros(M, N, device="cuda")
+        o2 = torch.zeros(M, N, device="cuda")
+        L.call("oasis_gemm_fp8", L.ptr(Ad), K, L.ptr(q), K, L.ptr(s), M, N, K,
+               ctypes.byref(_epi(kind=L.EPI_STORE_F32, out_f32=o1, ld_out=N)), tile, 1, stream())
+        L.call("oasis_gemm_fp8_a8", L.ptr(a8), K, L.ptr(a8s), K // 32, L.ptr(q), K, L.ptr(s), M, N, K,
+               ctypes.byref(_epi(kind=L.EPI_STORE_F32, out_f32=o2, ld_out=N)), tile, 1, stream())
+        sync()
+        assert torch.equal(o1, o2), "tile %d" % tile
+    m8 = torch.zeros(M, N, dtype=torch.uint8, device="cuda")
+    m8s = torch.zeros(M, N // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_gemm_fp8_a8", L.ptr(a8), K, L.ptr(a8s), K // 32, L.ptr(q), K, L.ptr(s), M, N, K,
+           ctypes.byref(_epi(kind=L.EPI_GELU_TANH_FP8, bias=dev(bias), out_fp8=m8, out_scale=m8s, ld_out=N,
+                             ld_scale=N // 32)), -1, 1, stream())
+    sync()
+    deq = m8.cpu().view(torch.float8_e4m3fn).float() * torch.pow(2.0, m8s.cpu().float() - 127).repeat_interleave(32, 1)
+    ref = oracle.quantize_act_blocks(oracle.gelu_tanh((_ref(A, W) + bias.double()).float()))
+    cos, rel = metrics(deq, ref)
+    print("fp8 GELU epilogue blocks: cos=%.7f rel=%.3e" % (cos, rel), flush=True)
+    assert cos >= 0.9999 and rel <= 7e-2, (cos, rel)  # a value near a rounding midpoint may move one e4m3 step
