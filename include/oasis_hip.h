@@ -419,6 +419,36 @@ int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                    float* tfreq, float* hid, float* cond, float* ada, float* v_out,
                    oasis_stream_t stream);
 
+/* Temporal K/V cache of the context frame for the KV-cache DiT passes. For temporal
+ * sub-block jt (sub-block j = 2*jt + 1), k + jt*S and v + jt*S (S = max_streams*P*2*D
+ * elements) hold bf16 [max_streams][P][n_heads][2][64]: slot 0 the context (past) frame,
+ * slot 1 the current frame. Caller-allocated, n_sub/2 * S elements each. */
+typedef struct {
+  void* k;
+  void* v;
+  int64_t max_streams;
+} oasis_kv_cache_t;
+
+/* Past-frame pass of the KV cache: buf->x [B*P, D] holds the B context frames' embedded
+ * tokens; runs all sub-blocks at T=1 (temporal attention collapses to V) and stores every
+ * temporal sub-block's rotated K and V in slot 0 of kv. No final layer; buf->x is left
+ * holding the past frames' last hidden state. Needs buf->max_rows >= 2*B*P, w->t_max >= 2.
+ * ada: the context frames' adaLN rows (stream b at ada + b*ada_fstride).
+ * (precompute_past_state, oasis_inference.py:1354-1370, with run_sub_block_t1 in "save"
+ * mode, oasis_inference.py:1218-1352.) */
+int oasis_dit_precompute_past(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                              const oasis_kv_cache_t* kv, int64_t B, const float* ada,
+                              int64_t ada_fstride, oasis_stream_t stream);
+
+/* Current-frame pass of the KV cache: buf->x [B*P, D] holds the B current frames; runs all
+ * sub-blocks at T=1, the temporal ones attending over [cached context K/V (slot 0), own K/V
+ * (written to slot 1)], then the final layer: v_out fp32 [B*P, 64]. Equal to the current
+ * rows of the T=2 forward (the context rows never see the current frame).
+ * (dit_forward_currentonly, oasis_inference.py:1372-1403.) */
+int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                              const oasis_kv_cache_t* kv, int64_t B, const float* ada,
+                              int64_t ada_fstride, float* v_out, oasis_stream_t stream);
+
 typedef struct {
   int depth;                 /* 12                                                 */
   int d_model;               /* 1024                                               */
@@ -478,13 +508,17 @@ int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* bu
  *   latent_dim] scratch; frame: fp32 [3, H, W] output. n_steps <= 15.
  * The adaLN projections of all conditioning rows run as one pass before the first step
  * (OASIS_ADALN_OVERLAP=1: on a library-owned side stream, overlapped with the first step).
+ * kv: NULL runs every step as the T=2 forward. Otherwise (a cache for >= 1 stream) step 0
+ * runs at T=2 and stores the context frame's temporal K/V, and steps 1.. run only the
+ * current frame at T=1 against that cache (the K/V-cache path of oasis_inference.py:
+ * 1934-1963, with the past-frame pass folded into the first step).
  * (ddim_step_fn and the traced frame, oasis_inference.py:1909-1932,2131-2148.) */
 int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                      const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
-                     float* chunk, const float* ctx_patches, const float* t, const float* action,
-                     int64_t n_steps, const float* coeffs, float* tfreq, float* hid, float* cond,
-                     float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
-                     oasis_stream_t stream);
+                     const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
+                     const float* action, int64_t n_steps, const float* coeffs, float* tfreq,
+                     float* hid, float* cond, float* ada, float* ctx_z, float* v_out, float* latent,
+                     float* frame, oasis_stream_t stream);
 
 /* ---- hipGraph capture of any sequence of the calls above on one stream ---------
  * Replaces ttnn.begin_trace_capture / end_trace_capture / execute_trace / release_trace

@@ -69,6 +69,10 @@ class DiTBuffers(ctypes.Structure):
                 ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p)]
 
 
+class KVCache(ctypes.Structure):
+    _fields_ = [("k", c_p), ("v", c_p), ("max_streams", c_i64)]
+
+
 class VAEWeights(ctypes.Structure):
     _fields_ = [
         ("depth", c_i), ("d_model", c_i), ("n_heads", c_i), ("d_mlp", c_i), ("latent_dim", c_i),
@@ -128,8 +132,10 @@ SIGNATURES = {
     "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
     "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
                        c_p],
-    "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p, c_p,
-                         c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
+    "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,
+                         c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
+    "oasis_dit_precompute_past": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p],
+    "oasis_dit_forward_current": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_graph_begin": [c_p],
     "oasis_graph_end": [c_p, P(c_p)],
     "oasis_graph_launch": [c_p, c_p],

@@ -217,7 +217,7 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
 // q,k,v: [B][P][H][T][64] bf16; out: token-major [(b*T + t)*P + p][h*64 + d]
 __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                        const bf16* __restrict__ v, bf16* __restrict__ out,
-                                                       int64_t G, int T, int P, int H, float scale_log2) {
+                                                       int64_t G, int T, int P, int H, float scale_log2, int qf) {
   const int64_t grp = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int j = threadIdx.x & 15;
   if (grp >= G) return;  // whole 16-lane groups exit together; no cross-group shuffles
@@ -226,6 +226,8 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
   const int p = (int)(bp % P);
   const int64_t b = bp / P;
   const int64_t base = grp * T * 64 + j * 4;
+  // qf >= 0: only query frame qf is computed, written as the single frame of a T=1 output
+  // (out row b*P + p); the K/V cache path runs the current frame against cached context K/V.
   if (T == 2) {  // the DiT's 2-frame window: one round trip for all six rows
     const bf16x4 q0 = *reinterpret_cast<const bf16x4*>(q + base), q1 = *reinterpret_cast<const bf16x4*>(q + base + 64);
     const bf16x4 k0 = *reinterpret_cast<const bf16x4*>(k + base), k1 = *reinterpret_cast<const bf16x4*>(k + base + 64);
@@ -247,15 +249,17 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     const float mx = fmaxf(x0, x1);
     const float p0 = exp2f(x0 - mx), p1 = exp2f(x1 - mx);
     const float inv = 1.0f / (p0 + p1);
-    bf16* dst0 = out + (b * T * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
-    bf16* dst1 = dst0 + (int64_t)P * H * 64;
-    *reinterpret_cast<bf16x4*>(dst0) = v0;
+    const int T_out = qf < 0 ? T : 1;
+    bf16* dst0 = out + (b * T_out * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
+    bf16* dst1 = qf < 0 ? dst0 + (int64_t)P * H * 64 : dst0;
+    if (qf <= 0) *reinterpret_cast<bf16x4*>(dst0) = v0;
+    if (qf == 0) return;
     *reinterpret_cast<bf16x4*>(dst1) =
         bf16x4{f2bf((p0 * bf2f(v0[0]) + p1 * bf2f(v1[0])) * inv), f2bf((p0 * bf2f(v0[1]) + p1 * bf2f(v1[1])) * inv),
                f2bf((p0 * bf2f(v0[2]) + p1 * bf2f(v1[2])) * inv), f2bf((p0 * bf2f(v0[3]) + p1 * bf2f(v1[3])) * inv)};
     return;
   }
-  for (int t = 0; t < T; ++t) {
+  for (int t = qf < 0 ? 0 : qf; t < (qf < 0 ? T : qf + 1); ++t) {
     const bf16x4 qv4 = *reinterpret_cast<const bf16x4*>(q + base + t * 64);
     float qv[4] = {bf2f(qv4[0]), bf2f(qv4[1]), bf2f(qv4[2]), bf2f(qv4[3])};
     float m = -INFINITY, l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -277,7 +281,8 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
       m = m_new;
     }
     const float inv = 1.0f / l;
-    bf16* dst = out + ((b * T + t) * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
+    const int64_t frame = qf < 0 ? b * T + t : b;
+    bf16* dst = out + (frame * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
     *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(acc[0] * inv), f2bf(acc[1] * inv), f2bf(acc[2] * inv),
                                               f2bf(acc[3] * inv)};
   }
@@ -332,15 +337,24 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
   return OASIS_ERR_DTYPE;
 }
 
-extern "C" int oasis_temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T,
-                                        int64_t P, int64_t n_heads, float scale, oasis_stream_t stream) {
+namespace oasis {
+
+int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
   OASIS_REQUIRE(B > 0 && T > 0 && P > 0 && n_heads > 0 && T <= 4096, OASIS_ERR_SHAPE,
                 "temporal_attention: bad shape");
+  OASIS_REQUIRE(q_frame < T, OASIS_ERR_ARG, "temporal_attention: q_frame must be < T");
   const int64_t G = B * P * n_heads;
-  hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                     static_cast<const bf16*>(v), static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads,
-                     scale * LOG2E);
-  return oasis::check_launch("temporal_attention");
+  hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0, stream,
+                     static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                     static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame);
+  return check_launch("temporal_attention");
+}
+
+}  // namespace oasis
+
+extern "C" int oasis_temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T,
+                                        int64_t P, int64_t n_heads, float scale, oasis_stream_t stream) {
+  return oasis::temporal_attention(q, k, v, out, B, T, P, n_heads, scale, -1, static_cast<hipStream_t>(stream));
 }

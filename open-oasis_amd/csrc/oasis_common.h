@@ -39,6 +39,10 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
                 hipStream_t s);
+// Causal temporal attention (attention.hip); q_frame >= 0 computes only that query frame of
+// each group and writes it as a single frame: out [B*P, n_heads*64].
+int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream);
 }  // namespace oasis
 
 #define OASIS_REQUIRE(cond, code, ...)          \

@@ -256,11 +256,25 @@ int check_dit_buf(const oasis_dit_buffers_t* buf, const oasis_dit_weights_t* w) 
   return OASIS_OK;
 }
 
+// How a forward pass uses the temporal K/V cache (oasis_kv_cache_t): SAVE_T2 is a T=2
+// pass whose temporal K/V go to the cache (context in slot 0, current in slot 1);
+// SAVE_T1 a T=1 pass over the context frames (slot 0, attention output = V); USE_T1 a T=1
+// pass over the current frames (slot 1) attending over both slots.
+enum { KV_NONE, KV_SAVE_T2, KV_SAVE_T1, KV_USE_T1 };
+struct KvPass {
+  bf16* k = nullptr;
+  bf16* v = nullptr;
+  int64_t sub_stride = 0;  // elements per temporal sub-block
+  int mode = KV_NONE;
+};
+
 // run_sub_block (oasis_inference.py:995-1215) for sub-blocks [j0, j1); sub-block j is
-// spatial for even j. The FC2 residual of the last sub-block is left pending.
+// spatial for even j. The FC2 residual of the last sub-block is left pending. With a
+// K/V-cache pass the temporal sub-blocks read and write the cache (run_sub_block_t1,
+// oasis_inference.py:1218-1352).
 int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T, const float* ada,
                int64_t fs, int64_t j0, int64_t j1, Pending* pend, oasis_stream_t stream,
-               const hipEvent_t* ada_ready = nullptr) {
+               const hipEvent_t* ada_ready = nullptr, const KvPass& kv = KvPass()) {
   const int64_t D = w->d_model, H = w->n_heads, Dm = w->d_mlp;
   const int64_t P = (int64_t)w->grid_h * w->grid_w;
   const int64_t M = B * T * P;
@@ -274,9 +288,6 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   oasis_epilogue_t qkv = epi_zero();
   qkv.kind = OASIS_EPI_QKV_ROPE;
   qkv.n_heads = (int)H;
-  qkv.q = buf->q;
-  qkv.k = buf->k;
-  qkv.v = buf->v;
   qkv.rows_per_frame = P;
   qkv.frames_per_stream = T;
   const bool fp8 = w->weight_format == OASIS_WEIGHTS_FP8;
@@ -303,6 +314,12 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
+    bf16* kc = nullptr;
+    bf16* vc = nullptr;
+    int qf = -1;  // temporal query frame (-1: all)
+    qkv.q = buf->q;
+    qkv.k = buf->k;
+    qkv.v = buf->v;
     if (spatial) {  // heads-first per frame: [(b*T + t)*H + h][p][64]
       qkv.s_b = T * H * P * 64;
       qkv.s_t = H * P * 64;
@@ -311,7 +328,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       qkv.rope_cos = w->s_cos;
       qkv.rope_sinp = w->s_sinp;
       qkv.rope_by_frame = 0;
-    } else {  // grouped by position: [b][p][h][t][64]
+    } else if (kv.mode == KV_NONE) {  // grouped by position: [b][p][h][t][64]
       qkv.s_b = P * H * T * 64;
       qkv.s_p = H * T * 64;
       qkv.s_h = T * 64;
@@ -319,13 +336,30 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       qkv.rope_cos = w->t_cos;
       qkv.rope_sinp = w->t_sinp;
       qkv.rope_by_frame = 1;
+    } else {  // the cache's 2-slot layout [b][p][h][2][64]; T=1 passes write one slot
+      kc = kv.k + (j / 2) * kv.sub_stride;
+      vc = kv.v + (j / 2) * kv.sub_stride;
+      const int slot = kv.mode == KV_USE_T1 ? 1 : 0;
+      qf = kv.mode == KV_SAVE_T2 ? -1 : slot;
+      qkv.s_b = P * H * 2 * 64;
+      qkv.s_p = H * 2 * 64;
+      qkv.s_h = 2 * 64;
+      qkv.s_t = 64;
+      qkv.q = static_cast<bf16*>(buf->q) + slot * 64;
+      qkv.k = kc + slot * 64;
+      qkv.v = vc + slot * 64;
+      qkv.rope_cos = w->t_cos + slot * 64;  // RoPE position = slot + t
+      qkv.rope_sinp = w->t_sinp + slot * 64;
+      qkv.rope_by_frame = 1;
     }
     OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
                    s));
     if (spatial)
       OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
-    else
+    else if (kv.mode == KV_NONE)
       OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
+    else
+      OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s));
     if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     // O projection as split-K partials; bias + gated residual + LN + modulate fused after
     OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
@@ -467,6 +501,47 @@ extern "C" int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_b
   return dit_final(w, buf, B * T * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, pend, v_out, stream);
 }
 
+namespace {
+
+int kv_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, const oasis_kv_cache_t* kv, int64_t B,
+            const float* ada, KvPass* out, int mode) {
+  OASIS_TRY(dit_args(w, buf, B, 1, ada));
+  OASIS_REQUIRE(kv && kv->k && kv->v, OASIS_ERR_NULL, "kv cache: null pointer");
+  OASIS_REQUIRE(B <= kv->max_streams, OASIS_ERR_SHAPE, "kv cache: %lld streams exceed its %lld", (long long)B,
+                (long long)kv->max_streams);
+  const int64_t P = (int64_t)w->grid_h * w->grid_w;
+  OASIS_REQUIRE(w->t_max >= 2, OASIS_ERR_SHAPE, "kv cache: temporal RoPE table needs >= 2 frames");
+  OASIS_REQUIRE(2 * B * P <= buf->max_rows, OASIS_ERR_SHAPE,
+                "kv cache: the q buffer holds 2 frames per stream; need max_rows >= %lld", (long long)(2 * B * P));
+  out->k = static_cast<bf16*>(kv->k);
+  out->v = static_cast<bf16*>(kv->v);
+  out->sub_stride = kv->max_streams * P * 2 * w->d_model;
+  out->mode = mode;
+  return OASIS_OK;
+}
+
+}  // namespace
+
+extern "C" int oasis_dit_precompute_past(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                                         const oasis_kv_cache_t* kv, int64_t B, const float* ada,
+                                         int64_t ada_fstride, oasis_stream_t stream) {
+  KvPass kp;
+  OASIS_TRY(kv_args(w, buf, kv, B, ada, &kp, KV_SAVE_T1));
+  Pending pend;
+  return dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, nullptr, kp);
+}
+
+extern "C" int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                                         const oasis_kv_cache_t* kv, int64_t B, const float* ada,
+                                         int64_t ada_fstride, float* v_out, oasis_stream_t stream) {
+  KvPass kp;
+  OASIS_TRY(kv_args(w, buf, kv, B, ada, &kp, KV_USE_T1));
+  OASIS_REQUIRE(v_out, OASIS_ERR_NULL, "dit_forward_current: null v_out");
+  Pending pend;
+  OASIS_TRY(dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, nullptr, kp));
+  return dit_final(w, buf, B * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, pend, v_out, stream);
+}
+
 extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, const float* latent,
                                 float* frame, oasis_stream_t stream) {
   OASIS_REQUIRE(w && buf && latent && frame, OASIS_ERR_NULL, "vae_decode: null pointer");
@@ -546,10 +621,11 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
 }
 
 extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
-                                const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf, float* chunk,
-                                const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
-                                const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
-                                float* v_out, float* latent, float* frame, oasis_stream_t stream) {
+                                const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                                const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
+                                const float* action, int64_t n_steps, const float* coeffs, float* tfreq, float* hid,
+                                float* cond, float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
+                                oasis_stream_t stream) {
   OASIS_TRY(check_dit(w));
   OASIS_TRY(check_dit_buf(buf, w));
   OASIS_REQUIRE(vw && vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
@@ -563,6 +639,12 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
                 "ddim_frame: VAE grid must be the 2x-upsampled DiT grid");
   const int64_t NA = ada_width(w), R = 1 + n_steps;
   hipStream_t s = (hipStream_t)stream;
+  KvPass save, use;
+  if (kv) {
+    OASIS_TRY(kv_args(w, buf, kv, 1, ada, &save, KV_SAVE_T2));
+    use = save;
+    use.mode = KV_USE_T1;
+  }
   // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
   // covers all rows (with the overlap option it streams on the side stream during step 0)
   OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
@@ -570,17 +652,27 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
   OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
   OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
   for (int64_t i = 0; i < n_steps; ++i) {
+    const bool t1 = kv && i > 0;  // K/V cache filled by step 0: the current frame alone
+    const float* c = coeffs + 6 * i;
+    Pending pend;
+    const bool wait = ss && i == 0;
+    if (t1) {
+      OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x, D, stream));
+      const float* ada_cur = ada + (1 + i) * NA;  // the generated frame's rows at step i
+      OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, nullptr, use));
+      OASIS_TRY(dit_final(w, buf, P, ada_cur, NA, pend, v_out, stream));
+      OASIS_TRY(oasis_ddim_update(chunk, v_out, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5], stream));
+      continue;
+    }
     // z = [context frame; patch-embedded chunk] (oasis_inference.py:1911-1913)
     if (hipMemcpyAsync(buf->x, ctx_z, P * D * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess)
       return oasis::check_launch("ddim_frame context copy");
     OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x + P * D, D,
                                  stream));
     const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
-    Pending pend;
-    const bool wait = ss && i == 0;
-    OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, wait ? ss->ev : nullptr));
+    OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, wait ? ss->ev : nullptr,
+                         kv ? save : KvPass()));
     OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream, wait ? ss->ev[w->n_sub] : nullptr));
-    const float* c = coeffs + 6 * i;
     OASIS_TRY(oasis_ddim_update(chunk, v_out + P * w->patch_dim, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5],
                                 stream));
   }

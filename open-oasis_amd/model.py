@@ -221,10 +221,34 @@ class DiT:
         L.call("oasis_dit_sub_blocks", ctypes.byref(self.struct), ctypes.byref(ws.struct), B, T,
                L.ptr(ada), ada_fstride, j0, j1, L.stream_handle(stream))
 
+    def precompute_past(self, ws, kv, B, ada, ada_fstride, stream=None):
+        """K/V-cache past pass on ws.x[:B*P] (precompute_past_state, oasis_inference.py:1354)."""
+        L.call("oasis_dit_precompute_past", ctypes.byref(self.struct), ctypes.byref(ws.struct),
+               ctypes.byref(kv.struct), B, L.ptr(ada), ada_fstride, L.stream_handle(stream))
+
+    def forward_current(self, ws, kv, B, ada, ada_fstride, v_out, stream=None):
+        """K/V-cache current-frame pass on ws.x[:B*P] (dit_forward_currentonly,
+        oasis_inference.py:1372)."""
+        L.call("oasis_dit_forward_current", ctypes.byref(self.struct), ctypes.byref(ws.struct),
+               ctypes.byref(kv.struct), B, L.ptr(ada), ada_fstride, L.ptr(v_out), L.stream_handle(stream))
+
     def forward_inplace(self, ws, B, T, ada, ada_fstride, v_out, stream=None):
         """Blocks + final layer on ws.x[:B*T*P] (in place); v_out [B*T*P, 64] fp32."""
         L.call("oasis_dit_forward", ctypes.byref(self.struct), ctypes.byref(ws.struct), B, T,
                L.ptr(ada), ada_fstride, L.ptr(v_out), L.stream_handle(stream))
+
+
+class KVCache:
+    """The context frame's rotated temporal K/V for every temporal sub-block, for up to
+    max_streams streams: k, v bf16 [n_sub/2, max_streams, P, H, 2, 64] (slot 0 context,
+    slot 1 current frame; the t1_past_k/v scratches of oasis_inference.py:1218-1352)."""
+
+    def __init__(self, dit, max_streams=1):
+        shape = (dit.n_sub // 2, max_streams, dit.P, dit.n_heads, 2, HEAD_DIM)
+        self.k = torch.zeros(shape, device=dit.device, dtype=torch.bfloat16)
+        self.v = torch.zeros(shape, device=dit.device, dtype=torch.bfloat16)
+        self.max_streams = max_streams
+        self.struct = L.KVCache(k=self.k.data_ptr(), v=self.v.data_ptr(), max_streams=max_streams)
 
 
 class DiTWorkspace:
@@ -416,13 +440,18 @@ class DiTStep:
 class FramePipeline:
     """One generated frame (reference traced frame, oasis_inference.py:2131-2148):
     conditioning for the context row and the n_steps generated rows, context patch
-    embed, n_steps T=2 DDIM v-prediction steps, bridge, VAE decode and unpatchify.
+    embed, n_steps DDIM v-prediction steps, bridge, VAE decode and unpatchify. With
+    kv_cache (the default, as the reference's OASIS_KV=1) the first step runs at T=2 and
+    stores the context frame's temporal K/V; the later steps run the generated frame alone
+    at T=1 against that cache. kv_cache=False runs every step at T=2.
     Inputs: self.chunk [P, 64] noise (patch space), self.ctx_patches [P, 64],
     self.ws.t / self.ws.act rows [0] context and [1+i] generated frame at step i."""
 
-    def __init__(self, dit, vae, steps, alphas_cumprod, stream=None):
+    def __init__(self, dit, vae, steps, alphas_cumprod, stream=None, kv_cache=True):
         from .schedule import ddim_coefficients
         self.dit, self.vae = dit, vae
+        # steps after the first run the generated frame alone against the context's cached K/V
+        self.kv = KVCache(dit, 1) if kv_cache else None
         self.steps = list(steps)
         self.n = len(self.steps)
         P, dev = dit.P, dit.device
@@ -450,7 +479,8 @@ class FramePipeline:
     def enqueue(self):
         d, ws = self.dit, self.ws
         L.call("oasis_ddim_frame", ctypes.byref(d.struct), ctypes.byref(ws.struct),
-               ctypes.byref(self.vae.struct), ctypes.byref(self.vws.struct), L.ptr(self.chunk),
+               ctypes.byref(self.vae.struct), ctypes.byref(self.vws.struct),
+               ctypes.byref(self.kv.struct) if self.kv is not None else None, L.ptr(self.chunk),
                L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
                ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
                L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent), L.ptr(self.vws.frame),
