@@ -520,6 +520,26 @@ int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* bu
                      float* hid, float* cond, float* ada, float* ctx_z, float* v_out, float* latent,
                      float* frame, oasis_stream_t stream);
 
+/* n_frames consecutive generated frames of one stream with the context window rolled on
+ * the device: frame f's context is frame f-1's denoised latent (frame 0: ctx_patches). Per
+ * frame: context patch embed, n_steps DDIM steps (K/V cache as in oasis_ddim_frame), then
+ * bridge + VAE decode: in order on `stream`, or with overlap_decode != 0 on a library-owned
+ * side stream overlapping frame f+1's DiT steps (joined back into `stream` at the end).
+ *   chunks: fp32 [n_frames, P, 64] noise in, denoised latents out;
+ *   t, action: fp32 [n_frames * (1 + n_steps)] and [n_frames * (1 + n_steps), ext_dim_pad]:
+ *        frame f's rows at f*(1 + n_steps), row 0 its context frame, row 1 + i step i;
+ *   tfreq/hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
+ *   frames: fp32 [n_frames, 3, H, W]; other arguments as in oasis_ddim_frame. n_frames <= 64.
+ * The calls into one (w, buf) pair must not overlap. (The interactive loop's context roll,
+ * oasis_inference.py:2296-2306, with play.py:241-531's per-frame DDIM + decode.) */
+int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                       const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                       const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
+                       const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
+                       const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
+                       float* v_out, float* latent, float* frames, int overlap_decode,
+                       oasis_stream_t stream);
+
 /* ---- hipGraph capture of any sequence of the calls above on one stream ---------
  * Replaces ttnn.begin_trace_capture / end_trace_capture / execute_trace / release_trace
  * (oasis_inference.py:2133-2146,2224; play.py:405-411). The stream must not be the

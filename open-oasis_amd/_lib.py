@@ -134,6 +134,8 @@ SIGNATURES = {
                        c_p],
     "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,
                          c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
+    "oasis_video_frames": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_i64, c_p, c_p,
+                           c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p],
     "oasis_dit_precompute_past": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p],
     "oasis_dit_forward_current": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_graph_begin": [c_p],

@@ -56,14 +56,22 @@ struct AttnArgs {
   int64_t o_sf, o_sh, o_si; // out offset = (bh/H)*o_sf + (bh%H)*o_sh + i*o_si + d
 };
 
-// KC keys per LDS chunk (KC = 192 stages a whole 144-token frame in one shot).
-template <int NW, int KC, typename T>
+// KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
+// sequence once, with no barrier in the key loop) and consumed in KC-key chunks.
+// V^T is built from 8x8 blocks: a thread loads 8 key rows x 8 dims, transposes them in
+// registers and writes 8 16-byte LDS rows.
+template <int NW, int KC, int KS, typename T>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                                                         const T* __restrict__ V, T* __restrict__ O, AttnArgs a) {
-  constexpr int VPITCH = KC + 8;
+  static_assert(KS % KC == 0 && KC % 32 == 0 && KS % 8 == 0, "chunking");
+  constexpr int VPITCH = KS + 8;
   constexpr int KT = KC / 16;   // 16-key tiles per chunk
-  constexpr int NL = 4;         // K/V chunk loads in flight per thread
-  __shared__ __attribute__((aligned(16))) bf16 Ks[KC * KPITCH];
+  constexpr int NT = NW * 64;
+  constexpr int KCH = KS * 8;             // 16-byte K chunks per stage
+  constexpr int VBL = KS;                 // 8x8 V blocks per stage (KS/8 key blocks x 8 dim blocks)
+  constexpr int KPER = (KCH + NT - 1) / NT;
+  constexpr int VPER = (VBL + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) bf16 Ks[KS * KPITCH];
   __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int bh = blockIdx.y;
@@ -84,45 +92,54 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kc0 = 0; kc0 < a.Lk; kc0 += KC) {
+  for (int ks0 = 0; ks0 < a.Lk; ks0 += KS) {
     __syncthreads();
-    // K rows and V^T columns of this chunk into LDS, NL loads in flight per thread
-    for (int c0 = tid; c0 < KC * 8; c0 += NW * 64 * NL) {
-      bf16x8 kv[NL], vv[NL];
+    {
+      bf16x8 kv[KPER], vv[VPER][8];
+      // all loads of the stage first (keys past Lk read the last key; masked below)
 #pragma unroll
-      for (int u = 0; u < NL; ++u) {
-        const int c = c0 + u * NW * 64;
-        const int gk = kc0 + (c >> 3), d0 = (c & 7) * 8;
-        if (c < KC * 8 && gk < a.Lk) {
-          kv[u] = load8_bf16<T>(Kb + (int64_t)gk * 64 + d0);
-          vv[u] = load8_bf16<T>(Vb + (int64_t)gk * 64 + d0);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            kv[u][j] = f2bf(0.f);
-            vv[u][j] = f2bf(0.f);
-          }
-        }
+      for (int u = 0; u < KPER; ++u) {
+        const int c = min(tid + u * NT, KCH - 1);
+        kv[u] = load8_bf16<T>(Kb + (int64_t)min(ks0 + (c >> 3), a.Lk - 1) * 64 + (c & 7) * 8);
       }
 #pragma unroll
-      for (int u = 0; u < NL; ++u) {
-        const int c = c0 + u * NW * 64;
-        if (c < KC * 8) {
-          const int key = c >> 3, d0 = (c & 7) * 8;
-          *reinterpret_cast<bf16x8*>(Ks + key * KPITCH + d0) = kv[u];
+      for (int u = 0; u < VPER; ++u) {
+        const int b = min(tid + u * NT, VBL - 1);
+        const int kb = b >> 3, db = b & 7;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VPITCH + key] = vv[u][j];
+        for (int r = 0; r < 8; ++r)
+          vv[u][r] = load8_bf16<T>(Vb + (int64_t)min(ks0 + kb * 8 + r, a.Lk - 1) * 64 + db * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < KPER; ++u) {
+        const int c = tid + u * NT;
+        if (c < KCH) *reinterpret_cast<bf16x8*>(Ks + (c >> 3) * KPITCH + (c & 7) * 8) = kv[u];
+      }
+#pragma unroll
+      for (int u = 0; u < VPER; ++u) {
+        const int b = tid + u * NT;
+        if (b < VBL) {
+          const int kb = b >> 3, db = b & 7;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            bf16x8 t;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) t[r] = vv[u][r][j];
+            *reinterpret_cast<bf16x8*>(Vt + (db * 8 + j) * VPITCH + kb * 8) = t;
+          }
         }
       }
     }
     __syncthreads();
     if (q0 >= a.Lq) continue;
 
+  for (int kc0 = ks0; kc0 < min(ks0 + KS, a.Lk); kc0 += KC) {
+    const int kl = kc0 - ks0;  // chunk offset inside the staged keys
     // S^T for KT key tiles of 16: s[kt][i] = score(key kc0 + kt*16 + 4g + i, query my_q)
     float s[KT][4];
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      const bf16* kp = Ks + (kt * 16 + lr) * KPITCH + g * 8;
+      const bf16* kp = Ks + (kl + kt * 16 + lr) * KPITCH + g * 8;
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
       acc = mfma16(*reinterpret_cast<const bf16x8*>(kp), qf0, acc);
       acc = mfma16(*reinterpret_cast<const bf16x8*>(kp + 32), qf1, acc);
@@ -174,13 +191,14 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
       }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16* vp = Vt + (dt * 16 + lr) * VPITCH + kc * 32 + 4 * g;
+        const bf16* vp = Vt + (dt * 16 + lr) * VPITCH + kl + kc * 32 + 4 * g;
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vp);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vp + 16);
         const bf16x8 va = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[dt] = mfma16(va, pb, o[dt]);
       }
     }
+  }
   }
   if (q0 >= a.Lq || my_q >= a.Lq) return;
   const float inv = 1.0f / lsum;
@@ -197,19 +215,21 @@ template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
-  const bool one_chunk = a.Lk <= 192;  // a whole 144-token frame: stage all keys at once
+  // staging: a whole 144-token frame in one 192-key chunk; up to 576 keys (the VAE) staged
+  // at once (158 KB of LDS) and consumed in 64-key chunks; longer sequences in 576-key stages
+  const bool short_seq = a.Lk <= 192;
   if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
     const dim3 g((unsigned)(a.Lq / 48), (unsigned)n_bh);
-    if (one_chunk)
-      hipLaunchKernelGGL((flash_kernel<3, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
+    if (short_seq)
+      hipLaunchKernelGGL((flash_kernel<3, 192, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
     else
-      hipLaunchKernelGGL((flash_kernel<3, 64, T>), g, dim3(192), 0, s, q, k, v, o, a);
+      hipLaunchKernelGGL((flash_kernel<3, 64, 576, T>), g, dim3(192), 0, s, q, k, v, o, a);
   } else {
     const dim3 g((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh);
-    if (one_chunk)
-      hipLaunchKernelGGL((flash_kernel<4, 192, T>), g, dim3(256), 0, s, q, k, v, o, a);
+    if (short_seq)
+      hipLaunchKernelGGL((flash_kernel<4, 192, 192, T>), g, dim3(256), 0, s, q, k, v, o, a);
     else
-      hipLaunchKernelGGL((flash_kernel<4, 64, T>), g, dim3(256), 0, s, q, k, v, o, a);
+      hipLaunchKernelGGL((flash_kernel<4, 64, 576, T>), g, dim3(256), 0, s, q, k, v, o, a);
   }
   return oasis::check_launch("attention");
 }

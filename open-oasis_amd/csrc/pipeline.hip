@@ -620,24 +620,16 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
                             s);
 }
 
-extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
-                                const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
-                                const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
-                                const float* action, int64_t n_steps, const float* coeffs, float* tfreq, float* hid,
-                                float* cond, float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
-                                oasis_stream_t stream) {
-  OASIS_TRY(check_dit(w));
-  OASIS_TRY(check_dit_buf(buf, w));
-  OASIS_REQUIRE(vw && vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
-                OASIS_ERR_NULL, "ddim_frame: null pointer");
-  OASIS_REQUIRE(n_steps > 0 && n_steps <= 15, OASIS_ERR_ARG, "ddim_frame: n_steps must be in [1, 15]");
-  OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "ddim_frame: missing patch-embed weights");
-  OASIS_REQUIRE(w->t_max >= 2, OASIS_ERR_SHAPE, "ddim_frame: temporal RoPE table needs >= 2 frames");
-  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
-  OASIS_REQUIRE(2 * P <= buf->max_rows, OASIS_ERR_SHAPE, "ddim_frame: workspace too small for T=2");
-  OASIS_REQUIRE((int64_t)vw->grid_h * vw->grid_w == 4 * P && vw->latent_dim >= C, OASIS_ERR_SHAPE,
-                "ddim_frame: VAE grid must be the 2x-upsampled DiT grid");
-  const int64_t NA = ada_width(w), R = 1 + n_steps;
+namespace {
+
+// The n_steps DDIM steps of one generated frame whose context is already embedded in
+// ctx_z; ada holds the frame's conditioning rows (0 context, 1 + i step i). With a K/V
+// cache, step 0 runs at T=2 storing the context's temporal K/V and later steps run the
+// generated frame alone at T=1. chunk is updated in place.
+int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, const oasis_kv_cache_t* kv,
+                float* chunk, const float* ctx_z, const float* ada, int64_t n_steps, const float* coeffs,
+                float* v_out, SideStream* ss, oasis_stream_t stream) {
+  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
   hipStream_t s = (hipStream_t)stream;
   KvPass save, use;
   if (kv) {
@@ -645,12 +637,6 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
     use = save;
     use.mode = KV_USE_T1;
   }
-  // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
-  // covers all rows (with the overlap option it streams on the side stream during step 0)
-  OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
-  SideStream* ss = nullptr;
-  OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
-  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
   for (int64_t i = 0; i < n_steps; ++i) {
     const bool t1 = kv && i > 0;  // K/V cache filled by step 0: the current frame alone
     const float* c = coeffs + 6 * i;
@@ -676,8 +662,92 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
     OASIS_TRY(oasis_ddim_update(chunk, v_out + P * w->patch_dim, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5],
                                 stream));
   }
-  OASIS_TRY(oasis_bridge(chunk, latent, w->grid_h, w->grid_w, C, vw->latent_dim, 1.0f / 0.07843137255f, stream));
+  return OASIS_OK;
+}
+
+int frame_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, const oasis_vae_weights_t* vw,
+               int64_t n_steps) {
+  OASIS_TRY(check_dit(w));
+  OASIS_TRY(check_dit_buf(buf, w));
+  OASIS_REQUIRE(vw, OASIS_ERR_NULL, "ddim_frame: null VAE weights");
+  OASIS_REQUIRE(n_steps > 0 && n_steps <= 15, OASIS_ERR_ARG, "ddim_frame: n_steps must be in [1, 15]");
+  OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "ddim_frame: missing patch-embed weights");
+  OASIS_REQUIRE(w->t_max >= 2, OASIS_ERR_SHAPE, "ddim_frame: temporal RoPE table needs >= 2 frames");
+  const int64_t P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
+  OASIS_REQUIRE(2 * P <= buf->max_rows, OASIS_ERR_SHAPE, "ddim_frame: workspace too small for T=2");
+  OASIS_REQUIRE((int64_t)vw->grid_h * vw->grid_w == 4 * P && vw->latent_dim >= C, OASIS_ERR_SHAPE,
+                "ddim_frame: VAE grid must be the 2x-upsampled DiT grid");
+  return OASIS_OK;
+}
+
+constexpr float kInvScaling = 1.0f / 0.07843137255f;  // 1 / scaling_factor (oasis_inference.py:107)
+
+}  // namespace
+
+extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                                const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                                const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
+                                const float* action, int64_t n_steps, const float* coeffs, float* tfreq, float* hid,
+                                float* cond, float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
+                                oasis_stream_t stream) {
+  OASIS_TRY(frame_args(w, buf, vw, n_steps));
+  OASIS_REQUIRE(vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
+                OASIS_ERR_NULL, "ddim_frame: null pointer");
+  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
+  // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
+  // covers all rows (with the overlap option it streams on the side stream during step 0)
+  OASIS_TRY(cond_mlp(w, t, action, 1 + n_steps, tfreq, hid, cond, stream));
+  SideStream* ss = nullptr;
+  OASIS_TRY(fork_adaln(w, cond, 1 + n_steps, ada, stream, &ss));
+  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
+  OASIS_TRY(frame_steps(w, buf, kv, chunk, ctx_z, ada, n_steps, coeffs, v_out, ss, stream));
+  OASIS_TRY(oasis_bridge(chunk, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
   return oasis_vae_decode(vw, vbuf, latent, frame, stream);
+}
+
+extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
+                                  const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                                  const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
+                                  const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
+                                  const float* coeffs, float* tfreq, float* hid, float* cond, float* ada,
+                                  float* ctx_z, float* v_out, float* latent, float* frames, int overlap_decode,
+                                  oasis_stream_t stream) {
+  OASIS_TRY(frame_args(w, buf, vw, n_steps));
+  OASIS_REQUIRE(vbuf && chunks && ctx_patches && t && action && coeffs && tfreq && hid && cond && ada && ctx_z &&
+                    v_out && latent && frames,
+                OASIS_ERR_NULL, "video_frames: null pointer");
+  OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_frames: n_frames must be in [1, %d]",
+                OASIS_MAX_SUB);
+  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4, NA = ada_width(w);
+  const int64_t R = 1 + n_steps, fsz = (int64_t)w->patch_dim * P;
+  const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
+  hipStream_t s = (hipStream_t)stream;
+  // every frame's conditioning rows at once: frame f's rows at f*R (context, then step i)
+  OASIS_TRY(cond_mlp(w, t, action, n_frames * R, tfreq, hid, cond, stream));
+  OASIS_TRY(oasis_gemv_bf16(cond, D, n_frames * R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE,
+                            0, stream));
+  SideStream* ss = nullptr;
+  if (overlap_decode) OASIS_TRY(side_stream(&ss));
+  for (int64_t f = 0; f < n_frames; ++f) {
+    // context = the previous frame's denoised latent (the rolled context window)
+    const float* ctx = f == 0 ? ctx_patches : chunks + (f - 1) * fsz;
+    OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
+    OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out, nullptr,
+                          stream));
+    // bridge + VAE of frame f, in order or on the side stream overlapping frame f + 1's DiT
+    hipStream_t ds = s;
+    if (ss) {
+      hipEvent_t ev = ss->ev[f % (OASIS_MAX_SUB + 1)];
+      if (hipEventRecord(ev, s) != hipSuccess || hipStreamWaitEvent(ss->s, ev, 0) != hipSuccess)
+        return oasis::check_launch("video_frames fork");
+      ds = ss->s;
+    }
+    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, ds));
+    OASIS_TRY(oasis_vae_decode(vw, vbuf, latent, frames + f * frame_elems, ds));
+  }
+  if (ss && (hipEventRecord(ss->fork, ss->s) != hipSuccess || hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess))
+    return oasis::check_launch("video_frames join");
+  return OASIS_OK;
 }
 
 extern "C" int oasis_graph_begin(oasis_stream_t stream) {

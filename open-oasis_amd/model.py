@@ -500,5 +500,72 @@ class FramePipeline:
         return self.vws.frame
 
 
+class VideoPipeline:
+    """n_frames consecutive frames of one stream in one call (oasis_video_frames): frame f's
+    context is frame f-1's denoised latent, rolled on the device (the interactive loop's
+    context window, oasis_inference.py:2296-2306). overlap_decode=True runs frame f's VAE
+    decode on a side stream during frame f+1's DDIM steps (measured slower on MI355X: the
+    latency-bound DiT kernels lose more to the shared CUs than the overlap hides).
+    Inputs: self.chunks [n_frames, P, 64] noise, self.ctx_patches [P, 64] the first context,
+    conditioning rows built by set_inputs (context t and action, then each step's t with
+    the frame's action; the context of frame f > 0 carries frame f-1's action)."""
+
+    def __init__(self, dit, vae, steps, alphas_cumprod, n_frames, stream=None, kv_cache=True, overlap_decode=False):
+        from .schedule import ddim_coefficients
+        self.dit, self.vae, self.n_frames = dit, vae, n_frames
+        self.overlap_decode = overlap_decode
+        self.steps = list(steps)
+        self.n = len(self.steps)
+        P, dev = dit.P, dit.device
+        R = n_frames * (1 + self.n)
+        self.ws = dit.workspace(2 * P, max_cond=max(16, R))
+        self.vws = vae.workspace()
+        self.kv = KVCache(dit, 1) if kv_cache else None
+        self.chunks = torch.zeros(n_frames, P, dit.patch_dim, device=dev)
+        self.ctx_patches = torch.zeros(P, dit.patch_dim, device=dev)
+        self.ctx_z = torch.zeros(P, dit.d, device=dev)
+        self.frames = torch.zeros(n_frames, *vae.frame_shape, device=dev)
+        self.coeffs = (ctypes.c_float * (6 * self.n))(*ddim_coefficients(alphas_cumprod, self.steps))
+        self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
+        self.graph = None
+
+    def set_inputs(self, noise_patches, ctx_patches, ctx_t, ctx_action, actions):
+        """noise_patches [n_frames, P, 64], ctx_patches [P, 64], actions [n_frames, ext_dim]."""
+        F, n, e = self.n_frames, self.n, self.dit.ext_dim
+        self.chunks.copy_(noise_patches.reshape(self.chunks.shape))
+        self.ctx_patches.copy_(ctx_patches)
+        t = torch.tensor(([float(ctx_t)] + [float(ts) for ts, _ in self.steps]) * F)
+        act = torch.zeros(F, 1 + n, self.dit.ext_pad)
+        acts = actions.detach().float().cpu().reshape(F, e)
+        act[0, 0, :e] = ctx_action.detach().float().cpu()
+        act[1:, 0, :e] = acts[:-1]
+        act[:, 1:, :e] = acts[:, None, :]
+        self.ws.t[:F * (1 + n)].copy_(t)
+        self.ws.act[:F * (1 + n)].copy_(act.reshape(F * (1 + n), -1))
+        torch.cuda.synchronize(self.dit.device)
+
+    def enqueue(self):
+        d, ws = self.dit, self.ws
+        L.call("oasis_video_frames", ctypes.byref(d.struct), ctypes.byref(ws.struct), ctypes.byref(self.vae.struct),
+               ctypes.byref(self.vws.struct), ctypes.byref(self.kv.struct) if self.kv is not None else None,
+               self.n_frames, L.ptr(self.chunks), L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
+               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
+               L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent), L.ptr(self.frames),
+               int(self.overlap_decode), L.stream_handle(self.stream))
+
+    def capture(self):
+        self.graph = Graph(self.enqueue, self.stream)
+        return self.graph
+
+    def run(self):
+        """Enqueue the frames on self.stream; the caller's current stream waits for them."""
+        if self.graph is not None:
+            self.graph.launch()
+        else:
+            self.enqueue()
+        torch.cuda.current_stream(self.dit.device).wait_stream(self.stream)
+        return self.frames
+
+
 def attention_scale(head_dim=HEAD_DIM):
     return 1.0 / math.sqrt(head_dim)
