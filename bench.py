@@ -249,7 +249,8 @@ def main():
         "step_weight_bytes": step_bytes,
         "step_hbm_floor_ms": round(step_floor_ms, 4),
         "step_roofline_frac": round(step_floor_ms / ms_step, 4),
-        "roofline": {"kernel": "gemm_bf16_kernel, FC1 projection + bias + tanh-GELU (M=288, N=4096, K=1024), "
+        "roofline": {"kernel": "gemm_lds_kernel<96,64> (direct-to-LDS bf16 GEMM), FC1 projection + bias + tanh-GELU "
+                               "(M=288, N=4096, K=1024), "
                                "the largest of the step's 128 GEMM launches",
                      "bound": "mfma", "achieved": round(fc1_tflops, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fc1_tflops / BF16_PEAK_TFLOPS, 4),

@@ -199,6 +199,157 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
   }
 }
 
+// Same product with the global -> LDS copies done by the memory pipeline itself
+// (global_load_lds_dwordx4: each lane's 16 bytes land at LDS base + 16 * lane), so tiles
+// take no VGPRs or LDS-store instructions in flight and STAGES K tiles can be queued per
+// workgroup. LDS rows are unpadded 128-byte rows of 16-byte chunks stored XOR-swizzled
+// (chunk c of row r at slot c ^ ((r >> 1) & 7)), which keeps the 16-row MFMA fragment
+// reads conflict-free. One wave instruction fills 8 rows; the A rows come first.
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds is
+// wave-uniform).
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, reinterpret_cast<uint32_t*>(lds), 16, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ A, int64_t lda,
+                                                       const bf16* __restrict__ B, int64_t ldb, int M, int N,
+                                                       int K, int splits, Epi e) {
+  static_assert(WM * WN == 4, "4 waves");
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
+  constexpr int ROWB = 128;                     // bytes per LDS row: 64 bf16 of K
+  constexpr int NBLK = (BM + BN) / 8;           // 1 KB blocks (8 rows) per stage
+  static_assert(BM % 8 == 0 && BN % 8 == 0 && NBLK % 4 == 0, "blocks split evenly over 4 waves");
+  constexpr int LPW = NBLK / 4;                 // loads per wave per stage
+  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int RING = STAGES * STAGE_BYTES;
+  constexpr int C_PITCH = BN + 4;
+  constexpr int C_BYTES = BM * C_PITCH * 4;
+  constexpr int SMEM = RING > C_BYTES ? RING : C_BYTES;
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
+  const int mt = pid % Mt;
+  const int rest = pid / Mt;
+  const int split = rest % splits, nt = rest / splits;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = K / 64 / splits;
+  const int kb = split * nk * 64;
+
+  // this lane's source in each of its LPW blocks: row r = 8 * blk + lane / 8 of the A|B stack,
+  // slot lane % 8 holds K chunk (lane % 8) ^ ((r >> 1) & 7)
+  const bf16* src[LPW];
+  int dst[LPW];
+#pragma unroll
+  for (int u = 0; u < LPW; ++u) {
+    const int blk = wave * LPW + u;
+    const int r = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < BM)
+      src[u] = A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 8;
+    else
+      src[u] = B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 8;
+    dst[u] = blk * 1024;
+  }
+  auto issue = [&](int kt, int buf) {
+    char* base = smem + buf * STAGE_BYTES;
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * 64, base + dst[u]);
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, g = lane >> 4;
+  auto compute = [&](int buf) {
+    const char* base = smem + buf * STAGE_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + g;  // 16-byte K chunk of this lane's 8 values
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 16 + lr;
+        af[i] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = BM + wn * TN + j * 16 + lr;
+        bfr[j] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  // vmcnt <= (STAGES - 2) * LPW: every load of the oldest in-flight stage has landed
+  constexpr int VM = (STAGES - 2) * LPW;
+  constexpr int WAIT = (VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(min(s, nk - 1), s);
+  for (int k = 0; k < nk; ++k) {
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    __builtin_amdgcn_s_barrier();
+    issue(min(k + STAGES - 1, nk - 1), (k + STAGES - 1) % STAGES);  // into the buffer read at k - 1
+    compute(k % STAGES);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the clamped tail loads must land before the ring is reused
+  __syncthreads();
+
+  float* Cs = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        Cs[(wm * TM + i * 16 + g * 4 + r) * C_PITCH + wn * TN + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+
+  constexpr int UNITS = BM * (BN / 8);
+  for (int u = tid; u < UNITS; u += 256) {
+    const int r = u / (BN / 8), c8 = (u % (BN / 8)) * 8;
+    const int gm = m0 + r, gn = n0 + c8;
+    if (gm >= M || gn >= N) continue;
+    float v[8];
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = c0[j];
+      v[j + 4] = c1[j];
+    }
+    if (e.kind == OASIS_EPI_PARTIAL_F32) {
+      float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+      *reinterpret_cast<f32x4*>(d) = c0;
+      *reinterpret_cast<f32x4*>(d + 4) = c1;
+    } else {
+      epilogue8(e, gm, gn, v);
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+hipError_t launch_lds(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
+                      const Epi& e, hipStream_t s) {
+  if ((K / splits) % 64 != 0) return hipErrorInvalidConfiguration;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_lds_kernel<BM, BN, WM, WN, STAGES>), dim3(Mt * Nt * splits), dim3(256), 0, s, A, lda, B,
+                     ldb, M, N, K, splits, e);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, bool BKN = false, int BKT = 64>
 hipError_t launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K,
                       int splits, const Epi& e, hipStream_t s) {
@@ -242,6 +393,20 @@ const TileCfg kTiles[] = {
     {64, 64, 2, 128, launch_cfg<64, 64, 2, 2, 2, false, 128>, launch_cfg<64, 64, 2, 2, 1>},     // 20
     {32, 128, 2, 128, launch_cfg<32, 128, 1, 4, 2, false, 128>, launch_cfg<32, 128, 1, 4, 1>},  // 21
     {32, 64, 4, 128, launch_cfg<32, 64, 1, 4, 4, false, 128>, launch_cfg<32, 64, 1, 4, 1>},     // 22
+    // direct-to-LDS K pipeline (any number of K tiles)
+    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 4>, launch_lds<32, 64, 1, 4, 4>},      // 23
+    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 4>, launch_lds<96, 64, 2, 2, 4>},      // 24
+    {64, 64, 1, 64, launch_lds<64, 64, 2, 2, 4>, launch_lds<64, 64, 2, 2, 4>},      // 25
+    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 6>, launch_lds<96, 64, 2, 2, 6>},      // 26
+    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 8>, launch_lds<32, 64, 1, 4, 8>},      // 27
+    {32, 128, 1, 64, launch_lds<32, 128, 1, 4, 4>, launch_lds<32, 128, 1, 4, 4>},   // 28
+    {64, 128, 1, 64, launch_lds<64, 128, 2, 2, 4>, launch_lds<64, 128, 2, 2, 4>},   // 29
+    {96, 128, 1, 64, launch_lds<96, 128, 2, 2, 3>, launch_lds<96, 128, 2, 2, 3>},   // 30
+    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 6>, launch_lds<32, 64, 1, 4, 6>},      // 31
+    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 3>, launch_lds<32, 64, 1, 4, 3>},      // 32
+    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 3>, launch_lds<96, 64, 2, 2, 3>},      // 33
+    {64, 64, 1, 64, launch_lds<64, 64, 2, 2, 6>, launch_lds<64, 64, 2, 2, 6>},      // 34
+    {96, 32, 1, 64, launch_lds<96, 32, 2, 2, 4>, launch_lds<96, 32, 2, 2, 4>},      // 35
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -252,17 +417,16 @@ namespace oasis {
 // Tile choice per shape. M is small (288 / 576 tokens) and the weights are streamed
 // once, so the tiles trade L2 re-reads of A and B against enough workgroups to keep
 // all 256 CUs issuing HBM loads.
-// Default tile per shape, from sweeps of the DiT / VAE projections on MI355X (M = 288 and
-// 576 tokens, weights streamed from HBM): 32 x 64 tiles with a 2-deep ring for the QKV-
-// and O-sized products, 96 x 64 tiles with a 4-deep ring for the 4096-wide MLP products;
-// 96 x 128 tiles from 2048 tokens up.
+// Default tile per shape, from in-situ sweeps of the captured DiT step and frame on MI355X:
+// the direct-to-LDS pipeline with 96 x 64 tiles (4 stages) for the MLP products, the split-K
+// slices and everything at the VAE's 576 tokens, 32 x 64 tiles (3 stages) for the QKV
+// product of the DiT (144 or 288 tokens); 96 x 128 register-ring tiles from 2048 tokens up.
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
-  if (M >= 2048) return 13;  // batched streams (thousands of tokens): 96 x 128 tiles
-  bool wide = false;
-  if (kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF) wide = N >= 2048;
-  if (kind == OASIS_EPI_PARTIAL_F32) wide = Kslice >= 1024;
-  if (wide && M >= 192) return 10;
-  return 7;
+  (void)N;
+  (void)Kslice;
+  if (M >= 2048) return 13;
+  const bool big = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF || kind == OASIS_EPI_PARTIAL_F32;
+  return big || M >= 512 ? 24 : 32;
 }
 
 int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,

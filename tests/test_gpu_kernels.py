@@ -401,7 +401,7 @@ def test_rope_layout_surface():
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(23)))
+@pytest.mark.parametrize("tile", list(range(36)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -412,6 +412,27 @@ def test_gemm_tile_configs(tile):
     L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(e), tile, 1, stream())
     sync()
     assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
+
+
+@pytest.mark.parametrize("tile", list(range(23, 36)))
+def test_gemm_direct_lds_ragged(tile):
+    """The direct-to-LDS configurations on a ragged shape: K = 5 tiles (not a multiple of the
+    stage count), M and N not multiples of the tile, GELU epilogue and split-K slices."""
+    M, N, K = 300, 520, 320
+    g = _gen(60 + tile)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    out = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+    e = _epi(kind=L.EPI_GELU_TANH, bias=dev(bias), out_bf16=out, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    part = torch.zeros(5, M, N, device="cuda")
+    ep = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(ep), tile, 5, stream())
+    sync()
+    ref = A.float() @ B.float().t()
+    assert_close(out, torch.nn.functional.gelu(ref + bias, approximate="tanh"), 0.99999, 1e-2, "tile %d gelu" % tile)
+    assert_close(part.sum(0), ref, 0.999999, 1e-4, "tile %d split-K x5" % tile)
 
 
 @pytest.mark.parametrize("splits", [1, 2, 4, 8])
