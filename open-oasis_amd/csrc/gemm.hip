@@ -407,6 +407,9 @@ const TileCfg kTiles[] = {
     {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 3>, launch_lds<96, 64, 2, 2, 3>},      // 33
     {64, 64, 1, 64, launch_lds<64, 64, 2, 2, 6>, launch_lds<64, 64, 2, 2, 6>},      // 34
     {96, 32, 1, 64, launch_lds<96, 32, 2, 2, 4>, launch_lds<96, 32, 2, 2, 4>},      // 35
+    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 3>, launch_lds<128, 128, 2, 2, 3>},  // 36
+    {128, 64, 1, 64, launch_lds<128, 64, 2, 2, 4>, launch_lds<128, 64, 2, 2, 4>},    // 37
+    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 4>, launch_lds<128, 128, 2, 2, 4>},  // 38
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 

@@ -80,7 +80,7 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       break;
     }
     case OASIS_EPI_GATED_RES: {
-      const int64_t f = m / e.rows_per_frame;
+      const int64_t f = (uint32_t)m / (uint32_t)e.rows_per_frame;
       const float* g = e.gate + f * e.gate_fstride + n0;
       float* d = e.out_f32 + m * e.ld_out + n0;
       f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
@@ -111,20 +111,26 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       const int which = n0 / D;          // 0 q, 1 k, 2 v
       const int nn = n0 - which * D;
       const int h = nn >> 6, d0 = nn & 63;
-      const int64_t f = m / e.rows_per_frame, p = m - f * e.rows_per_frame;
-      const int64_t b = f / e.frames_per_stream, t = f - b * e.frames_per_stream;
+      // 32-bit index math (M, rows and frames are < 2^31; checked on the host)
+      const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
+      const uint32_t f = (uint32_t)m / rpf, p = (uint32_t)m - f * rpf;
+      const uint32_t b = f / fps, t = f - b * fps;
       if (which < 2) {
-        const int64_t pos = e.rope_by_frame ? t : p;
-        const float* c = e.rope_cos + pos * 64 + d0;
-        const float* s = e.rope_sinp + pos * 64 + d0;
+        const uint32_t pos = e.rope_by_frame ? t : p;
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(e.rope_cos + pos * 64 + d0);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(e.rope_cos + pos * 64 + d0 + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(e.rope_sinp + pos * 64 + d0);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(e.rope_sinp + pos * 64 + d0 + 4);
+        const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+        const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
         float r[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * s[j];
+        for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * sn[j];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = r[j];
       }
       bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
-      store8_bf16(base + b * e.s_b + t * e.s_t + p * e.s_p + h * e.s_h + d0, v);
+      store8_bf16(base + (int64_t)b * e.s_b + (int64_t)t * e.s_t + (int64_t)p * e.s_p + (int64_t)h * e.s_h + d0, v);
       break;
     }
     case OASIS_EPI_UNPATCHIFY: {
@@ -226,6 +232,8 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
                                    "(multiple of 8), ld_scale >= N/32");
       break;
     case OASIS_EPI_QKV_ROPE:
+      OASIS_REQUIRE(e.rows_per_frame < (1ll << 31) && e.frames_per_stream < (1ll << 31), OASIS_ERR_SHAPE,
+                    "gemm: rows_per_frame / frames_per_stream too large");
       OASIS_REQUIRE(e.q && e.k && e.v && e.rope_cos && e.rope_sinp, OASIS_ERR_NULL,
                     "gemm: QKV_ROPE needs q/k/v and rope tables");
       OASIS_REQUIRE(e.n_heads > 0 && N == 3LL * e.n_heads * 64, OASIS_ERR_SHAPE,
