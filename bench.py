@@ -41,7 +41,7 @@ def _event_ms(fn, stream, n):
 # HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
 # scaled by what the same counter reads for a plain device copy of known size.
-TRAFFIC = {"fc1": 15625025, "gemv": 409840236}
+TRAFFIC = {"fc1": 15625025, "gemv": 409858666}
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100):
