@@ -221,8 +221,10 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
   static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
   constexpr int ROWB = 128;                     // bytes per LDS row: 64 bf16 of K
   constexpr int NBLK = (BM + BN) / 8;           // 1 KB blocks (8 rows) per stage
-  static_assert(BM % 8 == 0 && BN % 8 == 0 && NBLK % 4 == 0, "blocks split evenly over 4 waves");
-  constexpr int LPW = NBLK / 4;                 // loads per wave per stage
+  static_assert(BM % 8 == 0 && BN % 8 == 0, "whole 8-row blocks");
+  // loads per wave per stage; when NBLK % 4 != 0 the last wave re-loads the last block (same
+  // bytes to the same LDS slots), so every wave waits on the same vmcnt
+  constexpr int LPW = (NBLK + 3) / 4;
   constexpr int STAGE_BYTES = (BM + BN) * ROWB;
   constexpr int RING = STAGES * STAGE_BYTES;
   constexpr int C_PITCH = BN + 4;
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
   int dst[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
-    const int blk = wave * LPW + u;
+    const int blk = min(wave * LPW + u, NBLK - 1);
     const int r = blk * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     if (r < BM)
@@ -410,6 +412,13 @@ const TileCfg kTiles[] = {
     {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 3>, launch_lds<128, 128, 2, 2, 3>},  // 36
     {128, 64, 1, 64, launch_lds<128, 64, 2, 2, 4>, launch_lds<128, 64, 2, 2, 4>},    // 37
     {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 4>, launch_lds<128, 128, 2, 2, 4>},  // 38
+    {48, 64, 1, 64, launch_lds<48, 64, 1, 4, 4>, launch_lds<48, 64, 1, 4, 4>},      // 39
+    {144, 64, 1, 64, launch_lds<144, 64, 1, 4, 3>, launch_lds<144, 64, 1, 4, 3>},   // 40
+    {48, 128, 1, 64, launch_lds<48, 128, 1, 4, 4>, launch_lds<48, 128, 1, 4, 4>},   // 41
+    {16, 64, 1, 64, launch_lds<16, 64, 1, 4, 4>, launch_lds<16, 64, 1, 4, 4>},      // 42
+    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 2>, launch_lds<128, 128, 2, 2, 2>},  // 43
+    {128, 128, 2, 64, launch_cfg<128, 128, 2, 2, 2>, launch_cfg<128, 128, 2, 2, 1>},  // 44
+    {256, 128, 2, 64, launch_cfg<256, 128, 2, 2, 2>, launch_cfg<256, 128, 2, 2, 1>},  // 45
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 

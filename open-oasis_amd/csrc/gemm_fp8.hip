@@ -25,7 +25,11 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BK8 = 128;          // K per MFMA step and per pipeline step
-constexpr int P8 = BK8 + 16;      // LDS row pitch in bytes (16 B pad)
+constexpr int P8 = BK8;           // LDS row pitch in bytes: unpadded, 16-byte chunks XOR-swizzled
+
+// byte offset of (row r, byte column c) in a swizzled LDS tile: 16-byte chunk c/16 of row r
+// is stored at slot (c/16) ^ ((r >> 1) & 7), which keeps 16-row fragment reads conflict-free
+__device__ __forceinline__ int swz(int r, int c) { return r * P8 + ((((c >> 4) ^ (r >> 1)) & 7) << 4) + (c & 15); }
 constexpr int kScaleOne = 127;    // e8m0 encoding of 1.0
 
 // Quantizes 8 consecutive bf16 of one row whose 32-wide K block is shared with the
@@ -71,8 +75,8 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
   constexpr int C_BYTES = BM * C_PITCH * 4;
   constexpr int SMEM = RING > C_BYTES ? RING : C_BYTES;
   __shared__ __attribute__((aligned(16))) char smem[SMEM];
-  uint8_t* As = reinterpret_cast<uint8_t*>(smem);   // [2][BM][P8]
-  uint8_t* Bs = As + 2 * A_BYTES;                   // [2][BN][P8]
+  uint8_t* As = reinterpret_cast<uint8_t*>(smem);   // [2][BM][P8] swizzled
+  uint8_t* Bs = As + 2 * A_BYTES;                   // [2][BN][P8] swizzled
   uint8_t* Ss = Bs + 2 * B_BYTES;                   // [2][BM][4] e8m0 scales of A
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
     const int c = tid + i * 256;
     const int row = c / (BK8 / A_EPC), col = (c % (BK8 / A_EPC)) * A_EPC;
     a_src[i] = static_cast<const char*>(Av) + ((int64_t)min(m0 + row, M - 1) * lda + kb + col) * (AQ ? 1 : 2);
-    a_dst[i] = row * P8 + col;
+    a_dst[i] = swz(row, col);
     s_dst[i] = (col & 31) == 0 ? row * 4 + col / 32 : -1;
   }
   // AQ: thread t < BM copies row t's 4 block scales of each K tile (one 32-bit word)
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
     const int c = tid + i * 256;
     const int row = c / (BK8 / 16), col = (c % (BK8 / 16)) * 16;
     b_src[i] = B + (int64_t)min(n0 + row, N - 1) * ldb + kb + col;
-    b_dst[i] = row * P8 + col;
+    b_dst[i] = swz(row, col);
   }
 
   i32x4 ra[STAGES][A_PER], rb[STAGES][B_PER];
@@ -146,22 +150,24 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
 
   const int lr = lane & 15, g = lane >> 4;
   auto compute = [&](int buf) {
-    const uint8_t* as = As + buf * A_BYTES + (wm * TM + lr) * P8 + 16 * g;
-    const uint8_t* bs = Bs + buf * B_BYTES + (wn * TN + lr) * P8 + 16 * g;
+    const uint8_t* as = As + buf * A_BYTES;
+    const uint8_t* bs = Bs + buf * B_BYTES;
     const uint8_t* ss = Ss + buf * S_BYTES + (wm * TM + lr) * 4 + g;
     i32x8 af[FM], bfr[FN];
     int sa[FM];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const i32x4 x0 = *reinterpret_cast<const i32x4*>(as + i * 16 * P8);
-      const i32x4 x1 = *reinterpret_cast<const i32x4*>(as + i * 16 * P8 + 64);
+      const int r = wm * TM + i * 16 + lr;
+      const i32x4 x0 = *reinterpret_cast<const i32x4*>(as + swz(r, 16 * g));
+      const i32x4 x1 = *reinterpret_cast<const i32x4*>(as + swz(r, 64 + 16 * g));
       af[i] = i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
       sa[i] = ss[i * 16 * 4];
     }
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const i32x4 x0 = *reinterpret_cast<const i32x4*>(bs + j * 16 * P8);
-      const i32x4 x1 = *reinterpret_cast<const i32x4*>(bs + j * 16 * P8 + 64);
+      const int r = wn * TN + j * 16 + lr;
+      const i32x4 x0 = *reinterpret_cast<const i32x4*>(bs + swz(r, 16 * g));
+      const i32x4 x1 = *reinterpret_cast<const i32x4*>(bs + swz(r, 64 + 16 * g));
       bfr[j] = i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
     }
 #pragma unroll

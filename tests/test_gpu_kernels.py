@@ -401,7 +401,7 @@ def test_rope_layout_surface():
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(36)))
+@pytest.mark.parametrize("tile", list(range(46)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -414,7 +414,7 @@ def test_gemm_tile_configs(tile):
     assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
 
 
-@pytest.mark.parametrize("tile", list(range(23, 36)))
+@pytest.mark.parametrize("tile", list(range(23, 43)))
 def test_gemm_direct_lds_ragged(tile):
     """The direct-to-LDS configurations on a ragged shape: K = 5 tiles (not a multiple of the
     stage count), M and N not multiples of the tile, GELU epilogue and split-K slices."""
