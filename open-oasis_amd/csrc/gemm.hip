@@ -342,6 +342,164 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
   }
 }
 
+// Large-token variant (2048+ tokens: many frames or streams per pass): 8 waves (2 per SIMD)
+// share one tall tile such as 288 x 256 (two 144-token frames by 256 output channels), so
+// each K tile of 64 brings 4.7 MFLOP per 68 KB staged, and a 4608-token projection is one
+// round of 256 workgroups. Same direct-to-LDS ring and swizzle as gemm_lds_kernel (two
+// stages fit in LDS). Tiles are ordered (split, groups of GN n tiles, m, n within group) so
+// an XCD's consecutive ids cover a compact block of tiles: each XCD's L2 then holds a few
+// rows of A and a few weight slices instead of every row of A.
+// The epilogue stages 16 rows of a wave's tile at a time in LDS owned by that wave alone.
+__device__ __forceinline__ void grouped_tile(int pid, int Mt, int Nt, int GN, int& split, int& mt, int& nt) {
+  const int per = Mt * Nt;
+  split = pid / per;
+  const int t = pid - split * per;
+  const int in_group = GN * Mt;
+  const int grp = t / in_group, first = grp * GN;
+  const int gsz = min(Nt - first, GN);
+  const int r = t - grp * in_group;
+  mt = r / gsz;
+  nt = first + (r - mt * gsz);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __restrict__ A, int64_t lda,
+                                                               const bf16* __restrict__ B, int64_t ldb, int M,
+                                                               int N, int K, int splits, Epi e) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
+  constexpr int ROWB = 128;
+  constexpr int NBLK = (BM + BN) / 8;
+  static_assert(BM % 8 == 0 && BN % 8 == 0, "whole 8-row blocks");
+  constexpr int LPW = (NBLK + NW - 1) / NW;
+  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int RING = STAGES * STAGE_BYTES;
+  constexpr int EP = TN + 4;  // fp32 pitch of a wave's 16-row staging block
+  constexpr int EPI_BYTES = NW * 16 * EP * 4;
+  constexpr int SMEM = RING > EPI_BYTES ? RING : EPI_BYTES;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW <= 63, "vmcnt range");
+  constexpr int GN = 8;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  int split, mt, nt;
+  grouped_tile(xcd_remap(blockIdx.x, Mt * Nt * splits), Mt, Nt, GN, split, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = K / 64 / splits;
+  const int kb = split * nk * 64;
+
+  const bf16* src[LPW];
+  int dst[LPW];
+#pragma unroll
+  for (int u = 0; u < LPW; ++u) {
+    const int blk = min(wave * LPW + u, NBLK - 1);
+    const int r = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < BM)
+      src[u] = A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 8;
+    else
+      src[u] = B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 8;
+    dst[u] = blk * 1024;
+  }
+  auto issue = [&](int kt, int buf) {
+    char* base = smem + buf * STAGE_BYTES;
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * 64, base + dst[u]);
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, g = lane >> 4;
+  auto compute = [&](int buf) {
+    const char* base = smem + buf * STAGE_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + g;
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 16 + lr;
+        af[i] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = BM + wn * TN + j * 16 + lr;
+        bfr[j] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  constexpr int VM = (STAGES - 2) * LPW;
+  constexpr int WAIT = (VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(min(s, nk - 1), s);
+  for (int k = 0; k < nk; ++k) {
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    __builtin_amdgcn_s_barrier();
+    issue(min(k + STAGES - 1, nk - 1), (k + STAGES - 1) % STAGES);
+    compute(k % STAGES);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
+  // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
+  float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
+  constexpr int UPR = TN / 8;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[(g * 4 + r) * EP + j * 16 + lr] = acc[i][j][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int u = lane; u < 16 * UPR; u += 64) {
+      const int r = u / UPR, c8 = (u - r * UPR) * 8;
+      const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
+      if (gm < M && gn < N) {
+        if (e.kind == OASIS_EPI_PARTIAL_F32) {
+          float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+          *reinterpret_cast<f32x4*>(d) = c0;
+          *reinterpret_cast<f32x4*>(d + 4) = c1;
+        } else {
+          float v[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+          epilogue8(e, gm, gn, v);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
+                      const Epi& e, hipStream_t s) {
+  if ((K / splits) % 64 != 0) return hipErrorInvalidConfiguration;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s, A,
+                     lda, B, ldb, M, N, K, splits, e);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_lds(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
                       const Epi& e, hipStream_t s) {
@@ -369,6 +527,7 @@ struct TileCfg {
   int bm, bn, stages, bk;
   launch_fn fn;         // STAGES-deep prefetch ring (K tiles per split divisible by stages)
   launch_fn fn_single;  // one tile in flight, any K
+  int no_fp8_epi = 0;   // 1: its epilogue lanes do not cover aligned 32-column blocks
 };
 const TileCfg kTiles[] = {
     {32, 64, 4, 64, launch_cfg<32, 64, 1, 4, 4>, launch_cfg<32, 64, 1, 4, 1>},      // 0
@@ -419,6 +578,12 @@ const TileCfg kTiles[] = {
     {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 2>, launch_lds<128, 128, 2, 2, 2>},  // 43
     {128, 128, 2, 64, launch_cfg<128, 128, 2, 2, 2>, launch_cfg<128, 128, 2, 2, 1>},  // 44
     {256, 128, 2, 64, launch_cfg<256, 128, 2, 2, 2>, launch_cfg<256, 128, 2, 2, 1>},  // 45
+    // 8-wave large-token tiles (any number of K tiles)
+    {288, 256, 1, 64, launch_big<288, 256, 2, 4, 2>, launch_big<288, 256, 2, 4, 2>},  // 46
+    {288, 192, 1, 64, launch_big<288, 192, 2, 4, 2>, launch_big<288, 192, 2, 4, 2>, 1},  // 47
+    {288, 128, 1, 64, launch_big<288, 128, 2, 4, 2>, launch_big<288, 128, 2, 4, 2>},  // 48
+    {144, 256, 1, 64, launch_big<144, 256, 1, 8, 2>, launch_big<144, 256, 1, 8, 2>},  // 49
+    {256, 256, 1, 64, launch_big<256, 256, 2, 4, 2>, launch_big<256, 256, 2, 4, 2>},  // 50
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -433,12 +598,27 @@ namespace oasis {
 // the direct-to-LDS pipeline with 96 x 64 tiles (4 stages) for the MLP products, the split-K
 // slices and everything at the VAE's 576 tokens, 32 x 64 tiles (3 stages) for the QKV
 // product of the DiT (144 or 288 tokens); 96 x 128 register-ring tiles from 2048 tokens up.
+// From 2048 tokens up, the 8-wave 288-row tiles: 288 x 256 for N = 4096 (16 x 16 tiles at 4608
+// tokens), 288 x 192 for N = 3072 (16 x 16) and 288 x 128 otherwise (with 2 K slices at N = 1024).
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
-  (void)N;
   (void)Kslice;
-  if (M >= 2048) return 13;
+  if (M >= 2048) {
+    if (N % 256 == 0 && N >= 2048) return 46;
+    if (N % 192 == 0 && N >= 2048 && kind != OASIS_EPI_GELU_TANH_FP8) return 47;
+    return 48;
+  }
   const bool big = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF || kind == OASIS_EPI_PARTIAL_F32;
   return big || M >= 512 ? 24 : 32;
+}
+
+// Split-K count for the default tile of a large-token split-K product: K slices until the
+// launch has at least 256 workgroups (one per CU), within max_splits and whole 64-wide K tiles.
+int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits) {
+  const TileCfg& t = kTiles[auto_tile(M, N, K, OASIS_EPI_PARTIAL_F32)];
+  const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+  int s = 1;
+  while (tiles * s < 256 && 2 * s <= max_splits && 2 * s <= 8 && (K / 64) % (2 * s) == 0) s *= 2;
+  return s;
 }
 
 int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
@@ -458,6 +638,8 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
   if (tile < 0) tile = auto_tile(M, N, K / splits, e.kind);
   OASIS_REQUIRE(tile < kNumTiles, OASIS_ERR_ARG, "gemm: tile config %d out of range", tile);
   const TileCfg& t = kTiles[tile];
+  OASIS_REQUIRE(!(t.no_fp8_epi && e.kind == OASIS_EPI_GELU_TANH_FP8), OASIS_ERR_ARG,
+                "gemm: tile config %d cannot run the GELU_TANH_FP8 epilogue", tile);
   // the prefetch ring needs (K steps per split) % stages == 0; 128-wide configs also need
   // K % 128 per split, else their one-stage 64-wide twin runs
   const int64_t ks = K / splits / t.bk;

@@ -28,6 +28,8 @@ int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int6
 // explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
 int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                     const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
+// split-K count the default tile of a large-token (M >= 2048) split-K product wants
+int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits);
 // acc = A[M,K] @ (Bq[N,K] (e4m3) * w_scale[N])^T with the given epilogue (gemm_fp8.hip).
 // A_scale == nullptr: A is bf16; else A is e4m3 blocks with e8m0 scales A_scale[M, lds].
 int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t lds, const uint8_t* B, int64_t ldb,
@@ -85,9 +87,14 @@ OASIS_DEV float wave_max(float v) {
 // ---- activations ------------------------------------------------------------
 // tanh-GELU written as x * sigmoid(2u): 0.5 x (1 + tanh(u)) == x / (1 + exp(-2u)),
 // u = sqrt(2/pi) (x + 0.044715 x^3).
+// tanh-GELU as x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3), i.e. x / (1 + 2^t) with
+// t = -2 u log2(e), on the hardware exp2 and reciprocal (about 1 ulp each; the results are
+// stored as bf16 or e4m3). Large |x| saturates to x or -0.
 OASIS_DEV float gelu_tanh(float x) {
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return x / (1.0f + __expf(-2.0f * u));
+  constexpr float c1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float c3 = c1 * 0.044715f;
+  const float t = x * fmaf(c3, x * x, c1);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 OASIS_DEV float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }

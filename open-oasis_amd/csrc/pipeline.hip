@@ -221,8 +221,10 @@ extern "C" int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float*
 namespace {
 
 // Split-K count for an O / FC2 GEMM (tile 0: 32 x 64): enough workgroups to cover the
-// 256 CUs, each split still a multiple of the 4-deep prefetch ring.
+// 256 CUs, each split still a multiple of the 4-deep prefetch ring. From 2048 tokens up the
+// GEMM's own large-token tiles decide.
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t max_splits) {
+  if (M >= 2048) return oasis::gemm_auto_splits(M, N, K, (int)std::min<int64_t>(max_splits, 8));
   const int64_t tiles = ((M + 31) / 32) * ((N + 63) / 64);
   const int64_t nk = K / 64;
   int s = 1;

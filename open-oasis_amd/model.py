@@ -258,7 +258,7 @@ class DiTWorkspace:
         dev, d, bf = dit.device, dit.d, torch.bfloat16
         # split-K slices for the O / FC2 projections; small token counts need more splits
         if max_splits is None:
-            max_splits = 8 if max_rows <= 640 else (2 if max_rows <= 2048 else 1)
+            max_splits = 8 if max_rows <= 640 else 2
         self.max_rows, self.max_cond = max_rows, max_cond
         self.x = torch.zeros(max_rows, d, device=dev)
         self.h = torch.zeros(max_rows, d, device=dev, dtype=bf)

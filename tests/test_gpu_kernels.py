@@ -401,7 +401,7 @@ def test_rope_layout_surface():
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(46)))
+@pytest.mark.parametrize("tile", list(range(51)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -433,6 +433,49 @@ def test_gemm_direct_lds_ragged(tile):
     ref = A.float() @ B.float().t()
     assert_close(out, torch.nn.functional.gelu(ref + bias, approximate="tanh"), 0.99999, 1e-2, "tile %d gelu" % tile)
     assert_close(part.sum(0), ref, 0.999999, 1e-4, "tile %d split-K x5" % tile)
+
+
+@pytest.mark.parametrize("tile", list(range(46, 51)))
+def test_gemm_large_token_tiles_ragged(tile):
+    """The 8-wave large-token tiles on a ragged shape: M and N not multiples of the tile (the
+    last tile row and column are partial), K = 5 tiles, GELU epilogue with bias, split-K x5,
+    and the 4608 x 4096 x 1024 product they are sized for."""
+    M, N, K = 600, 520, 320
+    g = _gen(90 + tile)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    out = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+    e = _epi(kind=L.EPI_GELU_TANH, bias=dev(bias), out_bf16=out, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    part = torch.zeros(5, M, N, device="cuda")
+    ep = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(B)), K, M, N, K, ctypes.byref(ep), tile, 5, stream())
+    sync()
+    ref = A.float() @ B.float().t()
+    assert_close(out, torch.nn.functional.gelu(ref + bias, approximate="tanh"), 0.99999, 1e-2, "tile %d gelu" % tile)
+    assert_close(part.sum(0), ref, 0.999999, 1e-4, "tile %d split-K x5" % tile)
+    M, N, K = 4608, 4096, 1024
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    out = torch.zeros(M, N, device="cuda")
+    e = _epi(kind=L.EPI_STORE_F32, out_f32=out, ld_out=N)
+    Ad, Bd = dev(A), dev(B)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), K, L.ptr(Bd), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    sync()
+    assert_close(out, Ad.float() @ Bd.float().t(), 0.999999, 1e-4, "tile %d 4608x4096x1024" % tile)
+
+
+def test_gemm_fp8_epilogue_needs_aligned_lanes():
+    """A tile whose epilogue lanes do not cover whole 32-column blocks refuses GELU_TANH_FP8."""
+    M, N, K = 288, 384, 64
+    A = torch.zeros(M, K, device="cuda", dtype=torch.bfloat16)
+    B = torch.zeros(N, K, device="cuda", dtype=torch.bfloat16)
+    q = torch.zeros(M, N, device="cuda", dtype=torch.uint8)
+    sc = torch.zeros(M, N // 32, device="cuda", dtype=torch.uint8)
+    e = _epi(kind=L.EPI_GELU_TANH_FP8, out_fp8=q, out_scale=sc, ld_out=N, ld_scale=N // 32)
+    with pytest.raises(L.OasisError):
+        L.call("oasis_gemm_bf16_config", L.ptr(A), K, L.ptr(B), K, M, N, K, ctypes.byref(e), 47, 1, stream())
 
 
 @pytest.mark.parametrize("splits", [1, 2, 4, 8])

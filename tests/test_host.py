@@ -110,5 +110,6 @@ def test_workspace_split_sizing():
     dit = M.DiT(_small_dit(), "cpu")
     assert dit.workspace(288).max_splits == 8
     assert dit.workspace(2048).max_splits == 2
-    ws = dit.workspace(4608)
-    assert ws.max_splits == 1 and ws.struct.max_rows == 4608
+    ws = dit.workspace(4608)  # the large-token O / FC2 tiles use 2 K slices at N = 1024
+    assert ws.max_splits == 2 and ws.struct.max_rows == 4608
+    assert ws.partial.shape == (2, 4608, dit.d)
