@@ -115,24 +115,36 @@ __global__ void temb_kernel(const float* t, int64_t R, int half, float* out) {
   }
 }
 
-// out[m, n] = b[n] + sum_k x[m, k] W[n, k]; block = one row m, threads over n.
+// out[m, n] = b[n] + sum_k x[m, k] W[n, k]; block = R rows (staged in LDS), threads over n:
+// each thread reads its weight row once for R outputs.
+template <int R>
 __global__ __launch_bounds__(256) void small_linear_kernel(const float* x, int64_t ldx, int K, const bf16* W,
-                                                           int N, const float* b, float* out, int64_t ld_out) {
-  __shared__ float xs[256];
-  const int64_t m = blockIdx.y;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) xs[k] = x[m * ldx + k];
+                                                           int N, const float* b, float* out, int64_t ld_out,
+                                                           int64_t M) {
+  __shared__ float xs[R][256];
+  const int64_t m0 = (int64_t)blockIdx.y * R;
+  for (int i = threadIdx.x; i < R * K; i += blockDim.x) {
+    const int r = i / K, k = i - r * K;
+    xs[r][k] = m0 + r < M ? x[(m0 + r) * ldx + k] : 0.f;
+  }
   __syncthreads();
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
   const bf16* w = W + (int64_t)n * K;
-  float acc = b ? b[n] : 0.f;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = b ? b[n] : 0.f;
   for (int k = 0; k < K; k += 8) {
     float wv[8];
     unpack8(*reinterpret_cast<const bf16x8*>(w + k), wv);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc += xs[k + j] * wv[j];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[r] += xs[r][k + j] * wv[j];
   }
-  out[m * ld_out + n] = acc;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (m0 + r < M) out[(m0 + r) * ld_out + n] = acc[r];
 }
 
 // reference surface: out[r, n] = sum_k c[k] w[k, n] + b[n] (w is [K, N]), rows r < out_rows.
@@ -252,9 +264,15 @@ extern "C" int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K <= 256 && K % 8 == 0 && ldx >= K && ld_out >= N, OASIS_ERR_SHAPE,
                 "small_linear: need 0 < K <= 256, K % 8 == 0");
   OASIS_REQUIRE(M <= 65535, OASIS_ERR_SHAPE, "small_linear: M too large");
-  hipLaunchKernelGGL(small_linear_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, ldx, (int)K, static_cast<const bf16*>(W), (int)N, b, out,
-                     ld_out);
+  const dim3 blk(256);
+  const unsigned nb = (unsigned)((N + 255) / 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M >= 2048)
+    hipLaunchKernelGGL(small_linear_kernel<16>, dim3(nb, (unsigned)((M + 15) / 16)), blk, 0, s, x, ldx, (int)K,
+                       static_cast<const bf16*>(W), (int)N, b, out, ld_out, M);
+  else
+    hipLaunchKernelGGL(small_linear_kernel<4>, dim3(nb, (unsigned)((M + 3) / 4)), blk, 0, s, x, ldx, (int)K,
+                       static_cast<const bf16*>(W), (int)N, b, out, ld_out, M);
   return oasis::check_launch("small_linear");
 }
 

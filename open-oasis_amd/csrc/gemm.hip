@@ -205,12 +205,6 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const bf16* __restrict__
 // workgroup. LDS rows are unpadded 128-byte rows of 16-byte chunks stored XOR-swizzled
 // (chunk c of row r at slot c ^ ((r >> 1) & 7)), which keeps the 16-row MFMA fragment
 // reads conflict-free. One wave instruction fills 8 rows; the A rows come first.
-// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds is
-// wave-uniform).
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, reinterpret_cast<uint32_t*>(lds), 16, 0, 0);
-}
-
 template <int BM, int BN, int WM, int WN, int STAGES>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ A, int64_t lda,
                                                        const bf16* __restrict__ B, int64_t ldb, int M, int N,
@@ -350,17 +344,6 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
 // an XCD's consecutive ids cover a compact block of tiles: each XCD's L2 then holds a few
 // rows of A and a few weight slices instead of every row of A.
 // The epilogue stages 16 rows of a wave's tile at a time in LDS owned by that wave alone.
-__device__ __forceinline__ void grouped_tile(int pid, int Mt, int Nt, int GN, int& split, int& mt, int& nt) {
-  const int per = Mt * Nt;
-  split = pid / per;
-  const int t = pid - split * per;
-  const int in_group = GN * Mt;
-  const int grp = t / in_group, first = grp * GN;
-  const int gsz = min(Nt - first, GN);
-  const int r = t - grp * in_group;
-  mt = r / gsz;
-  nt = first + (r - mt * gsz);
-}
 
 template <int BM, int BN, int WM, int WN, int STAGES>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __restrict__ A, int64_t lda,
@@ -455,6 +438,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  // QKV rotation tables to LDS (above the epilogue staging) when they fit
+  float* tab = reinterpret_cast<float*>(smem + EPI_BYTES);
+  const int tab_rows = rope_lds_rows(e, M, SMEM - EPI_BYTES);
+  if (tab_rows) {
+    rope_to_lds(e, tab, tab_rows, tid, NW * 64);
+    __syncthreads();
+  }
+
   // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
   // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
@@ -480,7 +471,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
           *reinterpret_cast<f32x4*>(d + 4) = c1;
         } else {
           float v[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-          epilogue8(e, gm, gn, v);
+          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows);
         }
       }
     }
@@ -602,11 +593,7 @@ namespace oasis {
 // tokens), 288 x 192 for N = 3072 (16 x 16) and 288 x 128 otherwise (with 2 K slices at N = 1024).
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
   (void)Kslice;
-  if (M >= 2048) {
-    if (N % 256 == 0 && N >= 2048) return 46;
-    if (N % 192 == 0 && N >= 2048 && kind != OASIS_EPI_GELU_TANH_FP8) return 47;
-    return 48;
-  }
+  if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
   const bool big = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF || kind == OASIS_EPI_PARTIAL_F32;
   return big || M >= 512 ? 24 : 32;
 }

@@ -34,7 +34,29 @@ struct Epi {
   uint8_t* out_fp8;
   uint8_t* out_scale;
   int64_t ld_scale;
+  // n / rows_per_frame and n / frames_per_stream as (n * magic) >> shift (see DivMagic)
+  uint64_t rpf_magic, fps_magic;
+  int rpf_shift, fps_shift;
 };
+
+// Exact unsigned division by a fixed d >= 1 for any n < 2^31: magic = ceil(2^s / d) with
+// s = 32 + ceil(log2 d), so magic < 2^33, n * magic < 2^64, and the error n (magic - 2^s/d) / 2^s
+// stays below 1/d, which cannot carry floor(n/d) to the next integer.
+struct DivMagic {
+  uint64_t magic;
+  int shift;
+};
+inline DivMagic div_magic(uint64_t d) {
+  if (d == 0 || d >= (1ull << 31)) return DivMagic{0, 0};  // unused: the host checks reject such shapes
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  const int s = 32 + l;
+  const unsigned __int128 one = 1;
+  return DivMagic{(uint64_t)(((one << s) + d - 1) / d), s};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint64_t magic, int shift) {
+  return (uint32_t)(((uint64_t)n * magic) >> shift);
+}
 
 __device__ __forceinline__ int xcd_remap(int pid, int G) {
   const int q = G / NUM_XCD, r = G % NUM_XCD;
@@ -42,12 +64,110 @@ __device__ __forceinline__ int xcd_remap(int pid, int G) {
   return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
+// Large-token tile order: pid -> (split, m tile, n tile) with the split outermost, then groups
+// of GN n tiles in which n runs fastest, so consecutive ids (one XCD's share after xcd_remap)
+// cover a compact (count / GN) x GN block of tiles.
+__device__ __forceinline__ void grouped_tile(int pid, int Mt, int Nt, int GN, int& split, int& mt, int& nt) {
+  const int per = Mt * Nt;
+  split = pid / per;
+  const int t = pid - split * per;
+  const int in_group = GN * Mt;
+  const int grp = t / in_group, first = grp * GN;
+  const int gsz = min(Nt - first, GN);
+  const int r = t - grp * in_group;
+  mt = r / gsz;
+  nt = first + (r - mt * gsz);
+}
+
+// Large-token tile choice among 288 x 256, 288 x 192 (only when allow192) and 288 x 128 (ids
+// t256, t192, t128): among the widths that divide N, the one whose tile count fills its last
+// round of 256 workgroups best (ties: the wider tile); 288 x 128 when none divides N.
+inline int large_token_tile(int64_t M, int64_t N, bool allow192, int t256, int t192, int t128) {
+  const int64_t mt = (M + 287) / 288;
+  const int widths[3] = {256, 192, 128};
+  const int ids[3] = {t256, t192, t128};
+  int best = t128;
+  double best_fill = -1.0;
+  for (int i = 0; i < 3; ++i) {
+    if (N % widths[i] != 0 || (widths[i] == 192 && !allow192)) continue;
+    const int64_t tiles = mt * (N / widths[i]);
+    const int64_t rounds = (tiles + 255) / 256;
+    const double fill = (double)tiles / (double)(rounds * 256);
+    if (fill > best_fill + 1e-9) {
+      best_fill = fill;
+      best = ids[i];
+    }
+  }
+  return best;
+}
+
+// 16 (or 4) bytes per lane from global memory straight into LDS at lds + 16 * lane (4 * lane);
+// lds is wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, reinterpret_cast<uint32_t*>(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, reinterpret_cast<uint32_t*>(lds), 4, 0, 0);
+}
+
 __device__ __forceinline__ void store8_bf16(bf16* dst, const float* v) {
   *reinterpret_cast<bf16x8*>(dst) = pack8(v);
 }
 
-// Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N).
-__device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float* v) {
+// QKV_ROPE in two parts, so a caller can fetch the rotation tables of its next rows while it
+// finishes the current ones: the cos / signed-sin entries of (row m, columns n0..n0+7) (only
+// q and k columns are rotated), then the rotation, head split and store.
+// tab (optional): an LDS copy of the tables, tab_rows cos rows of 64 then tab_rows sin rows.
+__device__ __forceinline__ void qkv_rope_tables(const Epi& e, int64_t m, int n0, float* c, float* sn,
+                                                const float* tab = nullptr, int tab_rows = 0) {
+  const int D = e.n_heads * 64;
+  const int which = (n0 >= D) + (n0 >= 2 * D);  // 0 q, 1 k, 2 v
+  if (which == 2) return;
+  const int d0 = (n0 - which * D) & 63;
+  // 32-bit index math (M, rows and frames are < 2^31; checked on the host)
+  const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
+  const uint32_t f = fast_div((uint32_t)m, e.rpf_magic, e.rpf_shift), p = (uint32_t)m - f * rpf;
+  const uint32_t t = f - fast_div(f, e.fps_magic, e.fps_shift) * fps;
+  const uint32_t pos = e.rope_by_frame ? t : p;
+  const float* cp = tab ? tab + pos * 64 + d0 : e.rope_cos + pos * 64 + d0;
+  const float* sp = tab ? tab + (tab_rows + pos) * 64 + d0 : e.rope_sinp + pos * 64 + d0;
+  const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp);
+  const f32x4 c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c[j] = c0[j];
+    c[j + 4] = c1[j];
+    sn[j] = s0[j];
+    sn[j + 4] = s1[j];
+  }
+}
+
+__device__ __forceinline__ void qkv_rope_store(const Epi& e, int64_t m, int n0, float* v, const float* c,
+                                               const float* sn) {
+  const int D = e.n_heads * 64;
+  const int which = (n0 >= D) + (n0 >= 2 * D);
+  const int nn = n0 - which * D;
+  const int h = nn >> 6, d0 = nn & 63;
+  const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
+  const uint32_t f = fast_div((uint32_t)m, e.rpf_magic, e.rpf_shift), p = (uint32_t)m - f * rpf;
+  const uint32_t b = fast_div(f, e.fps_magic, e.fps_shift), t = f - b * fps;
+  if (which < 2) {
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * sn[j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = r[j];
+  }
+  bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
+  store8_bf16(base + (int64_t)b * e.s_b + (int64_t)t * e.s_t + (int64_t)p * e.s_p + (int64_t)h * e.s_h + d0, v);
+}
+
+// Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N). tab / tab_rows:
+// an LDS copy of the QKV rotation tables (see rope_lds_rows), or null.
+__device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float* v, const float* tab = nullptr,
+                                          int tab_rows = 0) {
   if (e.bias) {
     const f32x4 b0 = *reinterpret_cast<const f32x4*>(e.bias + n0);
     const f32x4 b1 = *reinterpret_cast<const f32x4*>(e.bias + n0 + 4);
@@ -80,7 +200,7 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       break;
     }
     case OASIS_EPI_GATED_RES: {
-      const int64_t f = (uint32_t)m / (uint32_t)e.rows_per_frame;
+      const int64_t f = fast_div((uint32_t)m, e.rpf_magic, e.rpf_shift);
       const float* g = e.gate + f * e.gate_fstride + n0;
       float* d = e.out_f32 + m * e.ld_out + n0;
       f32x4 x0 = *reinterpret_cast<f32x4*>(d), x1 = *reinterpret_cast<f32x4*>(d + 4);
@@ -107,30 +227,9 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       break;
     }
     case OASIS_EPI_QKV_ROPE: {
-      const int D = e.n_heads * 64;
-      const int which = n0 / D;          // 0 q, 1 k, 2 v
-      const int nn = n0 - which * D;
-      const int h = nn >> 6, d0 = nn & 63;
-      // 32-bit index math (M, rows and frames are < 2^31; checked on the host)
-      const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
-      const uint32_t f = (uint32_t)m / rpf, p = (uint32_t)m - f * rpf;
-      const uint32_t b = f / fps, t = f - b * fps;
-      if (which < 2) {
-        const uint32_t pos = e.rope_by_frame ? t : p;
-        const f32x4 c0 = *reinterpret_cast<const f32x4*>(e.rope_cos + pos * 64 + d0);
-        const f32x4 c1 = *reinterpret_cast<const f32x4*>(e.rope_cos + pos * 64 + d0 + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(e.rope_sinp + pos * 64 + d0);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(e.rope_sinp + pos * 64 + d0 + 4);
-        const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-        const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-        float r[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * sn[j];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = r[j];
-      }
-      bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
-      store8_bf16(base + (int64_t)b * e.s_b + (int64_t)t * e.s_t + (int64_t)p * e.s_p + (int64_t)h * e.s_h + d0, v);
+      float c[8], sn[8];
+      qkv_rope_tables(e, m, n0, c, sn, tab, tab_rows);
+      qkv_rope_store(e, m, n0, v, c, sn);
       break;
     }
     case OASIS_EPI_UNPATCHIFY: {
@@ -172,6 +271,26 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
   }
 }
 
+// Rows of the QKV rotation tables a large-token workgroup copies to LDS for its epilogue (the
+// cos rows, then the sin rows; 512 bytes per position): the positions of a frame for the
+// spatial tables, the frames of a stream for the temporal ones. 0 when the tables do not fit
+// in tab_bytes (the epilogue then reads them from global memory).
+__device__ __forceinline__ int rope_lds_rows(const Epi& e, int M, int tab_bytes) {
+  if (e.kind != OASIS_EPI_QKV_ROPE) return 0;
+  // only positions some row m < M reaches: m % rows_per_frame, or its frame's index in the stream
+  const int64_t frames = (M + e.rows_per_frame - 1) / e.rows_per_frame;
+  const int64_t rows = e.rope_by_frame ? min(e.frames_per_stream, frames) : min(e.rows_per_frame, (int64_t)M);
+  return rows * 512 <= tab_bytes ? (int)rows : 0;
+}
+// Workgroup-wide copy of those rows into tab (all threads of the workgroup call it).
+__device__ __forceinline__ void rope_to_lds(const Epi& e, float* tab, int rows, int tid, int nthreads) {
+  const int chunks = rows * 16;  // 16-byte chunks per table
+  for (int i = tid; i < 2 * chunks; i += nthreads) {
+    const float* src = i < chunks ? e.rope_cos + i * 4 : e.rope_sinp + (i - chunks) * 4;
+    *reinterpret_cast<f32x4*>(tab + i * 4) = *reinterpret_cast<const f32x4*>(src);
+  }
+}
+
 Epi to_epi(const oasis_epilogue_t& x) {
   Epi e;
   e.kind = x.kind;
@@ -184,6 +303,11 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.gate_fstride = x.gate_fstride;
   e.rows_per_frame = x.rows_per_frame > 0 ? x.rows_per_frame : 1;
   e.frames_per_stream = x.frames_per_stream > 0 ? x.frames_per_stream : 1;
+  const DivMagic dr = div_magic((uint64_t)e.rows_per_frame), df = div_magic((uint64_t)e.frames_per_stream);
+  e.rpf_magic = dr.magic;
+  e.rpf_shift = dr.shift;
+  e.fps_magic = df.magic;
+  e.fps_shift = df.shift;
   e.q = static_cast<bf16*>(x.q);
   e.k = static_cast<bf16*>(x.k);
   e.v = static_cast<bf16*>(x.v);
@@ -213,6 +337,8 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
     case OASIS_EPI_GATED_RES:
     case OASIS_EPI_RESIDUAL:
     case OASIS_EPI_PARTIAL_F32:
+      OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES || e.rows_per_frame < (1ll << 31), OASIS_ERR_SHAPE,
+                    "gemm: rows_per_frame too large");
       OASIS_REQUIRE(e.out_f32 && e.ld_out >= N && e.ld_out % 4 == 0, OASIS_ERR_ARG,
                     "gemm: fp32 epilogue needs out_f32 and ld_out >= N (multiple of 4)");
       OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES || e.gate, OASIS_ERR_NULL, "gemm: gate is NULL");

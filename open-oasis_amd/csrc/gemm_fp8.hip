@@ -228,6 +228,159 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
   }
 }
 
+// Large-token fp8 variant (2048+ tokens, A already in e4m3 blocks): 8 waves share a tall tile
+// (288 x 256 and the like, as the bf16 gemm_big_kernel) and the K tiles reach LDS through
+// global_load_lds, 128 fp8 per row (one 16x16x128 MFMA step) in the same swizzled 128-byte
+// rows, plus each A row's 4 block-scale bytes per K tile (4 bytes per lane, one wave per 64
+// rows). Two stages; the epilogue stages 16 rows of a wave's tile at a time in that wave's LDS.
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
+                                                                   const uint8_t* __restrict__ Ascale, int64_t lds,
+                                                                   const uint8_t* __restrict__ B, int64_t ldb,
+                                                                   const float* __restrict__ wscale, int M, int N,
+                                                                   int K, int splits, Epi e) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  static_assert(FM * 16 == TM && FN * 16 == TN, "wave tile must be a multiple of 16");
+  constexpr int NBLK = (BM + BN) / 8;  // 1 KB blocks of 8 rows per stage
+  static_assert(BM % 8 == 0 && BN % 8 == 0, "whole 8-row blocks");
+  constexpr int LPW = (NBLK + NW - 1) / NW;
+  constexpr int SWAVES = (BM + 63) / 64;  // waves that load the A scales (64 rows each)
+  static_assert(SWAVES <= NW, "scale rows");
+  constexpr int DATA = (BM + BN) * P8;
+  constexpr int STAGE = DATA + SWAVES * 256;
+  constexpr int RING = 2 * STAGE;
+  constexpr int EP = TN + 4;
+  constexpr int EPI_BYTES = NW * 16 * EP * 4;
+  constexpr int SMEM = RING > EPI_BYTES ? RING : EPI_BYTES;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  constexpr int GN = 8;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  int split, mt, nt;
+  grouped_tile(xcd_remap(blockIdx.x, Mt * Nt * splits), Mt, Nt, GN, split, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = K / BK8 / splits;
+  const int kb = split * nk * BK8;
+
+  const uint8_t* src[LPW];
+  int dst[LPW];
+#pragma unroll
+  for (int u = 0; u < LPW; ++u) {
+    const int blk = min(wave * LPW + u, NBLK - 1);
+    const int r = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (r < BM)
+      src[u] = A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 16;
+    else
+      src[u] = B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 16;
+    dst[u] = blk * 1024;
+  }
+  // scale word of A row wave*64 + lane (rows past the tile load a clamped row, never read)
+  const uint8_t* ssrc = Ascale + (int64_t)min(m0 + wave * 64 + lane, M - 1) * lds + kb / 32;
+  auto issue = [&](int kt, int buf) {
+    char* base = smem + buf * STAGE;
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * BK8, base + dst[u]);
+    if (wave < SWAVES) load_lds4(ssrc + kt * (BK8 / 32), base + DATA + wave * 256);
+  };
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, g = lane >> 4;
+  auto frag = [&](const char* base, int r) -> i32x8 {
+    const i32x4 x0 = *reinterpret_cast<const i32x4*>(base + r * P8 + (((g ^ (r >> 1)) & 7) << 4));
+    const i32x4 x1 = *reinterpret_cast<const i32x4*>(base + r * P8 + ((((4 + g) ^ (r >> 1)) & 7) << 4));
+    return i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  };
+  auto compute = [&](int buf) {
+    const char* base = smem + buf * STAGE;
+    const uint8_t* sb = reinterpret_cast<const uint8_t*>(base + DATA);
+    i32x8 af[FM], bfr[FN];
+    int sa[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = wm * TM + i * 16 + lr;
+      af[i] = frag(base, r);
+      sa[i] = sb[r * 4 + g];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[j] = frag(base, BM + wn * TN + j * 16 + lr);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bfr[j], acc[i][j], 0, 0, 0, sa[i], 0,
+                                                                      kScaleOne);
+  };
+
+  issue(0, 0);
+  for (int k = 0; k < nk; ++k) {
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0): tile k is in LDS
+    __builtin_amdgcn_s_barrier();
+    issue(min(k + 1, nk - 1), (k + 1) & 1);  // into the buffer read at k - 1
+    compute(k & 1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // QKV rotation tables to LDS (above the epilogue staging) when they fit
+  float* tab = reinterpret_cast<float*>(smem + EPI_BYTES);
+  const int tab_rows = rope_lds_rows(e, M, SMEM - EPI_BYTES);
+  if (tab_rows) {
+    rope_to_lds(e, tab, tab_rows, tid, NW * 64);
+    __syncthreads();
+  }
+  // lanes 4i..4i+3 cover one aligned 32-column block when TN % 32 == 0 (the host checks it for
+  // the GELU_TANH_FP8 epilogue)
+  float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
+  constexpr int UPR = TN / 8;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[(g * 4 + r) * EP + j * 16 + lr] = acc[i][j][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int u = lane; u < 16 * UPR; u += 64) {
+      const int r = u / UPR, c8 = (u - r * UPR) * 8;
+      const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
+      if (gm < M && gn < N) {
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(wscale + gn);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(wscale + gn + 4);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = c0[j] * s0[j];
+          v[j + 4] = c1[j] * s1[j];
+        }
+        if (e.kind == OASIS_EPI_PARTIAL_F32) {
+          float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+          *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+          *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        } else {
+          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 typedef hipError_t (*launch8_fn)(const void*, int64_t, const uint8_t*, int64_t, const uint8_t*, int64_t,
                                  const float*, int, int, int, int, const Epi&, hipStream_t);
 
@@ -240,27 +393,45 @@ hipError_t launch8(const void* A, int64_t lda, const uint8_t* As, int64_t lds, c
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WM, int WN>
+hipError_t launch8_big(const void* A, int64_t lda, const uint8_t* As, int64_t lds, const uint8_t* B, int64_t ldb,
+                       const float* ws, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
+                     static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K, splits, e);
+  return hipGetLastError();
+}
+
 struct Tile8 {
   int bm, bn, stages;
-  launch8_fn fn, fn_single;        // bf16 A
+  launch8_fn fn, fn_single;        // bf16 A (null: fp8 A only)
   launch8_fn fn_q, fn_q_single;    // fp8 A blocks
+  int no_fp8_epi;                  // 1: its epilogue lanes do not cover aligned 32-column blocks
 };
 #define OASIS_T8(BM, BN, WM, WN)                                                                       \
   {BM, BN, 2, launch8<BM, BN, WM, WN, 2, false>, launch8<BM, BN, WM, WN, 1, false>,                   \
-   launch8<BM, BN, WM, WN, 2, true>, launch8<BM, BN, WM, WN, 1, true>}
+   launch8<BM, BN, WM, WN, 2, true>, launch8<BM, BN, WM, WN, 1, true>, 0}
+#define OASIS_T8_BIG(BM, BN, WM, WN, NO_FP8_EPI) \
+  {BM, BN, 1, nullptr, nullptr, launch8_big<BM, BN, WM, WN>, launch8_big<BM, BN, WM, WN>, NO_FP8_EPI}
 const Tile8 kTiles8[] = {
-    OASIS_T8(128, 128, 2, 2),  // 0
-    OASIS_T8(128, 64, 2, 2),   // 1
-    OASIS_T8(64, 128, 2, 2),   // 2
-    OASIS_T8(64, 64, 2, 2),    // 3
-    OASIS_T8(32, 64, 1, 4),    // 4
+    OASIS_T8(128, 128, 2, 2),              // 0
+    OASIS_T8(128, 64, 2, 2),               // 1
+    OASIS_T8(64, 128, 2, 2),               // 2
+    OASIS_T8(64, 64, 2, 2),                // 3
+    OASIS_T8(32, 64, 1, 4),                // 4
+    OASIS_T8_BIG(288, 256, 2, 4, 0),       // 5  (fp8 A only)
+    OASIS_T8_BIG(288, 192, 2, 4, 1),       // 6
+    OASIS_T8_BIG(288, 128, 2, 4, 0),       // 7
 };
 #undef OASIS_T8
+#undef OASIS_T8_BIG
 constexpr int kNumTiles8 = sizeof(kTiles8) / sizeof(kTiles8[0]);
 
-// Default tile per shape, from sweeps of the DiT projections at M = 4608 on MI355X.
-int auto_tile8(int64_t M, int64_t N, bool aq) {
-  if (M >= 2048) return aq ? (N >= 2048 ? 1 : 2) : 2;
+// Default tile per shape, from sweeps of the DiT projections at M = 4608 on MI355X: with fp8 A
+// from 2048 tokens up the 8-wave 288-row tiles (as the bf16 GEMM picks them).
+int auto_tile8(int64_t M, int64_t N, bool aq, int kind) {
+  if (M >= 2048 && aq) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 5, 6, 7);
+  if (M >= 2048) return 2;
   if (M >= 256) return 3;
   return 4;
 }
@@ -334,9 +505,12 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
                 splits);
   const Epi e = to_epi(ex);
   if (const int rc = check_epilogue(e, M, N, splits)) return rc;
-  if (tile < 0) tile = auto_tile8(M, N, aq);
+  if (tile < 0) tile = auto_tile8(M, N, aq, e.kind);
   OASIS_REQUIRE(tile < kNumTiles8, OASIS_ERR_ARG, "gemm_fp8: tile config %d out of range", tile);
   const Tile8& t = kTiles8[tile];
+  OASIS_REQUIRE(!(t.no_fp8_epi && e.kind == OASIS_EPI_GELU_TANH_FP8), OASIS_ERR_ARG,
+                "gemm_fp8: tile config %d cannot run the GELU_TANH_FP8 epilogue", tile);
+  OASIS_REQUIRE(aq || t.fn, OASIS_ERR_ARG, "gemm_fp8: tile config %d needs A as fp8 blocks", tile);
   const bool ring = (K / BK8 / splits) % t.stages == 0;
   const launch8_fn fn = aq ? (ring ? t.fn_q : t.fn_q_single) : (ring ? t.fn : t.fn_single);
   const hipError_t err = fn(A, lda, A_scale, lds, B, ldb, w_scale, (int)M, (int)N, (int)K, splits, e, s);

@@ -216,3 +216,59 @@ def test_gemm_fp8_a8_equals_in_kernel_quantization():
     cos, rel = metrics(deq, ref)
     print("fp8 GELU epilogue blocks: cos=%.7f rel=%.3e" % (cos, rel), flush=True)
     assert cos >= 0.9999 and rel <= 7e-2, (cos, rel)  # a value near a rounding midpoint may move one e4m3 step
+
+
+@pytest.mark.parametrize("M,N", [(600, 520), (4608, 1024)])
+def test_gemm_fp8_large_token_tiles(M, N):
+    """The 8-wave large-token fp8 tiles (fp8 A only) equal the 4-wave tiles bit for bit (the same
+    MFMA sequence per output), on a ragged shape and on the config-4 projection shape, for plain,
+    split-K and GELU -> fp8-block epilogues; a tile whose lanes do not cover 32-column blocks
+    refuses the fp8 epilogue, and the large tiles refuse bf16 A."""
+    K = 1024
+    g = _gen(M + N)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    q, s = _quantize(W)
+    Ad = dev(A)
+    a8 = torch.zeros(M, K, dtype=torch.uint8, device="cuda")
+    a8s = torch.zeros(M, K // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_quantize_act_fp8", L.ptr(Ad), K, M, K, L.ptr(a8), K, L.ptr(a8s), K // 32, stream())
+
+    def run(tile, splits=1, kind=None):
+        if kind == "gelu8":
+            m8 = torch.zeros(M, N, dtype=torch.uint8, device="cuda")
+            m8s = torch.zeros(M, N // 32, dtype=torch.uint8, device="cuda")
+            e = _epi(kind=L.EPI_GELU_TANH_FP8, bias=dev(bias), out_fp8=m8, out_scale=m8s, ld_out=N, ld_scale=N // 32)
+            out = (m8, m8s)
+        elif splits > 1:
+            part = torch.zeros(splits, M, N, device="cuda")
+            e = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)
+            out = part
+        else:
+            o = torch.zeros(M, N, device="cuda")
+            e = _epi(kind=L.EPI_STORE_F32, bias=dev(bias), out_f32=o, ld_out=N)
+            out = o
+        L.call("oasis_gemm_fp8_a8", L.ptr(a8), K, L.ptr(a8s), K // 32, L.ptr(q), K, L.ptr(s), M, N, K,
+               ctypes.byref(e), tile, splits, stream())
+        sync()
+        return out
+
+    ref = run(0)
+    ref_part = run(0, 2)
+    ref8 = run(0, kind="gelu8") if N % 32 == 0 else None
+    for tile in (5, 6, 7):
+        assert torch.equal(run(tile), ref), "tile %d" % tile
+        assert torch.equal(run(tile, 2), ref_part), "tile %d split-K x2" % tile
+        if ref8 is not None and tile != 6:
+            m8, m8s = run(tile, kind="gelu8")
+            assert torch.equal(m8, ref8[0]) and torch.equal(m8s, ref8[1]), "tile %d gelu8" % tile
+    cos, rel = metrics(ref, _ref(A, W) + bias.double())
+    assert rel <= 1e-4, rel
+    if N % 32 == 0:
+        with pytest.raises(L.OasisError, match="GELU_TANH_FP8"):
+            run(6, kind="gelu8")
+    o = torch.zeros(M, N, device="cuda")
+    with pytest.raises(L.OasisError, match="fp8 blocks"):
+        L.call("oasis_gemm_fp8", L.ptr(Ad), K, L.ptr(q), K, L.ptr(s), M, N, K,
+               ctypes.byref(_epi(kind=L.EPI_STORE_F32, out_f32=o, ld_out=N)), 5, 1, stream())

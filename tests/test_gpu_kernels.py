@@ -288,7 +288,9 @@ def test_temporal_attention(T):
 
 # ---------------------------------------------------------------- skinny GEMM
 @pytest.mark.parametrize("R,K,N,act_in,act_out,acc", [(2, 1024, 6144 * 2 + 2048, 1, 0, 0), (5, 256, 1024, 0, 1, 0),
-                                                       (16, 1024, 1024, 0, 0, 1), (1, 64, 1024, 0, 0, 0)])
+                                                       (16, 1024, 1024, 0, 0, 1), (1, 64, 1024, 0, 0, 0),
+                                                       (32, 1024, 2048, 1, 0, 0), (23, 256, 1024, 0, 1, 1),
+                                                       (70, 1024, 512, 0, 0, 1), (40, 2048, 256, 0, 0, 0)])
 def test_gemv(R, K, N, act_in, act_out, acc):
     g = _gen(14 + R)
     x = torch.randn(R, K, generator=g)
@@ -328,6 +330,14 @@ def test_small_linear_and_ddim_and_bridge():
            1024, stream())
     sync()
     assert_close(out, x @ W.float().t() + b, 0.9999999, 1e-5, "small_linear")
+    for M in (147, 2050):  # ragged row blocks of the 4-row and 16-row variants
+        xm = torch.randn(M, 40, generator=g)
+        Wm = (torch.randn(1000, 32, generator=g) * 0.05).to(torch.bfloat16)
+        om = torch.full((M, 1000), 7.0, device="cuda")
+        L.call("oasis_small_linear", L.ptr(dev(xm)), 40, M, 32, L.ptr(dev(Wm)), 1000, None, L.ptr(om), 1000,
+               stream())
+        sync()
+        assert_close(om, xm[:, :32] @ Wm.float().t(), 0.9999999, 1e-5, "small_linear M=%d" % M)
 
     ac = oracle.cosine_alphas_cumprod()
     v = torch.randn(144, 64, generator=g)
