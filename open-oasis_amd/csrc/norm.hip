@@ -85,15 +85,16 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
   }
 }
 
-// Residual update fused with the next LayerNorm. One 256-thread workgroup per row
-// (VPT = D/256 floats per thread), every load issued up front so a row costs one memory
-// round trip; mean and variance by two block reductions:
+// Residual update fused with the next LayerNorm, for few rows (under 2048): one 256-thread
+// workgroup per row (VPT = D/256 floats per thread, so a row's latency is spread over 4 waves),
+// every load issued up front so a row costs one memory round trip; mean and variance by two
+// block reductions:
 //   x[m] += g * (sum_s partial[s][m] + bias)          (NP > 0; g = gate[f(m)] or 1)
 //   y[m]  = LN(x[m]) * a + b                           (a, b: modulate rows or affine)
 // y is bf16, or (y8 != nullptr, D >= 1024) fp8 activation blocks: e4m3 bytes y8[m, :] and
 // one e8m0 scale per 32 columns in ys[m, :] (8 consecutive threads share a block).
 template <int VPT, int NP>
-__global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
+__global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
                                                           int64_t pstride, const float* __restrict__ bias,
                                                           const float* __restrict__ gate, int64_t gate_fs,
                                                           int64_t rpf, const float* __restrict__ la,
@@ -198,14 +199,104 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
   }
 }
 
-template <int VPT>
+// The same from 2048 rows up: one 64-lane wave per row (4 rows per workgroup), the row in
+// registers as NC chunks of 256 columns (4 floats per lane each), every load of the row issued
+// up front; mean and variance by two wave reductions, no LDS or barriers:
+//   x[m] += g * (sum_s partial[s][m] + bias)          (NP > 0; g = gate[f(m)] or 1)
+//   y[m]  = LN(x[m]) * a + b                           (a, b: modulate rows or affine)
+// y is bf16, or (y8 != nullptr) fp8 activation blocks: e4m3 bytes y8[m, :] and one e8m0 scale
+// per 32 columns in ys[m, :] (8 consecutive lanes share a block).
+template <int NC, int NP>
+__global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
+                                                          int64_t pstride, const float* __restrict__ bias,
+                                                          const float* __restrict__ gate, int64_t gate_fs,
+                                                          int64_t rpf, const float* __restrict__ la,
+                                                          const float* __restrict__ lb, int64_t ln_fs,
+                                                          bf16* __restrict__ y, uint8_t* __restrict__ y8,
+                                                          uint8_t* __restrict__ ys, float eps) {
+  constexpr int D = NC * 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t f = row / rpf;
+  float* xr = x + row * D;
+  float v[NC][4], pv[NP > 0 ? NP : 1][NC][4], bv[NC][4], gv[NC][4], av[NC][4], cv[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 256 + lane * 4;
+    load4<float>(xr + k, v[c]);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) load4<float>(part + p * pstride + row * D + k, pv[p][c]);
+    if (NP > 0) {
+      if (bias) load4<float>(bias + k, bv[c]); else bv[c][0] = bv[c][1] = bv[c][2] = bv[c][3] = 0.f;
+      if (gate) load4<float>(gate + f * gate_fs + k, gv[c]); else gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 1.f;
+    }
+    if (y || y8) {
+      load4<float>(la + f * ln_fs + k, av[c]);
+      load4<float>(lb + f * ln_fs + k, cv[c]);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (NP > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = bv[c][j];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc += pv[p][c][j];
+        v[c][j] += gv[c][j] * acc;
+      }
+      store4<float>(xr + c * 256 + lane * 4, v[c]);
+    }
+    s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
+  }
+  if (!y && !y8) return;
+  const float mean = wave_sum(s) * (1.0f / D);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[c][j] -= mean;
+      q += v[c][j] * v[c][j];
+    }
+  const float rstd = rsqrtf(wave_sum(q) * (1.0f / D) + eps);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int k = c * 256 + lane * 4;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[c][j] * rstd * av[c][j] + cv[c][j];
+    if (y8) {
+      float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      const int sb = fp8_block_scale(amax);
+      const float inv = fp8_block_inv(sb);
+      *reinterpret_cast<uint32_t*>(y8 + row * D + k) = pack4_fp8(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+      if ((lane & 7) == 0) ys[row * (D / 32) + k / 32] = (uint8_t)sb;
+    } else {
+      store4<bf16>(y + row * D + k, o);
+    }
+  }
+}
+
+template <int NC>
 hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
                           bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s) {
-  const dim3 grid((unsigned)M), block(256);
-#define OASIS_RLN(NPV)                                                                                        \
-  hipLaunchKernelGGL((residual_ln_kernel<VPT, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, lb, \
-                     lfs, y, y8, ys, eps)
+  // few rows: a 256-thread workgroup per row (VPT = NC floats per thread); many: a wave per row
+  const bool wave_rows = M >= 2048;
+  const dim3 grid((unsigned)(wave_rows ? (M + 3) / 4 : M)), block(256);
+#define OASIS_RLN(NPV)                                                                                          \
+  if (wave_rows)                                                                                                \
+    hipLaunchKernelGGL((residual_ln_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, \
+                       lb, lfs, y, y8, ys, eps);                                                                \
+  else                                                                                                          \
+    hipLaunchKernelGGL((residual_ln_block_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, \
+                       la, lb, lfs, y, y8, ys, eps)
   switch (np) {
     case 0: OASIS_RLN(0); break;
     case 1: OASIS_RLN(1); break;
