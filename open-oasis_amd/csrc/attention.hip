@@ -215,18 +215,29 @@ template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
-  // staging: a whole 144-token frame in one 192-key chunk; up to 576 keys (the VAE) staged
-  // at once (158 KB of LDS) and consumed in 64-key chunks; longer sequences in 576-key stages
-  const bool short_seq = a.Lk <= 192;
+  // staging: a whole frame (up to 160 keys, 144 per DiT frame) in one chunk, up to 192 keys in
+  // one chunk of 192; up to 576 keys (the VAE) staged at once (158 KB of LDS) and consumed in
+  // 64-key chunks; longer sequences in 576-key stages. 144-query frames take 48 queries per
+  // workgroup, or with 256+ (frame, head) pairs all 144 (9 waves share one K/V staging).
+  const int kind = a.Lk <= 160 ? 0 : (a.Lk <= 192 ? 1 : 2);
   if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
-    const dim3 g((unsigned)(a.Lq / 48), (unsigned)n_bh);
-    if (short_seq)
-      hipLaunchKernelGGL((flash_kernel<3, 192, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
-    else
-      hipLaunchKernelGGL((flash_kernel<3, 64, 576, T>), g, dim3(192), 0, s, q, k, v, o, a);
+    if (kind == 0 && a.Lq % 144 == 0 && n_bh >= 256) {
+      hipLaunchKernelGGL((flash_kernel<9, 160, 160, T>), dim3((unsigned)(a.Lq / 144), (unsigned)n_bh), dim3(576), 0, s,
+                         q, k, v, o, a);
+    } else {
+      const dim3 g((unsigned)(a.Lq / 48), (unsigned)n_bh);
+      if (kind == 0)
+        hipLaunchKernelGGL((flash_kernel<3, 160, 160, T>), g, dim3(192), 0, s, q, k, v, o, a);
+      else if (kind == 1)
+        hipLaunchKernelGGL((flash_kernel<3, 192, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
+      else
+        hipLaunchKernelGGL((flash_kernel<3, 64, 576, T>), g, dim3(192), 0, s, q, k, v, o, a);
+    }
   } else {
     const dim3 g((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh);
-    if (short_seq)
+    if (kind == 0)
+      hipLaunchKernelGGL((flash_kernel<4, 160, 160, T>), g, dim3(256), 0, s, q, k, v, o, a);
+    else if (kind == 1)
       hipLaunchKernelGGL((flash_kernel<4, 192, 192, T>), g, dim3(256), 0, s, q, k, v, o, a);
     else
       hipLaunchKernelGGL((flash_kernel<4, 64, 576, T>), g, dim3(256), 0, s, q, k, v, o, a);

@@ -230,9 +230,12 @@ def test_ln_affine():
 
 
 # ---------------------------------------------------------------- attention
-@pytest.mark.parametrize("L_", [144, 576, 37])
-def test_attention_heads_first(L_):
-    F_, H = 2, 4
+@pytest.mark.parametrize("L_,F_", [(144, 2), (576, 2), (37, 2), (144, 64), (160, 2), (192, 2), (150, 64)])
+def test_attention_heads_first(L_, F_):
+    """Frames of L_ tokens: a whole frame staged at once (up to 160 or 192 keys), the VAE's
+    576, a ragged 37; 64 frames x 4 heads (256 pairs) take the 9-wave one-workgroup-per-frame path
+    at L = 144."""
+    H = 4
     g = _gen(11 + L_)
     q, k, v = (torch.randn(F_ * H, L_, 64, generator=g).to(torch.bfloat16) for _ in range(3))
     out = torch.zeros(F_ * L_, H * 64, device="cuda", dtype=torch.bfloat16)
