@@ -53,7 +53,10 @@ struct AttnArgs {
   const float* bias;        // [Lq, Lk] or nullptr
   int causal;
   int H;                    // heads per frame (output addressing)
-  int64_t o_sf, o_sh, o_si; // out offset = (bh/H)*o_sf + (bh%H)*o_sh + i*o_si + d
+  // out offset of query i, dim d of block bh: with f = bh / H, h = bh % H,
+  // (f / f_inner) * o_sfo + (f % f_inner) * o_sf + h * o_sh + i * o_si + d
+  int f_inner;
+  int64_t o_sfo, o_sf, o_sh, o_si;
 };
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
@@ -203,7 +206,8 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
   if (q0 >= a.Lq || my_q >= a.Lq) return;
   const float inv = 1.0f / lsum;
   const int f = bh / a.H, h = bh - f * a.H;
-  T* op = O + f * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
+  const int fo = f / a.f_inner, fi = f - fo * a.f_inner;
+  T* op = O + fo * a.o_sfo + fi * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const int d = dt * 16 + 4 * g;
@@ -215,10 +219,19 @@ template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
-  // staging: a whole frame (up to 160 keys, 144 per DiT frame) in one chunk, up to 192 keys in
-  // one chunk of 192; up to 576 keys (the VAE) staged at once (158 KB of LDS) and consumed in
-  // 64-key chunks; longer sequences in 576-key stages. 144-query frames take 48 queries per
-  // workgroup, or with 256+ (frame, head) pairs all 144 (9 waves share one K/V staging).
+  // staging: short sequences (up to 32 or 64 keys: the temporal windows) and whole frames (up
+  // to 160 keys, 144 per DiT frame; up to 192) in one chunk; up to 576 keys (the VAE) staged at
+  // once (158 KB of LDS) and consumed in 64-key chunks; longer sequences in 576-key stages.
+  // 144-query frames take 48 queries per workgroup, or with 256+ (frame, head) pairs all 144
+  // (9 waves share one K/V staging).
+  if (a.Lq <= 32 && a.Lk <= 32) {
+    hipLaunchKernelGGL((flash_kernel<2, 32, 32, T>), dim3(1, (unsigned)n_bh), dim3(128), 0, s, q, k, v, o, a);
+    return oasis::check_launch("attention");
+  }
+  if (a.Lq <= 64 && a.Lk <= 64) {
+    hipLaunchKernelGGL((flash_kernel<4, 64, 64, T>), dim3(1, (unsigned)n_bh), dim3(256), 0, s, q, k, v, o, a);
+    return oasis::check_launch("attention");
+  }
   const int kind = a.Lk <= 160 ? 0 : (a.Lk <= 192 ? 1 : 2);
   if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
     if (kind == 0 && a.Lq % 144 == 0 && n_bh >= 256) {
@@ -332,6 +345,8 @@ extern "C" int oasis_attention(const void* q, const void* k, const void* v, void
   a.bias = nullptr;
   a.causal = 0;
   a.H = (int)n_heads;
+  a.f_inner = 1 << 30;
+  a.o_sfo = 0;
   a.o_sf = L * n_heads * 64;
   a.o_sh = 64;
   a.o_si = n_heads * 64;
@@ -354,6 +369,8 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
   a.bias = bias;
   a.causal = causal;
   a.H = 1;
+  a.f_inner = 1 << 30;
+  a.o_sfo = 0;
   a.o_sf = sq * 64;
   a.o_sh = 0;
   a.o_si = 64;
@@ -377,6 +394,25 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
                 "temporal_attention: bad shape");
   OASIS_REQUIRE(q_frame < T, OASIS_ERR_ARG, "temporal_attention: q_frame must be < T");
   const int64_t G = B * P * n_heads;
+  if (T >= 8 && q_frame < 0) {
+    // long causal windows on the MFMA flash kernel: each (stream, position, head) group is a
+    // contiguous [T][64] block; outputs land token-major at row (b*T + t)*P + p
+    OASIS_REQUIRE(G <= 65535, OASIS_ERR_SHAPE, "temporal_attention: too many (stream, position, head) groups");
+    AttnArgs a;
+    a.Lq = a.Lk = (int)T;
+    a.q_bh = a.kv_bh = T * 64;
+    a.scale_log2 = scale * LOG2E;
+    a.bias = nullptr;
+    a.causal = 1;
+    a.H = (int)n_heads;
+    a.f_inner = (int)P;  // f = b*P + p
+    a.o_sfo = T * P * n_heads * 64;
+    a.o_sf = n_heads * 64;
+    a.o_sh = 64;
+    a.o_si = P * n_heads * 64;
+    return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                              static_cast<bf16*>(out), G, a, stream);
+  }
   hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0, stream,
                      static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                      static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame);

@@ -273,9 +273,9 @@ def test_sdpa_surface(dtype, causal, bias):
     assert_close(out, ref.reshape(nh * sq, 64), 0.9999, 2e-2, "sdpa %s causal=%s bias=%s" % (dtype, causal, bias))
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 32])
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 32, 48])
 def test_temporal_attention(T):
-    B_, P, H = 1, 144, 4
+    B_, P, H = 2, 144, 4
     g = _gen(13 + T)
     q, k, v = (torch.randn(B_, P, H, T, 64, generator=g).to(torch.bfloat16) for _ in range(3))
     out = torch.zeros(B_ * T * P, H * 64, device="cuda", dtype=torch.bfloat16)
