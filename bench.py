@@ -41,7 +41,7 @@ def _event_ms(fn, stream, n):
 # HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
 # scaled by what the same counter reads for a plain device copy of known size.
-TRAFFIC = {"fc1": 15625025, "gemv": 409858666}
+TRAFFIC = {"fc1": 15612665, "gemv": 409773602, "fc1_4608_bf16": 90728422, "fc1_4608_fp8": 46785135}
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100):
@@ -76,7 +76,8 @@ def _gemv_timing(pkg, dit, ws, stream, R=2, n=50):
 
 def probe(pkg, n=10):
     """Short run for hardware-counter passes: n launches each of the FC1 GEMM and the
-    adaLN GEMV on config-1 buffers, and n plain 256 MiB device copies (the calibration
+    adaLN GEMV on config-1 buffers, n each of the 4608-token FC1 GEMM in bf16 and in fp8
+    (config-4 shape, random operands), and n plain 256 MiB device copies (the calibration
     kernel, 268435456 bytes read and written per launch)."""
     import torch
     c1 = pkg.synth.config1()
@@ -89,12 +90,40 @@ def probe(pkg, n=10):
     torch.cuda.synchronize()
     _fc1_timing(pkg, dit, step.ws, step.stream, n)
     _gemv_timing(pkg, dit, step.ws, step.stream, n=n)
+    del step, dit
+    L = pkg._lib
+    M, D, Dm = 4608, 1024, 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    A = torch.randn(M, D, device="cuda", generator=g).to(torch.bfloat16)
+    W = (torch.randn(Dm, D, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    out = torch.empty(M, Dm, device="cuda", dtype=torch.bfloat16)
+    h = L.stream_handle(torch.cuda.current_stream())
+    e = L.Epilogue()
+    e.kind, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, out.data_ptr(), Dm
+    for _ in range(n + 1):
+        L.call("oasis_gemm_bf16", L.ptr(A), D, L.ptr(W), D, M, Dm, D, ctypes.byref(e), h)
+    q = torch.empty(Dm, D, device="cuda", dtype=torch.uint8)
+    sc = torch.empty(Dm, device="cuda")
+    a8 = torch.empty(M, D, device="cuda", dtype=torch.uint8)
+    a8s = torch.empty(M, D // 32, device="cuda", dtype=torch.uint8)
+    m8 = torch.empty(M, Dm, device="cuda", dtype=torch.uint8)
+    m8s = torch.empty(M, Dm // 32, device="cuda", dtype=torch.uint8)
+    L.call("oasis_quantize_fp8_rows", L.ptr(W), Dm, D, L.ptr(q), L.ptr(sc), h)
+    L.call("oasis_quantize_act_fp8", L.ptr(A), D, M, D, L.ptr(a8), D, L.ptr(a8s), D // 32, h)
+    e8 = L.Epilogue()
+    e8.kind, e8.out_fp8, e8.out_scale, e8.ld_out, e8.ld_scale = (L.EPI_GELU_TANH_FP8, m8.data_ptr(), m8s.data_ptr(),
+                                                                 Dm, Dm // 32)
+    for _ in range(n + 1):
+        L.call("oasis_gemm_fp8_a8", L.ptr(a8), D, L.ptr(a8s), D // 32, L.ptr(q), D, L.ptr(sc), M, Dm, D,
+               ctypes.byref(e8), -1, 1, h)
+    torch.cuda.synchronize()
     src = torch.ones(64 << 20, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(n):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "fc1 gemm x%d, adaLN gemv x%d, 256 MiB copy x%d" % (n + 1, n + 1, n)}), flush=True)
+    print(json.dumps({"probe": "fc1 gemm x%d, adaLN gemv x%d, 4608-token fc1 gemm bf16 and fp8 x%d each, "
+                               "256 MiB copy x%d" % (n + 1, n + 1, n + 1, n)}), flush=True)
 
 
 def _graph_step_ms(step, steps, warmup):
@@ -150,7 +179,8 @@ def config4(pkg, oracle, steps, warmup):
         gms = _event_ms(fn, step.stream, 50)
         tf = 2 * M * D * Dm / (gms * 1e-3) / 1e12
         res["fc1_gemm_" + fmt] = {"avg_launch_ms": round(gms, 5), "achieved": round(tf, 1), "peak": peak,
-                                  "unit": "TFLOP/s", "frac": round(tf / peak, 4)}
+                                  "unit": "TFLOP/s", "frac": round(tf / peak, 4),
+                                  "traffic": TRAFFIC.get("fc1_4608_" + fmt)}
         del step, dit
         torch.cuda.empty_cache()
     res["speedup_fp8_vs_bf16"] = round(res["ms_per_step_bf16"] / res["ms_per_step_fp8"], 3)
