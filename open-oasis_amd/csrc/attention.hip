@@ -337,6 +337,7 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
 extern "C" int oasis_attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
                                int64_t n_heads, float scale, oasis_stream_t stream) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "attention: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "attention: pointers must be 16-byte aligned");
   OASIS_REQUIRE(n_frames > 0 && L > 0 && n_heads > 0 && L < (1 << 30), OASIS_ERR_SHAPE, "attention: bad shape");
   AttnArgs a;
   a.Lq = a.Lk = (int)L;
@@ -358,6 +359,7 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
                           int64_t skv, int64_t head_dim, float scale, const float* bias, int causal, int dtype,
                           oasis_stream_t stream) {
   OASIS_REQUIRE(Q && K && V && out, OASIS_ERR_NULL, "sdpa: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, Q, K, V, out), OASIS_ERR_ARG, "sdpa: pointers must be 16-byte aligned");
   OASIS_REQUIRE(head_dim == 64, OASIS_ERR_SHAPE, "sdpa: head_dim must be 64");
   OASIS_REQUIRE(sq > 0 && skv > 0 && sq < (1 << 30) && skv < (1 << 30), OASIS_ERR_SHAPE, "sdpa: bad shape");
   AttnArgs a;
@@ -390,6 +392,7 @@ namespace oasis {
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
                        int64_t n_heads, float scale, int q_frame, hipStream_t stream) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "temporal_attention: pointers must be 16-byte aligned");
   OASIS_REQUIRE(B > 0 && T > 0 && P > 0 && n_heads > 0 && T <= 4096, OASIS_ERR_SHAPE,
                 "temporal_attention: bad shape");
   OASIS_REQUIRE(q_frame < T, OASIS_ERR_ARG, "temporal_attention: q_frame must be < T");

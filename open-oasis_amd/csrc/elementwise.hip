@@ -261,6 +261,7 @@ extern "C" int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, 
 extern "C" int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W, int64_t N,
                                   const float* b, float* out, int64_t ld_out, oasis_stream_t stream) {
   OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "small_linear: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, W), OASIS_ERR_ARG, "small_linear: W must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K <= 256 && K % 8 == 0 && ldx >= K && ld_out >= N, OASIS_ERR_SHAPE,
                 "small_linear: need 0 < K <= 256, K % 8 == 0");
   OASIS_REQUIRE(M <= 65535, OASIS_ERR_SHAPE, "small_linear: M too large");

@@ -611,6 +611,7 @@ int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits) {
 int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                     const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
   OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm: null operand");
+  OASIS_REQUIRE(aligned16(A) && aligned16(B), OASIS_ERR_ARG, "gemm: A and B must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0, OASIS_ERR_SHAPE, "gemm: empty shape M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
   OASIS_REQUIRE(K % BK == 0, OASIS_ERR_SHAPE, "gemm: K=%lld must be a multiple of 64", (long long)K);
@@ -652,6 +653,7 @@ int gemm_launch(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t 
 extern "C" int oasis_linear(const void* x, const void* w, void* out, int64_t M, int64_t K, int64_t N,
                             int w_layout, int out_dtype, oasis_stream_t stream) {
   OASIS_REQUIRE(x && w && out, OASIS_ERR_NULL, "linear: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x, w, out), OASIS_ERR_ARG, "linear: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K % BK == 0 && N % 8 == 0 && M < (1ll << 31) && N < (1ll << 31),
                 OASIS_ERR_SHAPE, "linear: need K %% 64 == 0 and N %% 8 == 0");
   OASIS_REQUIRE(w_layout == 0 || w_layout == 1, OASIS_ERR_ARG, "linear: w_layout must be 0 ([K,N]) or 1 ([N,K])");

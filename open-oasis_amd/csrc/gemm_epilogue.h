@@ -329,9 +329,17 @@ Epi to_epi(const oasis_epilogue_t& x) {
 }
 
 // Checks the epilogue against the GEMM shape; returns OASIS_OK or an error code (message set).
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
   OASIS_REQUIRE(splits == 1 || e.kind == OASIS_EPI_PARTIAL_F32, OASIS_ERR_ARG,
                 "gemm: split-K needs the PARTIAL_F32 epilogue");
+  // the epilogue moves 16-byte vectors (8-byte e4m3 groups): every base pointer it touches must
+  // be 16-byte aligned
+  OASIS_REQUIRE(aligned16(e.bias) && aligned16(e.out_f32) && aligned16(e.out_bf16) && aligned16(e.gate) &&
+                    aligned16(e.q) && aligned16(e.k) && aligned16(e.v) && aligned16(e.rope_cos) &&
+                    aligned16(e.rope_sinp) && aligned16(e.out_fp8),
+                OASIS_ERR_ARG, "gemm: epilogue pointers must be 16-byte aligned");
   switch (e.kind) {
     case OASIS_EPI_STORE_F32:
     case OASIS_EPI_GATED_RES:

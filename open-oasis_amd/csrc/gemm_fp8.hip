@@ -493,6 +493,8 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
                     int splits, hipStream_t s) {
   const bool aq = A_scale != nullptr;
   OASIS_REQUIRE(A && B && w_scale, OASIS_ERR_NULL, "gemm_fp8: null operand");
+  OASIS_REQUIRE(aligned16(A) && aligned16(B) && aligned16(w_scale) && (reinterpret_cast<uintptr_t>(A_scale) & 3) == 0,
+                OASIS_ERR_ARG, "gemm_fp8: A, B and w_scale must be 16-byte aligned, A_scale 4-byte aligned");
   OASIS_REQUIRE(!aq || (lds >= K / 32 && lds % 4 == 0 && lda % 16 == 0), OASIS_ERR_SHAPE,
                 "gemm_fp8: fp8 A needs lda %% 16 == 0 and lds >= K/32, lds %% 4 == 0");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE,
@@ -543,6 +545,7 @@ extern "C" int oasis_gemm_fp8_a8(const void* A8, int64_t lda, const void* A_scal
 extern "C" int oasis_quantize_act_fp8(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
                                       void* scale, int64_t lds, oasis_stream_t stream) {
   OASIS_REQUIRE(x && q && scale, OASIS_ERR_NULL, "quantize_act_fp8: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x) && oasis_aligned(8, q), OASIS_ERR_ARG, "quantize_act_fp8: x must be 16-byte, q 8-byte aligned");
   OASIS_REQUIRE(M > 0 && K > 0 && K % 32 == 0 && ldx >= K && ldx % 8 == 0 && ldq >= K && ldq % 8 == 0 && lds >= K / 32,
                 OASIS_ERR_SHAPE, "quantize_act_fp8: need K %% 32 == 0, ldx/ldq >= K (multiples of 8), lds >= K/32");
   const int64_t chunks = M * (K / 8);
@@ -557,6 +560,7 @@ extern "C" int oasis_quantize_act_fp8(const void* x, int64_t ldx, int64_t M, int
 extern "C" int oasis_quantize_fp8_rows(const void* W, int64_t N, int64_t K, void* q, float* scale,
                                        oasis_stream_t stream) {
   OASIS_REQUIRE(W && q && scale, OASIS_ERR_NULL, "quantize_fp8_rows: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, W) && oasis_aligned(8, q), OASIS_ERR_ARG, "quantize_fp8_rows: W must be 16-byte, q 8-byte aligned");
   OASIS_REQUIRE(N > 0 && K > 0 && K % 8 == 0 && N <= (1ll << 30), OASIS_ERR_SHAPE,
                 "quantize_fp8_rows: need N > 0 and K a positive multiple of 8");
   hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, static_cast<hipStream_t>(stream),

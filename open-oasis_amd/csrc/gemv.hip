@@ -117,6 +117,7 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
                                const float* b, float* out, int64_t ld_out, int act_in, int act_out, int accumulate,
                                oasis_stream_t stream) {
   OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "gemv: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, W), OASIS_ERR_ARG, "gemv: W must be 16-byte aligned");
   OASIS_REQUIRE(R > 0 && R <= 1024, OASIS_ERR_SHAPE, "gemv: R=%lld must be in [1, 1024]", (long long)R);
   OASIS_REQUIRE(K > 0 && K % KSTEP == 0 && K <= 2048, OASIS_ERR_SHAPE, "gemv: K=%lld must be a multiple of 64, <= 2048",
                 (long long)K);

@@ -343,6 +343,7 @@ extern "C" int oasis_ln_modulate(const float* x, int64_t M, int64_t D, const flo
                                  const float* scale_p1, int64_t ada_fstride, int64_t rows_per_frame,
                                  void* y_bf16, float eps, oasis_stream_t stream) {
   OASIS_REQUIRE(x && shift && scale_p1 && y_bf16, OASIS_ERR_NULL, "ln_modulate: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x, shift, scale_p1, y_bf16), OASIS_ERR_ARG, "ln_modulate: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && rows_per_frame > 0, OASIS_ERR_SHAPE, "ln_modulate: bad M/rows_per_frame");
   return finish(ln_dispatch<float, bf16, 0>(x, M, D, eps, shift, scale_p1, ada_fstride, rows_per_frame,
                                             static_cast<bf16*>(y_bf16), static_cast<hipStream_t>(stream)),
@@ -352,6 +353,7 @@ extern "C" int oasis_ln_modulate(const float* x, int64_t M, int64_t D, const flo
 extern "C" int oasis_ln_affine(const float* x, int64_t M, int64_t D, const float* w, const float* b,
                                void* y_bf16, float eps, oasis_stream_t stream) {
   OASIS_REQUIRE(x && w && b && y_bf16, OASIS_ERR_NULL, "ln_affine: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x, w, b, y_bf16), OASIS_ERR_ARG, "ln_affine: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0, OASIS_ERR_SHAPE, "ln_affine: bad M");
   return finish(ln_dispatch<float, bf16, 1>(x, M, D, eps, w, b, 0, 1, static_cast<bf16*>(y_bf16),
                                             static_cast<hipStream_t>(stream)),
@@ -362,6 +364,7 @@ extern "C" int oasis_layernorm(const void* x, const void* weight, const void* bi
                                void* out, int64_t rows, int64_t cols, float eps, int dtype,
                                oasis_stream_t stream) {
   OASIS_REQUIRE(x && weight && bias && out, OASIS_ERR_NULL, "layernorm: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x, weight, bias, out), OASIS_ERR_ARG, "layernorm: pointers must be 16-byte aligned");
   OASIS_REQUIRE(rows > 0 && wb_ld >= 0, OASIS_ERR_SHAPE, "layernorm: bad rows/wb_ld");
   hipStream_t s = static_cast<hipStream_t>(stream);
   // weight/bias are fp32 for both dtypes (the Python surface upcasts them once).
@@ -386,6 +389,8 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
                 hipStream_t s) {
   OASIS_REQUIRE(x, OASIS_ERR_NULL, "residual_ln: null x");
+  OASIS_REQUIRE(oasis_aligned(16, x, partial, bias, gate, ln_a, ln_b, y_bf16, y8), OASIS_ERR_ARG,
+                "residual_ln: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "residual_ln: bad M/rows_per_frame");
   OASIS_REQUIRE(n_partials == 0 || partial, OASIS_ERR_NULL, "residual_ln: null partials");
   OASIS_REQUIRE(n_partials <= 1 || partial_stride >= M * D, OASIS_ERR_ARG, "residual_ln: partial_stride too small");

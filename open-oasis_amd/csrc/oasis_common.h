@@ -55,6 +55,14 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
     }                                           \
   } while (0)
 
+// true when every given pointer (null allowed) is a multiple of `a` bytes: the kernels move 16-,
+// 8- or 4-byte vectors from their base pointers
+template <typename... P>
+inline bool oasis_aligned(size_t a, const P*... p) {
+  const uintptr_t m = (0 | ... | reinterpret_cast<uintptr_t>(p));
+  return (m & (a - 1)) == 0;
+}
+
 // ---- conversions ------------------------------------------------------------
 OASIS_DEV float bf2f(bf16 v) { return (float)v; }
 OASIS_DEV bf16 f2bf(float v) { return (bf16)v; }  // round-to-nearest-even

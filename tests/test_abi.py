@@ -104,6 +104,27 @@ def test_gemm_validation():
     assert rc == ERR_NULL
 
 
+ODD = ctypes.c_void_p(0x1004)  # 4-byte but not 16-byte aligned
+
+
+def test_misaligned_pointers_are_rejected():
+    """Kernels move 16-byte vectors from their base pointers: a misaligned pointer is an
+    argument error, never a launch."""
+    e = L.Epilogue(kind=L.EPI_STORE_F32, out_f32=FAKE, ld_out=64)
+    rc, msg = _rc("oasis_gemm_bf16", ODD, 64, FAKE, 64, 16, 64, 64, ctypes.byref(e), None)
+    assert rc == ERR_ARG and "aligned" in msg, msg
+    e = L.Epilogue(kind=L.EPI_STORE_F32, out_f32=ODD, ld_out=64)
+    rc, msg = _rc("oasis_gemm_bf16", FAKE, 64, FAKE, 64, 16, 64, 64, ctypes.byref(e), None)
+    assert rc == ERR_ARG and "aligned" in msg, msg
+    rc, msg = _rc("oasis_attention", FAKE, ODD, FAKE, FAKE, 2, 144, 16, ctypes.c_float(0.125), None)
+    assert rc == ERR_ARG and "aligned" in msg, msg
+    rc, msg = _rc("oasis_residual_ln", ODD, 288, 1024, FAKE, 1, 288 * 1024, None, None, 0, 144, FAKE, FAKE, 0, FAKE,
+                  ctypes.c_float(1e-6), None)
+    assert rc == ERR_ARG and "aligned" in msg, msg
+    rc, msg = _rc("oasis_gemv_bf16", FAKE, 64, 2, ODD, 64, 64, None, FAKE, 64, 0, 0, 0, None)
+    assert rc == ERR_ARG and "aligned" in msg, msg
+
+
 def test_model_entry_points_validate_structs():
     w = L.DiTWeights(n_sub=3, d_model=1024, n_heads=16)
     b = L.DiTBuffers()
