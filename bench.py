@@ -220,28 +220,124 @@ def config2(pkg, n=20):
             "floor_ms": round(flop / (BF16_PEAK_TFLOPS * 1e12) * 1e3, 4)}
 
 
-def cpu_baseline(cfg, oracle, seconds=15.0):
-    """The fp32 oracle's DiT step (same weights and inputs) on this host's cores."""
+def bandwidth_kernels(pkg, n=200):
+    """The memory-bound kernels on their own, D=1024, at the config-1 step's 288 rows and at
+    4608 rows (configs 2 and 4), each timed with HIP events over n launches on one stream.
+    Algorithmic bytes are every input and output read or written once:
+      residual_ln  (the step's fused split-K sum + bias + gated residual + LN + adaLN modulate,
+                   4 fp32 partials): x read and written (fp32), 4 partials, bias, one gate,
+                   shift and scale row per frame, the bf16 LN output;
+      adaln_modulate (bf16): x, shift, scale in, out;
+      layernorm (bf16, [D] fp32 weight and bias): x in, out;
+      rope_layout (bf16, heads-first): the [rows, 3D] QKV in, Q/K/V out, fp32 cos and sin
+                   tables of 144 positions x D."""
+    import torch
+    L = pkg._lib
+    D, P = 1024, 144
+    stream = torch.cuda.Stream()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    out = []
+
+    def rnd(*shape, dtype=torch.float32):
+        return torch.randn(*shape, device="cuda", generator=g).to(dtype)
+
+    def entry(name, rows, ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": name, "rows": rows, "bound": "hbm", "achieved": round(gbs, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "avg_launch_ms": round(ms, 5), "algorithmic_bytes": nbytes})
+
+    for M in (288, 4608):
+        F = M // P
+        x, part = rnd(M, D), rnd(4, M, D)
+        bias, gate, sh, sc = rnd(D), rnd(F, D), rnd(F, D), rnd(F, D)
+        y = torch.empty(M, D, device="cuda", dtype=torch.bfloat16)
+        x0 = x.clone()
+
+        def res_ln():
+            L.call("oasis_residual_ln", L.ptr(x), M, D, L.ptr(part), 4, M * D, L.ptr(bias), L.ptr(gate), D, P,
+                   L.ptr(sc), L.ptr(sh), D, L.ptr(y), 1e-6, L.stream_handle(stream))
+        ms = _event_ms(res_ln, stream, n)
+        x.copy_(x0)   # the residual grows by n updates; its magnitude does not change the work
+        entry("residual_ln (4 split-K partials + bias + gated residual + LN + modulate)", M, ms,
+              M * D * (4 + 4 * 4 + 4 + 2) + D * 4 + 3 * F * D * 4)
+
+        xb, shb, scb = rnd(M, D, dtype=torch.bfloat16), rnd(M, D, dtype=torch.bfloat16), rnd(M, D, dtype=torch.bfloat16)
+        ob = torch.empty_like(xb)
+        ms = _event_ms(lambda: L.call("oasis_adaln_modulate", L.ptr(xb), L.ptr(shb), L.ptr(scb), L.ptr(ob), M * D,
+                                      L.BF16, L.stream_handle(stream)), stream, n)
+        entry("adaln_modulate (bf16)", M, ms, 4 * M * D * 2)
+
+        lw, lb = rnd(D), rnd(D)
+        ms = _event_ms(lambda: L.call("oasis_layernorm", L.ptr(xb), L.ptr(lw), L.ptr(lb), 0, L.ptr(ob), M, D, 1e-6,
+                                      L.BF16, L.stream_handle(stream)), stream, n)
+        entry("layernorm (bf16, affine)", M, ms, 2 * M * D * 2 + 2 * D * 4)
+
+        qkv = rnd(M, 3 * D, dtype=torch.bfloat16)
+        cs, sn = rnd(P, D), rnd(P, D)
+        q, k, v = (torch.empty(M, D, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+        ms = _event_ms(lambda: L.call("oasis_rope_layout", L.ptr(qkv), 3 * D, L.ptr(cs), L.ptr(sn), D, 64, 1, P,
+                                      L.ptr(q), L.ptr(k), L.ptr(v), M, P, D // 64, 64, 0, L.BF16,
+                                      L.stream_handle(stream)), stream, n)
+        entry("rope_layout (bf16, heads-first)", M, ms, 6 * M * D * 2 + 2 * P * D * 4)
+    torch.cuda.synchronize()
+    return out
+
+
+def _median_ms(fn, runs=5, seconds=6.0):
+    """2 warm-ups, then the median of at least `runs` timed calls (more while `seconds` last, at most 20)."""
+    for _ in range(2):
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < runs or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return 1e3 * times[len(times) // 2], len(times)
+
+
+def cpu_baseline(cfg, oracle, pkg):
+    """The fp32 oracle (same weights and inputs) on this host's cores: the config-1 DiT step (the
+    headline figure), one config-0 spatial sub-block, and one config-3 frame (4 DDIM steps + VAE)."""
     import torch
     # the host cores this job may use (the GPU box exports its CPU share as OMP_NUM_THREADS)
     torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1)
-    w = cfg["w"]
-    z = oracle.patch_embed(cfg["latent"][0], w)
-    times = []
     with torch.inference_mode():
-        for i in range(2):  # warm-up
+        w = cfg["w"]
+
+        def step():
+            z = oracle.patch_embed(cfg["latent"][0], w)
             oracle.dit_forward(z, oracle.conditioning(cfg["t"], cfg["actions"], w), w)
-        t_end = time.perf_counter() + seconds
-        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 20):
-            t0 = time.perf_counter()
-            zz = oracle.patch_embed(cfg["latent"][0], w)
-            oracle.dit_forward(zz, oracle.conditioning(cfg["t"], cfg["actions"], w), w)
-            times.append(time.perf_counter() - t0)
-    times.sort()
-    return {"value": round(1e3 * times[len(times) // 2], 2), "unit": "ms/DiT step",
+        step_ms, n_step = _median_ms(step, seconds=5.0)
+
+        c0 = pkg.synth.config0()
+        blk = {k: v.float() for k, v in c0["w"].items()}
+        cs, ss = oracle.rope_cos_sinperm(oracle.spatial_rope_angles(c0["spatial_freqs"].float()), 64)
+        x0, sc0 = c0["x"][0].float(), oracle.silu(c0["cond"][0].float())
+        sub_ms, n_sub = _median_ms(lambda: oracle.sub_block(x0, sc0, blk, "s", cs, ss), seconds=2.0)
+
+        c3 = pkg.synth.config3()
+        w3, ac = c3["w"], pkg.schedule.cosine_alphas_cumprod()
+        noise = oracle.patchify_to_output_space(c3["x_T"])[0]
+
+        def frame():
+            ctx_z = oracle.patch_embed(c3["ctx_latent"], w3)[0]
+            ctx_cond = oracle.conditioning(torch.tensor([c3["ctx_t"]]), c3["ctx_action"][None], w3)[0]
+            gen = [oracle.conditioning(torch.tensor([float(t)]), c3["gen_action"][None], w3)[0] for t, _ in c3["steps"]]
+            oracle.ddim_frame(noise, ctx_z, ctx_cond, gen, w3, c3["vw"], ac, c3["steps"])
+        frame_ms, n_frame = _median_ms(frame, seconds=0.0)
+    return {"value": round(step_ms, 2), "unit": "ms/DiT step",
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": "median of %d full config-1 DiT steps (T=2, 16 blocks) of the fp32 CPU oracle "
-                      "after 2 warm-ups" % len(times)}
+                      "after 2 warm-ups" % n_step,
+            "config0_sub_block_ms": round(sub_ms, 2),
+            "config0_sample": "median of %d config-0 spatial sub-blocks (x [2,144,1024]) after 2 warm-ups" % n_sub,
+            "config3_frame_ms": round(frame_ms, 1),
+            "config3_fps": round(1e3 / frame_ms, 3),
+            "config3_sample": "median of %d config-3 frames (4 DDIM steps at T=2 + bridge + 12-block VAE decode) "
+                              "after 2 warm-ups" % n_frame}
 
 
 def main():
@@ -336,6 +432,7 @@ def main():
                          "bound": "hbm", "achieved": round(ada_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ada_gbs / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get("gemv"),
                          "avg_launch_ms": round(ada_ms, 5), "algorithmic_bytes": ada_bytes},
+        "roofline_bandwidth_kernels": bandwidth_kernels(pkg),
     }
 
     # ---------------- config 3: the DDIM + VAE frame ----------------
@@ -427,7 +524,7 @@ def main():
         out["config4"] = config4(pkg, oracle, max(10, args.steps // 4), max(3, args.warmup // 4))
 
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(c1, oracle)
+        out["cpu_baseline"] = cpu_baseline(c1, oracle, pkg)
     print(json.dumps(out), flush=True)
 
 
