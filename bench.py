@@ -45,15 +45,23 @@ TRAFFIC = {"fc1": 15612665, "gemv": 409773602, "fc1_4608_bf16": 90728422, "fc1_4
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100):
-    """One FC1 projection of the step (sub-block 0, same buffers, same tile choice),
-    timed alone with HIP events on the step stream."""
+    """The FC1 projection alone (same buffers, same tile choice as in the step), timed with HIP
+    events on the step stream. Launch i uses the weights of sub-block i % 32: as in the step, each
+    launch reads weights that 31 launches (268 MB of other weights, more than the 256 MB
+    memory-side cache) have passed over since their last use, so they come from HBM."""
     L = pkg._lib
     M, D, Dm = 288, dit.d, dit.d_mlp
-    e = L.Epilogue()
-    e.kind, e.bias, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, dit.struct.fc1_b[0], ws.mlp.data_ptr(), Dm
-    A, B = L.ptr(ws.h), ctypes.c_void_p(dit.struct.fc1_w[0])
+    S, n_sub = dit.struct, dit.n_sub
+    eps = []
+    for j in range(n_sub):
+        e = L.Epilogue()
+        e.kind, e.bias, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, S.fc1_b[j], ws.mlp.data_ptr(), Dm
+        eps.append((ctypes.c_void_p(S.fc1_w[j]), e))
+    A, it = L.ptr(ws.h), [0]
 
     def fc1():
+        B, e = eps[it[0] % n_sub]
+        it[0] += 1
         L.call("oasis_gemm_bf16", A, D, B, D, M, Dm, D, ctypes.byref(e), L.stream_handle(stream))
     ms = _event_ms(fc1, stream, n)
     flop = 2 * M * D * Dm
@@ -124,6 +132,40 @@ def probe(pkg, n=10):
     torch.cuda.synchronize()
     print(json.dumps({"probe": "fc1 gemm x%d, adaLN gemv x%d, 4608-token fc1 gemm bf16 and fp8 x%d each, "
                                "256 MiB copy x%d" % (n + 1, n + 1, n + 1, n)}), flush=True)
+
+
+def kernel_probe(pkg, n=10):
+    """Short run for hardware-counter passes over the other kernels, in order: two eager config-1
+    DiT steps (every step kernel, 32 sub-blocks each), two eager config-3 VAE decodes (12 blocks
+    each), the bandwidth kernels of `bandwidth_kernels` (n + 1 launches each), and n plain 256 MiB
+    device copies (the calibration kernel)."""
+    import torch
+    import oracle
+    c1 = pkg.synth.config1()
+    dit = pkg.DiT(c1["w"], "cuda")
+    step = pkg.DiTStep(dit, B=1, T=2)
+    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
+    for _ in range(2):
+        step.run()
+    torch.cuda.synchronize()
+    del step, dit
+    c3 = pkg.synth.config3()
+    vae = pkg.VAE(c3["vw"], "cuda")
+    vws = vae.workspace()
+    latent = c3["vae_latent"].cuda()
+    frame = torch.empty(vae.frame_shape, device="cuda")
+    for _ in range(2):
+        vae.decode_inplace(latent, frame, vws, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    bandwidth_kernels(pkg, n)
+    src = torch.ones(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "2 config-1 steps, 2 config-3 VAE decodes, bandwidth kernels x%d, 256 MiB copy x%d"
+                      % (n + 1, n)}), flush=True)
 
 
 def _graph_step_ms(step, steps, warmup):
@@ -222,7 +264,11 @@ def config2(pkg, n=20):
 
 def bandwidth_kernels(pkg, n=200):
     """The memory-bound kernels on their own, D=1024, at the config-1 step's 288 rows and at
-    4608 rows (configs 2 and 4), each timed with HIP events over n launches on one stream.
+    4608 rows (configs 2 and 4), each timed with HIP events over n launches on one stream. Launch i
+    works on operand set i % S, with S sets spanning at least 640 MB, so that every launch reads
+    operands the 256 MB memory-side cache no longer holds (`achieved`). `cache_warm` repeats one
+    operand set, which then stays in that cache, as in the step, where each of these kernels reads
+    what the kernel before it has just written.
     Algorithmic bytes are every input and output read or written once:
       residual_ln  (the step's fused split-K sum + bias + gated residual + LN + adaLN modulate,
                    4 fp32 partials): x read and written (fp32), 4 partials, bias, one gate,
@@ -238,49 +284,69 @@ def bandwidth_kernels(pkg, n=200):
     g = torch.Generator(device="cuda").manual_seed(7)
     out = []
 
+    def n_sets(set_bytes):
+        return max(2, -(-(640 << 20) // set_bytes))
+
     def rnd(*shape, dtype=torch.float32):
         return torch.randn(*shape, device="cuda", generator=g).to(dtype)
 
-    def entry(name, rows, ms, nbytes):
-        gbs = nbytes / (ms * 1e-3) / 1e9
+    def timed(name, rows, nbytes, launch):
+        """launch(i) enqueues the launch on operand set i; nbytes is the algorithmic bytes."""
+        sets, it = n_sets(nbytes), [0]
+
+        def fn():
+            launch(it[0] % sets)
+            it[0] += 1
+        ms = _event_ms(fn, stream, n)
+        ms_warm = _event_ms(lambda: launch(0), stream, n)
+        gbs, gbs_warm = nbytes / (ms * 1e-3) / 1e9, nbytes / (ms_warm * 1e-3) / 1e9
         out.append({"kernel": name, "rows": rows, "bound": "hbm", "achieved": round(gbs, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "avg_launch_ms": round(ms, 5), "algorithmic_bytes": nbytes})
+                    "avg_launch_ms": round(ms, 5), "algorithmic_bytes": nbytes, "operand_sets": sets,
+                    "cache_warm": {"achieved": round(gbs_warm, 1), "avg_launch_ms": round(ms_warm, 5)}})
+        return sets
 
+    h = L.stream_handle(stream)
+    bf = torch.bfloat16
     for M in (288, 4608):
         F = M // P
-        x, part = rnd(M, D), rnd(4, M, D)
+        E = M * D
+        # residual_ln: x (per set), partials (per set), per-frame rows (shared, small)
+        nb = E * (4 + 4 * 4 + 4 + 2) + D * 4 + 3 * F * D * 4
+        S_ = n_sets(nb)
+        x, part = rnd(S_, E), rnd(S_, 4, E)
+        y = torch.empty(S_, E, device="cuda", dtype=bf)
         bias, gate, sh, sc = rnd(D), rnd(F, D), rnd(F, D), rnd(F, D)
-        y = torch.empty(M, D, device="cuda", dtype=torch.bfloat16)
-        x0 = x.clone()
-
-        def res_ln():
-            L.call("oasis_residual_ln", L.ptr(x), M, D, L.ptr(part), 4, M * D, L.ptr(bias), L.ptr(gate), D, P,
-                   L.ptr(sc), L.ptr(sh), D, L.ptr(y), 1e-6, L.stream_handle(stream))
-        ms = _event_ms(res_ln, stream, n)
-        x.copy_(x0)   # the residual grows by n updates; its magnitude does not change the work
-        entry("residual_ln (4 split-K partials + bias + gated residual + LN + modulate)", M, ms,
-              M * D * (4 + 4 * 4 + 4 + 2) + D * 4 + 3 * F * D * 4)
-
-        xb, shb, scb = rnd(M, D, dtype=torch.bfloat16), rnd(M, D, dtype=torch.bfloat16), rnd(M, D, dtype=torch.bfloat16)
-        ob = torch.empty_like(xb)
-        ms = _event_ms(lambda: L.call("oasis_adaln_modulate", L.ptr(xb), L.ptr(shb), L.ptr(scb), L.ptr(ob), M * D,
-                                      L.BF16, L.stream_handle(stream)), stream, n)
-        entry("adaln_modulate (bf16)", M, ms, 4 * M * D * 2)
-
+        timed("residual_ln (4 split-K partials + bias + gated residual + LN + modulate)", M, nb,
+              lambda i: L.call("oasis_residual_ln", L.ptr(x[i]), M, D, L.ptr(part[i]), 4, E, L.ptr(bias),
+                               L.ptr(gate), D, P, L.ptr(sc), L.ptr(sh), D, L.ptr(y[i]), 1e-6, h))
+        del x, part, y
+        nb = 4 * E * 2
+        S_ = n_sets(nb)
+        xb, shb, scb, ob = (rnd(S_, E, dtype=bf) for _ in range(4))
+        timed("adaln_modulate (bf16)", M, nb,
+              lambda i: L.call("oasis_adaln_modulate", L.ptr(xb[i]), L.ptr(shb[i]), L.ptr(scb[i]), L.ptr(ob[i]), E,
+                               L.BF16, h))
+        del xb, shb, scb, ob
+        nb = 2 * E * 2 + 2 * D * 4
+        S_ = n_sets(nb)
+        xl, ol = rnd(S_, E, dtype=bf), torch.empty(S_, E, device="cuda", dtype=bf)
         lw, lb = rnd(D), rnd(D)
-        ms = _event_ms(lambda: L.call("oasis_layernorm", L.ptr(xb), L.ptr(lw), L.ptr(lb), 0, L.ptr(ob), M, D, 1e-6,
-                                      L.BF16, L.stream_handle(stream)), stream, n)
-        entry("layernorm (bf16, affine)", M, ms, 2 * M * D * 2 + 2 * D * 4)
-
-        qkv = rnd(M, 3 * D, dtype=torch.bfloat16)
+        timed("layernorm (bf16, affine)", M, nb,
+              lambda i: L.call("oasis_layernorm", L.ptr(xl[i]), L.ptr(lw), L.ptr(lb), 0, L.ptr(ol[i]), M, D, 1e-6,
+                               L.BF16, h))
+        del xl, ol
+        nb = 6 * E * 2 + 2 * P * D * 4
+        S_ = n_sets(nb)
+        qkv = rnd(S_, 3 * E, dtype=bf)
+        q, k, v = (torch.empty(S_, E, device="cuda", dtype=bf) for _ in range(3))
         cs, sn = rnd(P, D), rnd(P, D)
-        q, k, v = (torch.empty(M, D, device="cuda", dtype=torch.bfloat16) for _ in range(3))
-        ms = _event_ms(lambda: L.call("oasis_rope_layout", L.ptr(qkv), 3 * D, L.ptr(cs), L.ptr(sn), D, 64, 1, P,
-                                      L.ptr(q), L.ptr(k), L.ptr(v), M, P, D // 64, 64, 0, L.BF16,
-                                      L.stream_handle(stream)), stream, n)
-        entry("rope_layout (bf16, heads-first)", M, ms, 6 * M * D * 2 + 2 * P * D * 4)
+        timed("rope_layout (bf16, heads-first)", M, nb,
+              lambda i: L.call("oasis_rope_layout", L.ptr(qkv[i]), 3 * D, L.ptr(cs), L.ptr(sn), D, 64, 1, P,
+                               L.ptr(q[i]), L.ptr(k[i]), L.ptr(v[i]), M, P, D // 64, 64, 0, L.BF16, h))
+        del qkv, q, k, v
     torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return out
 
 
@@ -350,6 +416,8 @@ def main():
     ap.add_argument("--no-frame", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the config-4 (fp8, 8 streams x T=4) lines")
     ap.add_argument("--probe", action="store_true", help="short run of the roofline kernels for counter passes")
+    ap.add_argument("--probe-kernels", action="store_true",
+                    help="short run of the step, VAE and bandwidth kernels for counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build targets one MI355X; multi-GPU runs are not part of it "
@@ -361,6 +429,9 @@ def main():
     pkg = __graft_entry__.load_package()
     if args.probe:
         probe(pkg)
+        return
+    if args.probe_kernels:
+        kernel_probe(pkg)
         return
     import oracle
     synth = pkg.synth

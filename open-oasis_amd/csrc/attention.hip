@@ -14,6 +14,8 @@
 //   group. At T=2 each group is 2 queries x 2 keys, far below an MFMA tile, so it is a
 //   VALU kernel: 16 lanes per group, 4 head dims per lane, dot products by 16-lane
 //   butterfly reductions and an online softmax over the causal keys.
+#include <type_traits>
+
 #include "oasis_common.h"
 
 namespace {
@@ -63,13 +65,20 @@ struct AttnArgs {
 // sequence once, with no barrier in the key loop) and consumed in KC-key chunks.
 // V^T is built from 8x8 blocks: a thread loads 8 key rows x 8 dims, transposes them in
 // registers and writes 8 16-byte LDS rows.
-template <int NW, int KC, int KS, typename T>
-__global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q, const T* __restrict__ K,
-                                                        const T* __restrict__ V, T* __restrict__ O, AttnArgs a) {
+// KSPLIT = 2: two waves per 16-query block, each taking every other key chunk (two waves
+// per SIMD, half the serial softmax chain each); their running (max, sum, output) states
+// are merged through LDS at the end.
+// PLAIN: no bias and no causal mask (only keys past Lk are masked).
+template <int NW, int KC, int KS, typename T, int KSPLIT = 1, bool PLAIN = false>
+__global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                                                                 const T* __restrict__ V, T* __restrict__ O,
+                                                                 AttnArgs a) {
   static_assert(KS % KC == 0 && KC % 32 == 0 && KS % 8 == 0, "chunking");
+  static_assert(KSPLIT == 1 || KSPLIT == 2, "key split");
+  static_assert(KSPLIT == 1 || KS * KPITCH * 2 >= NW * 64 * 18 * 4, "merge slots fit in the K staging");
   constexpr int VPITCH = KS + 8;
   constexpr int KT = KC / 16;   // 16-key tiles per chunk
-  constexpr int NT = NW * 64;
+  constexpr int NT = NW * KSPLIT * 64;
   constexpr int KCH = KS * 8;             // 16-byte K chunks per stage
   constexpr int VBL = KS;                 // 8x8 V blocks per stage (KS/8 key blocks x 8 dim blocks)
   constexpr int KPER = (KCH + NT - 1) / NT;
@@ -77,8 +86,9 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
   __shared__ __attribute__((aligned(16))) bf16 Ks[KS * KPITCH];
   __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wq = wave % NW, wk = wave / NW;  // query block, key-chunk parity
   const int bh = blockIdx.y;
-  const int q0 = (blockIdx.x * NW + wave) * 16;
+  const int q0 = (blockIdx.x * NW + wq) * 16;
   const int lr = lane & 15, g = lane >> 4;
   const T* Qb = Q + (int64_t)bh * a.q_bh;
   const T* Kb = K + (int64_t)bh * a.kv_bh;
@@ -136,7 +146,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
     __syncthreads();
     if (q0 >= a.Lq) continue;
 
-  for (int kc0 = ks0; kc0 < min(ks0 + KS, a.Lk); kc0 += KC) {
+  for (int kc0 = ks0 + wk * KC; kc0 < min(ks0 + KS, a.Lk); kc0 += KC * KSPLIT) {
     const int kl = kc0 - ks0;  // chunk offset inside the staged keys
     // S^T for KT key tiles of 16: s[kt][i] = score(key kc0 + kt*16 + 4g + i, query my_q)
     float s[KT][4];
@@ -150,8 +160,8 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
       for (int i = 0; i < 4; ++i) {
         const int key = kc0 + kt * 16 + 4 * g + i;
         float x = acc[i] * a.scale_log2;
-        if (a.bias && key < a.Lk && my_q < a.Lq) x += a.bias[(int64_t)my_q * a.Lk + key] * LOG2E;
-        if (key >= a.Lk || (a.causal && key > my_q)) x = -INFINITY;
+        if (!PLAIN && a.bias && key < a.Lk && my_q < a.Lq) x += a.bias[(int64_t)my_q * a.Lk + key] * LOG2E;
+        if (key >= a.Lk || (!PLAIN && a.causal && key > my_q)) x = -INFINITY;
         s[kt][i] = x;
       }
     }
@@ -164,13 +174,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m - m_use);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
     float ps = 0.f;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[kt][i] = exp2f(s[kt][i] - m_use);
+        s[kt][i] = __builtin_amdgcn_exp2f(s[kt][i] - m_use);
         ps += s[kt][i];
       }
     ps += __shfl_xor(ps, 16, 64);
@@ -203,6 +213,29 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
     }
   }
   }
+  if (KSPLIT > 1) {
+    // lane-wise merge: both waves of a query block hold query lr's state in the same lanes
+    __syncthreads();  // every wave is done with the staged K / V^T
+    float* slot = reinterpret_cast<float*>(Ks) + (wq * 64 + lane) * 18;
+    if (wk == 1) {
+      slot[0] = m;
+      slot[1] = lsum;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) slot[2 + dt * 4 + i] = o[dt][i];
+    }
+    __syncthreads();
+    if (wk == 1) return;
+    const float m2 = slot[0], m_new = fmaxf(m, m2);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float a1 = __builtin_amdgcn_exp2f(m - m_use), a2 = __builtin_amdgcn_exp2f(m2 - m_use);
+    lsum = lsum * a1 + slot[1] * a2;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] = o[dt][i] * a1 + slot[2 + dt * 4 + i] * a2;
+  }
   if (q0 >= a.Lq || my_q >= a.Lq) return;
   const float inv = 1.0f / lsum;
   const int f = bh / a.H, h = bh - f * a.H;
@@ -215,45 +248,59 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(const T* __restrict__ Q,
   }
 }
 
+// PLAIN variants (no bias, not causal) exist for bf16, the dtype of the DiT and VAE paths
+template <int NW, int KC, int KS, typename T, int KSPLIT = 1>
+void flash_go(dim3 g, const T* q, const T* k, const T* v, T* o, const AttnArgs& a, hipStream_t s) {
+  const dim3 b(NW * KSPLIT * 64);
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (!a.bias && !a.causal) {
+      hipLaunchKernelGGL((flash_kernel<NW, KC, KS, T, KSPLIT, true>), g, b, 0, s, q, k, v, o, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((flash_kernel<NW, KC, KS, T, KSPLIT, false>), g, b, 0, s, q, k, v, o, a);
+}
+
 template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
   // staging: short sequences (up to 32 or 64 keys: the temporal windows) and whole frames (up
   // to 160 keys, 144 per DiT frame; up to 192) in one chunk; up to 576 keys (the VAE) staged at
-  // once (158 KB of LDS) and consumed in 64-key chunks; longer sequences in 576-key stages.
+  // once (158 KB of LDS) and consumed in 64-key chunks by two waves per query block; longer
+  // sequences in 576-key stages.
   // 144-query frames take 48 queries per workgroup, or with 256+ (frame, head) pairs all 144
   // (9 waves share one K/V staging).
+  const unsigned nb = (unsigned)n_bh;
   if (a.Lq <= 32 && a.Lk <= 32) {
-    hipLaunchKernelGGL((flash_kernel<2, 32, 32, T>), dim3(1, (unsigned)n_bh), dim3(128), 0, s, q, k, v, o, a);
+    flash_go<2, 32, 32>(dim3(1, nb), q, k, v, o, a, s);
     return oasis::check_launch("attention");
   }
   if (a.Lq <= 64 && a.Lk <= 64) {
-    hipLaunchKernelGGL((flash_kernel<4, 64, 64, T>), dim3(1, (unsigned)n_bh), dim3(256), 0, s, q, k, v, o, a);
+    flash_go<4, 64, 64>(dim3(1, nb), q, k, v, o, a, s);
     return oasis::check_launch("attention");
   }
   const int kind = a.Lk <= 160 ? 0 : (a.Lk <= 192 ? 1 : 2);
   if (a.Lq % 64 != 0 && a.Lq % 48 == 0) {
     if (kind == 0 && a.Lq % 144 == 0 && n_bh >= 256) {
-      hipLaunchKernelGGL((flash_kernel<9, 160, 160, T>), dim3((unsigned)(a.Lq / 144), (unsigned)n_bh), dim3(576), 0, s,
-                         q, k, v, o, a);
+      flash_go<9, 160, 160>(dim3((unsigned)(a.Lq / 144), nb), q, k, v, o, a, s);
     } else {
-      const dim3 g((unsigned)(a.Lq / 48), (unsigned)n_bh);
+      const dim3 g((unsigned)(a.Lq / 48), nb);
       if (kind == 0)
-        hipLaunchKernelGGL((flash_kernel<3, 160, 160, T>), g, dim3(192), 0, s, q, k, v, o, a);
+        flash_go<3, 160, 160>(g, q, k, v, o, a, s);
       else if (kind == 1)
-        hipLaunchKernelGGL((flash_kernel<3, 192, 192, T>), g, dim3(192), 0, s, q, k, v, o, a);
+        flash_go<3, 192, 192>(g, q, k, v, o, a, s);
       else
-        hipLaunchKernelGGL((flash_kernel<3, 64, 576, T>), g, dim3(192), 0, s, q, k, v, o, a);
+        flash_go<3, 64, 576, T, 2>(g, q, k, v, o, a, s);
     }
   } else {
-    const dim3 g((unsigned)((a.Lq + 63) / 64), (unsigned)n_bh);
+    const dim3 g((unsigned)((a.Lq + 63) / 64), nb);
     if (kind == 0)
-      hipLaunchKernelGGL((flash_kernel<4, 160, 160, T>), g, dim3(256), 0, s, q, k, v, o, a);
+      flash_go<4, 160, 160>(g, q, k, v, o, a, s);
     else if (kind == 1)
-      hipLaunchKernelGGL((flash_kernel<4, 192, 192, T>), g, dim3(256), 0, s, q, k, v, o, a);
+      flash_go<4, 192, 192>(g, q, k, v, o, a, s);
     else
-      hipLaunchKernelGGL((flash_kernel<4, 64, 576, T>), g, dim3(256), 0, s, q, k, v, o, a);
+      flash_go<4, 64, 576, T, 2>(g, q, k, v, o, a, s);
   }
   return oasis::check_launch("attention");
 }

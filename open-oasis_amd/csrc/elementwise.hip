@@ -4,7 +4,7 @@
 // adaln_matmul_expand and the standalone RoPE + head-split kernel.
 //
 // All of these are HBM-bound; they use grid-stride loops with one element (or one
-// 8-element group) per thread step and coalesced accesses.
+// 16-byte vector of each operand) per thread step and coalesced accesses.
 #include "oasis_common.h"
 
 namespace {
@@ -25,26 +25,78 @@ __device__ __forceinline__ void st<bf16>(bf16* p, int64_t i, float v) { p[i] = f
 
 enum { EW_SILU = 0, EW_MODULATE = 1, EW_GATED = 2, EW_BIAS_GATED = 3 };
 
+template <int OP>
+__device__ __forceinline__ float ew_op(float a, float b, float c, float d) {
+  if (OP == EW_SILU) return silu(a);
+  if (OP == EW_MODULATE) return a * (c + 1.0f) + b;  // x * (scale + 1) + shift ; a=x b=shift c=scale
+  if (OP == EW_GATED) return a + b * c;              // residual + x * gate ; a=res b=x c=gate
+  return a + (b + c) * d;                            // residual + (x + bias) * gate ; a=res b=x c=bias d=gate
+}
+
+// one element per thread step (any alignment)
 template <typename T, int OP>
 __global__ void ew_kernel(const T* a, const T* b, const T* c, const T* d, T* out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    float r;
-    if (OP == EW_SILU) {
-      r = silu(ld<T>(a, i));
-    } else if (OP == EW_MODULATE) {  // x * (scale + 1) + shift ; a=x b=shift c=scale
-      r = ld<T>(a, i) * (ld<T>(c, i) + 1.0f) + ld<T>(b, i);
-    } else if (OP == EW_GATED) {  // residual + x * gate ; a=res b=x c=gate
-      r = ld<T>(a, i) + ld<T>(b, i) * ld<T>(c, i);
-    } else {  // residual + (x + bias) * gate ; a=res b=x c=bias d=gate
-      r = ld<T>(a, i) + (ld<T>(b, i) + ld<T>(c, i)) * ld<T>(d, i);
+    const float vb = OP != EW_SILU ? ld<T>(b, i) : 0.f, vc = OP != EW_SILU ? ld<T>(c, i) : 0.f;
+    const float vd = OP == EW_BIAS_GATED ? ld<T>(d, i) : 0.f;
+    st<T>(out, i, ew_op<OP>(ld<T>(a, i), vb, vc, vd));
+  }
+}
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<float> {
+  using V = f32x4;
+  static constexpr int N = 4;
+};
+template <>
+struct Vec16<bf16> {
+  using V = bf16x8;
+  static constexpr int N = 8;
+};
+
+// 16 bytes of every operand per thread step (all pointers 16-byte aligned); the n % N tail
+// elements one per thread
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void ew_vec_kernel(const T* a, const T* b, const T* c, const T* d, T* out,
+                                                     int64_t n) {
+  using V = typename Vec16<T>::V;
+  constexpr int N = Vec16<T>::N;
+  const int64_t ng = n / N, stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t g = t0; g < ng; g += stride) {
+    const V va = reinterpret_cast<const V*>(a)[g];
+    V vb = va, vc = va, vd = va, r;
+    if (OP != EW_SILU) {
+      vb = reinterpret_cast<const V*>(b)[g];
+      vc = reinterpret_cast<const V*>(c)[g];
     }
-    st<T>(out, i, r);
+    if (OP == EW_BIAS_GATED) vd = reinterpret_cast<const V*>(d)[g];
+#pragma unroll
+    for (int j = 0; j < N; ++j) r[j] = (T)ew_op<OP>((float)va[j], (float)vb[j], (float)vc[j], (float)vd[j]);
+    reinterpret_cast<V*>(out)[g] = r;
+  }
+  for (int64_t i = ng * N + t0; i < n; i += stride) {
+    const float vb = OP != EW_SILU ? ld<T>(b, i) : 0.f, vc = OP != EW_SILU ? ld<T>(c, i) : 0.f;
+    const float vd = OP == EW_BIAS_GATED ? ld<T>(d, i) : 0.f;
+    st<T>(out, i, ew_op<OP>(ld<T>(a, i), vb, vc, vd));
   }
 }
 
 unsigned ew_grid(int64_t n) {
   int64_t g = (n + 255) / 256;
   return (unsigned)(g > 8192 ? 8192 : (g < 1 ? 1 : g));
+}
+
+template <typename T, int OP>
+void ew_dispatch(const void* a, const void* b, const void* c, const void* d, void* out, int64_t n, hipStream_t s) {
+  const T *pa = (const T*)a, *pb = (const T*)b, *pc = (const T*)c, *pd = (const T*)d;
+  if (oasis_aligned(16, pa, pb, pc, pd, (const T*)out))
+    hipLaunchKernelGGL((ew_vec_kernel<T, OP>), dim3(ew_grid(n / Vec16<T>::N)), dim3(256), 0, s, pa, pb, pc, pd,
+                       (T*)out, n);
+  else
+    hipLaunchKernelGGL((ew_kernel<T, OP>), dim3(ew_grid(n)), dim3(256), 0, s, pa, pb, pc, pd, (T*)out, n);
 }
 
 template <int OP>
@@ -54,11 +106,9 @@ int ew_launch(const void* a, const void* b, const void* c, const void* d, void* 
   if (n == 0) return OASIS_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == OASIS_F32) {
-    hipLaunchKernelGGL((ew_kernel<float, OP>), dim3(ew_grid(n)), dim3(256), 0, s, (const float*)a,
-                       (const float*)b, (const float*)c, (const float*)d, (float*)out, n);
+    ew_dispatch<float, OP>(a, b, c, d, out, n, s);
   } else if (dtype == OASIS_BF16) {
-    hipLaunchKernelGGL((ew_kernel<bf16, OP>), dim3(ew_grid(n)), dim3(256), 0, s, (const bf16*)a,
-                       (const bf16*)b, (const bf16*)c, (const bf16*)d, (bf16*)out, n);
+    ew_dispatch<bf16, OP>(a, b, c, d, out, n, s);
   } else {
     oasis::set_error("%s: unsupported dtype %d", what, dtype);
     return OASIS_ERR_DTYPE;

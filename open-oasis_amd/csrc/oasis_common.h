@@ -93,8 +93,6 @@ OASIS_DEV float wave_max(float v) {
 }
 
 // ---- activations ------------------------------------------------------------
-// tanh-GELU written as x * sigmoid(2u): 0.5 x (1 + tanh(u)) == x / (1 + exp(-2u)),
-// u = sqrt(2/pi) (x + 0.044715 x^3).
 // tanh-GELU as x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3), i.e. x / (1 + 2^t) with
 // t = -2 u log2(e), on the hardware exp2 and reciprocal (about 1 ulp each; the results are
 // stored as bf16 or e4m3). Large |x| saturates to x or -0.

@@ -230,11 +230,14 @@ def test_ln_affine():
 
 
 # ---------------------------------------------------------------- attention
-@pytest.mark.parametrize("L_,F_", [(144, 2), (576, 2), (37, 2), (144, 64), (160, 2), (192, 2), (150, 64)])
+@pytest.mark.parametrize("L_,F_", [(144, 2), (576, 2), (37, 2), (144, 64), (160, 2), (192, 2), (150, 64),
+                                   (240, 2), (600, 1), (1152, 1)])
 def test_attention_heads_first(L_, F_):
     """Frames of L_ tokens: a whole frame staged at once (up to 160 or 192 keys), the VAE's
     576, a ragged 37; 64 frames x 4 heads (256 pairs) take the 9-wave one-workgroup-per-frame path
-    at L = 144."""
+    at L = 144. From 193 keys two waves share each 16-query block, each taking every other 64-key
+    chunk: 240 (48-query workgroups), 600 (a ragged second 576-key stage where only one of the
+    two waves has a chunk) and 1152 (two full stages)."""
     H = 4
     g = _gen(11 + L_)
     q, k, v = (torch.randn(F_ * H, L_, 64, generator=g).to(torch.bfloat16) for _ in range(3))
@@ -246,10 +249,13 @@ def test_attention_heads_first(L_, F_):
     assert_close(out, ref, 0.9999, 1e-2, "attention L=%d" % L_)
 
 
-@pytest.mark.parametrize("dtype,causal,bias", [(torch.float32, False, False), (torch.bfloat16, True, False),
-                                               (torch.float32, False, True)])
-def test_sdpa_surface(dtype, causal, bias):
-    nh, sq, skv = 6, 32, 32
+@pytest.mark.parametrize("dtype,causal,bias,n", [(torch.float32, False, False, 32), (torch.bfloat16, True, False, 32),
+                                                 (torch.float32, False, True, 32), (torch.bfloat16, True, False, 320),
+                                                 (torch.float32, False, True, 320), (torch.bfloat16, False, True, 320)])
+def test_sdpa_surface(dtype, causal, bias, n):
+    """n = 320: the key-split kernel with a causal mask (whole chunks masked for one of the two
+    waves of the first query blocks) and with the additive bias."""
+    nh, sq, skv = 6, n, n
     g = _gen(12)
     Q, K, V = (torch.randn(nh * sq, 64, generator=g).to(dtype) for _ in range(3))
     bmask = None
@@ -364,13 +370,15 @@ def test_small_linear_and_ddim_and_bridge():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_elementwise_surface(dtype):
-    n = 160 * 1024 + 3
+@pytest.mark.parametrize("n,off", [(160 * 1024 + 3, 0), (5, 0), (160 * 1024 + 3, 1)])
+def test_elementwise_surface(dtype, n, off):
+    """16-byte vectors with a ragged tail (off 0), fewer elements than one vector, and operands one
+    element off 16-byte alignment (off 1: the one-element-per-step kernel)."""
     g = _gen(16)
     a, b, c, d = (torch.randn(n, generator=g).to(dtype) for _ in range(4))
     code = L.F32 if dtype == torch.float32 else L.BF16
-    out = torch.zeros(n, device="cuda", dtype=dtype)
-    A, Bd, C, Dd = dev(a), dev(b), dev(c), dev(d)
+    out = torch.zeros(n + off, device="cuda", dtype=dtype)[off:]
+    A, Bd, C, Dd = (torch.cat([torch.zeros(off, dtype=dtype), t]).cuda()[off:] for t in (a, b, c, d))
     af, bf_, cf, df = a.float(), b.float(), c.float(), d.float()
     tol = 1e-6 if dtype == torch.float32 else 1e-2
     L.call("oasis_silu", L.ptr(A), L.ptr(out), n, code, stream())
