@@ -594,8 +594,12 @@ namespace oasis {
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
   (void)Kslice;
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
-  const bool big = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF || kind == OASIS_EPI_PARTIAL_F32;
-  return big || M >= 512 ? 24 : 32;
+  const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
+  // one 144-token frame (the K/V-cache steps): 96 x 32 tiles for FC1 (256 workgroups) and
+  // 32 x 64 split-K tiles (5 row tiles, none mostly empty) time fastest at M = 144
+  if (M <= 160 && gelu) return 35;
+  if (M <= 160 && kind == OASIS_EPI_PARTIAL_F32) return 23;
+  return gelu || kind == OASIS_EPI_PARTIAL_F32 || M >= 512 ? 24 : 32;
 }
 
 // Split-K count for the default tile of a large-token split-K product: K slices until the
