@@ -575,6 +575,9 @@ const TileCfg kTiles[] = {
     {288, 128, 1, 64, launch_big<288, 128, 2, 4, 2>, launch_big<288, 128, 2, 4, 2>},  // 48
     {144, 256, 1, 64, launch_big<144, 256, 1, 8, 2>, launch_big<144, 256, 1, 8, 2>},  // 49
     {256, 256, 1, 64, launch_big<256, 256, 2, 4, 2>, launch_big<256, 256, 2, 4, 2>},  // 50
+    // the 8-wave kernel's grouped tile order and per-wave staged epilogue on a 4-wave 96 x 64
+    // tile: faster than tile 24 for FC1 / FC2 below 2048 tokens and for every VAE projection
+    {96, 64, 1, 64, launch_big<96, 64, 2, 2, 4>, launch_big<96, 64, 2, 2, 4>},  // 51
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -591,15 +594,19 @@ namespace oasis {
 // product of the DiT (144 or 288 tokens); 96 x 128 register-ring tiles from 2048 tokens up.
 // From 2048 tokens up, the 8-wave 288-row tiles: 288 x 256 for N = 4096 (16 x 16 tiles at 4608
 // tokens), 288 x 192 for N = 3072 (16 x 16) and 288 x 128 otherwise (with 2 K slices at N = 1024).
+// Default tile per shape, from timings of each projection on MI355X with cold weights:
+//   - 2048+ tokens: the 8-wave tall tiles;
+//   - FC1 (GELU): 96 x 32 at one 144-token frame (256 workgroups), else tile 51;
+//   - split-K partials: 32 x 64 tiles for short K slices (O: 256 at 144 tokens, 512 at 288),
+//     tile 51 for the longer slices (FC2) and from 320 tokens up (the VAE's 576);
+//   - other epilogues (QKV + RoPE, plain stores): 32 x 64, tile 51 from 512 tokens.
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
-  (void)Kslice;
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
   const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
-  // one 144-token frame (the K/V-cache steps): 96 x 32 tiles for FC1 (256 workgroups) and
-  // 32 x 64 split-K tiles (5 row tiles, none mostly empty) time fastest at M = 144
-  if (M <= 160 && gelu) return 35;
-  if (M <= 160 && kind == OASIS_EPI_PARTIAL_F32) return 23;
-  return gelu || kind == OASIS_EPI_PARTIAL_F32 || M >= 512 ? 24 : 32;
+  if (gelu) return M <= 160 ? 35 : 51;
+  if (kind == OASIS_EPI_PARTIAL_F32)
+    return (M <= 160 && Kslice <= 256) || (M <= 320 && Kslice <= 512) ? 23 : 51;
+  return M >= 512 ? 51 : 32;
 }
 
 // Split-K count for the default tile of a large-token split-K product: K slices until the

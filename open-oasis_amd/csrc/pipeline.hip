@@ -223,12 +223,14 @@ namespace {
 // Split-K count for an O / FC2 GEMM (tile 0: 32 x 64): enough workgroups to cover the
 // 256 CUs, each split still a multiple of the 4-deep prefetch ring. From 2048 tokens up the
 // GEMM's own large-token tiles decide.
+// Split-K count of a partial-sum projection (O: K = D, FC2: K = 4D). Below 2048 tokens, from
+// timings on MI355X: O in 4 slices at one 144-token frame and 2 above, FC2 in 8 slices at
+// one frame and 4 above; fewer when max_splits or whole 64-wide K tiles per slice require it.
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t max_splits) {
+  (void)N;
   if (M >= 2048) return oasis::gemm_auto_splits(M, N, K, (int)std::min<int64_t>(max_splits, 8));
-  const int64_t tiles = ((M + 31) / 32) * ((N + 63) / 64);
-  const int64_t nk = K / 64;
-  int s = 1;
-  while (2 * s <= max_splits && 2 * s <= 8 && tiles * s < 512 && nk % (2 * s) == 0 && (nk / (2 * s)) % 4 == 0) s *= 2;
+  int s = K > 1024 ? (M <= 160 ? 8 : 4) : (M <= 160 ? 4 : 2);
+  while (s > 1 && (s > max_splits || (K / 64) % s != 0)) s /= 2;
   return s;
 }
 

@@ -422,7 +422,7 @@ def test_rope_layout_surface():
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(51)))
+@pytest.mark.parametrize("tile", list(range(52)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -435,10 +435,11 @@ def test_gemm_tile_configs(tile):
     assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
 
 
-@pytest.mark.parametrize("tile", list(range(23, 43)))
+@pytest.mark.parametrize("tile", list(range(23, 43)) + [51])
 def test_gemm_direct_lds_ragged(tile):
-    """The direct-to-LDS configurations on a ragged shape: K = 5 tiles (not a multiple of the
-    stage count), M and N not multiples of the tile, GELU epilogue and split-K slices."""
+    """The direct-to-LDS configurations (23-42, and 51 on the 8-wave kernel's code) on a ragged
+    shape: K = 5 tiles (not a multiple of the stage count), M and N not multiples of the tile,
+    GELU epilogue and split-K slices."""
     M, N, K = 300, 520, 320
     g = _gen(60 + tile)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)

@@ -64,6 +64,19 @@ def test_temporal_sub_block_config2():
     _check_sub_block(c["x"][0], c["cond"][0], w, "t", 32, "config2 temporal sub-block T=32")
 
 
+@pytest.mark.parametrize("kind,T", [("s", 1), ("t", 1), ("s", 4), ("t", 4), ("t", 13)])
+def test_sub_blocks_between_sizes(kind, T):
+    """Sub-blocks at the token counts between configs: one 144-token frame (the K/V-cache
+    steps' tile and split choices), 576 tokens (tile 51 with the QKV + RoPE epilogue in both
+    layouts) and 1872 tokens (the largest count below the 8-wave tall tiles)."""
+    c0, c2 = synth.config0(), synth.config2()
+    dr = synth.Draw(70 + T)
+    x, cond = dr.normal(T, 144, 1024), dr.normal(T, 1024)
+    src = c0["w"] if kind == "s" else c2["w"]
+    w = _single_block_dit(src, kind, spatial_freqs=c0["spatial_freqs"], temporal_freqs=c2["temporal_freqs"])
+    _check_sub_block(x, cond, w, kind, T, "%s sub-block T=%d" % (kind, T))
+
+
 @pytest.fixture(scope="module")
 def c1():
     c = synth.config1()
