@@ -578,6 +578,8 @@ const TileCfg kTiles[] = {
     // the 8-wave kernel's grouped tile order and per-wave staged epilogue on a 4-wave 96 x 64
     // tile: faster than tile 24 for FC1 / FC2 below 2048 tokens and for every VAE projection
     {96, 64, 1, 64, launch_big<96, 64, 2, 2, 4>, launch_big<96, 64, 2, 2, 4>},  // 51
+    {64, 64, 1, 64, launch_big<64, 64, 2, 2, 4>, launch_big<64, 64, 2, 2, 4>},    // 52
+    {144, 64, 1, 64, launch_big<144, 64, 3, 2, 4>, launch_big<144, 64, 3, 2, 4>},  // 53: 6 waves
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -596,17 +598,18 @@ namespace oasis {
 // tokens), 288 x 192 for N = 3072 (16 x 16) and 288 x 128 otherwise (with 2 K slices at N = 1024).
 // Default tile per shape, from timings of each projection on MI355X with cold weights:
 //   - 2048+ tokens: the 8-wave tall tiles;
-//   - FC1 (GELU): 96 x 32 at one 144-token frame (256 workgroups), else tile 51;
+//   - FC1 (GELU): 64 x 64 (tile 52) at one 144-token frame, 144 x 64 on 6 waves (tile 53)
+//     from 512 tokens (the VAE's 576), else 96 x 64 (tile 51);
 //   - split-K partials: 32 x 64 tiles for short K slices (O: 256 at 144 tokens, 512 at 288),
-//     tile 51 for the longer slices (FC2) and from 320 tokens up (the VAE's 576);
-//   - other epilogues (QKV + RoPE, plain stores): 32 x 64, tile 51 from 512 tokens.
+//     tile 51 for the longer slices (FC2) and from 320 tokens up;
+//   - other epilogues (QKV + RoPE, plain stores): 32 x 64, tile 52 from 512 tokens.
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
   const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
-  if (gelu) return M <= 160 ? 35 : 51;
+  if (gelu) return M <= 160 ? 52 : (M >= 512 ? 53 : 51);
   if (kind == OASIS_EPI_PARTIAL_F32)
     return (M <= 160 && Kslice <= 256) || (M <= 320 && Kslice <= 512) ? 23 : 51;
-  return M >= 512 ? 51 : 32;
+  return M >= 512 ? 52 : 32;
 }
 
 // Split-K count for the default tile of a large-token split-K product: K slices until the

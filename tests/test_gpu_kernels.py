@@ -422,7 +422,7 @@ def test_rope_layout_surface():
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(52)))
+@pytest.mark.parametrize("tile", list(range(54)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -435,9 +435,9 @@ def test_gemm_tile_configs(tile):
     assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
 
 
-@pytest.mark.parametrize("tile", list(range(23, 43)) + [51])
+@pytest.mark.parametrize("tile", list(range(23, 43)) + [51, 52, 53])
 def test_gemm_direct_lds_ragged(tile):
-    """The direct-to-LDS configurations (23-42, and 51 on the 8-wave kernel's code) on a ragged
+    """The direct-to-LDS configurations (23-42, and 51-53 on the 8-wave kernel's code) on a ragged
     shape: K = 5 tiles (not a multiple of the stage count), M and N not multiples of the tile,
     GELU epilogue and split-K slices."""
     M, N, K = 300, 520, 320
