@@ -10,7 +10,10 @@
 //     bf16 hi + lo pair,
 //     x = hi + lo to ~16 mantissa bits, and both halves go through the MFMA, so the
 //     result keeps fp32-level accuracy although the MFMA inputs are bf16;
-//   - every wave walks its own 16-row weight tiles, so each byte of W is read once.
+//   - every wave walks its own 16-row weight tiles, so each byte of W is read once;
+//   - small N (the conditioning MLP's 1024 outputs): the four waves of a workgroup share
+//     each tile, one K quarter each, and add their partial sums through LDS, so that 4x
+//     more waves stream the matrix and each one's dependent load chain is 4x shorter.
 #include <algorithm>
 
 #include "oasis_common.h"
@@ -20,15 +23,18 @@ namespace {
 constexpr int KSTEP = 64;   // k per pipeline step (two MFMAs)
 constexpr int UNROLL = 4;   // pipeline steps whose loads are issued together
 
-template <int RG>
+template <int RG, int KS>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, int R,
                                                    const bf16* __restrict__ W, int N, int K,
                                                    const float* __restrict__ b, float* __restrict__ out,
                                                    int64_t ld_out, int act_in, int act_out, int accumulate) {
+  static_assert(KS == 1 || KS == 2 || KS == 4, "waves per tile");
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   const int pitch = K + 8;  // bf16 elements per LDS row
   bf16* xh = reinterpret_cast<bf16*>(smem_raw);
   bf16* xl = xh + R * pitch;
+  // KS > 1: partial sums of the waves sharing a tile, after the x rows (16-byte aligned)
+  f32x4* red = reinterpret_cast<f32x4*>(smem_raw + ((2 * R * pitch * sizeof(bf16) + 15) & ~size_t(15)));
   for (int i = threadIdx.x; i < R * K; i += blockDim.x) {
     const int r = i / K, kk = i - r * K;
     float val = x[(int64_t)r * ldx + kk];
@@ -39,9 +45,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, lr = lane & 15, g = lane >> 4;
-  const int waves_total = gridDim.x * (blockDim.x >> 6);
+  const int lane = threadIdx.x & 63, lr = lane & 15, g = lane >> 4, wave = threadIdx.x >> 6;
+  // KS waves per tile, each over K / KS (a multiple of KSTEP)
+  const int tiles_per_block = (blockDim.x >> 6) / KS;
+  const int waves_total = gridDim.x * tiles_per_block;
   const int tiles = N >> 4;
+  const int kpart = wave % KS, kq = K / KS;
   // row group q covers conditioning rows 16q..16q+15; lanes whose row is >= R feed zeros to the
   // MFMA B operand
   bool live[RG];
@@ -56,17 +65,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   bf16x8 zero;
 #pragma unroll
   for (int j = 0; j < 8; ++j) zero[j] = f2bf(0.f);
-  for (int tile = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); tile < tiles; tile += waves_total) {
-    const bf16* wp = W + ((int64_t)tile * 16 + lr) * K + g * 8;
+  // KS > 1: every wave of the workgroup runs the same number of iterations (one tile per
+  // workgroup per iteration), so the barriers of the reduction below are uniform
+  for (int tile0 = blockIdx.x * tiles_per_block; tile0 < tiles; tile0 += waves_total) {
+    const int tile = tile0 + wave / KS;
+    const bool has_tile = tile < tiles;
+    if (KS == 1 && !has_tile) continue;  // no barriers to keep in step with
+    const bf16* wp = W + ((int64_t)(has_tile ? tile : 0) * 16 + lr) * K + g * 8;
     f32x4 acc[RG];
 #pragma unroll
     for (int q = 0; q < RG; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += KSTEP * UNROLL) {
+    const int kend = (kpart + 1) * kq;
+    for (int k0 = kpart * kq; k0 < kend; k0 += KSTEP * UNROLL) {
       bf16x8 w[UNROLL][2];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const int kk = k0 + u * KSTEP;
-        if (kk < K) {
+        if (kk < kend) {
           w[u][0] = *reinterpret_cast<const bf16x8*>(wp + kk);
           w[u][1] = *reinterpret_cast<const bf16x8*>(wp + kk + 32);
         }
@@ -74,7 +89,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const int kk = k0 + u * KSTEP;
-        if (kk < K) {
+        if (kk < kend) {
 #pragma unroll
           for (int q = 0; q < RG; ++q) {
             const bf16x8 h0 = live[q] ? *reinterpret_cast<const bf16x8*>(xhp[q] + kk) : zero;
@@ -89,6 +104,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         }
       }
     }
+    if (KS > 1) {  // wave kpart 0 of each tile adds the other K parts
+#pragma unroll
+      for (int q = 0; q < RG; ++q) red[(wave * RG + q) * 64 + lane] = acc[q];
+      __syncthreads();
+      if (kpart == 0) {
+#pragma unroll
+        for (int p = 1; p < KS; ++p)
+#pragma unroll
+          for (int q = 0; q < RG; ++q) acc[q] += red[((wave + p) * RG + q) * 64 + lane];
+      }
+      __syncthreads();  // the slots are rewritten by the next iteration
+      if (kpart != 0) continue;
+    }
+    if (!has_tile) continue;
     // acc[q][i] = out[r = 16q + lr][n = tile*16 + 4g + i]
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
@@ -136,13 +165,28 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   }
   if (R > per_pass) R = per_pass;
   const int tiles = (int)(N / 16);
-  const size_t smem = 2 * (size_t)R * (size_t)(K + 8) * sizeof(bf16);
+  // waves per tile: with fewer tiles than 2 per CU, the largest of 4, 2 that splits K into
+  // whole 64-wide steps
+  int ks = 1;
+  if (tiles < 512) ks = (K / KSTEP) % 4 == 0 ? 4 : ((K / KSTEP) % 2 == 0 ? 2 : 1);
+  const int rg = R > 16 ? 2 : 1;
+  const size_t xbytes = 2 * (size_t)R * (size_t)(K + 8) * sizeof(bf16);
+  const size_t smem = ks > 1 ? ((xbytes + 15) & ~size_t(15)) + (size_t)4 * rg * 64 * sizeof(f32x4) : xbytes;
   // every workgroup stages x once, so the grid stays at about two waves of resident
   // workgroups (LDS-limited) and each wave walks many weight tiles
   const int resident = (int)std::min<size_t>(8, (160 * 1024) / std::max<size_t>(smem, 1));
-  int blocks = (tiles + 3) / 4;
+  const int per_block = 4 / ks;
+  int blocks = (tiles + per_block - 1) / per_block;
   blocks = std::min(std::min(blocks, 2048), std::max(1, resident) * 256 * 2);
-  const void* fn = R > 16 ? reinterpret_cast<const void*>(&gemv_kernel<2>) : reinterpret_cast<const void*>(&gemv_kernel<1>);
+  const void* fn = nullptr;
+#define OASIS_GEMV_FN(RGV, KSV) if (rg == RGV && ks == KSV) fn = reinterpret_cast<const void*>(&gemv_kernel<RGV, KSV>)
+  OASIS_GEMV_FN(1, 1);
+  OASIS_GEMV_FN(1, 2);
+  OASIS_GEMV_FN(1, 4);
+  OASIS_GEMV_FN(2, 1);
+  OASIS_GEMV_FN(2, 2);
+  OASIS_GEMV_FN(2, 4);
+#undef OASIS_GEMV_FN
   if (smem > 65536) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) {
@@ -150,11 +194,19 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
       return OASIS_ERR_LAUNCH;
     }
   }
-  if (R > 16)
-    hipLaunchKernelGGL(gemv_kernel<2>, dim3(blocks), dim3(256), smem, static_cast<hipStream_t>(stream), x, ldx, (int)R,
-                       static_cast<const bf16*>(W), (int)N, (int)K, b, out, ld_out, act_in, act_out, accumulate);
-  else
-    hipLaunchKernelGGL(gemv_kernel<1>, dim3(blocks), dim3(256), smem, static_cast<hipStream_t>(stream), x, ldx, (int)R,
-                       static_cast<const bf16*>(W), (int)N, (int)K, b, out, ld_out, act_in, act_out, accumulate);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bf16* Wb = static_cast<const bf16*>(W);
+  const int Ri = (int)R, Ni = (int)N, Ki = (int)K;
+#define OASIS_GEMV_GO(RGV, KSV)                                                                                   \
+  if (rg == RGV && ks == KSV)                                                                                     \
+  hipLaunchKernelGGL((gemv_kernel<RGV, KSV>), dim3(blocks), dim3(256), smem, s, x, ldx, Ri, Wb, Ni, Ki, b, out,   \
+                     ld_out, act_in, act_out, accumulate)
+  OASIS_GEMV_GO(1, 1);
+  OASIS_GEMV_GO(1, 2);
+  OASIS_GEMV_GO(1, 4);
+  OASIS_GEMV_GO(2, 1);
+  OASIS_GEMV_GO(2, 2);
+  OASIS_GEMV_GO(2, 4);
+#undef OASIS_GEMV_GO
   return oasis::check_launch("gemv");
 }

@@ -299,8 +299,13 @@ def test_temporal_attention(T):
 @pytest.mark.parametrize("R,K,N,act_in,act_out,acc", [(2, 1024, 6144 * 2 + 2048, 1, 0, 0), (5, 256, 1024, 0, 1, 0),
                                                        (16, 1024, 1024, 0, 0, 1), (1, 64, 1024, 0, 0, 0),
                                                        (32, 1024, 2048, 1, 0, 0), (23, 256, 1024, 0, 1, 1),
-                                                       (70, 1024, 512, 0, 0, 1), (40, 2048, 256, 0, 0, 0)])
+                                                       (70, 1024, 512, 0, 0, 1), (40, 2048, 256, 0, 0, 0),
+                                                       (3, 128, 1040, 0, 0, 0), (4, 192, 528, 1, 0, 1),
+                                                       (17, 512, 1040, 0, 1, 0)])
 def test_gemv(R, K, N, act_in, act_out, acc):
+    """Large N: one wave per 16-row weight tile. Small N: 4 waves (K = 128: 2; K = 192: 1) share
+    each tile over K quarters, with tile counts that leave the last workgroup's second tile
+    slot empty (N = 1040 with 2 waves per tile)."""
     g = _gen(14 + R)
     x = torch.randn(R, K, generator=g)
     W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
