@@ -269,8 +269,9 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
   // to 160 keys, 144 per DiT frame; up to 192) in one chunk; up to 576 keys (the VAE) staged at
   // once (158 KB of LDS) and consumed in 64-key chunks by two waves per query block; longer
   // sequences in 576-key stages.
-  // 144-query frames take 48 queries per workgroup, or with 256+ (frame, head) pairs all 144
-  // (9 waves share one K/V staging).
+  // 144-query frames take 48 queries per workgroup (each 16-query block on two waves taking
+  // alternate 32-key chunks), or with 256+ (frame, head) pairs all 144 (9 waves share one K/V
+  // staging).
   const unsigned nb = (unsigned)n_bh;
   if (a.Lq <= 32 && a.Lk <= 32) {
     flash_go<2, 32, 32>(dim3(1, nb), q, k, v, o, a, s);
@@ -286,8 +287,8 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
       flash_go<9, 160, 160>(dim3((unsigned)(a.Lq / 144), nb), q, k, v, o, a, s);
     } else {
       const dim3 g((unsigned)(a.Lq / 48), nb);
-      if (kind == 0)
-        flash_go<3, 160, 160>(g, q, k, v, o, a, s);
+      if (kind == 0)  // two waves per query block over alternate 32-key chunks
+        flash_go<3, 32, 160, T, 2>(g, q, k, v, o, a, s);
       else if (kind == 1)
         flash_go<3, 192, 192>(g, q, k, v, o, a, s);
       else
