@@ -390,9 +390,12 @@ class Graph:
         L.call("oasis_graph_launch", self.exec, L.stream_handle(self.stream))
 
     def __del__(self):
-        if getattr(self, "exec", None) is not None and self.exec.value:
-            L.lib().oasis_graph_destroy(self.exec)
-            self.exec = None
+        # at interpreter exit the module globals may already be gone; the process teardown
+        # releases the graph then
+        if L is None or getattr(self, "exec", None) is None or not self.exec.value:
+            return
+        L.lib().oasis_graph_destroy(self.exec)
+        self.exec = None
 
 
 class DiTStep:
