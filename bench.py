@@ -24,10 +24,23 @@ BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
 
 
-def _event_ms(fn, stream, n):
-    """Average duration of fn() over n launches, HIP events on `stream`."""
+def _event_ms(fn, stream, n, graph=None):
+    """Average duration of fn() over n launches, HIP events on `stream`. With `graph` (the
+    package's Graph class) the n launches are captured in one hipGraph and the timed region is
+    one replay, so host-side launch cost cannot stretch kernels of a few microseconds."""
     import torch
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if graph is not None:
+        def many():
+            for _ in range(n):
+                fn()
+        g = graph(many, stream)
+        g.launch()
+        s.record(stream)
+        g.launch()
+        e.record(stream)
+        e.synchronize()
+        return s.elapsed_time(e) / n
     with torch.cuda.stream(stream):
         fn()
         s.record(stream)
@@ -44,7 +57,7 @@ def _event_ms(fn, stream, n):
 TRAFFIC = {"fc1": 15612665, "gemv": 409773602, "fc1_4608_bf16": 90728422, "fc1_4608_fp8": 46785135}
 
 
-def _fc1_timing(pkg, dit, ws, stream, n=100):
+def _fc1_timing(pkg, dit, ws, stream, n=100, graph=True):
     """The FC1 projection alone (same buffers, same tile choice as in the step), timed with HIP
     events on the step stream. Launch i uses the weights of sub-block i % 32: as in the step, each
     launch reads weights that 31 launches (268 MB of other weights, more than the 256 MB
@@ -63,13 +76,13 @@ def _fc1_timing(pkg, dit, ws, stream, n=100):
         B, e = eps[it[0] % n_sub]
         it[0] += 1
         L.call("oasis_gemm_bf16", A, D, B, D, M, Dm, D, ctypes.byref(e), L.stream_handle(stream))
-    ms = _event_ms(fc1, stream, n)
+    ms = _event_ms(fc1, stream, n, pkg.Graph if graph else None)
     flop = 2 * M * D * Dm
     nbytes = M * D * 2 + Dm * D * 2 + Dm * 4 + M * Dm * 2   # A, W, bias, out (bf16)
     return ms, flop, nbytes
 
 
-def _gemv_timing(pkg, dit, ws, stream, R=2, n=50):
+def _gemv_timing(pkg, dit, ws, stream, R=2, n=50, graph=True):
     """The adaLN skinny GEMM over every sub-block's adaLN weights (406 MB bf16)."""
     L = pkg._lib
 
@@ -77,7 +90,7 @@ def _gemv_timing(pkg, dit, ws, stream, R=2, n=50):
         L.call("oasis_gemv_bf16", L.ptr(ws.cond), dit.d, R, L.ptr(dit.ada_w), dit.ada_width, dit.d,
                L.ptr(dit.ada_b), L.ptr(ws.ada), dit.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
                L.stream_handle(stream))
-    ms = _event_ms(gemv, stream, n)
+    ms = _event_ms(gemv, stream, n, pkg.Graph if graph else None)
     nbytes = dit.ada_width * dit.d * 2 + R * dit.d * 4 + R * dit.ada_width * 4 + dit.ada_width * 4
     return ms, nbytes
 
@@ -96,8 +109,8 @@ def probe(pkg, n=10):
     step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
     step.run()
     torch.cuda.synchronize()
-    _fc1_timing(pkg, dit, step.ws, step.stream, n)
-    _gemv_timing(pkg, dit, step.ws, step.stream, n=n)
+    _fc1_timing(pkg, dit, step.ws, step.stream, n, graph=False)
+    _gemv_timing(pkg, dit, step.ws, step.stream, n=n, graph=False)
     del step, dit
     L = pkg._lib
     M, D, Dm = 4608, 1024, 4096
@@ -158,7 +171,7 @@ def kernel_probe(pkg, n=10):
     for _ in range(2):
         vae.decode_inplace(latent, frame, vws, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    bandwidth_kernels(pkg, n)
+    bandwidth_kernels(pkg, n, graph=False)
     src = torch.ones(64 << 20, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(n):
@@ -249,7 +262,7 @@ def config2(pkg, n=20):
     x0 = c["x"][0].reshape(T * dit.P, -1).cuda()
     ws.x[:T * dit.P].copy_(x0)
     torch.cuda.synchronize()
-    ms = _event_ms(lambda: dit.sub_blocks_inplace(ws, 1, T, ada, dit.ada_width, 1, 2, stream), stream, n)
+    ms = _event_ms(lambda: dit.sub_blocks_inplace(ws, 1, T, ada, dit.ada_width, 1, 2, stream), stream, n, pkg.Graph)
     M, D, Dm = T * dit.P, dit.d, dit.d_mlp
     proj = 2 * M * D * (3 * D + D + 2 * Dm)
     attn = 4 * dit.P * (dit.d // 64) * (T * (T + 1) // 2) * 64   # causal QK^T and PV over 32 frames
@@ -262,7 +275,7 @@ def config2(pkg, n=20):
             "floor_ms": round(flop / (BF16_PEAK_TFLOPS * 1e12) * 1e3, 4)}
 
 
-def bandwidth_kernels(pkg, n=200):
+def bandwidth_kernels(pkg, n=200, graph=True):
     """The memory-bound kernels on their own, D=1024, at the config-1 step's 288 rows and at
     4608 rows (configs 2 and 4), each timed with HIP events over n launches on one stream. Launch i
     works on operand set i % S, with S sets spanning at least 640 MB, so that every launch reads
@@ -297,8 +310,9 @@ def bandwidth_kernels(pkg, n=200):
         def fn():
             launch(it[0] % sets)
             it[0] += 1
-        ms = _event_ms(fn, stream, n)
-        ms_warm = _event_ms(lambda: launch(0), stream, n)
+        gcls = pkg.Graph if graph else None
+        ms = _event_ms(fn, stream, n, gcls)
+        ms_warm = _event_ms(lambda: launch(0), stream, n, gcls)
         gbs, gbs_warm = nbytes / (ms * 1e-3) / 1e9, nbytes / (ms_warm * 1e-3) / 1e9
         out.append({"kernel": name, "rows": rows, "bound": "hbm", "achieved": round(gbs, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -469,8 +483,10 @@ def main():
     fc1_ai = fc1_flop / fc1_bytes
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     fc1_gbs = fc1_bytes / (fc1_ms * 1e-3) / 1e9
-    fc1_roofline = {"kernel": "gemm_lds_kernel<96,64> (direct-to-LDS bf16 GEMM), FC1 projection + bias + tanh-GELU "
-                              "(M=288, N=4096, K=1024), the largest of the step's 128 GEMM launches"}
+    fc1_roofline = {"kernel": "gemm_big_kernel<96,64,2,2,4> (direct-to-LDS bf16 MFMA GEMM), FC1 projection + bias + "
+                              "tanh-GELU (M=288, N=4096, K=1024), the largest of the step's 128 GEMM launches; "
+                              "launch i uses sub-block i % 32's weights (cold, as in the step); 100 launches in "
+                              "one hipGraph"}
     if fc1_ai < ridge:
         fc1_roofline.update({"bound": "hbm", "achieved": round(fc1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(fc1_gbs / HBM_PEAK_GBS, 4)})
@@ -499,7 +515,7 @@ def main():
         "step_hbm_floor_ms": round(step_floor_ms, 4),
         "step_roofline_frac": round(step_floor_ms / ms_step, 4),
         "roofline": fc1_roofline,
-        "roofline_hbm": {"kernel": "gemv_kernel, adaLN projections of all 33 consumers (R=2 rows)",
+        "roofline_hbm": {"kernel": "gemv_kernel<1,1>, adaLN projections of all 33 consumers (R=2 rows), 50 launches in one hipGraph",
                          "bound": "hbm", "achieved": round(ada_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ada_gbs / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get("gemv"),
                          "avg_launch_ms": round(ada_ms, 5), "algorithmic_bytes": ada_bytes},
