@@ -265,6 +265,25 @@ int oasis_temporal_attention(const void* q, const void* k, const void* v, void* 
                              int64_t B, int64_t T, int64_t P, int64_t n_heads, float scale,
                              oasis_stream_t stream);
 
+/* Temporal sub-block front half for a two-frame window in one launch: QKV projection,
+ * temporal RoPE and causal attention over the frames of each (stream, position, head).
+ *   h: bf16 LN output [B*T*P, ldh] (row (b*T + t)*P + p); w_qkv: bf16 [3D, D], D = 64 n_heads;
+ *   out: bf16 [B*T*P, D] token-major attention output; t_cos / t_sinp: fp32 temporal RoPE
+ *   tables [>= 2][64] (row = RoPE position, sinp with the rotate_half sign);
+ *   k_cache / v_cache: bf16 [B][P][n_heads][2][64] or both NULL.
+ * T = 2: both frames (positions 0, 1); query frame 0 attends to its own key, query frame 1 to
+ *   both. With a cache, slot t receives frame t's rotated K and its V.
+ * T = 1: the current frame at RoPE position 1 attends to cache slot 0 (the context frame's
+ *   rotated K and V) and to itself; the cache is read only.
+ * q, k and v are rounded to bf16 before the attention, as oasis_temporal_attention sees them.
+ * P must be a multiple of 16. (run_sub_block's temporal qkv linear + rope_temporal +
+ * sdpa_causal, oasis_inference.py:1060-1151, and run_sub_block_t1's, oasis_inference.py:
+ * 1218-1352.) */
+int oasis_temporal_qkv_attention(const void* h, int64_t ldh, const void* w_qkv, void* out, int64_t B,
+                                 int64_t T, int64_t P, int64_t n_heads, const float* t_cos,
+                                 const float* t_sinp, void* k_cache, void* v_cache, float scale,
+                                 oasis_stream_t stream);
+
 enum { OASIS_ACT_NONE = 0, OASIS_ACT_SILU = 1 };
 
 /* Skinny GEMM for R <= 1024 rows (one pass over W per 16 rows):

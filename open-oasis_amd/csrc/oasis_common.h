@@ -45,6 +45,14 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
 // each group and writes it as a single frame: out [B*P, n_heads*64].
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
                        int64_t n_heads, float scale, int q_frame, hipStream_t stream);
+// QKV projection + temporal RoPE + causal attention of a two-frame temporal window in one
+// kernel (temporal_qkv.hip). A: LN output [B*T*P, lda]; W: QKV weight [3D, D] (D = 64 H);
+// out: attention output [B*T*P, D]. T = 2: both frames (kc / vc, optional, receive both frames'
+// rotated K and V as cache slots 0 and 1); T = 1: the current frame (RoPE position 1)
+// against cache slot 0. The cache is [B][P][H][2][64] bf16. P must be a multiple of 16.
+int temporal_qkv_attention(const __bf16* A, int64_t lda, const __bf16* W, __bf16* out, int64_t B, int64_t T,
+                           int64_t P, int64_t H, const float* t_cos, const float* t_sinp, __bf16* kc, __bf16* vc,
+                           float scale, hipStream_t stream);
 }  // namespace oasis
 
 #define OASIS_REQUIRE(cond, code, ...)          \

@@ -84,6 +84,7 @@ struct Plan {
   int tile[ROLE_N];
   int splits[ROLE_N];
   bool overlap;
+  bool fused_temporal;  // two-frame temporal windows on temporal_qkv.hip (OASIS_TEMPORAL_FUSED=0: off)
 };
 
 const Plan& plan() {
@@ -94,6 +95,7 @@ const Plan& plan() {
       q.splits[i] = 0;
     }
     q.overlap = false;
+    q.fused_temporal = true;
     static const char* names[ROLE_N] = {"qkv", "o", "fc1", "fc2", "vqkv", "vo", "vfc1", "vfc2"};
     if (const char* env = getenv("OASIS_GEMM_PLAN")) {
       std::string str(env);
@@ -116,6 +118,7 @@ const Plan& plan() {
       }
     }
     if (const char* env = getenv("OASIS_ADALN_OVERLAP")) q.overlap = atoi(env) != 0;
+    if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env) != 0;
     return q;
   }();
   return p;
@@ -318,52 +321,64 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
-    bf16* kc = nullptr;
-    bf16* vc = nullptr;
-    int qf = -1;  // temporal query frame (-1: all)
-    qkv.q = buf->q;
-    qkv.k = buf->k;
-    qkv.v = buf->v;
-    if (spatial) {  // heads-first per frame: [(b*T + t)*H + h][p][64]
-      qkv.s_b = T * H * P * 64;
-      qkv.s_t = H * P * 64;
-      qkv.s_h = P * 64;
-      qkv.s_p = 64;
-      qkv.rope_cos = w->s_cos;
-      qkv.rope_sinp = w->s_sinp;
-      qkv.rope_by_frame = 0;
-    } else if (kv.mode == KV_NONE) {  // grouped by position: [b][p][h][t][64]
-      qkv.s_b = P * H * T * 64;
-      qkv.s_p = H * T * 64;
-      qkv.s_h = T * 64;
-      qkv.s_t = 64;
-      qkv.rope_cos = w->t_cos;
-      qkv.rope_sinp = w->t_sinp;
-      qkv.rope_by_frame = 1;
-    } else {  // the cache's 2-slot layout [b][p][h][2][64]; T=1 passes write one slot
-      kc = kv.k + (j / 2) * kv.sub_stride;
-      vc = kv.v + (j / 2) * kv.sub_stride;
-      const int slot = kv.mode == KV_USE_T1 ? 1 : 0;
-      qf = kv.mode == KV_SAVE_T2 ? -1 : slot;
-      qkv.s_b = P * H * 2 * 64;
-      qkv.s_p = H * 2 * 64;
-      qkv.s_h = 2 * 64;
-      qkv.s_t = 64;
-      qkv.q = static_cast<bf16*>(buf->q) + slot * 64;
-      qkv.k = kc + slot * 64;
-      qkv.v = vc + slot * 64;
-      qkv.rope_cos = w->t_cos + slot * 64;  // RoPE position = slot + t
-      qkv.rope_sinp = w->t_sinp + slot * 64;
-      qkv.rope_by_frame = 1;
+    // two-frame temporal windows (the T = 2 step, the K/V-cache passes of the frame): QKV,
+    // RoPE and the causal attention in one kernel
+    if (!spatial && !fp8 && pl.fused_temporal && pl.tile[ROLE_QKV] < 0 && P % 16 == 0 &&
+        ((kv.mode == KV_NONE && T == 2) || kv.mode == KV_SAVE_T2 || kv.mode == KV_USE_T1)) {
+      bf16* kcj = kv.mode == KV_NONE ? nullptr : kv.k + (j / 2) * kv.sub_stride;
+      bf16* vcj = kv.mode == KV_NONE ? nullptr : kv.v + (j / 2) * kv.sub_stride;
+      OASIS_TRY(oasis::temporal_qkv_attention(static_cast<const bf16*>(buf->h), D,
+                                              static_cast<const bf16*>(w->qkv_w[j]), static_cast<bf16*>(buf->attn),
+                                              B, kv.mode == KV_USE_T1 ? 1 : 2, P, H, w->t_cos, w->t_sinp, kcj, vcj,
+                                              kAttnScale, s));
+    } else {
+      bf16* kc = nullptr;
+      bf16* vc = nullptr;
+      int qf = -1;  // temporal query frame (-1: all)
+      qkv.q = buf->q;
+      qkv.k = buf->k;
+      qkv.v = buf->v;
+      if (spatial) {  // heads-first per frame: [(b*T + t)*H + h][p][64]
+        qkv.s_b = T * H * P * 64;
+        qkv.s_t = H * P * 64;
+        qkv.s_h = P * 64;
+        qkv.s_p = 64;
+        qkv.rope_cos = w->s_cos;
+        qkv.rope_sinp = w->s_sinp;
+        qkv.rope_by_frame = 0;
+      } else if (kv.mode == KV_NONE) {  // grouped by position: [b][p][h][t][64]
+        qkv.s_b = P * H * T * 64;
+        qkv.s_p = H * T * 64;
+        qkv.s_h = T * 64;
+        qkv.s_t = 64;
+        qkv.rope_cos = w->t_cos;
+        qkv.rope_sinp = w->t_sinp;
+        qkv.rope_by_frame = 1;
+      } else {  // the cache's 2-slot layout [b][p][h][2][64]; T=1 passes write one slot
+        kc = kv.k + (j / 2) * kv.sub_stride;
+        vc = kv.v + (j / 2) * kv.sub_stride;
+        const int slot = kv.mode == KV_USE_T1 ? 1 : 0;
+        qf = kv.mode == KV_SAVE_T2 ? -1 : slot;
+        qkv.s_b = P * H * 2 * 64;
+        qkv.s_p = H * 2 * 64;
+        qkv.s_h = 2 * 64;
+        qkv.s_t = 64;
+        qkv.q = static_cast<bf16*>(buf->q) + slot * 64;
+        qkv.k = kc + slot * 64;
+        qkv.v = vc + slot * 64;
+        qkv.rope_cos = w->t_cos + slot * 64;  // RoPE position = slot + t
+        qkv.rope_sinp = w->t_sinp + slot * 64;
+        qkv.rope_by_frame = 1;
+      }
+      OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
+                     s));
+      if (spatial)
+        OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
+      else if (kv.mode == KV_NONE)
+        OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
+      else
+        OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s));
     }
-    OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
-                   s));
-    if (spatial)
-      OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
-    else if (kv.mode == KV_NONE)
-      OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
-    else
-      OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s));
     if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     // O projection as split-K partials; bias + gated residual + LN + modulate fused after
     OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import L, assert_close, bf, cuda, stream, sync
+from helpers import L, assert_close, bf, cuda, pkg, stream, sync
 
 pytestmark = pytest.mark.gpu
 
@@ -293,6 +293,47 @@ def test_temporal_attention(T):
     assert_close(out, ref, 0.9999, 1e-2, "temporal T=%d" % T)
     if T == 1:  # a single causal key: out == v exactly (bf16 round trip)
         assert torch.equal(out.cpu(), v.permute(0, 3, 1, 2, 4).reshape(B_ * T * P, H * 64))
+
+
+@pytest.mark.parametrize("B_,T_", [(1, 2), (2, 2), (1, 1), (3, 1)])
+def test_temporal_qkv_attention(B_, T_):
+    """QKV projection + temporal RoPE + causal attention of a two-frame window in one kernel,
+    against the oracle's temporal branch. T = 2: both frames, with the K/V cache written
+    (slot t = frame t's rotated K and its V). T = 1: the current frame (RoPE position 1) against
+    a cache whose slot 0 holds the context frame's rotated K and V; the cache is read only."""
+    P, H = 144, 4
+    D = 64 * H
+    g = _gen(170 + 10 * B_ + T_)
+    h = torch.randn(B_ * T_ * P, D, generator=g).to(torch.bfloat16)
+    W = (torch.randn(3 * D, D, generator=g) * 0.05).to(torch.bfloat16)
+    cos, sp = oracle.rope_cos_sinperm(oracle.temporal_rope_angles(pkg.synth.theta_freqs(32, 64), 2), 64)
+    kc0 = (torch.randn(B_, P, H, 2, 64, generator=g) * 2).to(torch.bfloat16)
+    vc0 = torch.randn(B_, P, H, 2, 64, generator=g).to(torch.bfloat16)
+    kc, vc = dev(kc0), dev(vc0)
+    out = torch.zeros(B_ * T_ * P, D, device="cuda", dtype=torch.bfloat16)
+    L.call("oasis_temporal_qkv_attention", L.ptr(dev(h)), D, L.ptr(dev(W)), L.ptr(out), B_, T_, P, H,
+           L.ptr(dev(cos.contiguous())), L.ptr(dev(sp.contiguous())), L.ptr(kc), L.ptr(vc), 0.125, stream())
+    sync()
+    qkv = (h.float() @ W.float().t()).reshape(B_, T_, P, 3 * D)
+    q, k, v = qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:]
+    got = out.cpu().reshape(B_, T_, P, D)
+    if T_ == 2:
+        for b in range(B_):
+            ref = oracle.temporal_attention(q[b], k[b], v[b], cos, sp, H)          # [T, P, D]
+            assert_close(got[b], ref, 0.9999, 1e-2, "temporal qkv T=2 stream %d" % b)
+        kr = oracle.apply_rope_swap(k.reshape(B_, 2, P, H, 64), cos[None, :, None, None, :],
+                                    sp[None, :, None, None, :])
+        assert_close(kc.cpu(), kr.permute(0, 2, 3, 1, 4), 0.99999, 1e-2, "temporal qkv cache K")
+        assert_close(vc.cpu(), v.reshape(B_, 2, P, H, 64).permute(0, 2, 3, 1, 4), 0.99999, 1e-2, "cache V")
+    else:
+        qh = oracle.apply_rope_swap(q.reshape(B_, P, H, 64), cos[1], sp[1])
+        k1 = oracle.apply_rope_swap(k.reshape(B_, P, H, 64), cos[1], sp[1])
+        keys = torch.stack([kc0[:, :, :, 0].float(), k1], 3)                       # [B, P, H, 2, 64]
+        vals = torch.stack([vc0[:, :, :, 0].float(), v.reshape(B_, P, H, 64)], 3)
+        p = torch.softmax((qh[:, :, :, None, :] * keys).sum(-1) / 8.0, -1)          # [B, P, H, 2]
+        ref = (p[..., None] * vals).sum(3).reshape(B_, P, D)
+        assert_close(got[:, 0], ref, 0.9999, 1e-2, "temporal qkv T=1")
+        assert torch.equal(kc.cpu(), kc0) and torch.equal(vc.cpu(), vc0), "T=1 must not write the cache"
 
 
 # ---------------------------------------------------------------- skinny GEMM
