@@ -548,7 +548,9 @@ int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* bu
  *   t, action: fp32 [n_frames * (1 + n_steps)] and [n_frames * (1 + n_steps), ext_dim_pad]:
  *        frame f's rows at f*(1 + n_steps), row 0 its context frame, row 1 + i step i;
  *   tfreq/hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
- *   frames: fp32 [n_frames, 3, H, W]; other arguments as in oasis_ddim_frame. n_frames <= 64.
+ *   frames: fp32 [n_frames, 3, H, W], or NULL for the DiT half only (the chunks are the
+ *        output; vbuf and latent may then be NULL; oasis_video_decode is the other half);
+ *   other arguments as in oasis_ddim_frame. n_frames <= 64.
  * The calls into one (w, buf) pair must not overlap. (The interactive loop's context roll,
  * oasis_inference.py:2296-2306, with play.py:241-531's per-frame DDIM + decode.) */
 int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
@@ -558,6 +560,16 @@ int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* 
                        const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
                        float* v_out, float* latent, float* frames, int overlap_decode,
                        oasis_stream_t stream);
+
+/* The decode half of oasis_video_frames: for f < n_frames, the bridge of chunks[f] (denoised
+ * latents fp32 [P, 64], (p,q,c) columns) into latent (fp32 [4P, vae latent_dim] scratch), then
+ * the VAE decode into frames[f] (fp32 [3, H, W], in [-1, 1]). Run on a second stream while the
+ * next batch's oasis_video_frames(frames = NULL) runs on the first, the decodes overlap the
+ * DiT steps. (bridge_unpatchify + vae_decode_forward + vae_unpatchify per frame,
+ * oasis_inference.py:1651-1709,1546-1645; play.py:241-531's per-frame decode.) */
+int oasis_video_decode(const oasis_dit_weights_t* w, const oasis_vae_weights_t* vw,
+                       const oasis_vae_buffers_t* vbuf, int64_t n_frames, const float* chunks,
+                       float* latent, float* frames, oasis_stream_t stream);
 
 /* ---- hipGraph capture of any sequence of the calls above on one stream ---------
  * Replaces ttnn.begin_trace_capture / end_trace_capture / execute_trace / release_trace

@@ -732,8 +732,9 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
                                   float* ctx_z, float* v_out, float* latent, float* frames, int overlap_decode,
                                   oasis_stream_t stream) {
   OASIS_TRY(frame_args(w, buf, vw, n_steps));
-  OASIS_REQUIRE(vbuf && chunks && ctx_patches && t && action && coeffs && tfreq && hid && cond && ada && ctx_z &&
-                    v_out && latent && frames,
+  const bool decode = frames != nullptr;  // frames == NULL: the DiT half only
+  OASIS_REQUIRE(chunks && ctx_patches && t && action && coeffs && tfreq && hid && cond && ada && ctx_z && v_out &&
+                    (!decode || (vbuf && latent)),
                 OASIS_ERR_NULL, "video_frames: null pointer");
   OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_frames: n_frames must be in [1, %d]",
                 OASIS_MAX_SUB);
@@ -746,13 +747,14 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
   OASIS_TRY(oasis_gemv_bf16(cond, D, n_frames * R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE,
                             0, stream));
   SideStream* ss = nullptr;
-  if (overlap_decode) OASIS_TRY(side_stream(&ss));
+  if (overlap_decode && decode) OASIS_TRY(side_stream(&ss));
   for (int64_t f = 0; f < n_frames; ++f) {
     // context = the previous frame's denoised latent (the rolled context window)
     const float* ctx = f == 0 ? ctx_patches : chunks + (f - 1) * fsz;
     OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
     OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out, nullptr,
                           stream));
+    if (!decode) continue;
     // bridge + VAE of frame f, in order or on the side stream overlapping frame f + 1's DiT
     hipStream_t ds = s;
     if (ss) {
@@ -766,6 +768,24 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
   }
   if (ss && (hipEventRecord(ss->fork, ss->s) != hipSuccess || hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess))
     return oasis::check_launch("video_frames join");
+  return OASIS_OK;
+}
+
+extern "C" int oasis_video_decode(const oasis_dit_weights_t* w, const oasis_vae_weights_t* vw,
+                                  const oasis_vae_buffers_t* vbuf, int64_t n_frames, const float* chunks, float* latent,
+                                  float* frames, oasis_stream_t stream) {
+  OASIS_TRY(check_dit(w));
+  OASIS_REQUIRE(vw && vbuf && chunks && latent && frames, OASIS_ERR_NULL, "video_decode: null pointer");
+  OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_decode: n_frames must be in [1, %d]",
+                OASIS_MAX_SUB);
+  const int64_t P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4, fsz = (int64_t)w->patch_dim * P;
+  OASIS_REQUIRE((int64_t)vw->grid_h * vw->grid_w == 4 * P && vw->latent_dim >= C, OASIS_ERR_SHAPE,
+                "video_decode: VAE grid must be the 2x-upsampled DiT grid");
+  const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
+  for (int64_t f = 0; f < n_frames; ++f) {
+    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
+    OASIS_TRY(oasis_vae_decode(vw, vbuf, latent, frames + f * frame_elems, stream));
+  }
   return OASIS_OK;
 }
 

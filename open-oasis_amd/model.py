@@ -504,11 +504,20 @@ class FramePipeline:
 
 
 class VideoPipeline:
-    """n_frames consecutive frames of one stream in one call (oasis_video_frames): frame f's
+    """n_frames consecutive frames of one stream per batch (oasis_video_frames): frame f's
     context is frame f-1's denoised latent, rolled on the device (the interactive loop's
-    context window, oasis_inference.py:2296-2306). overlap_decode=True runs frame f's VAE
-    decode on a side stream during frame f+1's DDIM steps (measured slower on MI355X: the
-    latency-bound DiT kernels lose more to the shared CUs than the overlap hides).
+    context window, oasis_inference.py:2296-2306).
+
+    overlap_decode=False: one hipGraph per batch, each frame's DDIM steps then its VAE decode.
+    overlap_decode=True: the batch's DDIM steps (oasis_video_frames with frames = NULL) and its
+    decodes (oasis_video_decode) are two single-stream graphs on two streams, and batch k's
+    decodes run while batch k+1 denoises. launch() enqueues batch k, then waits on the host
+    for batch k-1's DDIM steps (batch k is already queued behind them) and launches its
+    decodes: a device-side wait of one stream on the other's event serialises the two graphs
+    on this runtime, a host-side wait does not. drain() launches the last batch's decodes.
+    Chunk and frame buffers alternate between two sets, so a batch's frames stay valid until
+    two batches later.
+
     Inputs: self.chunks [n_frames, P, 64] noise, self.ctx_patches [P, 64] the first context,
     conditioning rows built by set_inputs (context t and action, then each step's t with
     the frame's action; the context of frame f > 0 carries frame f-1's action)."""
@@ -524,18 +533,38 @@ class VideoPipeline:
         self.ws = dit.workspace(2 * P, max_cond=max(16, R))
         self.vws = vae.workspace()
         self.kv = KVCache(dit, 1) if kv_cache else None
-        self.chunks = torch.zeros(n_frames, P, dit.patch_dim, device=dev)
+        nb = 2 if overlap_decode else 1
+        self.chunk_bufs = [torch.zeros(n_frames, P, dit.patch_dim, device=dev) for _ in range(nb)]
+        self.frame_bufs = [torch.zeros(n_frames, *vae.frame_shape, device=dev) for _ in range(nb)]
         self.ctx_patches = torch.zeros(P, dit.patch_dim, device=dev)
         self.ctx_z = torch.zeros(P, dit.d, device=dev)
-        self.frames = torch.zeros(n_frames, *vae.frame_shape, device=dev)
         self.coeffs = (ctypes.c_float * (6 * self.n))(*ddim_coefficients(alphas_cumprod, self.steps))
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
+        self.decode_stream = torch.cuda.Stream(device=dev) if overlap_decode else None
         self.graph = None
+        self.graphs, self.decode_graphs = [], []
+        self._ev_dit = [torch.cuda.Event() for _ in range(nb)]
+        self._ev_dec = [torch.cuda.Event() for _ in range(nb)]
+        self._pending = [False] * nb  # decodes launched that read buffer set b
+        self._undecoded = None        # buffer set of the batch whose decodes are still to launch
+        self._k = 0
+        self._last = 0
+
+    @property
+    def chunks(self):
+        """Denoised latents of the last batch (noise before the first)."""
+        return self.chunk_bufs[self._last]
+
+    @property
+    def frames(self):
+        return self.frame_bufs[self._last]
 
     def set_inputs(self, noise_patches, ctx_patches, ctx_t, ctx_action, actions):
         """noise_patches [n_frames, P, 64], ctx_patches [P, 64], actions [n_frames, ext_dim]."""
         F, n, e = self.n_frames, self.n, self.dit.ext_dim
-        self.chunks.copy_(noise_patches.reshape(self.chunks.shape))
+        torch.cuda.synchronize(self.dit.device)  # no batch still reads or writes the buffers
+        for c in self.chunk_bufs:
+            c.copy_(noise_patches.reshape(c.shape))
         self.ctx_patches.copy_(ctx_patches)
         t = torch.tensor(([float(ctx_t)] + [float(ts) for ts, _ in self.steps]) * F)
         act = torch.zeros(F, 1 + n, self.dit.ext_pad)
@@ -547,27 +576,83 @@ class VideoPipeline:
         self.ws.act[:F * (1 + n)].copy_(act.reshape(F * (1 + n), -1))
         torch.cuda.synchronize(self.dit.device)
 
-    def enqueue(self):
+    def _enqueue_frames(self, b, decode):
         d, ws = self.dit, self.ws
         L.call("oasis_video_frames", ctypes.byref(d.struct), ctypes.byref(ws.struct), ctypes.byref(self.vae.struct),
-               ctypes.byref(self.vws.struct), ctypes.byref(self.kv.struct) if self.kv is not None else None,
-               self.n_frames, L.ptr(self.chunks), L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
+               ctypes.byref(self.vws.struct) if decode else None,
+               ctypes.byref(self.kv.struct) if self.kv is not None else None,
+               self.n_frames, L.ptr(self.chunk_bufs[b]), L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
                ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
-               L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent), L.ptr(self.frames),
-               int(self.overlap_decode), L.stream_handle(self.stream))
+               L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent) if decode else None,
+               L.ptr(self.frame_bufs[b]) if decode else None, 0, L.stream_handle(self.stream))
+
+    def _enqueue_decode(self, b):
+        L.call("oasis_video_decode", ctypes.byref(self.dit.struct), ctypes.byref(self.vae.struct),
+               ctypes.byref(self.vws.struct), self.n_frames, L.ptr(self.chunk_bufs[b]), L.ptr(self.vws.latent),
+               L.ptr(self.frame_bufs[b]), L.stream_handle(self.decode_stream))
+
+    def enqueue(self):
+        """One batch, uncaptured (overlap_decode=False)."""
+        self._enqueue_frames(0, True)
 
     def capture(self):
-        self.graph = Graph(self.enqueue, self.stream)
-        return self.graph
+        if not self.overlap_decode:
+            self.graph = Graph(self.enqueue, self.stream)
+            self.graphs = [self.graph]
+            return self.graph
+        self.graphs = [Graph(lambda b=b: self._enqueue_frames(b, False), self.stream) for b in range(2)]
+        self.decode_graphs = [Graph(lambda b=b: self._enqueue_decode(b), self.decode_stream) for b in range(2)]
+        return self.graphs
+
+    def launch(self):
+        """Enqueue one batch and return its frame buffer. With overlap_decode the frames are
+        complete once the next launch() or drain() has launched their decodes and the decode
+        stream has run them."""
+        if not self.overlap_decode:
+            if self.graph is not None:
+                self.graph.launch()
+            else:
+                self.enqueue()
+            return self.frame_bufs[0]
+        b = self._k % 2
+        self._k += 1
+        if self._pending[b]:  # the decodes that read chunk set b (two batches ago) are done
+            self._ev_dec[b].synchronize()
+            self._pending[b] = False
+        if self.graphs:
+            self.graphs[b].launch()
+        else:
+            self._enqueue_frames(b, False)
+        self._ev_dit[b].record(self.stream)
+        self.drain()
+        self._undecoded = b
+        self._last = b
+        return self.frame_bufs[b]
+
+    def drain(self):
+        """Launch the decodes still owed (those of the last launched batch), once that batch's
+        DDIM steps have finished; the decode stream runs them."""
+        pb = self._undecoded
+        if pb is None:
+            return
+        self._ev_dit[pb].synchronize()
+        if self.decode_graphs:
+            self.decode_graphs[pb].launch()
+        else:
+            self._enqueue_decode(pb)
+        self._ev_dec[pb].record(self.decode_stream)
+        self._pending[pb] = True
+        self._undecoded = None
 
     def run(self):
-        """Enqueue the frames on self.stream; the caller's current stream waits for them."""
-        if self.graph is not None:
-            self.graph.launch()
-        else:
-            self.enqueue()
-        torch.cuda.current_stream(self.dit.device).wait_stream(self.stream)
-        return self.frames
+        """Enqueue one batch and its decodes; the caller's current stream waits for its frames."""
+        frames = self.launch()
+        self.drain()
+        cur = torch.cuda.current_stream(self.dit.device)
+        cur.wait_stream(self.stream)
+        if self.decode_stream is not None:
+            cur.wait_stream(self.decode_stream)
+        return frames
 
 
 def attention_scale(head_dim=HEAD_DIM):
