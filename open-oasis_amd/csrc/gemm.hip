@@ -607,8 +607,10 @@ int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
   const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
   if (gelu) return M <= 160 ? 52 : (M >= 512 ? 53 : 51);
-  if (kind == OASIS_EPI_PARTIAL_F32)
-    return (M <= 160 && Kslice <= 256) || (M <= 320 && Kslice <= 512) ? 23 : 51;
+  if (kind == OASIS_EPI_PARTIAL_F32) {
+    if (M <= 160) return Kslice <= 256 ? 23 : 51;
+    return M <= 320 && Kslice <= 512 ? 23 : 51;
+  }
   return M >= 512 ? 52 : 32;
 }
 
