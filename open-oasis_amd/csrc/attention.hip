@@ -287,7 +287,9 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
       flash_go<9, 160, 160>(dim3((unsigned)(a.Lq / 144), nb), q, k, v, o, a, s);
     } else {
       const dim3 g((unsigned)(a.Lq / 48), nb);
-      if (kind == 0)  // two waves per query block over alternate 32-key chunks
+      if (kind == 0 && n_bh <= 16)  // one frame: a workgroup per 16-query block (3x the workgroups)
+        flash_go<1, 32, 160, T, 2>(dim3((unsigned)(a.Lq / 16), nb), q, k, v, o, a, s);
+      else if (kind == 0)  // two waves per query block over alternate 32-key chunks
         flash_go<3, 32, 160, T, 2>(g, q, k, v, o, a, s);
       else if (kind == 1)
         flash_go<3, 192, 192>(g, q, k, v, o, a, s);

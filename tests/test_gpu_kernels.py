@@ -230,12 +230,13 @@ def test_ln_affine():
 
 
 # ---------------------------------------------------------------- attention
-@pytest.mark.parametrize("L_,F_", [(144, 2), (576, 2), (37, 2), (144, 64), (160, 2), (192, 2), (150, 64),
-                                   (240, 2), (600, 1), (1152, 1)])
+@pytest.mark.parametrize("L_,F_", [(144, 2), (144, 5), (576, 2), (37, 2), (144, 64), (160, 2), (192, 2),
+                                   (150, 64), (240, 2), (600, 1), (1152, 1)])
 def test_attention_heads_first(L_, F_):
     """Frames of L_ tokens: a whole frame staged at once (up to 160 or 192 keys), the VAE's
-    576, a ragged 37; 64 frames x 4 heads (256 pairs) take the 9-wave one-workgroup-per-frame path
-    at L = 144. From 193 keys two waves share each 16-query block, each taking every other 64-key
+    576, a ragged 37. At L = 144: up to 16 (frame, head) pairs take one workgroup per 16-query
+    block (2 x 4 heads), up to 255 three blocks per workgroup (5 x 4), and 64 frames x 4 heads
+    (256 pairs) the 9-wave one-workgroup-per-frame path. From 193 keys two waves share each 16-query block, each taking every other 64-key
     chunk: 240 (48-query workgroups), 600 (a ragged second 576-key stage where only one of the
     two waves has a chunk) and 1152 (two full stages)."""
     H = 4
