@@ -104,6 +104,27 @@ def test_dit_step_config1(c1):
     assert cos >= COS_STEP, cos
 
 
+def test_dit_step_adaln_rows_of_every_consumer(c1):
+    """The adaLN rows a step computes for every consumer, the final layer's included, equal
+    silu(cond) @ ada_w^T + ada_b of the packed weights (fp64 on the CPU)."""
+    c, dit = c1
+    step = pkg.DiTStep(dit, B=1, T=2)
+    step.ws.ada.fill_(float("nan"))  # a slice that is never written stays NaN
+    patches = oracle.patchify_to_output_space(c["latent"][0]).reshape(-1, 64)
+    step.set_inputs(cuda(patches), cuda(c["t"]), cuda(c["actions"]))
+    step.run()
+    torch.cuda.synchronize()
+    cond = step.ws.cond[:2].double().cpu()
+    ref = torch.nn.functional.silu(cond) @ dit.ada_w.double().cpu().t() + dit.ada_b.double().cpu()
+    got = step.ws.ada[:2].double().cpu()
+    assert torch.isfinite(got).all(), "adaLN rows left unwritten"
+    D = dit.d
+    for j in range(dit.n_sub + 1):
+        a, b = j * 6 * D, min((j + 1) * 6 * D, dit.ada_width)
+        err = ((got[:, a:b] - ref[:, a:b]).abs().max() / ref[:, a:b].abs().max()).item()
+        assert err < 1e-4, (j, err)
+
+
 def test_dit_step_graph_replay_and_context_invariance(c1):
     c, dit = c1
     step = pkg.DiTStep(dit, B=1, T=2)
