@@ -589,6 +589,18 @@ def main():
             ms_video[overlap] = 1e3 * (time.perf_counter() - t0) / (reps * nv)
             del vp
         ms_video_frame = ms_video[False]
+        # the interactive loop (PlaySession, play.py:241-531): one frame per action, each frame
+        # drawing its noise, writing its conditioning rows, replaying the frame graph, rolling
+        # the context and waiting for the frame on the host
+        sess = pkg.PlaySession(dit3, vae3, c3["ctx_latent"], ddim_steps=len(c3["steps"]),
+                               alphas_cumprod=pkg.schedule.cosine_alphas_cumprod(), seed=1)
+        for _ in range(3):
+            sess.frame(c3["gen_action"])
+        t0 = time.perf_counter()
+        for _ in range(args.frames):
+            sess.frame(c3["gen_action"])
+        ms_play = 1e3 * (time.perf_counter() - t0) / args.frames
+        del sess
         out["frame_ms"] = round(ms_frame, 4)
         out["frame_fps"] = round(1e3 / ms_frame, 1)
         out["frame_hbm_floor_ms"] = round(frame_floor_ms, 4)
@@ -597,12 +609,16 @@ def main():
         out["frame_fps_all_t2"] = round(1e3 / ms_frame_t2, 1)
         out["video_fps"] = round(1e3 / ms_video_frame, 1)
         out["video_fps_overlap_decode"] = round(1e3 / ms_video[True], 1)
+        out["play_fps"] = round(1e3 / ms_play, 1)
         out["video_workload"] = ("batches of 16 consecutive frames, each frame's context = the previous frame's "
                                  "denoised latent rolled on the device; video_fps: one hipGraph per batch (DDIM "
                                  "steps then VAE decode per frame); video_fps_overlap_decode: the batch's DDIM "
                                  "steps and its 16 decodes as two single-stream hipGraphs on two streams, batch k's "
                                  "decodes (launched once its DDIM steps are done) overlapping batch k+1's DDIM "
                                  "steps")
+        out["play_workload"] = ("interactive loop (PlaySession): one config-3 frame per action, host-synchronised "
+                                "per frame; noise drawn on the device, conditioning rows written, frame graph "
+                                "replayed, context rolled on the device, frame [360,640,3] in [0,1] returned")
         out["frame_workload"] = ("config3: 4 DDIM v-prediction steps (t=999,749,499,249, cosine alphas) "
                                  "over the DiT (step 1 at T=2 storing the context frame's temporal K/V, steps "
                                  "2-4 on the generated frame at T=1 against that cache; frame_fps_all_t2: every "

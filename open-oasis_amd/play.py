@@ -1,0 +1,174 @@
+"""Interactive frame loop: one generated frame per action, as the reference's play loop runs it
+(play.py:241-531), without its file / HTTP interface to the browser UI (play_server.py).
+
+- One captured frame graph per DDIM step count, kept once built. The reference releases its
+  trace and re-traces when the slider changes ddim_steps (play.py:446-462). A change clamps
+  the count to [1, 12] (play.py:55-56,103-108) and resets the context to the prompt and the
+  frame index to 0, as the reference does.
+- Each frame draws fresh noise, N(0, 1) clamped to +-noise_abs_max (play.py:466-472). Patchify
+  is a permutation of iid noise, so it is drawn directly in patch space, on the device.
+- The context is the previous frame's denoised latent. Its conditioning is at
+  stabilization_level - 1 with the previous frame's action (play.py:486-496); the first context
+  is the prompt with the prompt action. After frame index k (k > 0, k % reset_every == 0) the
+  context returns to the prompt (play.py:497-500).
+- The action passes through the reference's hold: the last non-zero action is kept for
+  `hold` frames after a release (read_action, play.py:80-100).
+- Everything stays on the device. The context moves device-to-device. The frame comes back as
+  [H, W, 3] in [0, 1], that is (x + 1) / 2 of the decoder's clamped output (play.py:476-480).
+"""
+import time
+
+import torch
+
+from .model import FramePipeline
+from .schedule import ddim_steps as ddim_schedule
+from .schedule import sigmoid_alphas_cumprod
+
+MIN_DDIM_STEPS, MAX_DDIM_STEPS = 1, 12   # play.py:55-56
+NOISE_ABS_MAX = 20.0                     # play.py:58
+STABILIZATION_LEVEL = 15                 # play.py:59
+RESET_EVERY = 80                         # play.py:497
+ACTION_HOLD = 1                          # play.py:83
+FPS_WINDOW = 10                          # frames in the rolling FPS figure (play.py:519-522)
+
+
+def patchify_latent(latent, patch=2):
+    """[C, H, W] latent -> [(H/p)(W/p), p*p*C] patch rows with columns ordered (p, q, c), the
+    reference's patchify_to_output_space (oasis_inference.py:958-963)."""
+    C, H, W = latent.shape
+    x = latent.reshape(C, H // patch, patch, W // patch, patch).permute(1, 3, 2, 4, 0)
+    return x.reshape((H // patch) * (W // patch), patch * patch * C)
+
+
+class ActionHold:
+    """The reference's read_action hold (play.py:80-100): a non-zero action is returned and
+    remembered; after a release (all-zero action) the last non-zero one is returned for
+    `hold` more frames."""
+
+    def __init__(self, dim, hold=ACTION_HOLD):
+        self.last = torch.zeros(dim)
+        self.left = 0
+        self.hold = hold
+
+    def __call__(self, action):
+        cur = torch.as_tensor(action, dtype=torch.float32).reshape(-1).cpu()
+        if cur.abs().sum() > 0:
+            self.last = cur.clone()
+            self.left = self.hold
+            return cur
+        if self.left > 0:
+            self.left -= 1
+            return self.last
+        return cur
+
+
+class PlaySession:
+    """Frame-by-frame generation driven by one action per frame.
+
+    dit, vae: device-resident models. prompt_latent: [C, H, W] (or [1, C, H, W]) latent of the
+    prompt frame; prompt_action: [ext_dim] (zeros by default, as play.py:193).
+    alphas_cumprod defaults to the sigmoid schedule the play loop uses (play.py:188-191).
+    frame(action) returns the decoded frame; status() gives frame_index / fps / ddim_steps as
+    the reference's write_status does (play.py:121-126)."""
+
+    def __init__(self, dit, vae, prompt_latent, prompt_action=None, ddim_steps=4, alphas_cumprod=None,
+                 noise_abs_max=NOISE_ABS_MAX, stabilization_level=STABILIZATION_LEVEL,
+                 reset_every=RESET_EVERY, hold=ACTION_HOLD, seed=0, kv_cache=True, stream=None,
+                 keep_noise=False):
+        dev = dit.device
+        self.dit, self.vae, self.device = dit, vae, dev
+        self.alphas = alphas_cumprod if alphas_cumprod is not None else sigmoid_alphas_cumprod()
+        self.noise_abs_max = float(noise_abs_max)
+        self.ctx_t = float(stabilization_level - 1)
+        self.reset_every = int(reset_every)
+        self.kv_cache = kv_cache
+        self.keep_noise = keep_noise
+        self.last_noise = None
+        self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
+        lat = torch.as_tensor(prompt_latent, dtype=torch.float32)
+        while lat.dim() > 3:
+            lat = lat[0]
+        self.prompt = patchify_latent(lat).to(dev).contiguous()
+        e = dit.ext_dim
+        self.prompt_action = (torch.zeros(e) if prompt_action is None else
+                              torch.as_tensor(prompt_action, dtype=torch.float32).reshape(e).clone())
+        self.hold = ActionHold(e, hold)
+        self.gen = torch.Generator(device=dev)
+        self.gen.manual_seed(seed)
+        self.pipelines = {}
+        # action rows go up through a pinned buffer; the event guards its reuse
+        self.act_host = torch.zeros(1 + MAX_DDIM_STEPS, dit.ext_pad, pin_memory=True)
+        self.act_copied = torch.cuda.Event()
+        self.stream.wait_stream(torch.cuda.current_stream(dev))  # the prompt rows are ready
+        self.set_ddim_steps(ddim_steps)
+
+    def _pipeline(self, n):
+        fp = self.pipelines.get(n)
+        if fp is None:
+            fp = FramePipeline(self.dit, self.vae, ddim_schedule(n), self.alphas, stream=self.stream,
+                               kv_cache=self.kv_cache)
+            # the timestep rows (context, then each DDIM step) are fixed for a step count
+            t_rows = torch.tensor([self.ctx_t] + [float(t) for t, _ in fp.steps], dtype=torch.float32)
+            with torch.cuda.stream(self.stream):
+                fp.ws.t[:1 + n].copy_(t_rows)
+            fp.capture()
+            self.pipelines[n] = fp
+        return fp
+
+    def set_ddim_steps(self, n):
+        """Switch to n DDIM steps per frame (clamped to [1, 12]); resets the context to the
+        prompt and the frame index to 0."""
+        n = max(MIN_DDIM_STEPS, min(MAX_DDIM_STEPS, int(n)))
+        self.ddim_steps = n
+        self.fp = self._pipeline(n)
+        self.reset_context()
+        self.frame_index = 0
+        self.frame_times = []
+
+    def reset_context(self):
+        """The context window back to the prompt frame and the prompt action."""
+        with torch.cuda.stream(self.stream):
+            self.fp.ctx_patches.copy_(self.prompt)
+        self.ctx_action = self.prompt_action.clone()
+
+    def frame(self, action, sync=True):
+        """Generate the next frame for `action` ([ext_dim]). Returns [H, W, 3] in [0, 1] on the
+        device; the caller's current stream waits for it. sync=True also waits on the host
+        and counts the frame in the FPS figure."""
+        t0 = time.perf_counter()
+        a = self.hold(action)
+        fp, n, e = self.fp, self.ddim_steps, self.dit.ext_dim
+        R = 1 + n
+        self.act_copied.synchronize()  # the previous frame's copy out of act_host is done
+        rows = self.act_host[:R]
+        rows.zero_()
+        rows[0, :e] = self.ctx_action
+        rows[1:, :e] = a
+        with torch.cuda.stream(self.stream):
+            fp.chunk.normal_(generator=self.gen).clamp_(-self.noise_abs_max, self.noise_abs_max)
+            if self.keep_noise:
+                self.last_noise = fp.chunk.clone()
+            fp.ws.act[:R].copy_(rows, non_blocking=True)
+            self.act_copied.record(self.stream)
+        fp.graph.launch()
+        with torch.cuda.stream(self.stream):
+            img = ((fp.vws.frame + 1.0) * 0.5).clamp_(0.0, 1.0).permute(1, 2, 0).contiguous()
+            fp.ctx_patches.copy_(fp.chunk)  # this frame's denoised latent is the next context
+        self.ctx_action = a.clone()
+        cur = torch.cuda.current_stream(self.device)
+        cur.wait_stream(self.stream)
+        img.record_stream(cur)
+        if self.frame_index > 0 and self.frame_index % self.reset_every == 0:
+            self.reset_context()
+        self.frame_index += 1
+        if sync:
+            self.stream.synchronize()
+            self.frame_times = (self.frame_times + [time.perf_counter() - t0])[-FPS_WINDOW:]
+        return img
+
+    @property
+    def fps(self):
+        return len(self.frame_times) / sum(self.frame_times) if self.frame_times else 0.0
+
+    def status(self):
+        return {"frame_index": self.frame_index, "fps": round(self.fps, 1), "ddim_steps": self.ddim_steps}

@@ -1,0 +1,33 @@
+"""Host logic of the interactive frame loop (open-oasis_amd/play.py) on the CPU: the action
+hold of the reference's read_action (play.py:80-100) and the patch layout of the prompt."""
+import torch
+
+import oracle
+from helpers import pkg
+
+play = pkg.play
+
+
+def test_action_hold_keeps_the_last_action_one_frame_after_a_release():
+    hold = play.ActionHold(25, hold=1)
+    a, b, z = torch.zeros(25), torch.zeros(25), torch.zeros(25)
+    a[3], b[7] = 1.0, 1.0
+    seq = [hold(x) for x in (a, z, z, b, b, z, z)]
+    expect = [a, a, z, b, b, b, z]
+    for i, (got, want) in enumerate(zip(seq, expect)):
+        assert torch.equal(got, want), i
+
+
+def test_action_hold_zero_frames_passes_actions_through():
+    hold = play.ActionHold(25, hold=0)
+    a, z = torch.zeros(25), torch.zeros(25)
+    a[1] = 1.0
+    assert torch.equal(hold(a), a) and torch.equal(hold(z), z)
+
+
+def test_patchify_latent_matches_the_oracle_layout():
+    g = torch.Generator().manual_seed(3)
+    lat = torch.randn(16, 18, 32, generator=g)
+    got = play.patchify_latent(lat)
+    assert got.shape == (144, 64)
+    assert torch.equal(got, oracle.patchify_to_output_space(lat[None])[0])
