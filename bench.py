@@ -546,11 +546,12 @@ def main():
         ctx_h = ctx.pin_memory()
         t0 = time.perf_counter()
         for _ in range(args.frames):
-            fp.chunk.copy_(noise_h, non_blocking=True)
-            fp.ctx_patches.copy_(ctx_h, non_blocking=True)
-            fp.stream.wait_stream(torch.cuda.current_stream())
+            # the copies go on the frame's own stream: a per-frame device-side wait between it
+            # and torch's default stream costs ~0.5 ms here
+            with torch.cuda.stream(fp.stream):
+                fp.chunk.copy_(noise_h, non_blocking=True)
+                fp.ctx_patches.copy_(ctx_h, non_blocking=True)
             fp.graph.launch()
-            torch.cuda.current_stream().wait_stream(fp.stream)
         torch.cuda.synchronize()
         ms_frame_h2d = 1e3 * (time.perf_counter() - t0) / args.frames
         frame_floor_ms = (len(c3["steps"]) * dit3.weight_bytes + vae3.weight_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
