@@ -161,9 +161,7 @@ class PlaySession:
         fp.graph.launch()
         with torch.cuda.stream(self.stream):
             img = ((fp.vws.frame + 1.0) * 0.5).clamp_(0.0, 1.0).permute(1, 2, 0).contiguous()
-            # this frame's denoised latent is the next context, copied by an elementwise kernel:
-            # a memcpy on the stream between two frame graphs costs ~0.5 ms here
-            torch.add(fp.chunk, 0.0, out=fp.ctx_patches)
+            fp.ctx_patches.copy_(fp.chunk)  # this frame's denoised latent is the next context
         self.ctx_action = a.clone()
         cur = torch.cuda.current_stream(self.device)
         img.record_stream(cur)
