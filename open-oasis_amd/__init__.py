@@ -8,4 +8,4 @@ from . import _lib  # noqa: F401
 from ._lib import OasisError  # noqa: F401
 from .model import DiT, VAE, DiTStep, FramePipeline, VideoPipeline, Graph  # noqa: F401
 from .play import PlaySession, ActionHold, patchify_latent  # noqa: F401
-from . import kernels, schedule, synth  # noqa: F401
+from . import checkpoint, kernels, schedule, synth  # noqa: F401
