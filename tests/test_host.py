@@ -113,3 +113,17 @@ def test_workspace_split_sizing():
     ws = dit.workspace(4608)  # the large-token O / FC2 tiles use 2 K slices at N = 1024
     assert ws.max_splits == 2 and ws.struct.max_rows == 4608
     assert ws.partial.shape == (2, 4608, dit.d)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU's share; --gpus N > 1 (or a multi-rank launch) exits with a
+    message before touching a device."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for extra_env, argv in (({}, ["--gpus", "2"]), ({"WORLD_SIZE": "8"}, [])):
+        env = dict(os.environ, **extra_env)
+        r = subprocess.run([sys.executable, os.path.join(root, "bench.py")] + argv, capture_output=True,
+                           text=True, timeout=120, env=env)
+        assert r.returncode != 0 and "one MI355X" in (r.stdout + r.stderr), (argv, r.returncode, r.stderr[-300:])
