@@ -75,6 +75,12 @@ class PlaySession:
                  noise_abs_max=NOISE_ABS_MAX, stabilization_level=STABILIZATION_LEVEL,
                  reset_every=RESET_EVERY, hold=ACTION_HOLD, seed=0, kv_cache=True, stream=None,
                  keep_noise=False):
+        lat = torch.as_tensor(prompt_latent, dtype=torch.float32)
+        while lat.dim() > 3:
+            if lat.shape[0] != 1:
+                raise ValueError("prompt_latent: one frame [C, H, W] (leading dims of size 1 allowed), got %s"
+                                 % (tuple(prompt_latent.shape),))
+            lat = lat[0]
         dev = dit.device
         self.dit, self.vae, self.device = dit, vae, dev
         self.alphas = alphas_cumprod if alphas_cumprod is not None else sigmoid_alphas_cumprod()
@@ -85,9 +91,6 @@ class PlaySession:
         self.keep_noise = keep_noise
         self.last_noise = None
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
-        lat = torch.as_tensor(prompt_latent, dtype=torch.float32)
-        while lat.dim() > 3:
-            lat = lat[0]
         self.prompt = patchify_latent(lat).to(dev).contiguous()
         e = dit.ext_dim
         self.prompt_action = (torch.zeros(e) if prompt_action is None else

@@ -1,5 +1,6 @@
 """Host logic of the interactive frame loop (open-oasis_amd/play.py) on the CPU: the action
 hold of the reference's read_action (play.py:80-100) and the patch layout of the prompt."""
+import pytest
 import torch
 
 import oracle
@@ -31,3 +32,15 @@ def test_patchify_latent_matches_the_oracle_layout():
     got = play.patchify_latent(lat)
     assert got.shape == (144, 64)
     assert torch.equal(got, oracle.patchify_to_output_space(lat[None])[0])
+
+
+def test_session_rejects_a_batch_of_prompts():
+    """Only one prompt frame: leading dims of size 1 are dropped, anything else is an error
+    (raised before any device work)."""
+
+    class Fake:
+        device = torch.device("cpu")
+        ext_dim = 25
+
+    with pytest.raises(ValueError, match="one frame"):
+        play.PlaySession(Fake(), None, torch.zeros(2, 16, 18, 32))
