@@ -199,3 +199,24 @@ def test_ddim_frame_config3(c3):
     cf, rf = metrics(frame, ref_frame)
     print("config3 frame: chunk cos=%.6f rel=%.3e | frame cos=%.6f rel=%.3e" % (cc, rc, cf, rf), flush=True)
     assert cc >= COS_STEP and cf >= COS_STEP, (cc, cf)
+
+
+def test_dit_from_an_upstream_checkpoint_steps_identically(tmp_path):
+    """A DiT built from an upstream-named safetensors checkpoint (checkpoint.load_dit) runs the
+    same step, bit for bit, as one built from the weight dict it was written from."""
+    from safetensors.torch import save_file
+    ck = pkg.checkpoint
+    dr = pkg.synth.Draw(81)
+    w = pkg.synth.dit_weights(dr, n_blocks=2)
+    path = str(tmp_path / "dit.safetensors")
+    save_file({up: w[me].contiguous() for up, me in ck.dit_names(2)}, path)
+    outs = []
+    for weights in (w, ck.load_dit(path)):
+        dit = pkg.DiT(weights, "cuda")
+        step = pkg.DiTStep(dit, B=1, T=2)
+        lat = pkg.synth.Draw(82).normal(2, 16, 18, 32)
+        step.set_inputs(cuda(oracle.patchify_to_output_space(lat).reshape(-1, 64)), cuda(torch.tensor([10.0, 500.0])),
+                        cuda(torch.zeros(2, 25)))
+        outs.append(step.run().clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
