@@ -68,11 +68,13 @@ def _ref(A, W):
     return oracle.quantize_act_blocks(A).double() @ (q.double() * s.double()[:, None]).t()
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4])
-@pytest.mark.parametrize("M,N,K", [(300, 384, 512), (4608, 1024, 1024), (33, 64, 256)])
+# every tile on the small shapes; the 4608-row shape on the default and the wide tiles
+_FP8_CASES = [(t, 300, 384, 512) for t in (-1, 0, 1, 2, 3, 4)] + [(t, 4608, 1024, 1024) for t in (-1, 0, 1)] + \
+    [(t, 33, 64, 256) for t in (-1, 0, 1, 2, 3, 4)]
+
+
+@pytest.mark.parametrize("tile,M,N,K", _FP8_CASES)
 def test_gemm_fp8_store_f32(tile, M, N, K):
-    if M > 1000 and tile not in (-1, 0, 1):
-        pytest.skip("large shape covered by the wide tiles")
     g = _gen(M + N + K)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
     A[:, :32] *= 100.0  # blocks of very different magnitude
