@@ -35,11 +35,12 @@ def _session_chain(noises, prompt, prompt_action, actions, w, vw, ac, steps, res
     return out
 
 
-def test_session_frames_match_the_oracle_chain():
+@pytest.mark.parametrize("kv", [True, False])
+def test_session_frames_match_the_oracle_chain(kv):
     prompt, w, vw = _models(61)
     dit, vae = pkg.DiT(w, "cuda"), pkg.VAE(vw, "cuda")
     ac = pkg.schedule.sigmoid_alphas_cumprod()
-    s = pkg.PlaySession(dit, vae, prompt, ddim_steps=2, reset_every=2, seed=5, keep_noise=True)
+    s = pkg.PlaySession(dit, vae, prompt, ddim_steps=2, reset_every=2, seed=5, keep_noise=True, kv_cache=kv)
     a0, a3 = torch.zeros(25), torch.zeros(25)
     a0[4], a3[9] = 1.0, 1.0
     z = torch.zeros(25)
@@ -60,7 +61,7 @@ def test_session_frames_match_the_oracle_chain():
         got = frames[f]
         assert got.shape == want.shape and got.min() >= 0 and got.max() <= 1
         cf, rf = metrics(got, want)
-        print("session frame %d: cos=%.6f rel=%.2e" % (f, cf, rf), flush=True)
+        print("session (kv=%s) frame %d: cos=%.6f rel=%.2e" % (kv, f, cf, rf), flush=True)
         assert cf >= COS_STEP, (f, cf)
 
 
