@@ -352,24 +352,26 @@ def test_vae_unpatchify_pixels():
         assert fr[c, y, x].item() == v.item()
 
 
-def test_vae_decode_against_loops():
-    g = _g(16)
-    D, L_ = 128, 4 * 4
+def _tiny_vae_w(g, D=128, lat=8, out=12):
     r = lambda *s: torch.randn(*s, generator=g) * 0.1  # noqa: E731
-    w = {"pq_w": r(D, 8), "pq_b": r(D), "dec.0.n1_w": 1 + r(D), "dec.0.n1_b": r(D), "dec.0.qkv_w": r(3 * D, D),
-         "dec.0.qkv_b": r(3 * D), "dec.0.proj_w": r(D, D), "dec.0.proj_b": r(D), "dec.0.n2_w": 1 + r(D),
-         "dec.0.n2_b": r(D), "dec.0.fc1_w": r(2 * D, D), "dec.0.fc1_b": r(2 * D), "dec.0.fc2_w": r(D, 2 * D),
-         "dec.0.fc2_b": r(D), "norm_w": 1 + r(D), "norm_b": r(D), "pred_w": r(12, D), "pred_b": r(12),
-         "rope.vae_freqs": torch.rand(8, generator=g)}
-    lat = torch.randn(L_, 8, generator=g)
-    got = oracle.vae_decode(lat, w, grid=(4, 4))
+    return {"pq_w": r(D, lat), "pq_b": r(D), "dec.0.n1_w": 1 + r(D), "dec.0.n1_b": r(D), "dec.0.qkv_w": r(3 * D, D),
+            "dec.0.qkv_b": r(3 * D), "dec.0.proj_w": r(D, D), "dec.0.proj_b": r(D), "dec.0.n2_w": 1 + r(D),
+            "dec.0.n2_b": r(D), "dec.0.fc1_w": r(2 * D, D), "dec.0.fc1_b": r(2 * D), "dec.0.fc2_w": r(D, 2 * D),
+            "dec.0.fc2_b": r(D), "norm_w": 1 + r(D), "norm_b": r(D), "pred_w": r(out, D), "pred_b": r(out),
+            "rope.vae_freqs": torch.rand(8, generator=g)}
+
+
+def _vae_loops(lat, w, grid):
+    """fp64 restatement of vae_decode_forward (oasis_inference.py:1546-1618) for one block,
+    with the attention and RoPE as loops (2 heads of 64, dims >= 32 unrotated)."""
     W = {k: v.double() for k, v in w.items()}
+    L_, D = grid[0] * grid[1], W["pq_w"].shape[0]
     x = lat.double() @ W["pq_w"].t() + W["pq_b"]
-    ang = oracle.vae_rope_angles(w["rope.vae_freqs"], 4, 4).double()   # [16, 32]
+    ang = oracle.vae_rope_angles(w["rope.vae_freqs"], *grid).double()   # [L, 32]
     h = _ln64(x) * W["dec.0.n1_w"] + W["dec.0.n1_b"]
     qkv = h @ W["dec.0.qkv_w"].t() + W["dec.0.qkv_b"]
     att = torch.zeros(L_, D, dtype=torch.float64)
-    for hd in range(2):
+    for hd in range(D // 64):
         sl = slice(64 * hd, 64 * hd + 64)
         q, k, v = qkv[:, sl], qkv[:, D:][:, sl], qkv[:, 2 * D:][:, sl]
         full = torch.cat([ang, torch.zeros(L_, 32, dtype=torch.float64)], -1)  # dims >= 32 unrotated
@@ -379,8 +381,239 @@ def test_vae_decode_against_loops():
     gg = hh @ W["dec.0.fc1_w"].t() + W["dec.0.fc1_b"]
     gg = 0.5 * gg * (1 + torch.erf(gg / math.sqrt(2)))
     x = x + gg @ W["dec.0.fc2_w"].t() + W["dec.0.fc2_b"]
-    ref = (_ln64(x) * W["norm_w"] + W["norm_b"]) @ W["pred_w"].t() + W["pred_b"]
-    _close(got, ref, 1e-4)
+    return (_ln64(x) * W["norm_w"] + W["norm_b"]) @ W["pred_w"].t() + W["pred_b"]
+
+
+def test_vae_decode_against_loops():
+    g = _g(16)
+    w = _tiny_vae_w(g)
+    lat = torch.randn(16, 8, generator=g)
+    _close(oracle.vae_decode(lat, w, grid=(4, 4)), _vae_loops(lat, w, (4, 4)), 1e-4)
+
+
+# ----------------------------------------------------------------- final layer, DiT forward, DDIM frame
+# Loop-level fp64 restatements of the compositions (oasis_inference.py:1438-1526 and
+# 1909-1932, 2131-2148), each followed by checks that a planted mistake in the oracle
+# (monkeypatched on the CPU) is caught by the same comparison.
+
+def _err(a, b):
+    a, b = a.double(), b.double()
+    return (a - b).abs().max().item() / max(b.abs().max().item(), 1e-30)
+
+
+def _final_loops(x, c, w):
+    """final layer (oasis_inference.py:1497-1521) per token: adaLN of silu(c) has two
+    chunks, shift = cols [0, D) and scale = cols [D, 2D) (the reference folds +1 into the
+    scale half, 528-532); LN without affine, eps 1e-6; then Linear(D -> 64) + bias."""
+    T, P, D = x.shape
+    Wa, ba = w["final.ada_w"].double(), w["final.ada_b"].double()
+    Wf, bfin = w["final.w"].double(), w["final.b"].double()
+    n_out = Wf.shape[0]
+    out = torch.zeros(T, P, n_out, dtype=torch.float64)
+    for t in range(T):
+        cc = c[t].double()
+        s = [v / (1 + math.exp(-v)) for v in cc.tolist()]
+        shift = [sum(Wa[o, k].item() * s[k] for k in range(D)) + ba[o].item() for o in range(D)]
+        scale_p1 = [1.0 + sum(Wa[D + o, k].item() * s[k] for k in range(D)) + ba[D + o].item() for o in range(D)]
+        for p in range(P):
+            row = x[t, p].double().tolist()
+            mean = sum(row) / D
+            var = sum((v - mean) ** 2 for v in row) / D
+            h = [(row[k] - mean) / math.sqrt(var + 1e-6) * scale_p1[k] + shift[k] for k in range(D)]
+            for n in range(n_out):
+                out[t, p, n] = sum(h[k] * Wf[n, k].item() for k in range(D)) + bfin[n].item()
+    return out
+
+
+def _tiny_dit_w(g, D=32, n_blocks=1, n_out=64):
+    r = lambda *s: torch.randn(*s, generator=g) * 0.1  # noqa: E731
+    w = {"rope.spatial_freqs": torch.rand(16, generator=g) * 3, "rope.temporal_freqs": torch.rand(32, generator=g),
+         "final.ada_w": r(2 * D, D), "final.ada_b": r(2 * D), "final.w": r(n_out, D), "final.b": r(n_out),
+         "x_emb.w": r(D, 16, 2, 2), "x_emb.b": r(D)}
+    for i in range(n_blocks):
+        for kind in "st":
+            for k, v in _tiny_sub_w(g, D).items():
+                w["blocks.%d.%s.%s" % (i, kind, k)] = v
+    return w
+
+
+def test_final_layer_against_loops_and_planted_mistakes(monkeypatch):
+    g = _g(20)
+    D = 32
+    w = _tiny_dit_w(g, D, n_out=8)
+    x = torch.randn(2, 3, D, generator=g) * 2 + 0.5
+    c = torch.randn(2, D, generator=g)
+    ref = _final_loops(x, c, w)
+    _close(oracle.final_layer(x, oracle.silu(c), w), ref, 1e-5)
+    ref_mod = oracle.oasis_ref.modulate
+    planted = {
+        "shift and scale swapped": lambda h, shift, scale: h * (1.0 + shift) + scale,
+        "+1 of the scale dropped": lambda h, shift, scale: h * scale + shift,
+        "shift dropped": lambda h, shift, scale: h * (1.0 + scale),
+    }
+    for name, bad in planted.items():
+        monkeypatch.setattr(oracle.oasis_ref, "modulate", bad)
+        assert _err(oracle.final_layer(x, oracle.silu(c), w), ref) > 1e-2, name
+    monkeypatch.setattr(oracle.oasis_ref, "modulate", ref_mod)
+    # chunks read in the wrong order (scale from cols [0, D))
+    w_sw = dict(w)
+    w_sw["final.ada_w"] = torch.cat([w["final.ada_w"][D:], w["final.ada_w"][:D]])
+    w_sw["final.ada_b"] = torch.cat([w["final.ada_b"][D:], w["final.ada_b"][:D]])
+    assert _err(oracle.final_layer(x, oracle.silu(c), w_sw), ref) > 1e-2
+    # LN over the wrong axis (tokens instead of features) is caught too
+    monkeypatch.setattr(oracle.oasis_ref, "layer_norm",
+                        lambda t, *a, **k: (t - t.mean(-2, keepdim=True)) / t.std(-2, keepdim=True))
+    assert _err(oracle.final_layer(x, oracle.silu(c), w), ref) > 1e-2
+
+
+def _dit_loops(z, c, w, grid):
+    """dit_forward_device (oasis_inference.py:1438-1526): SiLU of each frame's cond once,
+    then per block the spatial sub-block (blocks.i.s) followed by the temporal one
+    (blocks.i.t), then the final layer; every piece as the fp64 loops above."""
+    T = z.shape[0]
+    s_ang = oracle.spatial_rope_angles(w["rope.spatial_freqs"].float(), *grid).double()
+    t_ang = oracle.temporal_rope_angles(w["rope.temporal_freqs"].float(), T).double()
+    x = z.double()
+    i = 0
+    while "blocks.%d.s.ada_w" % i in w:
+        for kind, ang in (("s", s_ang), ("t", t_ang)):
+            p = "blocks.%d.%s." % (i, kind)
+            bw = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
+            x = _sub_block_loops(x, c, bw, kind, ang)
+        i += 1
+    return _final_loops(x, c, w)
+
+
+def test_dit_forward_against_loops_and_planted_mistakes(monkeypatch):
+    g = _g(21)
+    D = 128
+    w = _tiny_dit_w(g, D, n_out=8)
+    z = torch.randn(2, 6, D, generator=g)
+    c = torch.randn(2, D, generator=g)
+    ref = _dit_loops(z, c, w, (2, 3))
+    _close(oracle.dit_forward(z, c, w, grid=(2, 3)), ref, 1e-4)
+    # SiLU skipped (raw cond into the adaLN projections)
+    monkeypatch.setattr(oracle.oasis_ref, "silu", lambda t: t)
+    assert _err(oracle.dit_forward(z, c, w, grid=(2, 3)), ref) > 1e-2
+    monkeypatch.undo()
+    # temporal sub-block run before the spatial one of each block
+    monkeypatch.setattr(oracle.oasis_ref, "_blk",
+                        lambda ww, i, kind: {k[len("blocks.%d.%s." % (i, "ts"[kind == "t"])):]: v
+                                             for k, v in ww.items()
+                                             if k.startswith("blocks.%d.%s." % (i, "ts"[kind == "t"]))})
+    assert _err(oracle.dit_forward(z, c, w, grid=(2, 3)), ref) > 1e-2
+    monkeypatch.undo()
+    # the temporal attention made non-causal (frame 0 sees frame 1)
+    orig = oracle.oasis_ref.attention
+    monkeypatch.setattr(oracle.oasis_ref, "attention", lambda q, k, v, causal=False, pad_keys_to=None:
+                        orig(q, k, v, causal=False, pad_keys_to=pad_keys_to))
+    assert _err(oracle.dit_forward(z, c, w, grid=(2, 3)), ref) > 1e-2
+
+
+def _frame_loops(x_noise, ctx_z, ctx_cond, gen_conds, w, vae_w, ac, steps, grid, vae_grid):
+    """One generated frame (oasis_inference.py:1909-1932, traced as 2131-2148), loop form:
+      - W_rt[(p*2+q)*C + c, d] = conv_w[d, c, p, q] (1821-1826); gen_z = chunk @ W_rt + b;
+      - z = [context frame; generated frame] (1912), cond likewise (cond_traced_per_step);
+      - v = the DiT output rows of frame 1 (1915-1916);
+      - a = alphas[t], a' = alphas[t_next] or 1 on the last step (1843-1852);
+        x0 = sqrt(a) x - sqrt(1-a) v and eps = sqrt(1-a) x + sqrt(a) v (the v-parametrisation
+        solved for eps, equal to the reference's (x/sqrt(a) - x0)/sqrt(1/a - 1));
+        x <- sqrt(a') x0 + sqrt(1-a') eps;
+      - bridge (1651-1709): VAE row (2h+p)*(2gw) + (2w+q), channel c <- chunk[h*gw + w,
+        (p*2+q)*C + c] / 0.07843137255;
+      - VAE decoder, then unpatchify (c, y, x) <- pred[(y//20)*vgw + x//20, c*400 + (y%20)*20 + x%20],
+        clamped to [-1, 1] (1636-1645, 2292)."""
+    gh, gw = grid
+    C = 16
+    cw = w["x_emb.w"].double()
+    D = cw.shape[0]
+    W_rt = torch.zeros(4 * C, D, dtype=torch.float64)
+    for d in range(D):
+        for cc in range(C):
+            for p in range(2):
+                for q in range(2):
+                    W_rt[(p * 2 + q) * C + cc, d] = cw[d, cc, p, q]
+    chunk = x_noise.double()
+    for i, (t, tn) in enumerate(steps):
+        gen_z = chunk @ W_rt + w["x_emb.b"].double()
+        z = torch.stack([ctx_z.double(), gen_z])
+        cond = torch.stack([ctx_cond.double(), gen_conds[i].double()])
+        v = _dit_loops(z, cond, w, grid)[1]
+        a = ac[t].item()
+        an = 1.0 if i == len(steps) - 1 else ac[tn].item()
+        x0 = math.sqrt(a) * chunk - math.sqrt(1 - a) * v
+        eps = math.sqrt(1 - a) * chunk + math.sqrt(a) * v
+        chunk = math.sqrt(an) * x0 + math.sqrt(1 - an) * eps
+    vgh, vgw = vae_grid
+    lat = torch.zeros(vgh * vgw, 32, dtype=torch.float64)
+    for h in range(gh):
+        for ww in range(gw):
+            for p in range(2):
+                for q in range(2):
+                    r = (2 * h + p) * vgw + (2 * ww + q)
+                    for cc in range(C):
+                        lat[r, cc] = chunk[h * gw + ww, (p * 2 + q) * C + cc] / 0.07843137255
+    pred = _vae_loops(lat, vae_w, vae_grid)
+    frame = torch.zeros(3, vgh * 20, vgw * 20, dtype=torch.float64)
+    for cc in range(3):
+        for y in range(vgh * 20):
+            for xx in range(vgw * 20):
+                val = pred[(y // 20) * vgw + xx // 20, cc * 400 + (y % 20) * 20 + xx % 20].item()
+                frame[cc, y, xx] = min(1.0, max(-1.0, val))
+    return chunk, frame
+
+
+def test_ddim_frame_against_loops_and_planted_mistakes(monkeypatch):
+    g = _g(22)
+    D, grid, vae_grid = 128, (2, 3), (4, 6)
+    w = _tiny_dit_w(g, D, n_out=64)
+    vae_w = _tiny_vae_w(g, D, lat=32, out=1200)
+    vae_w["pred_w"] = vae_w["pred_w"] * 5   # frame values reach the clamp at +-1
+    ac = oracle.cosine_alphas_cumprod()
+    steps = oracle.ddim_timesteps(2)          # [(999, 499), (499, -1)]
+    assert steps == [(999, 499), (499, -1)]
+    x_noise = torch.randn(6, 64, generator=g)
+    ctx_z = torch.randn(6, D, generator=g)
+    ctx_cond = torch.randn(D, generator=g)
+    gen_conds = [torch.randn(D, generator=g) for _ in steps]
+    args = (x_noise, ctx_z, ctx_cond, gen_conds, w, vae_w, ac, steps)
+    ref_chunk, ref_frame = _frame_loops(*args, grid, vae_grid)
+    assert ref_frame.abs().max().item() == 1.0 and ref_frame.abs().min().item() < 0.9
+    chunk, frame = oracle.ddim_frame(*args, grid=grid, vae_grid=vae_grid)
+    _close(chunk, ref_chunk, 1e-4)
+    _close(frame, ref_frame, 1e-4)
+
+    def planted(name):
+        c2, f2 = oracle.ddim_frame(*args, grid=grid, vae_grid=vae_grid)
+        monkeypatch.undo()
+        assert _err(c2, ref_chunk) > 1e-3, name
+
+    orig_dit = oracle.oasis_ref.dit_forward
+    monkeypatch.setattr(oracle.oasis_ref, "dit_forward", lambda *a, **k: orig_dit(*a, **k).flip(0))
+    planted("v taken from the context frame (frame 0)")
+    monkeypatch.setattr(oracle.oasis_ref, "dit_forward",
+                        lambda z, c, *a, **k: orig_dit(z.flip(0), c.flip(0), *a, **k).flip(0))
+    planted("generated frame stacked before the context frame")
+    orig_c = oracle.oasis_ref.ddim_coeffs
+    monkeypatch.setattr(oracle.oasis_ref, "ddim_coeffs", lambda ac_, t, tn, last: orig_c(ac_, t, tn, False))
+    planted("a' = 1 not applied on the last step")
+    monkeypatch.setattr(oracle.oasis_ref, "ddim_coeffs", lambda ac_, t, tn, last: orig_c(ac_, tn if tn >= 0 else t,
+                                                                                          tn, last))
+    planted("alphas read at the next timestep")
+    orig_pe = oracle.oasis_ref.patch_embed_roundtrip_weight
+    monkeypatch.setattr(oracle.oasis_ref, "patch_embed_roundtrip_weight",
+                        lambda ww: ww["x_emb.w"].float().permute(0, 1, 2, 3).reshape(ww["x_emb.w"].shape[0], -1)
+                        .t().contiguous())
+    planted("W_rt columns in (c, p, q) order instead of (p, q, c)")
+    del orig_pe
+    # the bridge's row order: a transposed pixel grid changes the frame, not the chunk
+    orig_b = oracle.oasis_ref.bridge
+    monkeypatch.setattr(oracle.oasis_ref, "bridge",
+                        lambda ch, gh, gw, *a: orig_b(ch, gh, gw, *a).reshape(2 * gh, 2 * gw, -1)
+                        .transpose(0, 1).reshape(4 * gh * gw, -1))
+    _, f2 = oracle.ddim_frame(*args, grid=grid, vae_grid=vae_grid)
+    monkeypatch.undo()
+    assert _err(f2, ref_frame) > 1e-2
 
 
 # ----------------------------------------------------------------- fp8 (config 4)
