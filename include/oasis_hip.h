@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define OASIS_ABI_VERSION 1
+#define OASIS_ABI_VERSION 2
 #define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
 
 enum {
@@ -284,7 +284,7 @@ int oasis_temporal_qkv_attention(const void* h, int64_t ldh, const void* w_qkv, 
                                  const float* t_sinp, void* k_cache, void* v_cache, float scale,
                                  oasis_stream_t stream);
 
-enum { OASIS_ACT_NONE = 0, OASIS_ACT_SILU = 1 };
+enum { OASIS_ACT_NONE = 0, OASIS_ACT_SILU = 1, OASIS_ACT_TEMB = 2 };
 
 /* Skinny GEMM for R <= 1024 rows (one pass over W per 16 rows):
  * out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]).
@@ -296,17 +296,30 @@ int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64
                     int64_t K, const float* b, float* out, int64_t ld_out, int act_in,
                     int act_out, int accumulate, oasis_stream_t stream);
 
+/* The same product with fp32 weights and fp32 arithmetic throughout:
+ * out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]), W fp32 [N, K] (K % 4 == 0,
+ * K <= 4096), R <= 1024. act_in = OASIS_ACT_TEMB: x is fp32 [R, ldx] with one timestep per
+ * row (x[r*ldx]) and the row multiplied is its embedding [cos(t f_i), sin(t f_i)],
+ * f_i = exp(-ln(10000) i / (K/2)) (timestep_embedding, oasis_inference.py:307-311).
+ * (The projections the reference keeps in fp32: the conditioning MLP and action projection,
+ * oasis_inference.py:512-520,1406-1427, and the final layer's adaLN,
+ * oasis_inference.py:527-532,1499-1511.) */
+int oasis_gemv_f32(const float* x, int64_t ldx, int64_t R, const float* W, int64_t N,
+                   int64_t K, const float* b, float* out, int64_t ld_out, int act_in,
+                   int act_out, int accumulate, oasis_stream_t stream);
+
 /* out[r, :] = [cos(t_r f), sin(t_r f)], f_i = exp(-ln(10000) i / (dim/2)), dim even.
  * (timestep_embedding, oasis_inference.py:307-311.) */
 int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, float* out,
                              oasis_stream_t stream);
 
-/* out[m, n] = b[n] + sum_k x[m, k] W[n, k] in fp32 (W bf16 [N, K], K <= 256), for the
- * small-K projections: patch embed (K=64, oasis_inference.py:1911) and the VAE
- * post_quant linear (K=32, oasis_inference.py:1551). */
+/* out[m, n] = b[n] + sum_k x[m, k] W(n, k) in fp32 (K <= 256; w_dtype OASIS_F32 or OASIS_BF16;
+ * w_layout 0: W is [N, K], 1: W is [K, N]), for the small-K projections: patch embed (K=64, the
+ * reference's fp32 W_rt [64, D], oasis_inference.py:1821-1826,1911) and the VAE post_quant
+ * linear (K=32, bf16, oasis_inference.py:686-690,1551). */
 int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W,
-                       int64_t N, const float* b, float* out, int64_t ld_out,
-                       oasis_stream_t stream);
+                       int w_dtype, int w_layout, int64_t N, const float* b, float* out,
+                       int64_t ld_out, oasis_stream_t stream);
 
 /* chunk <- c4*x0 + c5*eps with x0 = c0*chunk - c1*v, eps = (c2*chunk - x0)*c3, n elements.
  * (DDIM update, oasis_inference.py:1919-1931.) */
@@ -328,11 +341,14 @@ int oasis_vae_unpatchify(const float* patches, float* frame, int64_t gh, int64_t
  * Composite entry points: the DiT step, the VAE decoder and the DDIM frame.
  * ==================================================================== */
 
-/* Device pointers of one DiT (weights bf16 [out, in], biases and tables fp32).
+/* Device pointers of one DiT ([out, in] weights; biases and tables fp32).
  * Sub-block j = 2*i + (0 spatial | 1 temporal) of block i.
- * ada_w/ada_b hold every sub-block's adaLN projection back to back, then the final
- * layer's: rows [j*6D, (j+1)*6D) for sub-block j, [n_sub*6D, n_sub*6D + 2D) for the
- * final layer, with +1 folded into the bias of each scale chunk. */
+ * ada_w/ada_b (bf16 / fp32) hold every sub-block's adaLN projection back to back: rows
+ * [j*6D, (j+1)*6D) for sub-block j, with +1 folded into the bias of each scale chunk.
+ * The pieces the reference keeps in fp32 are fp32 here too: the conditioning MLP and action
+ * projection (oasis_inference.py:512-520), the patch embed W_rt (1821-1826), and the final
+ * layer's adaLN and linear (527-532). The adaLN rows of all consumers go to one buffer of
+ * width n_sub*6D + 2D: sub-block j at column j*6D, the final layer at n_sub*6D. */
 typedef struct {
   int n_sub;                 /* 2 * blocks                                         */
   int d_model;               /* 1024                                               */
@@ -342,8 +358,10 @@ typedef struct {
   int patch_dim;             /* 64 = 2*2*16                                        */
   int freq_dim;              /* 256                                                */
   int ext_dim_pad;           /* 64 (25 action dims zero-padded)                    */
-  const void* ada_w;         /* [n_sub*6D + 2D, D]                                 */
-  const float* ada_b;
+  const void* ada_w;         /* [n_sub*6D, D] bf16                                 */
+  const float* ada_b;        /* [n_sub*6D]                                         */
+  const float* final_ada_w;  /* [2D, D] fp32: shift, scale                         */
+  const float* final_ada_b;  /* [2D], +1 folded into the scale half                */
   const void* qkv_w[OASIS_MAX_SUB];   /* [3D, D], no bias                          */
   const void* out_w[OASIS_MAX_SUB];   /* [D, D]                                    */
   const float* out_b[OASIS_MAX_SUB];
@@ -351,16 +369,15 @@ typedef struct {
   const float* fc1_b[OASIS_MAX_SUB];
   const void* fc2_w[OASIS_MAX_SUB];   /* [D, Dm]                                   */
   const float* fc2_b[OASIS_MAX_SUB];
-  const void* final_w;       /* [64, D]                                            */
+  const float* final_w;      /* [64, D] fp32                                       */
   const float* final_b;
-  const void* xemb_w;        /* [D, 64] patch embed with columns in (p, q, c) order */
+  const float* xemb_w;       /* [D, 64] fp32 patch embed, columns in (p, q, c) order */
   const float* xemb_b;
-  const void* temb_w0;       /* [D, 256]                                           */
+  const float* temb_w0;      /* [D, 256] fp32                                      */
   const float* temb_b0;
-  const void* temb_w2;       /* [D, D]                                             */
-  const float* temb_b2;
-  const void* ext_w;         /* [D, ext_dim_pad]                                   */
-  const float* ext_b;
+  const float* cond_w;       /* [D, D + ext_dim_pad] fp32: the MLP's second linear in
+                                cols [0, D), the action projection in [D, D + ext_dim_pad) */
+  const float* cond_b;       /* [D]: the sum of their two biases                   */
   const float* s_cos;        /* [grid_h*grid_w, 64] spatial RoPE (sin with sign)  */
   const float* s_sinp;
   const float* t_cos;        /* [t_max, 64] temporal RoPE                          */
@@ -396,15 +413,16 @@ typedef struct {
   void* mlp8_scale;  /* [max_rows, Dm/32] e8m0                                      */
 } oasis_dit_buffers_t;
 
-/* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action), then
- * ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b for every sub-block and the final layer.
- *   t: fp32 [R]; action: fp32 [R, ext_dim_pad]; tfreq: fp32 [R, freq_dim] scratch;
- *   hid: fp32 [R, D] scratch; cond: fp32 [R, D]; ada: fp32 [R, n_sub*6D + 2D].  R <= 1024.
+/* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action) in fp32, then
+ * ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b for every sub-block (bf16 weights) and the final
+ * layer (fp32 weights).
+ *   t: fp32 [R]; action: fp32 [R, ext_dim_pad]; hid: fp32 [R, D] scratch; cond: fp32 [R, D];
+ *   ada: fp32 [R, n_sub*6D + 2D].  R <= 1024.
  * (compute_cond_for_frame, oasis_inference.py:1406-1427; build_per_frame_adaln,
  * oasis_inference.py:971-993; silu_kernel call, oasis_inference.py:1459-1463.) */
 int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action,
-                           int64_t R, float* tfreq, float* hid, float* cond, float* ada,
-                           oasis_stream_t stream);
+                           int64_t R, float* hid, float* cond, float* ada, oasis_stream_t stream);
+
 
 /* Sub-blocks [j0, j1) of the DiT on x[B*T*P, D] in place (j even: spatial, odd: temporal),
  * ada as in oasis_dit_forward.  (run_sub_block, oasis_inference.py:995-1215.) */
@@ -412,8 +430,8 @@ int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t
                          int64_t T, const float* ada, int64_t ada_fstride, int64_t j0, int64_t j1,
                          oasis_stream_t stream);
 
-/* Final layer on x[M, D]: v_out[M, 64] = (LN(x) * scale_p1 + shift) @ final_w^T + final_b.
- * (oasis_inference.py:1497-1521.) */
+/* Final layer on x[M, D], fp32 throughout:
+ * v_out[M, 64] = (LN(x) * scale_p1 + shift) @ final_w^T + final_b. (oasis_inference.py:1497-1521.) */
 int oasis_dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M,
                     const float* ada, int64_t ada_fstride, float* v_out, oasis_stream_t stream);
 
@@ -428,15 +446,14 @@ int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* b
 /* One full DiT denoising step for B streams of T frames (B*T <= 1024): conditioning MLP
  * (t fp32 [B*T], action fp32 [B*T, ext_dim_pad]), patch embed of patches fp32 [B*T*P, 64]
  * into buf->x, every sub-block and the final layer; v_out fp32 [B*T*P, 64].
- * tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The
+ * hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The
  * adaLN projections of all sub-blocks run as one pass over the stacked adaLN weights before
  * the first sub-block (with OASIS_ADALN_OVERLAP=1 in the environment: on a library-owned
  * side stream, each sub-block waiting only for its own rows).
  * (dit_forward_device with compute_cond_for_frame, oasis_inference.py:1406-1526.) */
 int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
                    int64_t T, const float* t, const float* action, const float* patches,
-                   float* tfreq, float* hid, float* cond, float* ada, float* v_out,
-                   oasis_stream_t stream);
+                   float* hid, float* cond, float* ada, float* v_out, oasis_stream_t stream);
 
 /* Temporal K/V cache of the context frame for the KV-cache DiT passes. For temporal
  * sub-block jt (sub-block j = 2*jt + 1), k + jt*S and v + jt*S (S = max_streams*P*2*D
@@ -522,7 +539,7 @@ int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* bu
  *   t, action: fp32 [1 + n_steps] timesteps and [1 + n_steps, ext_dim_pad] actions; row 0 is
  *        the context frame, row 1 + i the generated frame at step i;
  *   coeffs: HOST array of n_steps x 6 DDIM coefficients (oasis_ddim_update order);
- *   tfreq/hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (1 + n_steps rows);
+ *   hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (1 + n_steps rows);
  *   ctx_z: fp32 [P, D] scratch; v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae
  *   latent_dim] scratch; frame: fp32 [3, H, W] output. n_steps <= 15.
  * The adaLN projections of all conditioning rows run as one pass before the first step
@@ -535,8 +552,8 @@ int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* bu
 int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                      const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
                      const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
-                     const float* action, int64_t n_steps, const float* coeffs, float* tfreq,
-                     float* hid, float* cond, float* ada, float* ctx_z, float* v_out, float* latent,
+                     const float* action, int64_t n_steps, const float* coeffs, float* hid,
+                     float* cond, float* ada, float* ctx_z, float* v_out, float* latent,
                      float* frame, oasis_stream_t stream);
 
 /* n_frames consecutive generated frames of one stream with the context window rolled on
@@ -547,7 +564,7 @@ int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* bu
  *   chunks: fp32 [n_frames, P, 64] noise in, denoised latents out;
  *   t, action: fp32 [n_frames * (1 + n_steps)] and [n_frames * (1 + n_steps), ext_dim_pad]:
  *        frame f's rows at f*(1 + n_steps), row 0 its context frame, row 1 + i step i;
- *   tfreq/hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
+ *   hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
  *   frames: fp32 [n_frames, 3, H, W], or NULL for the DiT half only (the chunks are the
  *        output; vbuf and latent may then be NULL; oasis_video_decode is the other half);
  *   other arguments as in oasis_ddim_frame. n_frames <= 64.
@@ -557,7 +574,7 @@ int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* 
                        const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
                        const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
                        const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
-                       const float* coeffs, float* tfreq, float* hid, float* cond, float* ada, float* ctx_z,
+                       const float* coeffs, float* hid, float* cond, float* ada, float* ctx_z,
                        float* v_out, float* latent, float* frames, int overlap_decode,
                        oasis_stream_t stream);
 

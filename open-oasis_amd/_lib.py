@@ -16,7 +16,8 @@ MAX_SUB = 64
 EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32, EPI_GELU_TANH_FP8 = 8, 9
-ACT_NONE, ACT_SILU = 0, 1
+ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
+ABI_VERSION = 2
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
@@ -50,13 +51,12 @@ class DiTWeights(ctypes.Structure):
     _fields_ = [
         ("n_sub", c_i), ("d_model", c_i), ("n_heads", c_i), ("d_mlp", c_i), ("grid_h", c_i),
         ("grid_w", c_i), ("patch_dim", c_i), ("freq_dim", c_i), ("ext_dim_pad", c_i),
-        ("ada_w", c_p), ("ada_b", c_p),
+        ("ada_w", c_p), ("ada_b", c_p), ("final_ada_w", c_p), ("final_ada_b", c_p),
         ("qkv_w", c_p * MAX_SUB), ("out_w", c_p * MAX_SUB), ("out_b", c_p * MAX_SUB),
         ("fc1_w", c_p * MAX_SUB), ("fc1_b", c_p * MAX_SUB), ("fc2_w", c_p * MAX_SUB),
         ("fc2_b", c_p * MAX_SUB),
         ("final_w", c_p), ("final_b", c_p), ("xemb_w", c_p), ("xemb_b", c_p),
-        ("temb_w0", c_p), ("temb_b0", c_p), ("temb_w2", c_p), ("temb_b2", c_p),
-        ("ext_w", c_p), ("ext_b", c_p),
+        ("temb_w0", c_p), ("temb_b0", c_p), ("cond_w", c_p), ("cond_b", c_p),
         ("s_cos", c_p), ("s_sinp", c_p), ("t_cos", c_p), ("t_sinp", c_p), ("t_max", c_i),
         ("weight_format", c_i), ("qkv_s", c_p * MAX_SUB), ("out_s", c_p * MAX_SUB), ("fc1_s", c_p * MAX_SUB),
         ("fc2_s", c_p * MAX_SUB),
@@ -122,23 +122,23 @@ SIGNATURES = {
     "oasis_temporal_qkv_attention": [c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_f,
                                      c_p],
     "oasis_gemv_bf16": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
+    "oasis_gemv_f32": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
     "oasis_timestep_embedding": [c_p, c_i64, c_i64, c_p, c_p],
-    "oasis_small_linear": [c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_p, c_i64, c_p],
+    "oasis_small_linear": [c_p, c_i64, c_i64, c_i64, c_p, c_i, c_i, c_i64, c_p, c_p, c_i64, c_p],
     "oasis_ddim_update": [c_p, c_p, c_i64, c_f, c_f, c_f, c_f, c_f, c_f, c_p],
     "oasis_bridge": [c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_vae_unpatchify": [c_p, c_p, c_i64, c_i64, c_i64, c_p],
-    "oasis_dit_conditioning": [P(DiTWeights), c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p],
+    "oasis_dit_conditioning": [P(DiTWeights), c_p, c_p, c_i64, c_p, c_p, c_p, c_p],
     "oasis_dit_forward": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "oasis_dit_sub_blocks": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
     "oasis_video_decode": [P(DiTWeights), P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_p, c_p],
-    "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p,
-                       c_p],
+    "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,
-                         c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
+                         c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_video_frames": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_i64, c_p, c_p,
-                           c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p],
+                           c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p],
     "oasis_dit_precompute_past": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p],
     "oasis_dit_forward_current": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_graph_begin": [c_p],
@@ -167,6 +167,10 @@ def lib():
             f.argtypes = argt
             f.restype = c_i
         _LIB = h
+        if h.oasis_abi_version() != ABI_VERSION:
+            _LIB = None
+            raise ImportError("liboasis_hip.so has ABI version %d, this binding expects %d; rebuild it"
+                              % (h.oasis_abi_version(), ABI_VERSION))
         check_struct_layouts()
     return _LIB
 

@@ -6,15 +6,18 @@ its file discovery by key prefix (_find_weights_by_prefix, oasis_inference.py:48
 
 Tensors keep their checkpoint layout: linear weights [out, in], the patch-embed conv
 [D, C, 2, 2]. DiT / VAE fold the adaLN +1 and convert dtypes when they place them on the device.
-The VAE's RoPE frequencies are not in its checkpoint: the upstream vae.py computes them.
-vae_rope_freqs gives theta-10000 frequencies over a quarter of each head's dims, the same
-assumption synth.vae_weights makes for the decoder.
+The VAE decoder's RoPE angles are not in its checkpoint: the reference reads them from the
+upstream model's non-persistent ``rotary_freqs`` buffer, an (18, 32, 32) table of per-pixel angles
+for the first 32 dims of each head (precompute_vae_rope, oasis_inference.py:455-468), which the
+upstream vae.py computes and which is not available here. load_vae_decoder therefore takes that
+table as a required input (``rope_angles``); nothing fills in a guess. Its values are parity
+unpinned: no fixture of the reference holds them.
 """
 import os
 
 from safetensors import safe_open
 
-from .synth import theta_freqs
+import torch
 
 DIT_PREFIX = "blocks."       # find_dit_weights (oasis_inference.py:499-500)
 VAE_PREFIX = "encoder."      # find_vae_weights (oasis_inference.py:502-503)
@@ -61,12 +64,6 @@ def vae_decoder_names(depth):
     return pairs
 
 
-def vae_rope_freqs(head_dim):
-    """The decoder's axial RoPE frequencies (not stored in the checkpoint): theta 10000 over
-    head_dim / 4 rotated dims per axis, head_dim / 8 frequencies."""
-    return theta_freqs(head_dim // 8, head_dim // 4)
-
-
 def _count(keys, fmt):
     n = 0
     while fmt % n in keys:
@@ -91,11 +88,24 @@ def load_dit(path):
     return _read(path, dit_names, "blocks.%d.s_adaLN_modulation.1.weight", "DiT")
 
 
-def load_vae_decoder(path, head_dim=64):
+def load_vae_decoder(path, rope_angles):
     """ViT VAE decoder weight dict (for model.VAE) from an upstream VAE checkpoint (the encoder's
-    tensors are not read)."""
+    tensors are not read).
+
+    rope_angles: the decoder attention's RoPE angle table, the upstream model's
+    ``decoder[0].attn.rotary_freqs`` buffer: [grid_h, grid_w, rot] or [grid_h*grid_w, rot] with
+    rot <= head_dim (18 x 32 x 32 at Oasis-500M, oasis_inference.py:460-462). It is stored as
+    ``rope.vae_angles`` and used as given. Required: the checkpoint does not hold it."""
+    if rope_angles is None:
+        raise ValueError("load_vae_decoder needs rope_angles: the decoder's RoPE angle table "
+                         "(the upstream model's rotary_freqs buffer) is not in the checkpoint")
+    a = torch.as_tensor(rope_angles).float()
+    if a.dim() == 3:
+        a = a.reshape(-1, a.shape[-1])
+    if a.dim() != 2 or a.shape[1] % 2:
+        raise ValueError("rope_angles must be [grid_h, grid_w, rot] or [grid_h*grid_w, rot] with rot even")
     w = _read(path, vae_decoder_names, "decoder.%d.attn.qkv.weight", "VAE decoder")
-    w["rope.vae_freqs"] = vae_rope_freqs(head_dim)
+    w["rope.vae_angles"] = a.contiguous()
     return w
 
 

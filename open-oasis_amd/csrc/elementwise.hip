@@ -165,32 +165,45 @@ __global__ void temb_kernel(const float* t, int64_t R, int half, float* out) {
   }
 }
 
-// out[m, n] = b[n] + sum_k x[m, k] W[n, k]; block = R rows (staged in LDS), threads over n:
-// each thread reads its weight row once for R outputs.
-template <int R>
-__global__ __launch_bounds__(256) void small_linear_kernel(const float* x, int64_t ldx, int K, const bf16* W,
+// out[m, n] = b[n] + sum_k x[m, k] W(n, k); block = R rows (staged in LDS), threads over n:
+// each thread reads its weight row once for R outputs. W is bf16 or fp32 (TW), all sums fp32.
+// KMAJOR: W(n, k) = W[k * N + n] (consecutive threads read consecutive addresses); else W[n * K + k].
+template <int R, typename TW, bool KMAJOR>
+__global__ __launch_bounds__(256) void small_linear_kernel(const float* x, int64_t ldx, int K, const TW* W,
                                                            int N, const float* b, float* out, int64_t ld_out,
                                                            int64_t M) {
   __shared__ float xs[R][256];
   const int64_t m0 = (int64_t)blockIdx.y * R;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
   for (int i = threadIdx.x; i < R * K; i += blockDim.x) {
     const int r = i / K, k = i - r * K;
     xs[r][k] = m0 + r < M ? x[(m0 + r) * ldx + k] : 0.f;
   }
   __syncthreads();
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
-  const bf16* w = W + (int64_t)n * K;
+  const TW* w = W + (int64_t)n * K;
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = b ? b[n] : 0.f;
   for (int k = 0; k < K; k += 8) {
     float wv[8];
-    unpack8(*reinterpret_cast<const bf16x8*>(w + k), wv);
+    if constexpr (KMAJOR) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wv[j] = (float)W[(int64_t)(k + j) * N + n];
+    } else if constexpr (sizeof(TW) == 2) {
+      unpack8(*reinterpret_cast<const bf16x8*>(w + k), wv);
+    } else {
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(w + k), hi = *reinterpret_cast<const f32x4*>(w + k + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wv[j] = lo[j];
+        wv[4 + j] = hi[j];
+      }
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[r] += xs[r][k + j] * wv[j];
+      for (int j = 0; j < 8; ++j) acc[r] = fmaf(xs[r][k + j], wv[j], acc[r]);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -308,22 +321,35 @@ extern "C" int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, 
   return oasis::check_launch("timestep_embedding");
 }
 
-extern "C" int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W, int64_t N,
-                                  const float* b, float* out, int64_t ld_out, oasis_stream_t stream) {
+extern "C" int oasis_small_linear(const float* x, int64_t ldx, int64_t M, int64_t K, const void* W, int w_dtype,
+                                  int w_layout, int64_t N, const float* b, float* out, int64_t ld_out,
+                                  oasis_stream_t stream) {
   OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "small_linear: null pointer");
   OASIS_REQUIRE(oasis_aligned(16, W), OASIS_ERR_ARG, "small_linear: W must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0 && K <= 256 && K % 8 == 0 && ldx >= K && ld_out >= N, OASIS_ERR_SHAPE,
                 "small_linear: need 0 < K <= 256, K % 8 == 0");
-  OASIS_REQUIRE(M <= 65535, OASIS_ERR_SHAPE, "small_linear: M too large");
+  OASIS_REQUIRE(M <= 65535 * 16, OASIS_ERR_SHAPE, "small_linear: M too large");
+  OASIS_REQUIRE(w_dtype == OASIS_F32 || w_dtype == OASIS_BF16, OASIS_ERR_DTYPE, "small_linear: unsupported w_dtype %d",
+                w_dtype);
+  OASIS_REQUIRE(w_layout == 0 || w_layout == 1, OASIS_ERR_ARG, "small_linear: w_layout must be 0 ([N,K]) or 1 ([K,N])");
   const dim3 blk(256);
   const unsigned nb = (unsigned)((N + 255) / 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (M >= 2048)
-    hipLaunchKernelGGL(small_linear_kernel<16>, dim3(nb, (unsigned)((M + 15) / 16)), blk, 0, s, x, ldx, (int)K,
-                       static_cast<const bf16*>(W), (int)N, b, out, ld_out, M);
-  else
-    hipLaunchKernelGGL(small_linear_kernel<4>, dim3(nb, (unsigned)((M + 3) / 4)), blk, 0, s, x, ldx, (int)K,
-                       static_cast<const bf16*>(W), (int)N, b, out, ld_out, M);
+  const bool big = M >= 2048;
+  const dim3 grid(nb, (unsigned)(big ? (M + 15) / 16 : (M + 3) / 4));
+  OASIS_REQUIRE(grid.y <= 65535, OASIS_ERR_SHAPE, "small_linear: M too large");
+#define OASIS_SL(RV, TW, KM) \
+  hipLaunchKernelGGL((small_linear_kernel<RV, TW, KM>), grid, blk, 0, s, x, ldx, (int)K, static_cast<const TW*>(W), \
+                     (int)N, b, out, ld_out, M)
+#define OASIS_SL2(TW, KM) \
+  if (big) OASIS_SL(16, TW, KM); else OASIS_SL(4, TW, KM)
+  if (w_dtype == OASIS_BF16) {
+    if (w_layout) { OASIS_SL2(bf16, true); } else { OASIS_SL2(bf16, false); }
+  } else {
+    if (w_layout) { OASIS_SL2(float, true); } else { OASIS_SL2(float, false); }
+  }
+#undef OASIS_SL2
+#undef OASIS_SL
   return oasis::check_launch("small_linear");
 }
 

@@ -210,3 +210,175 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
 #undef OASIS_GEMV_GO
   return oasis::check_launch("gemv");
 }
+
+// ---------------------------------------------------------------------------------------
+// fp32 weights: out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]), everything fp32
+// (fp32 products and sums, no bf16 anywhere). For the projections the reference keeps in fp32:
+// the conditioning MLP and action projection (computed on the host in fp32,
+// oasis_inference.py:512-520,1406-1427) and the final layer's adaLN
+// (oasis_inference.py:527-532,1499-1511).
+//   - up to RP conditioning rows per pass are staged in LDS as fp32 (act_in applied once;
+//     act_in == OASIS_ACT_TEMB: x holds one timestep per row and the staged row is its
+//     sinusoidal embedding [cos(t f_i), sin(t f_i)], f_i = exp(-ln(10000) i / (K/2)));
+//   - a wave streams NU weight rows at a time as 1 KB coalesced vectors (lane l owns k = 4l..4l+3
+//     of every 256-wide K chunk), multiplies them against every staged row, and reduces each
+//     (n, r) dot product across the wave;
+//   - every W byte is read once per pass.
+constexpr int F32_RP = 8;    // conditioning rows per pass
+constexpr int F32_NU = 2;    // weight rows per wave
+constexpr int F32_CH = 4;    // 256-wide K chunks of a weight row held in registers at once
+
+// Every wave owns F32_NU weight rows and issues the loads of their first 1024 columns before the
+// workgroup stages x, so the HBM latency overlaps the staging; longer rows take further groups of
+// 1024 columns. The multiplied row can be two inputs side by side: columns [0, K1) from x and
+// [K1, K) from x2 (K1 = K without a second input).
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ x, int64_t ldx, int K1,
+                                                       const float* __restrict__ x2, int64_t ldx2, int R,
+                                                       const float* __restrict__ W, int N, int K,
+                                                       const float* __restrict__ b, float* __restrict__ out,
+                                                       int64_t ld_out, int act_in, int act_out, int accumulate) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  float* xs = reinterpret_cast<float*>(smem_raw);  // [F32_RP][K]
+  const int lane = threadIdx.x & 63;
+  const int64_t n0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * F32_NU;
+  auto load_group = [&](int kb, f32x4 (&w)[F32_NU][F32_CH]) {
+#pragma unroll
+    for (int u = 0; u < F32_NU; ++u)
+#pragma unroll
+      for (int c = 0; c < F32_CH; ++c) {
+        const int k = kb + c * 256 + lane * 4;
+        w[u][c] = (n0 + u < N && k < K) ? *reinterpret_cast<const f32x4*>(W + (n0 + u) * K + k)
+                                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  f32x4 w[F32_NU][F32_CH];
+  load_group(0, w);
+  // stage the R live rows (rows >= R are never read): 16-byte pieces, 4 per thread in flight
+  const int k4 = K / 4, nvec = R * k4;
+  for (int i0 = threadIdx.x; i0 < nvec; i0 += 4 * blockDim.x) {
+    f32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * blockDim.x;
+      if (i >= nvec) break;
+      const int r = i / k4, kk = 4 * (i - r * k4);
+      if (act_in == OASIS_ACT_TEMB) {
+        const float t = x[(int64_t)r * ldx];
+        const int half = K / 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int kj = kk + e, jj = kj < half ? kj : kj - half;
+          const float a = t * expf(-9.210340371976184f * (float)jj / (float)half);  // ln(10000)
+          v[j][e] = kj < half ? cosf(a) : sinf(a);
+        }
+      } else if (kk < K1) {
+        v[j] = *reinterpret_cast<const f32x4*>(x + (int64_t)r * ldx + kk);
+      } else {
+        v[j] = *reinterpret_cast<const f32x4*>(x2 + (int64_t)r * ldx2 + (kk - K1));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * blockDim.x;
+      if (i >= nvec) break;
+      const int r = i / k4, kk = 4 * (i - r * k4);
+      if (act_in == OASIS_ACT_SILU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[j][e] = silu(v[j][e]);
+      }
+      *reinterpret_cast<f32x4*>(xs + r * K + kk) = v[j];
+    }
+  }
+  __syncthreads();
+  if (n0 >= N) return;  // after the only barrier
+  float acc[F32_NU][F32_RP];
+#pragma unroll
+  for (int u = 0; u < F32_NU; ++u)
+#pragma unroll
+    for (int r = 0; r < F32_RP; ++r) acc[u][r] = 0.f;
+  for (int kb = 0; kb < K; kb += 256 * F32_CH) {
+    if (kb > 0) load_group(kb, w);
+#pragma unroll
+    for (int c = 0; c < F32_CH; ++c) {
+      const int k = kb + c * 256 + lane * 4;
+      if (k >= K) break;
+#pragma unroll
+      for (int r = 0; r < F32_RP; ++r) {
+        if (r >= R) break;
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + r * K + k);
+#pragma unroll
+        for (int u = 0; u < F32_NU; ++u)
+          acc[u][r] = fmaf(w[u][c][3], xv[3], fmaf(w[u][c][2], xv[2], fmaf(w[u][c][1], xv[1],
+                      fmaf(w[u][c][0], xv[0], acc[u][r]))));
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < F32_NU; ++u) {
+#pragma unroll
+    for (int r = 0; r < F32_RP; ++r) {
+      if (r >= R) break;
+      const float s = wave_sum(acc[u][r]);
+      const int64_t n = n0 + u;
+      if (lane == r && n < N) {
+        float v = s + (b ? b[n] : 0.f);
+        if (act_out == OASIS_ACT_SILU) v = silu(v);
+        float* o = out + (int64_t)r * ld_out + n;
+        *o = accumulate ? *o + v : v;
+      }
+    }
+  }
+}
+
+namespace oasis {
+
+int gemv_f32_cat(const float* x, int64_t ldx, int64_t K1, const float* x2, int64_t ldx2, int64_t R, const float* W,
+                 int64_t N, int64_t K, const float* b, float* out, int64_t ld_out, int act_in, int act_out,
+                 int accumulate, hipStream_t s) {
+  OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "gemv_f32: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, W), OASIS_ERR_ARG, "gemv_f32: W must be 16-byte aligned");
+  OASIS_REQUIRE(R > 0 && R <= 1024, OASIS_ERR_SHAPE, "gemv_f32: R=%lld must be in [1, 1024]", (long long)R);
+  OASIS_REQUIRE(K > 0 && K % 4 == 0 && K <= 4096, OASIS_ERR_SHAPE, "gemv_f32: K=%lld must be a multiple of 4, <= 4096",
+                (long long)K);
+  OASIS_REQUIRE(N > 0 && N < (1ll << 31), OASIS_ERR_SHAPE, "gemv_f32: bad N=%lld", (long long)N);
+  OASIS_REQUIRE(K1 > 0 && K1 <= K && K1 % 4 == 0 && (K1 == K || (x2 && act_in != OASIS_ACT_TEMB)), OASIS_ERR_ARG,
+                "gemv_f32: bad split of K between the two inputs");
+  OASIS_REQUIRE((act_in == OASIS_ACT_TEMB ? ldx >= 1 : ldx >= K1 && ldx % 4 == 0) &&
+                    (K1 == K || (ldx2 >= K - K1 && ldx2 % 4 == 0)) && ld_out >= N,
+                OASIS_ERR_SHAPE, "gemv_f32: ldx/ld_out too small (x rows must be multiples of 4 floats)");
+  OASIS_REQUIRE(act_in == OASIS_ACT_TEMB || oasis_aligned(16, x, x2), OASIS_ERR_ARG,
+                "gemv_f32: x must be 16-byte aligned");
+  OASIS_REQUIRE((act_in == OASIS_ACT_NONE || act_in == OASIS_ACT_SILU || act_in == OASIS_ACT_TEMB) &&
+                    (act_out == OASIS_ACT_NONE || act_out == OASIS_ACT_SILU),
+                OASIS_ERR_ARG, "gemv_f32: bad activation");
+  const size_t smem = (size_t)F32_RP * K * sizeof(float);
+  if (smem > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_f32_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) {
+      oasis::set_error("gemv_f32: cannot reserve %zu bytes of LDS: %s", smem, hipGetErrorString(e));
+      return OASIS_ERR_LAUNCH;
+    }
+  }
+  // one wave per F32_NU weight rows
+  const int64_t rows_per_block = 4 * F32_NU;
+  const int64_t blocks = (N + rows_per_block - 1) / rows_per_block;
+  for (int64_t r0 = 0; r0 < R; r0 += F32_RP) {
+    const int rc = (int)std::min<int64_t>(F32_RP, R - r0);
+    hipLaunchKernelGGL(gemv_f32_kernel, dim3((unsigned)blocks), dim3(256), smem, s, x + r0 * ldx, ldx, (int)K1,
+                       x2 ? x2 + r0 * ldx2 : nullptr, ldx2, rc, W, (int)N, (int)K, b, out + r0 * ld_out, ld_out, act_in,
+                       act_out, accumulate);
+    const int e = oasis::check_launch("gemv_f32");
+    if (e != OASIS_OK) return e;
+  }
+  return OASIS_OK;
+}
+
+}  // namespace oasis
+
+extern "C" int oasis_gemv_f32(const float* x, int64_t ldx, int64_t R, const float* W, int64_t N, int64_t K,
+                              const float* b, float* out, int64_t ld_out, int act_in, int act_out, int accumulate,
+                              oasis_stream_t stream) {
+  return oasis::gemv_f32_cat(x, ldx, K, nullptr, 0, R, W, N, K, b, out, ld_out, act_in, act_out, accumulate,
+                             static_cast<hipStream_t>(stream));
+}

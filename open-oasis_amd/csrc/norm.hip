@@ -283,6 +283,165 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
   }
 }
 
+// The DiT's final layer in one launch, fp32 end to end as the reference keeps it
+// (oasis_inference.py:1497-1521). A workgroup takes RB = 4 rows and half of the 64 outputs:
+//   x[m] += g * (sum_s partial[s][m] + bias)                 (NP > 0: the pending FC2 residual)
+//   h[m]  = LN(x[m]) * scale_p1[f(m)] + shift[f(m)]          (fp32, kept in LDS)
+//   v[m, n] = sum_k h[m, k] W[n, k] + b[n]                    (W fp32 [64, D])
+// Phase 1 gives each wave one row (the row in registers, two wave reductions); the workgroup of
+// output half 0 writes x back. Phase 2: wave w owns 8 outputs, read as whole weight rows (lane l
+// holds columns 4l..4l+3 of each 256-wide chunk, so each load instruction reads 1 KB of one row);
+// the first 4 rows' loads are issued before phase 1. Each lane multiplies its columns against the
+// 4 h rows (held in registers), and every (output, row) dot product is reduced across the wave.
+template <int NC, int NP>
+__global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
+                                                          int64_t pstride, const float* __restrict__ bias,
+                                                          const float* __restrict__ gate, int64_t gate_fs, int64_t rpf,
+                                                          const float* __restrict__ scale_p1,
+                                                          const float* __restrict__ shift, int64_t ada_fs,
+                                                          const float* __restrict__ W, const float* __restrict__ fb,
+                                                          float* __restrict__ v_out, float eps) {
+  constexpr int D = NC * 256;
+  constexpr int RB = 4;     // rows per workgroup (one wave each in phase 1)
+  constexpr int NW = 8;     // outputs per wave (32 per workgroup, two workgroups per row block)
+  constexpr int NU = NC <= 4 ? 4 : 2;  // weight rows in registers at once
+  __shared__ __attribute__((aligned(16))) float hs[RB][D];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = blockIdx.x & 1;
+  const int64_t m0 = (int64_t)(blockIdx.x >> 1) * RB;
+  const int nbase = half * 32 + wave * NW;
+  f32x4 w[NU][NC];
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) w[u][c] = *reinterpret_cast<const f32x4*>(W + (int64_t)(nbase + u) * D + c * 256 + 4 * lane);
+  // ---- phase 1: residual + LN + modulate of row m0 + wave
+  {
+    const int rr = wave;
+    const int64_t row = m0 + rr;
+    if (row >= M) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) *reinterpret_cast<f32x4*>(&hs[rr][c * 256 + lane * 4]) = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      const int64_t f = row / rpf;
+      float* xr = x + row * D;
+      float v[NC][4];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) load4<float>(xr + c * 256 + lane * 4, v[c]);
+      if (NP > 0) {
+        float pv[NP > 0 ? NP : 1][NC][4], bv[NC][4], gv[NC][4];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int k = c * 256 + lane * 4;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) load4<float>(part + p * pstride + row * D + k, pv[p][c]);
+          if (bias) load4<float>(bias + k, bv[c]); else bv[c][0] = bv[c][1] = bv[c][2] = bv[c][3] = 0.f;
+          if (gate) load4<float>(gate + f * gate_fs + k, gv[c]); else gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 1.f;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float acc = bv[c][j];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) acc += pv[p][c][j];
+            v[c][j] += gv[c][j] * acc;
+          }
+          if (half == 0) store4<float>(xr + c * 256 + lane * 4, v[c]);
+        }
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
+      const float mean = wave_sum(s) * (1.0f / D);
+      float q = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[c][j] -= mean;
+          q += v[c][j] * v[c][j];
+        }
+      const float rstd = rsqrtf(wave_sum(q) * (1.0f / D) + eps);
+      const float* a = scale_p1 + f * ada_fs;
+      const float* b = shift + f * ada_fs;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int k = c * 256 + lane * 4;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(a + k);
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(b + k);
+        *reinterpret_cast<f32x4*>(&hs[rr][k]) = f32x4{v[c][0] * rstd * av[0] + bv[0], v[c][1] * rstd * av[1] + bv[1],
+                                                      v[c][2] * rstd * av[2] + bv[2], v[c][3] * rstd * av[3] + bv[3]};
+      }
+    }
+  }
+  __syncthreads();
+  // ---- phase 2: this lane's columns of the 4 h rows against the wave's 8 weight rows; the next
+  // NU weight rows are in flight while the current ones are multiplied
+  float part_sum[NW * RB];  // (output u, row r) at u * RB + r, this lane's columns only
+#pragma unroll
+  for (int nb = 0; nb < NW; nb += NU) {
+    f32x4 wn[NU][NC];
+    if (nb + NU < NW) {
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          wn[u][c] = *reinterpret_cast<const f32x4*>(W + (int64_t)(nbase + nb + NU + u) * D + c * 256 + 4 * lane);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      f32x4 hv[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) hv[c] = *reinterpret_cast<const f32x4*>(&hs[r][c * 256 + 4 * lane]);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          acc = fmaf(hv[c][3], w[u][c][3], fmaf(hv[c][2], w[u][c][2], fmaf(hv[c][1], w[u][c][1],
+                fmaf(hv[c][0], w[u][c][0], acc))));
+        part_sum[(nb + u) * RB + r] = acc;
+      }
+    }
+    if (nb + NU < NW) {
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) w[u][c] = wn[u][c];
+    }
+  }
+  // the 32 sums across the wave: lane l ends with (output, row) index l >> 1
+  static_assert(NW * RB == 32, "one value per lane pair");
+  wave_sum_n<NW * RB>(part_sum, lane);
+  const float total = part_sum[0];
+  const int idx = lane >> 1, u = idx / RB, r = idx % RB;
+  const int64_t row = m0 + r;
+  const int n = nbase + u;
+  if ((lane & 1) == 0 && row < M) v_out[row * 64 + n] = total + (fb ? fb[n] : 0.f);
+}
+
+template <int NC>
+hipError_t final_layer_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
+                          const float* gate, int64_t gfs, int64_t rpf, const float* scale_p1, const float* shift,
+                          int64_t afs, const float* W, const float* fb, float* v_out, float eps, hipStream_t s) {
+  const dim3 grid((unsigned)(2 * ((M + 3) / 4))), block(256);  // 4 rows x 2 output halves per row block
+#define OASIS_FIN(NPV)                                                                                            \
+  hipLaunchKernelGGL((final_layer_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, scale_p1, \
+                     shift, afs, W, fb, v_out, eps)
+  switch (np) {
+    case 0: OASIS_FIN(0); break;
+    case 1: OASIS_FIN(1); break;
+    case 2: OASIS_FIN(2); break;
+    case 3: OASIS_FIN(3); break;
+    case 4: OASIS_FIN(4); break;
+    case 8: OASIS_FIN(8); break;
+    default: return hipErrorInvalidConfiguration;
+  }
+#undef OASIS_FIN
+  return hipGetLastError();
+}
+
 template <int NC>
 hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
@@ -413,6 +572,37 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
   }
   if (e != hipSuccess) {
     set_error("residual_ln launch failed: %s", hipGetErrorString(e));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
+int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
+                const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* scale_p1,
+                const float* shift, int64_t ada_fstride, const float* W, const float* b, float* v_out, float eps,
+                hipStream_t s) {
+  OASIS_REQUIRE(x && scale_p1 && shift && W && v_out, OASIS_ERR_NULL, "final_layer: null pointer");
+  OASIS_REQUIRE(oasis_aligned(16, x, partial, bias, gate, scale_p1, shift, W), OASIS_ERR_ARG,
+                "final_layer: pointers must be 16-byte aligned");
+  OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "final_layer: bad M/rows_per_frame");
+  OASIS_REQUIRE(n_partials == 0 || partial, OASIS_ERR_NULL, "final_layer: null partials");
+  OASIS_REQUIRE(n_partials <= 1 || partial_stride >= M * D, OASIS_ERR_ARG, "final_layer: partial_stride too small");
+  hipError_t e;
+  switch (D) {
+    case 256: e = final_layer_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
+    case 512: e = final_layer_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
+    case 1024: e = final_layer_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
+    case 2048: e = final_layer_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
+    default:
+      set_error("final_layer: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
+      return OASIS_ERR_SHAPE;
+  }
+  if (e == hipErrorInvalidConfiguration) {
+    set_error("final_layer: n_partials=%d must be one of 0-4 or 8", n_partials);
+    return OASIS_ERR_ARG;
+  }
+  if (e != hipSuccess) {
+    set_error("final_layer launch failed: %s", hipGetErrorString(e));
     return OASIS_ERR_LAUNCH;
   }
   return OASIS_OK;

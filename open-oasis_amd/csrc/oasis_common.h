@@ -41,6 +41,18 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
                 hipStream_t s);
+// The DiT's final layer in fp32 (norm.hip): the pending residual (n_partials split-K slices +
+// bias, gated), LN, modulate with the frame's (scale_p1, shift) rows, then v_out[M, 64] =
+// h @ W^T + b with W fp32 [64, D].
+int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
+                const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* scale_p1,
+                const float* shift, int64_t ada_fstride, const float* W, const float* b, float* v_out, float eps,
+                hipStream_t s);
+// oasis_gemv_f32 whose multiplied row is two inputs side by side: columns [0, K1) from x
+// [R, ldx] and [K1, K) from x2 [R, ldx2] (gemv.hip).
+int gemv_f32_cat(const float* x, int64_t ldx, int64_t K1, const float* x2, int64_t ldx2, int64_t R, const float* W,
+                 int64_t N, int64_t K, const float* b, float* out, int64_t ld_out, int act_in, int act_out,
+                 int accumulate, hipStream_t s);
 // Causal temporal attention (attention.hip); q_frame >= 0 computes only that query frame of
 // each group and writes it as a single frame: out [B*P, n_heads*64].
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
@@ -98,6 +110,31 @@ OASIS_DEV float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
+}
+
+// Sums of N values (N a power of two, 2..64) across the 64 lanes at once, v[i] holding this
+// lane's part of value i. Recursive halving: at each level every lane keeps the half of its
+// values selected by one lane bit and adds its partner's copy of that half (N/2 + N/4 + ... + 1
+// shuffles instead of 6 per value); the lane bits left over at the end are plain sums. On return
+// v[0] of lane l holds the full sum of value l / (64 / N). CNT is the level's count (template,
+// so every index is a compile-time constant).
+template <int N, int CNT = N>
+OASIS_DEV void wave_sum_n(float* v, int lane) {
+  static_assert(N >= 2 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two in [2, 64]");
+  if constexpr (CNT > 1) {
+    constexpr int o = 32 * CNT / N;
+    const bool upper = (lane & o) != 0;
+#pragma unroll
+    for (int i = 0; i < CNT / 2; ++i) {
+      const float give = upper ? v[i] : v[i + CNT / 2];
+      const float keep = upper ? v[i + CNT / 2] : v[i];
+      v[i] = keep + __shfl_xor(give, o, 64);
+    }
+    wave_sum_n<N, CNT / 2>(v, lane);
+  } else {
+#pragma unroll
+    for (int o = 32 / N; o >= 1; o >>= 1) v[0] += __shfl_xor(v[0], o, 64);
+  }
 }
 
 // ---- activations ------------------------------------------------------------

@@ -165,8 +165,8 @@ int check_dit(const oasis_dit_weights_t* w) {
                 "dit: d_model must be n_heads * 64");
   OASIS_REQUIRE(w->grid_h > 0 && w->grid_w > 0 && w->patch_dim == 64 && w->d_mlp > 0, OASIS_ERR_SHAPE,
                 "dit: bad grid/patch/mlp dims");
-  OASIS_REQUIRE(w->ada_w && w->ada_b && w->final_w && w->final_b && w->s_cos && w->s_sinp && w->t_cos &&
-                    w->t_sinp,
+  OASIS_REQUIRE(w->ada_w && w->ada_b && w->final_ada_w && w->final_ada_b && w->final_w && w->final_b && w->s_cos &&
+                    w->s_sinp && w->t_cos && w->t_sinp,
                 OASIS_ERR_NULL, "dit: missing weight pointer");
   for (int j = 0; j < w->n_sub; ++j)
     OASIS_REQUIRE(w->qkv_w[j] && w->out_w[j] && w->out_b[j] && w->fc1_w[j] && w->fc1_b[j] && w->fc2_w[j] &&
@@ -203,22 +203,39 @@ int64_t ada_width(const oasis_dit_weights_t* w) { return (int64_t)w->n_sub * 6 *
 
 }  // namespace
 
-extern "C" int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action, int64_t R,
-                                      float* tfreq, float* hid, float* cond, float* ada, oasis_stream_t stream) {
-  OASIS_TRY(check_dit(w));
-  OASIS_REQUIRE(t && action && tfreq && hid && cond && ada, OASIS_ERR_NULL, "dit_conditioning: null buffer");
-  OASIS_REQUIRE(w->temb_w0 && w->temb_b0 && w->temb_w2 && w->temb_b2 && w->ext_w && w->ext_b, OASIS_ERR_NULL,
-                "dit_conditioning: missing conditioning weights");
+namespace {
+
+// conditioning MLP for R rows in fp32: cond = W2 silu(W0 temb(t) + b0) + b2 + Wext action + bext
+// (compute_cond_for_frame, oasis_inference.py:1406-1427) in two launches: the embedding is
+// formed inside the first GEMV, and the second multiplies [hid | action] by [W2 | Wext]
+int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, int64_t R, float* hid, float* cond,
+             oasis_stream_t stream) {
+  OASIS_REQUIRE(t && action && hid && cond, OASIS_ERR_NULL, "conditioning: null buffer");
+  OASIS_REQUIRE(w->temb_w0 && w->temb_b0 && w->cond_w && w->cond_b, OASIS_ERR_NULL,
+                "conditioning: missing conditioning weights");
   const int64_t D = w->d_model, F = w->freq_dim, E = w->ext_dim_pad;
-  OASIS_TRY(oasis_timestep_embedding(t, R, F, tfreq, stream));
-  OASIS_TRY(oasis_gemv_bf16(tfreq, F, R, w->temb_w0, D, F, w->temb_b0, hid, D, OASIS_ACT_NONE, OASIS_ACT_SILU, 0,
-                            stream));
-  OASIS_TRY(oasis_gemv_bf16(action, E, R, w->ext_w, D, E, w->ext_b, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 0,
-                            stream));
-  OASIS_TRY(oasis_gemv_bf16(hid, D, R, w->temb_w2, D, D, w->temb_b2, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 1,
-                            stream));
-  const int64_t NA = ada_width(w);
-  return oasis_gemv_bf16(cond, D, R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, stream);
+  OASIS_TRY(oasis_gemv_f32(t, 1, R, w->temb_w0, D, F, w->temb_b0, hid, D, OASIS_ACT_TEMB, OASIS_ACT_SILU, 0, stream));
+  return oasis::gemv_f32_cat(hid, D, D, action, E, R, w->cond_w, D, D + E, w->cond_b, cond, D, OASIS_ACT_NONE,
+                             OASIS_ACT_NONE, 0, (hipStream_t)stream);
+}
+
+// adaLN rows of R conditioning rows: the sub-blocks' (bf16 weights) in one pass, then the
+// final layer's (fp32 weights) at column n_sub*6D
+int adaln_rows(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, hipStream_t s) {
+  const int64_t D = w->d_model, NA = ada_width(w), NS = (int64_t)w->n_sub * 6 * D;
+  OASIS_TRY(oasis_gemv_bf16(cond, D, R, w->ada_w, NS, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, s));
+  return oasis_gemv_f32(cond, D, R, w->final_ada_w, 2 * D, D, w->final_ada_b, ada + NS, NA, OASIS_ACT_SILU,
+                        OASIS_ACT_NONE, 0, s);
+}
+
+}  // namespace
+
+extern "C" int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action, int64_t R,
+                                      float* hid, float* cond, float* ada, oasis_stream_t stream) {
+  OASIS_TRY(check_dit(w));
+  OASIS_REQUIRE(t && action && hid && cond && ada, OASIS_ERR_NULL, "dit_conditioning: null buffer");
+  OASIS_TRY(cond_mlp(w, t, action, R, hid, cond, stream));
+  return adaln_rows(w, cond, R, ada, (hipStream_t)stream);
 }
 
 namespace {
@@ -412,36 +429,14 @@ int dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int6
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w;
   if (ada_ready && hipStreamWaitEvent((hipStream_t)stream, ada_ready, 0) != hipSuccess)
     return oasis::check_launch("wait for adaLN rows");
-  const float* fa = ada + (int64_t)w->n_sub * 6 * D;
-  OASIS_TRY(oasis_residual_ln(buf->x, M, D, buf->partial, pend.n, M * D, pend.bias, pend.gate, fs, P, fa + D, fa, fs,
-                              buf->h, kLnEps, stream));
-  oasis_epilogue_t fin = epi_zero();
-  fin.kind = OASIS_EPI_STORE_F32;
-  fin.bias = w->final_b;
-  fin.out_f32 = v_out;
-  fin.ld_out = w->patch_dim;
-  return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->final_w, D, M, w->patch_dim, D, fin,
-                            (hipStream_t)stream);
+  const float* fa = ada + (int64_t)w->n_sub * 6 * D;  // shift, scale_p1
+  return oasis::final_layer(buf->x, M, D, buf->partial, pend.n, M * D, pend.bias, pend.gate, fs, P, fa + D, fa, fs,
+                            w->final_w, w->final_b, v_out, kLnEps, (hipStream_t)stream);
 }
 
 }  // namespace
 
 namespace {
-
-// conditioning MLP for R rows: cond = W2 silu(W0 temb(t) + b0) + b2 + Wext action + bext
-int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, int64_t R, float* tfreq, float* hid,
-             float* cond, oasis_stream_t stream) {
-  OASIS_REQUIRE(t && action && tfreq && hid && cond, OASIS_ERR_NULL, "conditioning: null buffer");
-  OASIS_REQUIRE(w->temb_w0 && w->temb_b0 && w->temb_w2 && w->temb_b2 && w->ext_w && w->ext_b, OASIS_ERR_NULL,
-                "conditioning: missing conditioning weights");
-  const int64_t D = w->d_model, F = w->freq_dim, E = w->ext_dim_pad;
-  OASIS_TRY(oasis_timestep_embedding(t, R, F, tfreq, stream));
-  OASIS_TRY(oasis_gemv_bf16(tfreq, F, R, w->temb_w0, D, F, w->temb_b0, hid, D, OASIS_ACT_NONE, OASIS_ACT_SILU, 0,
-                            stream));
-  OASIS_TRY(oasis_gemv_bf16(action, E, R, w->ext_w, D, E, w->ext_b, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 0,
-                            stream));
-  return oasis_gemv_bf16(hid, D, R, w->temb_w2, D, D, w->temb_b2, cond, D, OASIS_ACT_NONE, OASIS_ACT_NONE, 1, stream);
-}
 
 // ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b on the side stream, one event per consumer
 // (sub-block j -> ev[j], final layer -> ev[n_sub]); returns the side-stream table.
@@ -449,8 +444,7 @@ int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float
                SideStream** out) {
   const int64_t D = w->d_model, NA = ada_width(w);
   if (!plan().overlap) {  // all projections in one pass on the caller's stream; no waits needed
-    OASIS_TRY(oasis_gemv_bf16(cond, D, R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
-                              stream));
+    OASIS_TRY(adaln_rows(w, cond, R, ada, (hipStream_t)stream));
     *out = nullptr;
     return OASIS_OK;
   }
@@ -459,9 +453,13 @@ int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float
   if (hipEventRecord(ss->fork, (hipStream_t)stream) != hipSuccess || hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
     return oasis::check_launch("adaLN fork");
   for (int j = 0; j <= w->n_sub; ++j) {
-    const int64_t r0 = (int64_t)j * 6 * D, n = j < w->n_sub ? 6 * D : 2 * D;
-    OASIS_TRY(oasis_gemv_bf16(cond, D, R, static_cast<const bf16*>(w->ada_w) + r0 * D, n, D, w->ada_b + r0, ada + r0,
-                              NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, ss->s));
+    const int64_t r0 = (int64_t)j * 6 * D;
+    if (j < w->n_sub)
+      OASIS_TRY(oasis_gemv_bf16(cond, D, R, static_cast<const bf16*>(w->ada_w) + r0 * D, 6 * D, D, w->ada_b + r0,
+                                ada + r0, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, ss->s));
+    else
+      OASIS_TRY(oasis_gemv_f32(cond, D, R, w->final_ada_w, 2 * D, D, w->final_ada_b, ada + r0, NA, OASIS_ACT_SILU,
+                               OASIS_ACT_NONE, 0, ss->s));
     if (hipEventRecord(ss->ev[j], ss->s) != hipSuccess) return oasis::check_launch("adaLN event");
   }
   *out = ss;
@@ -471,18 +469,18 @@ int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float
 }  // namespace
 
 extern "C" int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T,
-                              const float* t, const float* action, const float* patches, float* tfreq, float* hid,
-                              float* cond, float* ada, float* v_out, oasis_stream_t stream) {
+                              const float* t, const float* action, const float* patches, float* hid, float* cond,
+                              float* ada, float* v_out, oasis_stream_t stream) {
   OASIS_TRY(dit_args(w, buf, B, T, ada));
   OASIS_REQUIRE(patches && v_out, OASIS_ERR_NULL, "dit_step: null patches/v_out");
   OASIS_REQUIRE(w->xemb_w && w->xemb_b, OASIS_ERR_NULL, "dit_step: missing patch-embed weights");
   const int64_t R = B * T, D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
   OASIS_REQUIRE(R <= 1024, OASIS_ERR_SHAPE, "dit_step: at most 1024 frames per call (got %lld)", (long long)R);
-  OASIS_TRY(cond_mlp(w, t, action, R, tfreq, hid, cond, stream));
+  OASIS_TRY(cond_mlp(w, t, action, R, hid, cond, stream));
   SideStream* ss = nullptr;
   OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
-  OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x, D,
-                               stream));
+  OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
+                               buf->x, D, stream));
   Pending pend;
   OASIS_TRY(dit_blocks(w, buf, B, T, ada, NA, 0, w->n_sub, &pend, stream, ss ? ss->ev : nullptr));
   return dit_final(w, buf, B * T * P, ada, NA, pend, v_out, stream, ss ? ss->ev[w->n_sub] : nullptr);
@@ -580,7 +578,8 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
                                         : choose_splits(L, D, D, buf->max_splits);
   const int sf = pl.splits[ROLE_VFC2] > 0 ? std::min<int>(pl.splits[ROLE_VFC2], buf->max_splits)
                                           : choose_splits(L, D, Dm, buf->max_splits);
-  OASIS_TRY(oasis_small_linear(latent, w->latent_dim, L, w->latent_dim, w->pq_w, D, w->pq_b, buf->x, D, stream));
+  OASIS_TRY(oasis_small_linear(latent, w->latent_dim, L, w->latent_dim, w->pq_w, OASIS_BF16, 0, D, w->pq_b, buf->x, D,
+                               stream));
 
   oasis_epilogue_t qkv = epi_zero();
   qkv.kind = OASIS_EPI_QKV_ROPE;
@@ -662,7 +661,8 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     Pending pend;
     const bool wait = ss && i == 0;
     if (t1) {
-      OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x, D, stream));
+      OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, buf->x, D,
+                                   stream));
       const float* ada_cur = ada + (1 + i) * NA;  // the generated frame's rows at step i
       OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, nullptr, use));
       OASIS_TRY(dit_final(w, buf, P, ada_cur, NA, pend, v_out, stream));
@@ -672,8 +672,8 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     // z = [context frame; patch-embedded chunk] (oasis_inference.py:1911-1913)
     if (hipMemcpyAsync(buf->x, ctx_z, P * D * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess)
       return oasis::check_launch("ddim_frame context copy");
-    OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, buf->x + P * D, D,
-                                 stream));
+    OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
+                                 buf->x + P * D, D, stream));
     const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
     OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, wait ? ss->ev : nullptr,
                          kv ? save : KvPass()));
@@ -706,8 +706,8 @@ constexpr float kInvScaling = 1.0f / 0.07843137255f;  // 1 / scaling_factor (oas
 extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
                                 const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
                                 const oasis_kv_cache_t* kv, float* chunk, const float* ctx_patches, const float* t,
-                                const float* action, int64_t n_steps, const float* coeffs, float* tfreq, float* hid,
-                                float* cond, float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
+                                const float* action, int64_t n_steps, const float* coeffs, float* hid, float* cond,
+                                float* ada, float* ctx_z, float* v_out, float* latent, float* frame,
                                 oasis_stream_t stream) {
   OASIS_TRY(frame_args(w, buf, vw, n_steps));
   OASIS_REQUIRE(vbuf && chunk && ctx_patches && coeffs && ada && ctx_z && v_out && latent && frame,
@@ -715,10 +715,11 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
   // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
   // covers all rows (with the overlap option it streams on the side stream during step 0)
-  OASIS_TRY(cond_mlp(w, t, action, 1 + n_steps, tfreq, hid, cond, stream));
+  OASIS_TRY(cond_mlp(w, t, action, 1 + n_steps, hid, cond, stream));
   SideStream* ss = nullptr;
   OASIS_TRY(fork_adaln(w, cond, 1 + n_steps, ada, stream, &ss));
-  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
+  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z,
+                               D, stream));
   OASIS_TRY(frame_steps(w, buf, kv, chunk, ctx_z, ada, n_steps, coeffs, v_out, ss, stream));
   OASIS_TRY(oasis_bridge(chunk, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
   return oasis_vae_decode(vw, vbuf, latent, frame, stream);
@@ -728,12 +729,12 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
                                   const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
                                   const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
                                   const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
-                                  const float* coeffs, float* tfreq, float* hid, float* cond, float* ada,
-                                  float* ctx_z, float* v_out, float* latent, float* frames, int overlap_decode,
+                                  const float* coeffs, float* hid, float* cond, float* ada, float* ctx_z,
+                                  float* v_out, float* latent, float* frames, int overlap_decode,
                                   oasis_stream_t stream) {
   OASIS_TRY(frame_args(w, buf, vw, n_steps));
   const bool decode = frames != nullptr;  // frames == NULL: the DiT half only
-  OASIS_REQUIRE(chunks && ctx_patches && t && action && coeffs && tfreq && hid && cond && ada && ctx_z && v_out &&
+  OASIS_REQUIRE(chunks && ctx_patches && t && action && coeffs && hid && cond && ada && ctx_z && v_out &&
                     (!decode || (vbuf && latent)),
                 OASIS_ERR_NULL, "video_frames: null pointer");
   OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_frames: n_frames must be in [1, %d]",
@@ -743,15 +744,15 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
   const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
   hipStream_t s = (hipStream_t)stream;
   // every frame's conditioning rows at once: frame f's rows at f*R (context, then step i)
-  OASIS_TRY(cond_mlp(w, t, action, n_frames * R, tfreq, hid, cond, stream));
-  OASIS_TRY(oasis_gemv_bf16(cond, D, n_frames * R, w->ada_w, NA, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE,
-                            0, stream));
+  OASIS_TRY(cond_mlp(w, t, action, n_frames * R, hid, cond, stream));
+  OASIS_TRY(adaln_rows(w, cond, n_frames * R, ada, s));
   SideStream* ss = nullptr;
   if (overlap_decode && decode) OASIS_TRY(side_stream(&ss));
   for (int64_t f = 0; f < n_frames; ++f) {
     // context = the previous frame's denoised latent (the rolled context window)
     const float* ctx = f == 0 ? ctx_patches : chunks + (f - 1) * fsz;
-    OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, D, w->xemb_b, ctx_z, D, stream));
+    OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z, D,
+                                 stream));
     OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out, nullptr,
                           stream));
     if (!decode) continue;

@@ -5,14 +5,16 @@ workspaces (allocated up front, so nothing allocates inside a step or a captured
 graph), fills the C structs of include/oasis_hip.h and calls the composite entry
 points of liboasis_hip.so on a torch-ROCm stream.
 
-HBM layout (bf16 weights in the nn.Linear [out, in] layout, fp32 biases/tables):
-  - ``ada_w``: every sub-block's adaLN projection stacked, then the final layer's:
-    [n_sub*6D + 2D, D] (406 MB at Oasis-500M). One skinny-GEMM pass over it produces
-    the adaLN rows of all 33 consumers for every conditioning row at once.
-  - per sub-block: qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
+HBM layout (nn.Linear [out, in] weights, fp32 biases/tables):
+  - ``ada_w`` (bf16): every sub-block's adaLN projection stacked, [n_sub*6D, D] (403 MB at
+    Oasis-500M). One skinny-GEMM pass over it produces the adaLN rows of all 32 sub-blocks
+    for every conditioning row at once.
+  - per sub-block (bf16): qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
     contiguous (37.7 MB of the 1.21 GB weight set per sub-block incl. adaLN).
-  - small: final_w [64, D], patch-embed [D, 64] in (p, q, c) column order, conditioning
-    MLP and action projection (zero-padded to 64 inputs), RoPE cos/sin tables.
+  - fp32, as the reference keeps them (oasis_inference.py:512-532,1821-1826): the
+    conditioning MLP and action projection (zero-padded to 64 inputs), the patch embed
+    [D, 64] in (p, q, c) column order, the final layer's adaLN [2D, D] and linear [64, D].
+  - RoPE cos/sin tables (fp32).
 """
 import ctypes
 import math
@@ -68,7 +70,8 @@ class DiT:
     weights="bf16" keeps the projection weights in bf16. weights="fp8" stores the QKV, O,
     FC1 and FC2 weights as OCP e4m3 with one fp32 scale per output channel (quantized on
     the device by oasis_quantize_fp8_rows) and runs those projections on the fp8 GEMM;
-    adaLN, conditioning, patch embed and the final layer stay bf16."""
+    the sub-blocks' adaLN stays bf16, and conditioning, patch embed and the final layer
+    fp32, in both modes."""
 
     def __init__(self, w, device="cuda", grid=(9, 16), t_max=32, weights="bf16"):
         if weights not in ("bf16", "fp8"):
@@ -99,7 +102,9 @@ class DiT:
             keep.append(x)
             return x
 
-        # adaLN projections of all sub-blocks + the final layer, +1 folded into each scale chunk
+        f32 = torch.float32
+        # adaLN projections of all sub-blocks (bf16), +1 folded into each scale chunk
+        # (oasis_inference.py:549-556); the final layer's in fp32 (527-532)
         ws, bs = [], []
         for i in range(self.n_blocks):
             for kind in "st":
@@ -108,20 +113,21 @@ class DiT:
                 b[d:2 * d] += 1.0
                 b[4 * d:5 * d] += 1.0
                 bs.append(b)
-        ws.append(w["final.ada_w"])
+        self.ada_width = self.n_sub * 6 * d + 2 * d   # adaLN row width: every sub-block, then the final layer
+        self.ada_w = put(torch.cat([x.to(bf) for x in ws], 0), bf)
+        self.ada_b = put(torch.cat(bs, 0), f32)
+        del ws, bs
         fb = w["final.ada_b"].float().clone()
         fb[d:2 * d] += 1.0
-        bs.append(fb)
-        self.ada_width = self.n_sub * 6 * d + 2 * d
-        self.ada_w = put(torch.cat([x.to(bf) for x in ws], 0), bf)
-        self.ada_b = put(torch.cat(bs, 0), torch.float32)
-        del ws, bs
+        self.final_ada_w = put(w["final.ada_w"], f32)
+        self.final_ada_b = put(fb, f32)
 
         S = L.DiTWeights()
         S.n_sub, S.d_model, S.n_heads, S.d_mlp = self.n_sub, d, self.n_heads, self.d_mlp
         S.grid_h, S.grid_w, S.patch_dim = grid[0], grid[1], self.patch_dim
         S.freq_dim, S.ext_dim_pad = self.freq_dim, self.ext_pad
         S.ada_w, S.ada_b = self.ada_w.data_ptr(), self.ada_b.data_ptr()
+        S.final_ada_w, S.final_ada_b = self.final_ada_w.data_ptr(), self.final_ada_b.data_ptr()
         fp8 = weights == "fp8"
         if fp8 and self.device.type != "cuda":
             raise ValueError("fp8 weights are quantized on the GPU")
@@ -151,20 +157,21 @@ class DiT:
             S.fc2_b[j] = put(w[p + "fc2_b"], torch.float32).data_ptr()
         if fp8:
             torch.cuda.synchronize(dev)
-        S.final_w = put(w["final.w"], bf).data_ptr()
-        S.final_b = put(w["final.b"], torch.float32).data_ptr()
-        # patch embed: conv [D, C, 2, 2] -> [D, (p, q, c)] (W_rt of oasis_inference.py:1821-1826)
+        S.final_w = put(w["final.w"], f32).data_ptr()
+        S.final_b = put(w["final.b"], f32).data_ptr()
+        # patch embed: conv [D, C, 2, 2] -> [D, (p, q, c)], W_rt^T (oasis_inference.py:1821-1826)
         cw = w["x_emb.w"]
-        S.xemb_w = put(cw.permute(0, 2, 3, 1).reshape(d, -1), bf).data_ptr()
-        S.xemb_b = put(w["x_emb.b"], torch.float32).data_ptr()
-        S.temb_w0 = put(w["t_emb.w0"], bf).data_ptr()
-        S.temb_b0 = put(w["t_emb.b0"], torch.float32).data_ptr()
-        S.temb_w2 = put(w["t_emb.w2"], bf).data_ptr()
-        S.temb_b2 = put(w["t_emb.b2"], torch.float32).data_ptr()
-        ext = torch.zeros(d, self.ext_pad, dtype=bf)
-        ext[:, :self.ext_dim] = w["ext.w"].to(bf)
-        S.ext_w = put(ext, bf).data_ptr()
-        S.ext_b = put(w["ext.b"], torch.float32).data_ptr()
+        S.xemb_w = put(cw.float().permute(0, 2, 3, 1).reshape(d, -1), f32).data_ptr()
+        S.xemb_b = put(w["x_emb.b"], f32).data_ptr()
+        S.temb_w0 = put(w["t_emb.w0"], f32).data_ptr()
+        S.temb_b0 = put(w["t_emb.b0"], f32).data_ptr()
+        # the MLP's second linear and the action projection side by side: one GEMV multiplies
+        # [hid | action] by [W2 | Wext] (action zero-padded to ext_pad inputs)
+        cw2 = torch.zeros(d, d + self.ext_pad, dtype=f32)
+        cw2[:, :d] = w["t_emb.w2"].float()
+        cw2[:, d:d + self.ext_dim] = w["ext.w"].float()
+        S.cond_w = put(cw2, f32).data_ptr()
+        S.cond_b = put(w["t_emb.b2"].float() + w["ext.b"].float(), f32).data_ptr()
         sc, ss = rope_tables(_axial_angles(w["rope.spatial_freqs"].float(), *grid))
         tc, ts = rope_tables(temporal_angles(w["rope.temporal_freqs"].float(), t_max))
         self.s_cos, self.s_sinp = put(sc, torch.float32), put(ss, torch.float32)
@@ -197,23 +204,27 @@ class DiT:
     def conditioning_inplace(self, R, ws, stream=None):
         """Conditioning from ws.t[:R] / ws.act[:R] into ws.cond / ws.ada (no host work)."""
         L.call("oasis_dit_conditioning", ctypes.byref(self.struct), L.ptr(ws.t), L.ptr(ws.act), R,
-               L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada), L.stream_handle(stream))
+               L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada), L.stream_handle(stream))
 
     def adaln_from_cond(self, cond, ws, stream=None):
         """ada rows from given (pre-SiLU) cond vectors [R, D] (the reference passes cond
         computed on the host, oasis_inference.py:1406-1427)."""
         R = cond.shape[0]
         ws.cond[:R].copy_(cond)
-        L.call("oasis_gemv_bf16", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), self.ada_width, self.d,
-               L.ptr(self.ada_b), L.ptr(ws.ada), self.ada_width, L.ACT_SILU, L.ACT_NONE, 0,
-               L.stream_handle(stream))
+        ns = self.n_sub * 6 * self.d
+        h = L.stream_handle(stream)
+        L.call("oasis_gemv_bf16", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), ns, self.d,
+               L.ptr(self.ada_b), L.ptr(ws.ada), self.ada_width, L.ACT_SILU, L.ACT_NONE, 0, h)
+        L.call("oasis_gemv_f32", L.ptr(ws.cond), self.d, R, L.ptr(self.final_ada_w), 2 * self.d, self.d,
+               L.ptr(self.final_ada_b), ctypes.c_void_p(ws.ada.data_ptr() + 4 * ns), self.ada_width, L.ACT_SILU,
+               L.ACT_NONE, 0, h)
         return ws.ada[:R]
 
     def patch_embed(self, patches, out, stream=None):
         """out[M, D] = patches[M, 64] @ W_rt + b (patches in (p, q, c) column order)."""
         M = patches.shape[0]
         L.call("oasis_small_linear", L.ptr(patches), self.patch_dim, M, self.patch_dim,
-               ctypes.c_void_p(self.struct.xemb_w), self.d, ctypes.c_void_p(self.struct.xemb_b),
+               ctypes.c_void_p(self.struct.xemb_w), L.F32, 0, self.d, ctypes.c_void_p(self.struct.xemb_b),
                L.ptr(out), self.d, L.stream_handle(stream))
 
     def sub_blocks_inplace(self, ws, B, T, ada, ada_fstride, j0, j1, stream=None):
@@ -272,7 +283,6 @@ class DiTWorkspace:
         self.v_out = torch.zeros(max_rows, dit.patch_dim, device=dev)
         self.t = torch.zeros(max_cond, device=dev)
         self.act = torch.zeros(max_cond, dit.ext_pad, device=dev)
-        self.tfreq = torch.zeros(max_cond, dit.freq_dim, device=dev)
         self.hid = torch.zeros(max_cond, d, device=dev)
         self.cond = torch.zeros(max_cond, d, device=dev)
         self.ada = torch.zeros(max_cond, dit.ada_width, device=dev)
@@ -327,7 +337,13 @@ class VAE:
             S.fc2_w[i], S.fc2_b[i] = put(vw[p + "fc2_w"], bf), put(vw[p + "fc2_b"], f32)
         S.norm_w, S.norm_b = put(vw["norm_w"], f32), put(vw["norm_b"], f32)
         S.pred_w, S.pred_b = put(vw["pred_w"], bf), put(vw["pred_b"], f32)
-        c, s = rope_tables(_axial_angles(vw["rope.vae_freqs"].float(), *grid))
+        # the angle table as given (the upstream model's rotary_freqs buffer, oasis_inference.py:
+        # 455-468), else the axial construction from frequencies (synthetic weights)
+        if "rope.vae_angles" in vw:
+            ang = vw["rope.vae_angles"].double().reshape(self.L, -1)
+        else:
+            ang = _axial_angles(vw["rope.vae_freqs"].float(), *grid)
+        c, s = rope_tables(ang)
         S.rope_cos, S.rope_sinp = put(c, f32), put(s, f32)
         self.struct = S
         self._keep = keep
@@ -423,7 +439,7 @@ class DiTStep:
     def enqueue(self):
         d, ws = self.dit, self.ws
         L.call("oasis_dit_step", ctypes.byref(d.struct), ctypes.byref(ws.struct), self.B, self.T, L.ptr(ws.t),
-               L.ptr(ws.act), L.ptr(self.patches), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada),
+               L.ptr(ws.act), L.ptr(self.patches), L.ptr(ws.hid), L.ptr(ws.cond), L.ptr(ws.ada),
                L.ptr(ws.v_out), L.stream_handle(self.stream))
 
     def capture(self):
@@ -448,7 +464,10 @@ class FramePipeline:
     stores the context frame's temporal K/V; the later steps run the generated frame alone
     at T=1 against that cache. kv_cache=False runs every step at T=2.
     Inputs: self.chunk [P, 64] noise (patch space), self.ctx_patches [P, 64],
-    self.ws.t / self.ws.act rows [0] context and [1+i] generated frame at step i."""
+    self.ws.t / self.ws.act rows [0] context and [1+i] generated frame at step i.
+    run() denoises self.chunk in place: the next frame needs new noise in self.chunk and its
+    context in self.ctx_patches first (set_inputs, or PlaySession, which does both on the
+    device)."""
 
     def __init__(self, dit, vae, steps, alphas_cumprod, stream=None, kv_cache=True):
         from .schedule import ddim_coefficients
@@ -485,7 +504,7 @@ class FramePipeline:
                ctypes.byref(self.vae.struct), ctypes.byref(self.vws.struct),
                ctypes.byref(self.kv.struct) if self.kv is not None else None, L.ptr(self.chunk),
                L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
-               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
+               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.hid), L.ptr(ws.cond),
                L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent), L.ptr(self.vws.frame),
                L.stream_handle(self.stream))
 
@@ -520,7 +539,13 @@ class VideoPipeline:
 
     Inputs: self.chunks [n_frames, P, 64] noise, self.ctx_patches [P, 64] the first context,
     conditioning rows built by set_inputs (context t and action, then each step's t with
-    the frame's action; the context of frame f > 0 carries frame f-1's action)."""
+    the frame's action; the context of frame f > 0 carries frame f-1's action).
+
+    Each launch denoises the chunk buffers in place and starts from self.ctx_patches; it does
+    not draw new noise or carry the context over from the previous batch. A continuing video
+    calls set_inputs before every batch with fresh noise and, as ctx_patches, the previous
+    batch's last latent (self.chunks[-1] once that batch is done). Launches without it re-run
+    the same batch on the previous outputs (what a timing loop does)."""
 
     def __init__(self, dit, vae, steps, alphas_cumprod, n_frames, stream=None, kv_cache=True, overlap_decode=False):
         from .schedule import ddim_coefficients
@@ -582,7 +607,7 @@ class VideoPipeline:
                ctypes.byref(self.vws.struct) if decode else None,
                ctypes.byref(self.kv.struct) if self.kv is not None else None,
                self.n_frames, L.ptr(self.chunk_bufs[b]), L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
-               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.tfreq), L.ptr(ws.hid), L.ptr(ws.cond),
+               ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.hid), L.ptr(ws.cond),
                L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent) if decode else None,
                L.ptr(self.frame_bufs[b]) if decode else None, 0, L.stream_handle(self.stream))
 

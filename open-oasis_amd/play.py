@@ -185,4 +185,7 @@ class PlaySession:
         return len(self.frame_times) / sum(self.frame_times) if self.frame_times else 0.0
 
     def status(self):
-        return {"frame_index": self.frame_index, "fps": round(self.fps, 1), "ddim_steps": self.ddim_steps}
+        """frame_index is the index of the last generated frame, numbered from 0 as the reference's
+        write_status(frame_idx, ...) reports it before its frame_idx += 1 (play.py:517-525); -1
+        before the first frame. self.frame_index counts the frames generated so far."""
+        return {"frame_index": self.frame_index - 1, "fps": round(self.fps, 1), "ddim_steps": self.ddim_steps}

@@ -510,7 +510,10 @@ def vae_decode(latent, w, n_heads=None, grid=(VAE_GRID_H, VAE_GRID_W)):
     D = x.shape[-1]
     n_heads = n_heads or D // D_HEAD
     d = D // n_heads
-    ang = vae_rope_angles(_f(w["rope.vae_freqs"]), *grid)
+    if "rope.vae_angles" in w:     # the model's own angle table (oasis_inference.py:455-468)
+        ang = _f(w["rope.vae_angles"]).reshape(x.shape[0], -1)
+    else:
+        ang = vae_rope_angles(_f(w["rope.vae_freqs"]), *grid)
     cos, sinp = rope_cos_sinperm(ang, d)
     for i in range(_count(w, "dec.%d.qkv_w")):
         p = "dec.%d." % i

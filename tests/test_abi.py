@@ -50,7 +50,8 @@ def test_binding_covers_the_header_with_matching_arity():
 
 
 def test_abi_version_and_struct_sizes(h):
-    assert h.oasis_abi_version() == 1
+    assert h.oasis_abi_version() == L.ABI_VERSION == int(
+        re.search(r"#define OASIS_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
     for i, st in enumerate(L.STRUCTS):
         assert h.oasis_abi_struct_size(i) == ctypes.sizeof(st)
     assert h.oasis_abi_struct_size(99) == -1
@@ -73,7 +74,11 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails val
     ("oasis_silu", (FAKE, FAKE, 16, 7, None), ERR_DTYPE, "dtype"),
     ("oasis_gated_residual", (FAKE, FAKE, None, FAKE, 8, 0, None), ERR_NULL, "null"),
     ("oasis_timestep_embedding", (FAKE, 1, 255, FAKE, None), ERR_SHAPE, "shape"),
-    ("oasis_small_linear", (FAKE, 512, 1, 512, FAKE, 64, None, FAKE, 64, None), ERR_SHAPE, ""),
+    ("oasis_small_linear", (FAKE, 512, 1, 512, FAKE, 0, 0, 64, None, FAKE, 64, None), ERR_SHAPE, ""),
+    ("oasis_small_linear", (FAKE, 64, 1, 64, FAKE, 5, 0, 64, None, FAKE, 64, None), ERR_DTYPE, "w_dtype"),
+    ("oasis_small_linear", (FAKE, 64, 1, 64, FAKE, 0, 2, 64, None, FAKE, 64, None), ERR_ARG, "w_layout"),
+    ("oasis_gemv_f32", (FAKE, 64, 2, FAKE, 64, 62, None, FAKE, 64, 0, 0, 0, None), ERR_SHAPE, "multiple of 4"),
+    ("oasis_gemv_f32", (FAKE, 64, 2, FAKE, 64, 64, None, FAKE, 64, 7, 0, 0, None), ERR_ARG, "activation"),
     ("oasis_rope_layout", (FAKE, 3 * 1024, FAKE, FAKE, 288, 144, 16, 32, FAKE, FAKE, FAKE, 1, 1, 1, 1, 0, 1, None),
      ERR_SHAPE, "head_dim"),
     ("oasis_bridge", (FAKE, FAKE, 0, 32, 16, 16, 1.0, None), ERR_SHAPE, "shape"),

@@ -12,6 +12,7 @@ from helpers import pkg
 
 ck = pkg.checkpoint
 synth = pkg.synth
+M = pkg.model
 
 
 def _small():
@@ -42,10 +43,20 @@ def test_vae_decoder_checkpoint_round_trip_ignores_the_encoder(tmp_path):
     path = str(tmp_path / "vae.safetensors")
     enc = {"encoder.0.attn.qkv.weight": torch.zeros(3, 3), "quant_conv.weight": torch.zeros(2, 2)}
     _write(path, ck.vae_decoder_names(2), vw, enc)
-    got = ck.load_vae_decoder(path, head_dim=64)
-    assert set(got) == set(vw)
+    with pytest.raises(ValueError, match="rope_angles"):
+        ck.load_vae_decoder(path, None)
+    angles = torch.rand(18, 32, 32, generator=torch.Generator().manual_seed(5))
+    got = ck.load_vae_decoder(path, angles)
+    assert set(got) == (set(vw) - {"rope.vae_freqs"}) | {"rope.vae_angles"}
     for k in vw:
-        assert torch.equal(got[k], vw[k]), k
+        if k != "rope.vae_freqs":
+            assert torch.equal(got[k], vw[k]), k
+    # the angle table is used as given: the model's RoPE tables are its cos / signed sin
+    assert torch.equal(got["rope.vae_angles"], angles.reshape(576, 32))
+    vae = M.VAE(got, "cpu")
+    cos = vae._keep[[t.data_ptr() for t in vae._keep].index(vae.struct.rope_cos)]
+    assert torch.allclose(cos[:, :32], angles.reshape(576, 32).double().cos().float(), atol=1e-6)
+    assert torch.equal(cos[:, 32:], torch.ones(576, 32))
 
 
 def test_find_checkpoint_by_prefix_skips_other_files(tmp_path):

@@ -367,6 +367,39 @@ def test_gemv(R, K, N, act_in, act_out, acc):
     assert_close(out, ref, 0.9999999, 1e-4, "gemv R=%d K=%d N=%d" % (R, K, N))
 
 
+@pytest.mark.parametrize("R,K,N,act_in,act_out,acc", [(2, 1024, 2048, 1, 0, 0), (5, 256, 1024, 2, 1, 0),
+                                                       (5, 1024, 1024, 0, 0, 1), (13, 64, 1024, 0, 0, 0),
+                                                       (3, 4096, 20, 1, 1, 1), (80, 256, 1024, 2, 1, 0)])
+def test_gemv_f32(R, K, N, act_in, act_out, acc):
+    """fp32 weights and arithmetic: within 1e-6 of an fp64 product (the bf16 GEMV keeps ~1e-5).
+    act_in 2 forms the timestep embedding of x[r, 0] in LDS; 13 and 80 rows take 2 and 10
+    passes of 8 rows; N = 20 leaves part of a wave's 4-row group past N."""
+    g = _gen(40 + R)
+    if act_in == 2:
+        x = torch.rand(R, 1, generator=g) * 1000
+    else:
+        x = torch.randn(R, K, generator=g)
+    W = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g)
+    out0 = torch.randn(R, N, generator=g)
+    out = dev(out0)
+    L.call("oasis_gemv_f32", L.ptr(dev(x)), x.shape[1], R, L.ptr(dev(W)), N, K, L.ptr(dev(b)), L.ptr(out), N,
+           act_in, act_out, acc, stream())
+    sync()
+    if act_in == 2:
+        xi = oracle.timestep_embedding(x[:, 0].double(), K).double()
+    else:
+        xi = oracle.silu(x.double()) if act_in else x.double()
+    ref = xi @ W.double().t() + b.double()
+    if act_out:
+        ref = oracle.silu(ref)
+    if acc:
+        ref = ref + out0.double()
+    err = ((out.double().cpu() - ref).abs().max() / ref.abs().max()).item()
+    print("gemv_f32 R=%d K=%d N=%d: max rel %.2e" % (R, K, N, err), flush=True)
+    assert err < (2e-5 if act_in == 2 else 1e-6), err
+
+
 # ---------------------------------------------------------------- small ops
 def test_timestep_embedding():
     t = torch.tensor([0.0, 14.0, 249.0, 999.0, 517.0])
@@ -382,16 +415,25 @@ def test_small_linear_and_ddim_and_bridge():
     W = (torch.randn(1024, 64, generator=g) * 0.05).to(torch.bfloat16)
     b = torch.randn(1024, generator=g)
     out = torch.zeros(144, 1024, device="cuda")
-    L.call("oasis_small_linear", L.ptr(dev(x)), 64, 144, 64, L.ptr(dev(W)), 1024, L.ptr(dev(b)), L.ptr(out),
-           1024, stream())
+    L.call("oasis_small_linear", L.ptr(dev(x)), 64, 144, 64, L.ptr(dev(W)), L.BF16, 0, 1024, L.ptr(dev(b)),
+           L.ptr(out), 1024, stream())
     sync()
     assert_close(out, x @ W.float().t() + b, 0.9999999, 1e-5, "small_linear")
+    # fp32 weights (the patch embed's W_rt), both layouts: fp32 arithmetic, against an fp64 product
+    W32 = torch.randn(1024, 64, generator=g) * 0.05
+    ref = x.double() @ W32.double().t() + b.double()
+    for layout, wt in ((0, W32), (1, W32.t().contiguous())):
+        out.zero_()
+        L.call("oasis_small_linear", L.ptr(dev(x)), 64, 144, 64, L.ptr(dev(wt)), L.F32, layout, 1024, L.ptr(dev(b)),
+               L.ptr(out), 1024, stream())
+        sync()
+        assert ((out.double().cpu() - ref).abs().max() / ref.abs().max()).item() < 1e-6, layout
     for M in (147, 2050):  # ragged row blocks of the 4-row and 16-row variants
         xm = torch.randn(M, 40, generator=g)
         Wm = (torch.randn(1000, 32, generator=g) * 0.05).to(torch.bfloat16)
         om = torch.full((M, 1000), 7.0, device="cuda")
-        L.call("oasis_small_linear", L.ptr(dev(xm)), 40, M, 32, L.ptr(dev(Wm)), 1000, None, L.ptr(om), 1000,
-               stream())
+        L.call("oasis_small_linear", L.ptr(dev(xm)), 40, M, 32, L.ptr(dev(Wm)), L.BF16, 0, 1000, None, L.ptr(om),
+               1000, stream())
         sync()
         assert_close(om, xm[:, :32] @ Wm.float().t(), 0.9999999, 1e-5, "small_linear M=%d" % M)
 

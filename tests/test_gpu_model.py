@@ -3,6 +3,8 @@
 context-frame invariance property. References are the fp32 CPU oracle run on the same
 bf16-valued weights the GPU holds.
 """
+import ctypes
+
 import pytest
 import torch
 
@@ -104,9 +106,65 @@ def test_dit_step_config1(c1):
     assert cos >= COS_STEP, cos
 
 
+def _rel(got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    return ((got - ref).abs().max() / ref.abs().max()).item()
+
+
+def test_fp32_islands_match_the_fp32_oracle_on_unrounded_weights():
+    """The pieces the reference keeps in fp32 (oasis_inference.py:512-532,1406-1427,1497-1521,
+    1821-1826) run in fp32 here: a DiT built from fp32 weights that were never rounded to bf16
+    gives the conditioning rows, the final layer's adaLN rows, the final layer and the patch
+    embed within rel 1e-4 of the fp32 oracle on those same weights (bf16 storage of any of
+    them would leave ~4e-3)."""
+    dr = synth.Draw(31)
+    w = synth.dit_weights(dr, n_blocks=1, dtype=torch.float32)
+    for k in ("t_emb.b0", "t_emb.b2", "ext.b", "final.ada_b", "final.b", "x_emb.b"):
+        w[k] = dr.normal(*w[k].shape, std=0.1)
+    for k in ("t_emb.w0", "t_emb.w2", "ext.w", "final.ada_w", "final.w"):
+        w[k] = w[k] * 3   # larger projections: any bf16 rounding shows clearly above 1e-4
+    dit = pkg.DiT(w, "cuda")
+    R, D, P = 3, dit.d, dit.P
+    ws = dit.workspace(R * P, max_cond=16)
+    t = torch.tensor([14.0, 749.0, 249.0])
+    act = torch.zeros(R, 25)
+    act[0, 3] = act[1, 11] = act[2, 24] = 1.0
+    ada = dit.conditioning(cuda(t), cuda(act), ws)
+    torch.cuda.synchronize()
+    cond_ref = oracle.conditioning(t, act, w)
+    assert _rel(ws.cond[:R], cond_ref) < 1e-4, _rel(ws.cond[:R], cond_ref)
+    ns = dit.n_sub * 6 * D
+    fin_ref = oracle.silu(cond_ref) @ w["final.ada_w"].t() + w["final.ada_b"]
+    fin_ref[:, D:] += 1.0   # scale_p1
+    e = _rel(ada[:, ns:], fin_ref)
+    print("fp32 islands: cond %.2e, final adaLN %.2e" % (_rel(ws.cond[:R], cond_ref), e), flush=True)
+    assert e < 1e-4, e
+    # final layer on a given hidden state (3 frames of 144 tokens), against the oracle
+    x = dr.normal(R, P, D) * 2 + 0.3
+    ws.x[:R * P].copy_(cuda(x.reshape(R * P, D)))
+    v = torch.zeros(R * P, 64, device="cuda")
+    L = pkg._lib
+    L.call("oasis_dit_final", ctypes.byref(dit.struct), ctypes.byref(ws.struct), R * P, L.ptr(ada), dit.ada_width,
+           L.ptr(v), L.stream_handle())
+    torch.cuda.synchronize()
+    v_ref = oracle.final_layer(x, oracle.silu(cond_ref), w).reshape(R * P, 64)
+    e = _rel(v, v_ref)
+    print("fp32 islands: final layer %.2e" % e, flush=True)
+    assert e < 1e-4, e
+    # patch embed with the fp32 W_rt
+    lat = dr.normal(2, 16, 18, 32)
+    patches = oracle.patchify_to_output_space(lat).reshape(2 * P, 64)
+    z = torch.zeros(2 * P, D, device="cuda")
+    dit.patch_embed(cuda(patches), z)
+    torch.cuda.synchronize()
+    e = _rel(z, oracle.patch_embed(lat, w).reshape(2 * P, D))
+    assert e < 1e-5, e
+
+
 def test_dit_step_adaln_rows_of_every_consumer(c1):
     """The adaLN rows a step computes for every consumer, the final layer's included, equal
-    silu(cond) @ ada_w^T + ada_b of the packed weights (fp64 on the CPU)."""
+    silu(cond) @ W^T + b of the packed weights (fp64 on the CPU): the sub-blocks' bf16 stack
+    and the final layer's fp32 projection."""
     c, dit = c1
     step = pkg.DiTStep(dit, B=1, T=2)
     step.ws.ada.fill_(float("nan"))  # a slice that is never written stays NaN
@@ -115,7 +173,9 @@ def test_dit_step_adaln_rows_of_every_consumer(c1):
     step.run()
     torch.cuda.synchronize()
     cond = step.ws.cond[:2].double().cpu()
-    ref = torch.nn.functional.silu(cond) @ dit.ada_w.double().cpu().t() + dit.ada_b.double().cpu()
+    W = torch.cat([dit.ada_w.double().cpu(), dit.final_ada_w.double().cpu()])
+    B_ = torch.cat([dit.ada_b.double().cpu(), dit.final_ada_b.double().cpu()])
+    ref = torch.nn.functional.silu(cond) @ W.t() + B_
     got = step.ws.ada[:2].double().cpu()
     assert torch.isfinite(got).all(), "adaLN rows left unwritten"
     D = dit.d

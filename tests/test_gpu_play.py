@@ -51,7 +51,8 @@ def test_session_frames_match_the_oracle_chain(kv):
         frames.append(s.frame(a).clone())
         noises.append(s.last_noise.cpu())
     torch.cuda.synchronize()
-    assert s.status()["frame_index"] == 4 and s.status()["ddim_steps"] == 2 and s.fps > 0
+    # the reference's numbering: the 4th frame is frame 3 (play.py:517-525)
+    assert s.frame_index == 4 and s.status()["frame_index"] == 3 and s.status()["ddim_steps"] == 2 and s.fps > 0
     for x in noises:
         assert x.abs().max() <= 20.0
     steps = pkg.schedule.ddim_steps(2)

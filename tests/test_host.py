@@ -56,7 +56,8 @@ def _small_dit(seed=3):
 def test_dit_packing_adaln_rows():
     w = _small_dit()
     dit = M.DiT(w, "cpu")
-    assert dit.ada_width == 4 * 6 * 128 + 2 * 128 and dit.ada_w.shape == (dit.ada_width, 128)
+    assert dit.ada_width == 4 * 6 * 128 + 2 * 128 and dit.ada_w.shape == (4 * 6 * 128, 128)
+    assert dit.ada_w.dtype == torch.bfloat16 and dit.final_ada_w.dtype == torch.float32
     cond = torch.randn(3, 128, generator=torch.Generator().manual_seed(1))
     rows = oracle.silu(cond) @ dit.ada_w.float().t() + dit.ada_b
     for j in range(4):  # sub-block j: blocks.(j//2).(s|t), chunks shift, scale+1, gate, shift, scale+1, gate
@@ -66,8 +67,10 @@ def test_dit_packing_adaln_rows():
         for c in range(6):
             add = 1.0 if c in (1, 4) else 0.0
             assert torch.allclose(got[:, c * 128:(c + 1) * 128], ref[:, c * 128:(c + 1) * 128] + add, atol=1e-4)
+    # the final layer's adaLN stays fp32 and unrounded (oasis_inference.py:527-532)
+    assert torch.equal(dit.final_ada_w, w["final.ada_w"].float())
     ref = oracle.silu(cond) @ w["final.ada_w"].float().t() + w["final.ada_b"]
-    fin = rows[:, 4 * 768:]
+    fin = oracle.silu(cond) @ dit.final_ada_w.t() + dit.final_ada_b
     assert torch.allclose(fin[:, :128], ref[:, :128], atol=1e-4)
     assert torch.allclose(fin[:, 128:], ref[:, 128:] + 1.0, atol=1e-4)
 
@@ -78,11 +81,19 @@ def test_dit_packing_patch_embed_and_action_pad():
     lat = torch.randn(2, 16, 18, 32, generator=torch.Generator().manual_seed(2))
     patches = oracle.patchify_to_output_space(lat)                  # [2, 144, 64], (p, q, c) columns
     xw = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.xemb_w)]
-    got = patches @ xw.float().t() + w["x_emb.b"]
+    assert xw.dtype == torch.float32 and xw.shape == (128, 64)  # the reference's fp32 W_rt^T (1821-1826)
+    got = patches @ xw.t() + w["x_emb.b"]
     ref = oracle.patch_embed(lat, {k: v.float() for k, v in w.items()})
-    assert torch.allclose(got, ref, atol=2e-2 * ref.abs().max().item())
-    ext = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.ext_w)]
-    assert ext.shape == (128, 64) and torch.equal(ext[:, 25:], torch.zeros(128, 39, dtype=ext.dtype))
+    assert torch.allclose(got, ref, atol=1e-5 * ref.abs().max().item())
+    cw = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.cond_w)]
+    assert cw.shape == (128, 128 + 64)       # [W2 | Wext], the action zero-padded to 64 inputs
+    assert torch.equal(cw[:, :128], w["t_emb.w2"].float()) and torch.equal(cw[:, 128:153], w["ext.w"].float())
+    assert torch.equal(cw[:, 153:], torch.zeros(128, 39))
+    cb = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.cond_b)]
+    assert torch.equal(cb, w["t_emb.b2"].float() + w["ext.b"].float())
+    for name in ("temb_w0", "cond_w", "final_w"):   # conditioning and final layer: fp32
+        t = dit._keep[[t.data_ptr() for t in dit._keep].index(getattr(dit.struct, name))]
+        assert t.dtype == torch.float32, name
     assert dit.struct.n_sub == 4 and dit.struct.d_model == 128 and dit.struct.t_max == 32
 
 
