@@ -423,6 +423,16 @@ typedef struct {
 int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float* t, const float* action,
                            int64_t R, float* hid, float* cond, float* ada, oasis_stream_t stream);
 
+/* oasis_dit_conditioning with no scratch argument, for callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. The MLP's hidden rows use a static device array of the
+ * library (64 rows x 2048 columns of fp32, 512 KiB per GPU, held until the process ends), so
+ * R <= 64 and d_model <= 2048 (larger: OASIS_ERR_SHAPE). Nothing is allocated; the first call on
+ * a device looks up that device's copy of the array. Results equal oasis_dit_conditioning's
+ * bit for bit. Calls that overlap on one GPU (concurrent streams or threads) share the array
+ * and race; calls in sequence on one stream do not. */
+int oasis_dit_conditioning_noalloc(const oasis_dit_weights_t* w, const float* t, const float* action,
+                                   int64_t R, float* cond, float* ada, oasis_stream_t stream);
 
 /* Sub-blocks [j0, j1) of the DiT on x[B*T*P, D] in place (j even: spatial, odd: temporal),
  * ada as in oasis_dit_forward.  (run_sub_block, oasis_inference.py:995-1215.) */

@@ -129,6 +129,7 @@ SIGNATURES = {
     "oasis_bridge": [c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_vae_unpatchify": [c_p, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_dit_conditioning": [P(DiTWeights), c_p, c_p, c_i64, c_p, c_p, c_p, c_p],
+    "oasis_dit_conditioning_noalloc": [P(DiTWeights), c_p, c_p, c_i64, c_p, c_p, c_p],
     "oasis_dit_forward": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_p, c_p],
     "oasis_dit_sub_blocks": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],

@@ -238,6 +238,58 @@ extern "C" int oasis_dit_conditioning(const oasis_dit_weights_t* w, const float*
   return adaln_rows(w, cond, R, ada, (hipStream_t)stream);
 }
 
+// ---- oasis_dit_conditioning without a caller-supplied scratch buffer -------------------
+// The MLP's hidden rows live in `scratch`, a file-scope device array: each GPU the library
+// runs on holds its own copy (512 KiB) until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device address): the first
+// call on a device looks up that device's address with hipGetSymbolAddress and keeps it.
+namespace {
+
+constexpr int64_t kScratchRows = 64;    // conditioning rows per call
+constexpr int64_t kScratchCols = 2048;  // d_model
+static __device__ __align__(256) float scratch[kScratchRows * kScratchCols];
+
+int scratch_ptr(float** out) {
+  static std::mutex mu;
+  static float* table[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    oasis::set_error("dit_conditioning_noalloc: no current device");
+    return OASIS_ERR_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!table[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      oasis::set_error("dit_conditioning_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return OASIS_ERR_LAUNCH;
+    }
+    table[dev] = static_cast<float*>(p);
+  }
+  *out = table[dev];
+  return OASIS_OK;
+}
+
+}  // namespace
+
+extern "C" int oasis_dit_conditioning_noalloc(const oasis_dit_weights_t* w, const float* t, const float* action,
+                                              int64_t R, float* cond, float* ada, oasis_stream_t stream) {
+  OASIS_TRY(check_dit(w));
+  OASIS_REQUIRE(t && action && cond && ada, OASIS_ERR_NULL, "dit_conditioning_noalloc: null buffer");
+  OASIS_REQUIRE(R > 0 && R <= kScratchRows, OASIS_ERR_SHAPE,
+                "dit_conditioning_noalloc: R=%lld exceeds the %lld rows of its static scratch (use "
+                "oasis_dit_conditioning)", (long long)R, (long long)kScratchRows);
+  OASIS_REQUIRE(w->d_model <= kScratchCols, OASIS_ERR_SHAPE,
+                "dit_conditioning_noalloc: d_model=%d exceeds the static scratch's %lld columns", w->d_model,
+                (long long)kScratchCols);
+  float* hid = nullptr;
+  OASIS_TRY(scratch_ptr(&hid));
+  // every row of hid that the second GEMV reads is written by the first one: nothing to clear
+  OASIS_TRY(cond_mlp(w, t, action, R, hid, cond, stream));
+  return adaln_rows(w, cond, R, ada, (hipStream_t)stream);
+}
+
 namespace {
 
 // Split-K count for an O / FC2 GEMM (tile 0: 32 x 64): enough workgroups to cover the
