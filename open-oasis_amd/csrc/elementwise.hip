@@ -5,6 +5,8 @@
 //
 // All of these are HBM-bound; they use grid-stride loops with one element (or one
 // 16-byte vector of each operand) per thread step and coalesced accesses.
+#include <algorithm>
+
 #include "oasis_common.h"
 
 namespace {
@@ -220,41 +222,81 @@ __global__ void adaln_expand_kernel(const float* c, const bf16* w, const float* 
   for (int64_t r = 0; r < rows; ++r) out[r * N + n] = acc;
 }
 
-// Standalone RoPE + head split: one thread per 8 consecutive dims of one (row, q|k|v, head).
+// Standalone RoPE + head split: one workgroup per row, one thread per 8 consecutive dims of one
+// (q|k|v, head) of it, every operand moved as 16-byte vectors (the tables as two 4-float vectors).
 template <typename T>
-__global__ void rope_layout_kernel(const T* qkv, int64_t ldq, const float* cs, const float* sn, int64_t tab_ld,
-                                   int64_t tab_hs, int64_t pos_div, int64_t pos_mod, T* qo, T* ko, T* vo,
-                                   int64_t rows, int64_t seq, int H, int mode) {
+__device__ __forceinline__ void ld8(const T* p, float* v);
+template <>
+__device__ __forceinline__ void ld8<float>(const float* p, float* v) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = a[j];
+    v[4 + j] = b[j];
+  }
+}
+template <>
+__device__ __forceinline__ void ld8<bf16>(const bf16* p, float* v) {
+  unpack8(*reinterpret_cast<const bf16x8*>(p), v);
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void st8<float>(float* p, const float* v) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+template <>
+__device__ __forceinline__ void st8<bf16>(bf16* p, const float* v) {
+  *reinterpret_cast<bf16x8*>(p) = pack8(v);
+}
+
+// A workgroup takes up to RPG rows that share one table position (rows
+// (q * pos_mod + pos) * pos_div + rem): thread t owns column group c8 = 8t of Q, K and V, loads its
+// 8 cos / sin values once for all of them, and issues the loads of all its rows before any store.
+constexpr int RPG = 4;
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t ldq, const float* cs, const float* sn,
+                                                          int64_t tab_ld, int64_t tab_hs, int64_t pos_div,
+                                                          int64_t pos_mod, T* qo, T* ko, T* vo, int64_t rows,
+                                                          int64_t seq, int H) {
   const int D = H * 64;
-  const int64_t n = rows * 3 * (D / 8);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = i / (3 * (D / 8));
-    const int rem = (int)(i % (3 * (D / 8)));
-    const int which = rem / (D / 8), c8 = (rem % (D / 8)) * 8;
-    const int h = c8 >> 6, d0 = c8 & 63;
-    float v[8];
+  const int64_t pos = blockIdx.x;
+  int64_t row[RPG];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = ld<T>(qkv, row * ldq + which * D + c8 + j);
-    if (which < 2) {
-      const int64_t pos = (row / pos_div) % pos_mod;
-      const float* c = cs + pos * tab_ld + h * tab_hs + d0;
-      const float* s = sn + pos * tab_ld + h * tab_hs + d0;
-      float r[8];
+  for (int i = 0; i < RPG; ++i) {  // the j-th row of this position, j = blockIdx.y * RPG + i (rows: -1 past the end)
+    const int64_t j = (int64_t)blockIdx.y * RPG + i;
+    const int64_t q = j / pos_div, rem = j - q * pos_div;
+    const int64_t r = (q * pos_mod + pos) * pos_div + rem;
+    row[i] = r < rows ? r : -1;
+  }
+  if (row[0] < 0) return;  // no row of this workgroup exists (nor does its table row, necessarily)
+  for (int t = threadIdx.x; t < D / 8; t += blockDim.x) {
+    const int c8 = t * 8, h = c8 >> 6, d0 = c8 & 63;
+    float c[8], s[8], v[RPG][3][8];
+    ld8<float>(cs + pos * tab_ld + h * tab_hs + d0, c);
+    ld8<float>(sn + pos * tab_ld + h * tab_hs + d0, s);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * s[j];
+    for (int i = 0; i < RPG; ++i)
+      if (row[i] >= 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = r[j];
+        for (int w = 0; w < 3; ++w) ld8<T>(qkv + row[i] * ldq + w * D + c8, v[i][w]);
+      }
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      if (row[i] < 0) break;
+      const int64_t f = row[i] / seq, p = row[i] - f * seq;
+      float r[2][8];
+#pragma unroll
+      for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[w][e] = v[i][w][e] * c[e] + v[i][w][e ^ 1] * s[e];
+      const int64_t off = MODE == 0 ? ((f * H + h) * seq + p) * 64 + d0 : row[i] * D + c8;
+      st8<T>(qo + off, r[0]);
+      st8<T>(ko + off, r[1]);
+      st8<T>(vo + off, v[i][2]);
     }
-    T* dst = which == 0 ? qo : (which == 1 ? ko : vo);
-    int64_t off;
-    if (mode == 0) {
-      const int64_t f = row / seq, p = row % seq;
-      off = ((f * H + h) * seq + p) * 64 + d0;
-    } else {
-      off = row * D + c8;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) st<T>(dst, off + j, v[j]);
   }
 }
 
@@ -373,19 +415,29 @@ extern "C" int oasis_rope_layout(const void* qkv, int64_t ld_qkv, const float* c
                 OASIS_ERR_SHAPE, "rope_layout: bad shape");
   OASIS_REQUIRE(mode == 0 || mode == 1, OASIS_ERR_ARG, "rope_layout: mode must be 0 or 1");
   OASIS_REQUIRE(mode == 1 || rows % seq == 0, OASIS_ERR_SHAPE, "rope_layout: rows must be a multiple of seq");
-  const int64_t n = rows * 3 * n_heads * 8;
+  const size_t esz = dtype == OASIS_F32 ? 4 : 2;
+  OASIS_REQUIRE(oasis_aligned(16, qkv, q_out, k_out, v_out, cos, sinp) && (ld_qkv * esz) % 16 == 0 && tab_ld % 4 == 0 &&
+                    tab_head_stride % 4 == 0,
+                OASIS_ERR_ARG, "rope_layout: pointers, ld_qkv rows and table strides must be 16-byte aligned");
+  OASIS_REQUIRE(rows < (1ll << 31), OASIS_ERR_SHAPE, "rope_layout: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // rows per table position, then workgroups of up to RPG of them per position
+  const int64_t per_pos = ((rows + pos_mod * pos_div - 1) / (pos_mod * pos_div)) * pos_div;
+  const int64_t groups = (per_pos + RPG - 1) / RPG;
+  OASIS_REQUIRE(pos_mod < (1ll << 31) && groups <= 65535, OASIS_ERR_SHAPE, "rope_layout: too many rows per position");
+  const dim3 grid((unsigned)pos_mod, (unsigned)groups);
+  const int threads = (int)std::min<int64_t>(256, n_heads * 8);
+#define OASIS_ROPE(TT, MM)                                                                                        \
+  hipLaunchKernelGGL((rope_layout_kernel<TT, MM>), grid, dim3(threads), 0, s, (const TT*)qkv, ld_qkv, cos, sinp, tab_ld, \
+                     tab_head_stride, pos_div, pos_mod, (TT*)q_out, (TT*)k_out, (TT*)v_out, rows, seq, (int)n_heads)
   if (dtype == OASIS_F32) {
-    hipLaunchKernelGGL((rope_layout_kernel<float>), dim3(ew_grid(n)), dim3(256), 0, s, (const float*)qkv, ld_qkv,
-                       cos, sinp, tab_ld, tab_head_stride, pos_div, pos_mod, (float*)q_out, (float*)k_out,
-                       (float*)v_out, rows, seq, (int)n_heads, mode);
+    if (mode == 0) OASIS_ROPE(float, 0); else OASIS_ROPE(float, 1);
   } else if (dtype == OASIS_BF16) {
-    hipLaunchKernelGGL((rope_layout_kernel<bf16>), dim3(ew_grid(n)), dim3(256), 0, s, (const bf16*)qkv, ld_qkv, cos,
-                       sinp, tab_ld, tab_head_stride, pos_div, pos_mod, (bf16*)q_out, (bf16*)k_out, (bf16*)v_out,
-                       rows, seq, (int)n_heads, mode);
+    if (mode == 0) OASIS_ROPE(bf16, 0); else OASIS_ROPE(bf16, 1);
   } else {
     oasis::set_error("rope_layout: unsupported dtype %d", dtype);
     return OASIS_ERR_DTYPE;
   }
+#undef OASIS_ROPE
   return oasis::check_launch("rope_layout");
 }

@@ -85,6 +85,81 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
   }
 }
 
+// The same LayerNorm with 16-byte accesses for D % 512 == 0: lane l holds columns
+// v*512 + 8l .. v*512 + 8l + 7 of each 512-wide chunk v (one 16-byte bf16 vector, or two fp32).
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* v) {
+  load4<float>(p, v);
+  load4<float>(p + 4, v + 4);
+}
+template <>
+__device__ __forceinline__ void load8<bf16>(const bf16* p, float* v) {
+  unpack8(*reinterpret_cast<const bf16x8*>(p), v);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float* v) {
+  store4<float>(p, v);
+  store4<float>(p + 4, v + 4);
+}
+template <>
+__device__ __forceinline__ void store8<bf16>(bf16* p, const float* v) {
+  *reinterpret_cast<bf16x8*>(p) = pack8(v);
+}
+
+template <int NV, typename TIn, typename TOut, int MODE>
+__global__ __launch_bounds__(256) void ln8_kernel(const TIn* __restrict__ x, int64_t M, float eps,
+                                                  const float* __restrict__ p0, const float* __restrict__ p1,
+                                                  int64_t pstride, int64_t rows_per_frame, TOut* __restrict__ y) {
+  constexpr int D = NV * 512;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float* a;
+  const float* b;
+  if (MODE == 0) {
+    const int64_t f = row / rows_per_frame;
+    a = p1 + f * pstride;
+    b = p0 + f * pstride;
+  } else {
+    a = p0 + row * pstride;
+    b = p1 + row * pstride;
+  }
+  float v[NV][8], av[NV][8], bv[NV][8];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int k = c * 512 + lane * 8;
+    load8<TIn>(x + row * D + k, v[c]);
+    load8<float>(a + k, av[c]);
+    load8<float>(b + k, bv[c]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[c][j];
+  const float mean = wave_sum(s) * (1.0f / D);
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NV; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[c][j] -= mean;
+      q += v[c][j] * v[c][j];
+    }
+  const float rstd = rsqrtf(wave_sum(q) * (1.0f / D) + eps);
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = v[c][j] * rstd * av[c][j] + bv[c][j];
+    store8<TOut>(y + row * D + c * 512 + lane * 8, o);
+  }
+}
+
 // Residual update fused with the next LayerNorm, for few rows (under 2048): one 256-thread
 // workgroup per row (VPT = D/256 floats per thread, so a row's latency is spread over 4 waves),
 // every load issued up front so a row costs one memory round trip; mean and variance by two
@@ -475,10 +550,10 @@ hipError_t ln_dispatch(const TIn* x, int64_t M, int64_t D, float eps, const floa
   const dim3 grid((unsigned)((M + 3) / 4)), block(256);
   switch (D) {
     case 256: hipLaunchKernelGGL((ln_kernel<1, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
-    case 512: hipLaunchKernelGGL((ln_kernel<2, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
-    case 1024: hipLaunchKernelGGL((ln_kernel<4, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
-    case 2048: hipLaunchKernelGGL((ln_kernel<8, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
-    case 4096: hipLaunchKernelGGL((ln_kernel<16, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 512: hipLaunchKernelGGL((ln8_kernel<1, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 1024: hipLaunchKernelGGL((ln8_kernel<2, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 2048: hipLaunchKernelGGL((ln8_kernel<4, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
+    case 4096: hipLaunchKernelGGL((ln8_kernel<8, TIn, TOut, MODE>), grid, block, 0, s, x, M, eps, p0, p1, pstride, rpf, y); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

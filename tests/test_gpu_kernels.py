@@ -201,16 +201,20 @@ def test_ln_modulate():
     assert_close(out, ref, 0.99999, 1e-2, "ln_modulate")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_layernorm_surface(dtype):
-    rows, cols = 160, 1024
+@pytest.mark.parametrize("dtype,cols,expanded", [(torch.float32, 1024, False), (torch.bfloat16, 1024, False),
+                                                 (torch.bfloat16, 256, True), (torch.float32, 512, True),
+                                                 (torch.bfloat16, 2048, False), (torch.bfloat16, 4096, True)])
+def test_layernorm_surface(dtype, cols, expanded):
+    """Every column count the kernel takes (256: 4 floats per lane; 512 and up: 16-byte vectors),
+    with [cols] affine vectors or the reference's row-expanded [rows, cols] ones."""
+    rows = 160
     g = _gen(9)
     x = (torch.randn(rows, cols, generator=g) * 2).to(dtype)
-    w = torch.randn(cols, generator=g)
-    b = torch.randn(cols, generator=g)
+    w = torch.randn(rows if expanded else 1, cols, generator=g)
+    b = torch.randn(rows if expanded else 1, cols, generator=g)
     out = torch.zeros(rows, cols, device="cuda", dtype=dtype)
-    L.call("oasis_layernorm", L.ptr(dev(x)), L.ptr(dev(w)), L.ptr(dev(b)), 0, L.ptr(out), rows, cols, 1e-6,
-           L.F32 if dtype == torch.float32 else L.BF16, stream())
+    L.call("oasis_layernorm", L.ptr(dev(x)), L.ptr(dev(w)), L.ptr(dev(b)), cols if expanded else 0, L.ptr(out),
+           rows, cols, 1e-6, L.F32 if dtype == torch.float32 else L.BF16, stream())
     sync()
     ref = oracle.layer_norm(x.float(), w, b)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
@@ -484,12 +488,15 @@ def test_elementwise_surface(dtype, n, off):
     assert_close(out, af + (bf_ + cf) * df, 0.99999, tol, "bias_gated_residual")
 
 
-def test_rope_layout_surface():
-    """Reference-layout inputs: qkv_full [SEQ, 5D] with swap columns and [SEQ, D] tables."""
+@pytest.mark.parametrize("dt,mode", [(torch.float32, 0), (torch.bfloat16, 0), (torch.bfloat16, 1),
+                                     (torch.float32, 1)])
+def test_rope_layout_surface(dt, mode):
+    """Reference-layout inputs: qkv_full [SEQ, 5D] with swap columns and [SEQ, D] tables; heads-first
+    (mode 0) and token-major (mode 1) outputs, fp32 and bf16."""
     T, S, H = 2, 160, 4
     D = H * 64
     g = _gen(17)
-    qkv = torch.randn(T * S, 5 * D, generator=g)
+    qkv = torch.randn(T * S, 5 * D, generator=g).to(dt).float()
     ang = oracle.spatial_rope_angles(torch.rand(16, generator=g), 9, 16)
     cos, sinp = oracle.rope_cos_sinperm(ang, 64)
     ctab = torch.zeros(T * S, D)
@@ -497,17 +504,22 @@ def test_rope_layout_surface():
     for t in range(T):
         ctab[t * S:t * S + 144] = cos.repeat(1, H)
         stab[t * S:t * S + 144] = sinp.repeat(1, H)
-    qo, ko, vo = (torch.zeros(T * H * S, 64, device="cuda") for _ in range(3))
-    L.call("oasis_rope_layout", L.ptr(dev(qkv)), 5 * D, L.ptr(dev(ctab)), L.ptr(dev(stab)), D, 64, 1, T * S,
-           L.ptr(qo), L.ptr(ko), L.ptr(vo), T * S, S, H, 64, 0, L.F32, stream())
+    qo, ko, vo = (torch.zeros(T * H * S, 64, device="cuda", dtype=dt) for _ in range(3))
+    L.call("oasis_rope_layout", L.ptr(dev(qkv.to(dt))), 5 * D, L.ptr(dev(ctab)), L.ptr(dev(stab)), D, 64, 1, T * S,
+           L.ptr(qo), L.ptr(ko), L.ptr(vo), T * S, S, H, 64, mode, L.F32 if dt == torch.float32 else L.BF16,
+           stream())
     sync()
     x = qkv.reshape(T, S, 5, H, 64)
     c4 = ctab.reshape(T, S, H, 64)
     s4 = stab.reshape(T, S, H, 64)
+    tol = 1e-5 if dt == torch.float32 else 8e-3
+
+    def layout(t):   # [T, S, H, 64] -> the output layout of the mode
+        return t.permute(0, 2, 1, 3).reshape(-1, 64) if mode == 0 else t.reshape(-1, 64)
     for i, (name, got) in enumerate((("q", qo), ("k", ko))):
-        ref = oracle.apply_rope_swap(x[:, :, i], c4, s4).permute(0, 2, 1, 3).reshape(-1, 64)
-        assert_close(got, ref, 0.999999, 1e-5, "rope_layout " + name)
-    assert torch.equal(vo.cpu(), x[:, :, 2].permute(0, 2, 1, 3).reshape(-1, 64))
+        ref = layout(oracle.apply_rope_swap(x[:, :, i], c4, s4))
+        assert_close(got.float(), ref, 0.99999, tol, "rope_layout %s %s mode %d" % (name, dt, mode))
+    assert torch.equal(vo.float().cpu(), layout(x[:, :, 2]))
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
