@@ -198,7 +198,8 @@ def _graph_step_ms(step, steps, warmup):
 def config4(pkg, oracle, steps, warmup):
     """Config 4: 8 independent streams x T=4 frames (4608 tokens) per DiT step, QKV/O/FC1/FC2
     on e4m3 weights, against the same batch on bf16 weights. A generated frame needs 4 DDIM
-    steps, so DiT frames/s = 8 streams / (4 x step time) (VAE decode not included)."""
+    steps, so DiT frames/s = 8 streams / (4 x step time); with the decodes, frames/s =
+    8 / (4 x step time + the 8 streams' bridges and VAE decodes, batched as one 4608-token pass)."""
     import torch
     c = pkg.synth.config4()
     B, T = 8, 4
@@ -240,6 +241,32 @@ def config4(pkg, oracle, steps, warmup):
         del step, dit
         torch.cuda.empty_cache()
     res["speedup_fp8_vs_bf16"] = round(res["ms_per_step_bf16"] / res["ms_per_step_fp8"], 3)
+    # the 8 streams' decodes: bridge of each denoised latent, then one VAE decode of the 8 latents
+    # (4608 tokens) as a captured graph; beside it the same 8 decodes one after another
+    dr = pkg.synth.Draw(4)
+    vae = pkg.VAE(pkg.synth.vae_weights(dr), "cuda")
+    dit = pkg.DiT(pkg.synth.dit_weights(dr, n_blocks=1), "cuda")   # only its grid is read
+    chunks = dr.normal(B, dit.P, 64).cuda()
+    L = pkg._lib
+    stream = torch.cuda.Stream()
+    for nb in (B, 1):
+        vws = vae.workspace(max_frames=nb)
+        lat = torch.zeros(nb * vae.L, vae.latent_dim, device="cuda")
+        frames = torch.zeros(B, *vae.frame_shape, device="cuda")
+        fn = lambda: L.call("oasis_video_decode", ctypes.byref(dit.struct), ctypes.byref(vae.struct),  # noqa: E731
+                            ctypes.byref(vws.struct), B, L.ptr(chunks), L.ptr(lat), L.ptr(frames),
+                            L.stream_handle(stream))
+        dms = _event_ms(fn, stream, 10, pkg.Graph)
+        res["decode_%d_streams_ms_%s" % (B, "batched" if nb == B else "one_by_one")] = round(dms, 4)
+        del vws, lat, frames
+    dms = res["decode_%d_streams_ms_batched" % B]
+    for fmt in ("bf16", "fp8"):
+        res["frames_per_s_with_decode_" + fmt] = round(B * 1e3 / (4 * res["ms_per_step_" + fmt] + dms), 1)
+    res["decode_workload"] = ("8 bridges + one VAE decode of the 8 latents (12 ViT blocks over 8 x 576 = 4608 "
+                              "tokens, attention per latent) + unpatchify, one hipGraph; frames_per_s_with_decode = "
+                              "8 / (4 DDIM steps + that decode)")
+    del vae, dit
+    torch.cuda.empty_cache()
     return res
 
 
@@ -616,11 +643,11 @@ def main():
                                  "previous frame's denoised latent rolled on the device; the timed batches are "
                                  "repeated replays of one batch's graph (each replay starts from the same first "
                                  "context and denoises the chunk buffers in place; the work is data-independent); "
-                                 "video_fps: one hipGraph per batch (DDIM "
-                                 "steps then VAE decode per frame); video_fps_overlap_decode: the batch's DDIM "
-                                 "steps and its 16 decodes as two single-stream hipGraphs on two streams, batch k's "
-                                 "decodes (launched once its DDIM steps are done) overlapping batch k+1's DDIM "
-                                 "steps")
+                                 "video_fps: one hipGraph per batch (the 16 frames' DDIM "
+                                 "steps, then their 16 decodes as one batched VAE pass of 16 x 576 tokens); "
+                                 "video_fps_overlap_decode: the batch's DDIM steps and its batched decodes as two "
+                                 "single-stream hipGraphs on two streams, batch k's decodes (launched once its DDIM "
+                                 "steps are done) overlapping batch k+1's DDIM steps")
         out["play_workload"] = ("interactive loop (PlaySession): one config-3 frame per action, host-synchronised "
                                 "per frame; noise drawn on the device, conditioning rows written, frame graph "
                                 "replayed, context rolled on the device, frame [360,640,3] in [0,1] returned")

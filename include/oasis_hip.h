@@ -142,7 +142,8 @@ enum {
   OASIS_EPI_GATED_RES = 4,    /* out_f32[m, n] += gate[f(m), n] * (acc + bias)     */
   OASIS_EPI_RESIDUAL = 5,     /* out_f32[m, n] += acc + bias                       */
   OASIS_EPI_QKV_ROPE = 6,     /* RoPE on Q,K + head split into q/k/v (bf16)         */
-  OASIS_EPI_UNPATCHIFY = 7,   /* VAE predictor -> clamp(-1,1) CHW frame (fp32)      */
+  OASIS_EPI_UNPATCHIFY = 7,   /* VAE predictor -> clamp(-1,1) CHW frames (fp32): rows of
+                                 frame f (rows_per_frame each) to out_f32 + f*3*H*W     */
   OASIS_EPI_PARTIAL_F32 = 8,  /* split-K slice s: out_f32[s*split_stride + m*ld_out + n] = acc
                                  (no bias; summed by oasis_residual_ln)                */
   OASIS_EPI_GELU_TANH_FP8 = 9 /* g = gelu_tanh(acc + bias) as fp8 activation blocks:
@@ -525,15 +526,17 @@ typedef struct {
   const float* rope_sinp;
 } oasis_vae_weights_t;
 
+/* Activation workspace for up to max_rows tokens (max_rows / L latents of L = grid_h*grid_w). */
 typedef struct {
-  float* x;        /* [L, D] fp32   */
-  void* h;         /* [L, D] bf16   */
-  void* q;         /* [L, D] bf16   */
+  int64_t max_rows;
+  float* x;        /* [max_rows, D] fp32   */
+  void* h;         /* [max_rows, D] bf16   */
+  void* q;         /* [max_rows, D] bf16   */
   void* k;
   void* v;
-  void* attn;      /* [L, D] bf16   */
-  void* mlp;       /* [L, Dm] bf16  */
-  float* partial;  /* [max_splits, L, D] fp32 split-K slices */
+  void* attn;      /* [max_rows, D] bf16   */
+  void* mlp;       /* [max_rows, Dm] bf16  */
+  float* partial;  /* [max_splits, max_rows, D] fp32 split-K slices */
   int64_t max_splits;
 } oasis_vae_buffers_t;
 
@@ -541,6 +544,14 @@ typedef struct {
  * (vae_decode_forward, oasis_inference.py:1546-1618, + vae_unpatchify and clamp.) */
 int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf,
                      const float* latent, float* frame, oasis_stream_t stream);
+
+/* B latents fp32 [B, L, latent_dim] -> B frames fp32 [B, 3, H, W], as one pass of B*L tokens
+ * through every projection (attention stays within each latent); buf->max_rows >= B*L.
+ * Results equal B calls of oasis_vae_decode up to the projections' summation order. (The
+ * reference decodes one frame per vae_decode_forward call, oasis_inference.py:1546-1618; this
+ * batches the decodes of several frames or streams.) */
+int oasis_vae_decode_batch(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
+                           const float* latents, float* frames, oasis_stream_t stream);
 
 /* One generated frame at T=2: conditioning, n_steps DDIM v-prediction steps, then bridge +
  * VAE decode.
@@ -568,15 +579,17 @@ int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* bu
 
 /* n_frames consecutive generated frames of one stream with the context window rolled on
  * the device: frame f's context is frame f-1's denoised latent (frame 0: ctx_patches). Per
- * frame: context patch embed, n_steps DDIM steps (K/V cache as in oasis_ddim_frame), then
- * bridge + VAE decode: in order on `stream`, or with overlap_decode != 0 on a library-owned
- * side stream overlapping frame f+1's DiT steps (joined back into `stream` at the end).
+ * frame: context patch embed and n_steps DDIM steps (K/V cache as in oasis_ddim_frame). The
+ * bridges + VAE decodes run after the last frame on `stream`, batched as oasis_video_decode
+ * runs them; or, with overlap_decode != 0, one per frame on a library-owned side stream
+ * overlapping frame f+1's DiT steps (joined back into `stream` at the end).
  *   chunks: fp32 [n_frames, P, 64] noise in, denoised latents out;
  *   t, action: fp32 [n_frames * (1 + n_steps)] and [n_frames * (1 + n_steps), ext_dim_pad]:
  *        frame f's rows at f*(1 + n_steps), row 0 its context frame, row 1 + i step i;
  *   hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
  *   frames: fp32 [n_frames, 3, H, W], or NULL for the DiT half only (the chunks are the
  *        output; vbuf and latent may then be NULL; oasis_video_decode is the other half);
+ *   latent: scratch as in oasis_video_decode (one latent with overlap_decode);
  *   other arguments as in oasis_ddim_frame. n_frames <= 64.
  * The calls into one (w, buf) pair must not overlap. (The interactive loop's context roll,
  * oasis_inference.py:2296-2306, with play.py:241-531's per-frame DDIM + decode.) */
@@ -589,8 +602,10 @@ int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* 
                        oasis_stream_t stream);
 
 /* The decode half of oasis_video_frames: for f < n_frames, the bridge of chunks[f] (denoised
- * latents fp32 [P, 64], (p,q,c) columns) into latent (fp32 [4P, vae latent_dim] scratch), then
- * the VAE decode into frames[f] (fp32 [3, H, W], in [-1, 1]). Run on a second stream while the
+ * latents fp32 [P, 64], (p,q,c) columns) into latent, then the VAE decode into frames[f] (fp32
+ * [3, H, W], in [-1, 1]). The decodes run batched, as many latents per oasis_vae_decode_batch as
+ * vbuf holds (vbuf->max_rows / 4P); latent is fp32 [that many, 4P, vae latent_dim] scratch. Run on
+ * a second stream while the
  * next batch's oasis_video_frames(frames = NULL) runs on the first, the decodes overlap the
  * DiT steps. (bridge_unpatchify + vae_decode_forward + vae_unpatchify per frame,
  * oasis_inference.py:1651-1709,1546-1645; play.py:241-531's per-frame decode.) */

@@ -88,7 +88,7 @@ class VAEWeights(ctypes.Structure):
 
 
 class VAEBuffers(ctypes.Structure):
-    _fields_ = [("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p), ("attn", c_p),
+    _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p), ("attn", c_p),
                 ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64)]
 
 
@@ -134,6 +134,7 @@ SIGNATURES = {
     "oasis_dit_sub_blocks": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
+    "oasis_vae_decode_batch": [P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_p],
     "oasis_video_decode": [P(DiTWeights), P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_p, c_p],
     "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,

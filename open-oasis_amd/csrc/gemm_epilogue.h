@@ -233,18 +233,20 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       break;
     }
     case OASIS_EPI_UNPATCHIFY: {
-      // m = hh*gw + ww; n = (c*ps + pp)*ps + qq -> frame[c][hh*ps + pp][ww*ps + qq]
+      // m = f*gh*gw + hh*gw + ww; n = (c*ps + pp)*ps + qq -> frame f [c][hh*ps + pp][ww*ps + qq]
       const int ps = e.unpatch_patch, gw = e.unpatch_grid_w;
-      const int64_t hh = m / gw, ww = m - hh * gw;
+      const int64_t f = m / e.rows_per_frame, mm = m - f * e.rows_per_frame;
+      const int64_t hh = mm / gw, ww = mm - hh * gw;
       const int64_t W = (int64_t)gw * ps;
       const int64_t H = e.rows_per_frame / gw * ps;  // rows_per_frame = gh*gw
+      float* out = e.out_f32 + f * 3 * H * W;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int n = n0 + j;
         const int c = n / (ps * ps), rem = n - c * ps * ps;
         const int pp = rem / ps, qq = rem - pp * ps;
         const float val = fminf(fmaxf(v[j], -1.0f), 1.0f);
-        e.out_f32[(c * H + hh * ps + pp) * W + ww * ps + qq] = val;
+        out[(c * H + hh * ps + pp) * W + ww * ps + qq] = val;
       }
       break;
     }
@@ -376,8 +378,8 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
     case OASIS_EPI_UNPATCHIFY:
       OASIS_REQUIRE(e.out_f32 && e.unpatch_patch > 0 && e.unpatch_grid_w > 0, OASIS_ERR_ARG,
                     "gemm: UNPATCHIFY needs out_f32, patch and grid_w");
-      OASIS_REQUIRE(N == 3LL * e.unpatch_patch * e.unpatch_patch && e.rows_per_frame == M &&
-                        M % e.unpatch_grid_w == 0,
+      OASIS_REQUIRE(N == 3LL * e.unpatch_patch * e.unpatch_patch && e.rows_per_frame > 0 &&
+                        M % e.rows_per_frame == 0 && e.rows_per_frame % e.unpatch_grid_w == 0,
                     OASIS_ERR_SHAPE, "gemm: UNPATCHIFY shape mismatch");
       break;
     default:

@@ -150,6 +150,7 @@ namespace {
 
 constexpr float kLnEps = 1e-6f;
 constexpr float kAttnScale = 0.125f;  // 1/sqrt(64)
+constexpr float kInvScaling = 1.0f / 0.07843137255f;  // 1 / scaling_factor (oasis_inference.py:107)
 
 oasis_epilogue_t epi_zero() {
   oasis_epilogue_t e;
@@ -611,8 +612,12 @@ extern "C" int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oas
   return dit_final(w, buf, B * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, pend, v_out, stream);
 }
 
-extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, const float* latent,
-                                float* frame, oasis_stream_t stream) {
+namespace {
+
+// vae_decode_forward (oasis_inference.py:1546-1618) + vae_unpatchify for B latents at once: every
+// projection runs over B*L tokens, the attention per latent (B frames of L tokens).
+int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B, const float* latent,
+               float* frame, oasis_stream_t stream) {
   OASIS_REQUIRE(w && buf && latent && frame, OASIS_ERR_NULL, "vae_decode: null pointer");
   OASIS_REQUIRE(w->depth > 0 && w->depth <= OASIS_MAX_SUB && w->n_heads > 0 && w->d_model == w->n_heads * 64,
                 OASIS_ERR_SHAPE, "vae_decode: bad depth/heads/d_model");
@@ -623,7 +628,11 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
                     w->rope_sinp,
                 OASIS_ERR_NULL, "vae_decode: missing weight pointer");
   const int64_t D = w->d_model, H = w->n_heads, Dm = w->d_mlp;
-  const int64_t L = (int64_t)w->grid_h * w->grid_w;
+  const int64_t Lf = (int64_t)w->grid_h * w->grid_w;  // tokens per latent
+  OASIS_REQUIRE(B > 0 && B * Lf <= buf->max_rows, OASIS_ERR_SHAPE,
+                "vae_decode: %lld latents of %lld tokens exceed the workspace (%lld rows)", (long long)B,
+                (long long)Lf, (long long)buf->max_rows);
+  const int64_t L = B * Lf;  // rows of every projection
   hipStream_t s = (hipStream_t)stream;
   const Plan& pl = plan();
   const int sp = pl.splits[ROLE_VO] > 0 ? std::min<int>(pl.splits[ROLE_VO], buf->max_splits)
@@ -639,10 +648,11 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
   qkv.q = buf->q;
   qkv.k = buf->k;
   qkv.v = buf->v;
-  qkv.rows_per_frame = L;
+  qkv.rows_per_frame = Lf;  // latent b = row / Lf, heads-first per latent: [(b*H + h)][Lf][64]
   qkv.frames_per_stream = 1;
-  qkv.s_b = qkv.s_t = 0;
-  qkv.s_h = L * 64;
+  qkv.s_b = H * Lf * 64;
+  qkv.s_t = 0;
+  qkv.s_h = Lf * 64;
   qkv.s_p = 64;
   qkv.rope_cos = w->rope_cos;
   qkv.rope_sinp = w->rope_sinp;
@@ -663,7 +673,7 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
     qkv.bias = w->qkv_b[i];
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[i], D, L, 3 * D, D, qkv,
                                      pl.tile[ROLE_VQKV], 1, s));
-    OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, 1, L, H, kAttnScale, stream));
+    OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B, Lf, H, kAttnScale, stream));
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, part,
                                      pl.tile[ROLE_VO], sp, s));
     OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, sp, L * D, w->proj_b[i], nullptr, 0, L, w->n2_w[i],
@@ -682,13 +692,47 @@ extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_bu
   pred.kind = OASIS_EPI_UNPATCHIFY;
   pred.bias = w->pred_b;
   pred.out_f32 = frame;
-  pred.rows_per_frame = L;
+  pred.rows_per_frame = Lf;
   pred.unpatch_grid_w = w->grid_w;
   pred.unpatch_patch = w->patch;
   pred.unpatch_channels = 3;
   return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->pred_w, D, L, 3LL * w->patch * w->patch, D, pred,
                             s);
 }
+
+}  // namespace
+
+extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, const float* latent,
+                                float* frame, oasis_stream_t stream) {
+  return vae_decode(w, buf, 1, latent, frame, stream);
+}
+
+extern "C" int oasis_vae_decode_batch(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
+                                      const float* latents, float* frames, oasis_stream_t stream) {
+  return vae_decode(w, buf, B, latents, frames, stream);
+}
+
+namespace {
+
+// the bridge of chunks[0, n) into latents, then their decodes, as batches of as many latents as the
+// VAE workspace holds (latent: [that many, 4P, latent_dim] scratch)
+int decode_chunks(const oasis_dit_weights_t* w, const oasis_vae_weights_t* vw, const oasis_vae_buffers_t* vbuf,
+                  int64_t n, const float* chunks, float* latent, float* frames, oasis_stream_t stream) {
+  const int64_t P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4, fsz = (int64_t)w->patch_dim * P;
+  const int64_t Lf = (int64_t)vw->grid_h * vw->grid_w, lsz = Lf * vw->latent_dim;
+  const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
+  const int64_t per = std::max<int64_t>(1, vbuf->max_rows / Lf);
+  for (int64_t f0 = 0; f0 < n; f0 += per) {
+    const int64_t b = std::min(per, n - f0);
+    for (int64_t i = 0; i < b; ++i)
+      OASIS_TRY(oasis_bridge(chunks + (f0 + i) * fsz, latent + i * lsz, w->grid_h, w->grid_w, C, vw->latent_dim,
+                             kInvScaling, stream));
+    OASIS_TRY(vae_decode(vw, vbuf, b, latent, frames + f0 * frame_elems, stream));
+  }
+  return OASIS_OK;
+}
+
+}  // namespace
 
 namespace {
 
@@ -751,8 +795,6 @@ int frame_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, con
   return OASIS_OK;
 }
 
-constexpr float kInvScaling = 1.0f / 0.07843137255f;  // 1 / scaling_factor (oasis_inference.py:107)
-
 }  // namespace
 
 extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
@@ -807,20 +849,17 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
                                  stream));
     OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out, nullptr,
                           stream));
-    if (!decode) continue;
-    // bridge + VAE of frame f, in order or on the side stream overlapping frame f + 1's DiT
-    hipStream_t ds = s;
-    if (ss) {
-      hipEvent_t ev = ss->ev[f % (OASIS_MAX_SUB + 1)];
-      if (hipEventRecord(ev, s) != hipSuccess || hipStreamWaitEvent(ss->s, ev, 0) != hipSuccess)
-        return oasis::check_launch("video_frames fork");
-      ds = ss->s;
-    }
-    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, ds));
-    OASIS_TRY(oasis_vae_decode(vw, vbuf, latent, frames + f * frame_elems, ds));
+    if (!ss) continue;  // in order: the decodes run after the last frame, batched
+    // bridge + VAE of frame f on the side stream, overlapping frame f + 1's DiT
+    hipEvent_t ev = ss->ev[f % (OASIS_MAX_SUB + 1)];
+    if (hipEventRecord(ev, s) != hipSuccess || hipStreamWaitEvent(ss->s, ev, 0) != hipSuccess)
+      return oasis::check_launch("video_frames fork");
+    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, ss->s));
+    OASIS_TRY(vae_decode(vw, vbuf, 1, latent, frames + f * frame_elems, ss->s));
   }
   if (ss && (hipEventRecord(ss->fork, ss->s) != hipSuccess || hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess))
     return oasis::check_launch("video_frames join");
+  if (decode && !ss) OASIS_TRY(decode_chunks(w, vw, vbuf, n_frames, chunks, latent, frames, stream));
   return OASIS_OK;
 }
 
@@ -831,15 +870,10 @@ extern "C" int oasis_video_decode(const oasis_dit_weights_t* w, const oasis_vae_
   OASIS_REQUIRE(vw && vbuf && chunks && latent && frames, OASIS_ERR_NULL, "video_decode: null pointer");
   OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_decode: n_frames must be in [1, %d]",
                 OASIS_MAX_SUB);
-  const int64_t P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4, fsz = (int64_t)w->patch_dim * P;
+  const int64_t P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
   OASIS_REQUIRE((int64_t)vw->grid_h * vw->grid_w == 4 * P && vw->latent_dim >= C, OASIS_ERR_SHAPE,
                 "video_decode: VAE grid must be the 2x-upsampled DiT grid");
-  const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
-  for (int64_t f = 0; f < n_frames; ++f) {
-    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
-    OASIS_TRY(oasis_vae_decode(vw, vbuf, latent, frames + f * frame_elems, stream));
-  }
-  return OASIS_OK;
+  return decode_chunks(w, vw, vbuf, n_frames, chunks, latent, frames, stream);
 }
 
 extern "C" int oasis_graph_begin(oasis_stream_t stream) {

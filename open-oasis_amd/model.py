@@ -353,17 +353,27 @@ class VAE:
     def weight_bytes(self):
         return sum(t.numel() * t.element_size() for t in self._keep)
 
-    def workspace(self):
-        return VAEWorkspace(self)
+    def workspace(self, max_frames=1):
+        return VAEWorkspace(self, max_frames)
 
     def decode_inplace(self, latent, frame, ws, stream=None):
         L.call("oasis_vae_decode", ctypes.byref(self.struct), ctypes.byref(ws.struct),
                L.ptr(latent), L.ptr(frame), L.stream_handle(stream))
 
+    def decode_batch(self, latents, frames, ws, stream=None):
+        """B latents [B, L, latent_dim] -> frames [B, 3, H, W] in one pass of B*L tokens."""
+        B = latents.shape[0]
+        L.call("oasis_vae_decode_batch", ctypes.byref(self.struct), ctypes.byref(ws.struct), B,
+               L.ptr(latents), L.ptr(frames), L.stream_handle(stream))
+
 
 class VAEWorkspace:
-    def __init__(self, vae):
-        dev, d, n, bf = vae.device, vae.d, vae.L, torch.bfloat16
+    """Activation buffers for up to max_frames latents decoded together (max_frames * L rows)."""
+
+    def __init__(self, vae, max_frames=1):
+        dev, d, bf = vae.device, vae.d, torch.bfloat16
+        n = vae.L * max_frames
+        self.max_frames = max_frames
         self.x = torch.zeros(n, d, device=dev)
         self.h = torch.zeros(n, d, device=dev, dtype=bf)
         self.q = torch.zeros(n, d, device=dev, dtype=bf)
@@ -376,6 +386,7 @@ class VAEWorkspace:
         self.latent = torch.zeros(n, vae.latent_dim, device=dev)
         self.frame = torch.zeros(*vae.frame_shape, device=dev)
         S = L.VAEBuffers()
+        S.max_rows = n
         for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
             setattr(S, name, getattr(self, name).data_ptr())
         S.max_splits = self.max_splits
@@ -527,9 +538,10 @@ class VideoPipeline:
     context is frame f-1's denoised latent, rolled on the device (the interactive loop's
     context window, oasis_inference.py:2296-2306).
 
-    overlap_decode=False: one hipGraph per batch, each frame's DDIM steps then its VAE decode.
+    overlap_decode=False: one hipGraph per batch, the frames' DDIM steps, then their VAE decodes
+    as one batched decode of the n_frames latents.
     overlap_decode=True: the batch's DDIM steps (oasis_video_frames with frames = NULL) and its
-    decodes (oasis_video_decode) are two single-stream graphs on two streams, and batch k's
+    batched decodes (oasis_video_decode) are two single-stream graphs on two streams, and batch k's
     decodes run while batch k+1 denoises. launch() enqueues batch k, then waits on the host
     for batch k-1's DDIM steps (batch k is already queued behind them) and launches its
     decodes: a device-side wait of one stream on the other's event serialises the two graphs
@@ -556,7 +568,8 @@ class VideoPipeline:
         P, dev = dit.P, dit.device
         R = n_frames * (1 + self.n)
         self.ws = dit.workspace(2 * P, max_cond=max(16, R))
-        self.vws = vae.workspace()
+        # the decodes of a batch run batched: the VAE workspace holds all n_frames latents
+        self.vws = vae.workspace(max_frames=n_frames)
         self.kv = KVCache(dit, 1) if kv_cache else None
         nb = 2 if overlap_decode else 1
         self.chunk_bufs = [torch.zeros(n_frames, P, dit.patch_dim, device=dev) for _ in range(nb)]

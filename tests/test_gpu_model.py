@@ -239,6 +239,31 @@ def test_vae_decode_config3(c3):
     assert cos >= COS_STEP and rel <= 5e-2, (cos, rel)
 
 
+@pytest.mark.parametrize("B", [3, 8])
+def test_vae_decode_batch_matches_single_decodes(c3, B):
+    """B latents decoded as one pass of B*576 tokens (B = 3: the small-token tiles; B = 8: 4608
+    tokens on the large-token tiles, config 4's 8 streams) give each latent's frame as its own
+    decode does, and the first one matches the oracle."""
+    c, _, vae = c3
+    dr = synth.Draw(90 + B)
+    lats = dr.normal(B, 576, 32)
+    ws = vae.workspace(max_frames=B)
+    frames = torch.zeros(B, *vae.frame_shape, device="cuda")
+    vae.decode_batch(cuda(lats), frames, ws)
+    one = vae.workspace()
+    single = torch.zeros(B, *vae.frame_shape, device="cuda")
+    for b in range(B):
+        vae.decode_inplace(cuda(lats[b]), single[b], one)
+    torch.cuda.synchronize()
+    for b in range(B):
+        # two bf16 paths (4608 tokens run the large-token tiles, another summation order)
+        assert_close(frames[b], single[b], 0.9999, 5e-2, "batched VAE decode B=%d, latent %d vs alone" % (B, b))
+    ref = oracle.vae_unpatchify(oracle.vae_decode(lats[0], c["vw"]))
+    assert_close(frames[0], ref, COS_STEP, 5e-2, "batched VAE decode B=%d, latent 0 vs oracle" % B)
+    with pytest.raises(pkg._lib.OasisError, match="exceed the workspace"):
+        vae.decode_batch(cuda(lats), frames, one)
+
+
 def test_ddim_frame_config3(c3):
     c, dit, vae = c3
     ac = pkg.schedule.cosine_alphas_cumprod()
