@@ -3,13 +3,18 @@
 //   acc[M,N] = A[M,K] @ B[N,K]^T, A = activations (bf16, row-major), B = weights in
 //   the nn.Linear layout [out, in] (bf16), fp32 accumulation, then one epilogue
 //   (bias, tanh/erf GELU, gated residual into the fp32 stream, RoPE + head split,
-//   VAE unpatchify) applied on the way out.
+//   VAE unpatchify, split-K slices) applied on the way out.
 //
-// Tiling: a 256-thread workgroup (4 waves of 64) owns a BM x BN output tile and walks
-// K in BK=64 steps. A and B tiles go global -> registers -> LDS with a double-buffered
-// LDS ring (the next tile's global loads are in flight while the current tile feeds
-// v_mfma_f32_16x16x32_bf16). Each wave owns a (BM/WM) x (BN/WN) sub-tile. After the
-// K loop the fp32 tile is staged through LDS so each thread handles 8 consecutive
+// Kernels (v_mfma_f32_16x16x32_bf16 throughout; K in 64-wide tiles):
+//   - gemm_lds_kernel: 4 waves, the K tiles copied global -> LDS by the memory pipeline itself
+//     (global_load_lds_dwordx4) into a ring of STAGES tiles; small tiles for the split-K slices
+//     and the QKV + RoPE product at 144 / 288 tokens.
+//   - gemm_big_kernel: the same ring with a grouped tile order and a per-wave staged epilogue, on
+//     4-, 6- and 8-wave tiles: the MLP products, every VAE projection, and the 8-wave 288-row
+//     tiles from 2048 tokens up.
+//   - gemm_bf16_kernel: global -> registers -> LDS, for the reference-surface oasis_linear with
+//     its [K, N] weight layout (the weights transposed into LDS).
+// After the K loop the fp32 tile is staged through LDS so each thread handles 8 consecutive
 // columns of one row: coalesced 16/32-byte stores and in-register RoPE pair swaps.
 //
 // Workgroup -> tile order is XCD-aware: MI355X dispatches workgroup i to XCD i % 8,
@@ -511,75 +516,28 @@ hipError_t launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, in
   return hipGetLastError();
 }
 
-// Tile configurations (id -> BM x BN, wave grid, prefetch depth).
+// Tile configurations (id -> BM x BN, wave grid, prefetch depth): the ones the default choice
+// below uses, for the shapes of the DiT step, the frame, the VAE and the large-token batches.
 typedef hipError_t (*launch_fn)(const bf16*, int64_t, const bf16*, int64_t, int, int, int, int, const Epi&,
                                 hipStream_t);
 struct TileCfg {
-  int bm, bn, stages, bk;
-  launch_fn fn;         // STAGES-deep prefetch ring (K tiles per split divisible by stages)
-  launch_fn fn_single;  // one tile in flight, any K
+  int bm, bn;
+  launch_fn fn;
   int no_fp8_epi = 0;   // 1: its epilogue lanes do not cover aligned 32-column blocks
 };
 const TileCfg kTiles[] = {
-    {32, 64, 4, 64, launch_cfg<32, 64, 1, 4, 4>, launch_cfg<32, 64, 1, 4, 1>},      // 0
-    {64, 64, 4, 64, launch_cfg<64, 64, 2, 2, 4>, launch_cfg<64, 64, 2, 2, 1>},      // 1
-    {32, 128, 4, 64, launch_cfg<32, 128, 1, 4, 4>, launch_cfg<32, 128, 1, 4, 1>},   // 2
-    {64, 128, 2, 64, launch_cfg<64, 128, 2, 2, 2>, launch_cfg<64, 128, 2, 2, 1>},   // 3
-    {96, 64, 2, 64, launch_cfg<96, 64, 2, 2, 2>, launch_cfg<96, 64, 2, 2, 1>},      // 4
-    {32, 32, 8, 64, launch_cfg<32, 32, 2, 2, 8>, launch_cfg<32, 32, 2, 2, 1>},      // 5
-    {128, 64, 2, 64, launch_cfg<128, 64, 2, 2, 2>, launch_cfg<128, 64, 2, 2, 1>},   // 6
-    {32, 64, 2, 64, launch_cfg<32, 64, 1, 4, 2>, launch_cfg<32, 64, 1, 4, 1>},      // 7
-    {32, 64, 8, 64, launch_cfg<32, 64, 1, 4, 8>, launch_cfg<32, 64, 1, 4, 1>},      // 8
-    {64, 32, 4, 64, launch_cfg<64, 32, 2, 2, 4>, launch_cfg<64, 32, 2, 2, 1>},      // 9
-    {96, 64, 4, 64, launch_cfg<96, 64, 2, 2, 4>, launch_cfg<96, 64, 2, 2, 1>},      // 10
-    {96, 32, 8, 64, launch_cfg<96, 32, 2, 2, 8>, launch_cfg<96, 32, 2, 2, 1>},      // 11
-    {128, 64, 4, 64, launch_cfg<128, 64, 2, 2, 4>, launch_cfg<128, 64, 2, 2, 1>},   // 12
-    {96, 128, 2, 64, launch_cfg<96, 128, 2, 2, 2>, launch_cfg<96, 128, 2, 2, 1>},   // 13
-    {64, 64, 8, 64, launch_cfg<64, 64, 2, 2, 8>, launch_cfg<64, 64, 2, 2, 1>},      // 14
-    {96, 64, 8, 64, launch_cfg<96, 64, 2, 2, 8>, launch_cfg<96, 64, 2, 2, 1>},      // 15
-    {128, 32, 8, 64, launch_cfg<128, 32, 2, 2, 8>, launch_cfg<128, 32, 2, 2, 1>},   // 16
-    {64, 128, 4, 64, launch_cfg<64, 128, 2, 2, 4>, launch_cfg<64, 128, 2, 2, 1>},   // 17
-    // 128-wide K steps: half the pipeline iterations (and barriers) per tile
-    {32, 64, 2, 128, launch_cfg<32, 64, 1, 4, 2, false, 128>, launch_cfg<32, 64, 1, 4, 1>},     // 18
-    {96, 64, 2, 128, launch_cfg<96, 64, 2, 2, 2, false, 128>, launch_cfg<96, 64, 2, 2, 1>},     // 19
-    {64, 64, 2, 128, launch_cfg<64, 64, 2, 2, 2, false, 128>, launch_cfg<64, 64, 2, 2, 1>},     // 20
-    {32, 128, 2, 128, launch_cfg<32, 128, 1, 4, 2, false, 128>, launch_cfg<32, 128, 1, 4, 1>},  // 21
-    {32, 64, 4, 128, launch_cfg<32, 64, 1, 4, 4, false, 128>, launch_cfg<32, 64, 1, 4, 1>},     // 22
-    // direct-to-LDS K pipeline (any number of K tiles)
-    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 4>, launch_lds<32, 64, 1, 4, 4>},      // 23
-    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 4>, launch_lds<96, 64, 2, 2, 4>},      // 24
-    {64, 64, 1, 64, launch_lds<64, 64, 2, 2, 4>, launch_lds<64, 64, 2, 2, 4>},      // 25
-    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 6>, launch_lds<96, 64, 2, 2, 6>},      // 26
-    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 8>, launch_lds<32, 64, 1, 4, 8>},      // 27
-    {32, 128, 1, 64, launch_lds<32, 128, 1, 4, 4>, launch_lds<32, 128, 1, 4, 4>},   // 28
-    {64, 128, 1, 64, launch_lds<64, 128, 2, 2, 4>, launch_lds<64, 128, 2, 2, 4>},   // 29
-    {96, 128, 1, 64, launch_lds<96, 128, 2, 2, 3>, launch_lds<96, 128, 2, 2, 3>},   // 30
-    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 6>, launch_lds<32, 64, 1, 4, 6>},      // 31
-    {32, 64, 1, 64, launch_lds<32, 64, 1, 4, 3>, launch_lds<32, 64, 1, 4, 3>},      // 32
-    {96, 64, 1, 64, launch_lds<96, 64, 2, 2, 3>, launch_lds<96, 64, 2, 2, 3>},      // 33
-    {64, 64, 1, 64, launch_lds<64, 64, 2, 2, 6>, launch_lds<64, 64, 2, 2, 6>},      // 34
-    {96, 32, 1, 64, launch_lds<96, 32, 2, 2, 4>, launch_lds<96, 32, 2, 2, 4>},      // 35
-    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 3>, launch_lds<128, 128, 2, 2, 3>},  // 36
-    {128, 64, 1, 64, launch_lds<128, 64, 2, 2, 4>, launch_lds<128, 64, 2, 2, 4>},    // 37
-    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 4>, launch_lds<128, 128, 2, 2, 4>},  // 38
-    {48, 64, 1, 64, launch_lds<48, 64, 1, 4, 4>, launch_lds<48, 64, 1, 4, 4>},      // 39
-    {144, 64, 1, 64, launch_lds<144, 64, 1, 4, 3>, launch_lds<144, 64, 1, 4, 3>},   // 40
-    {48, 128, 1, 64, launch_lds<48, 128, 1, 4, 4>, launch_lds<48, 128, 1, 4, 4>},   // 41
-    {16, 64, 1, 64, launch_lds<16, 64, 1, 4, 4>, launch_lds<16, 64, 1, 4, 4>},      // 42
-    {128, 128, 1, 64, launch_lds<128, 128, 2, 2, 2>, launch_lds<128, 128, 2, 2, 2>},  // 43
-    {128, 128, 2, 64, launch_cfg<128, 128, 2, 2, 2>, launch_cfg<128, 128, 2, 2, 1>},  // 44
-    {256, 128, 2, 64, launch_cfg<256, 128, 2, 2, 2>, launch_cfg<256, 128, 2, 2, 1>},  // 45
-    // 8-wave large-token tiles (any number of K tiles)
-    {288, 256, 1, 64, launch_big<288, 256, 2, 4, 2>, launch_big<288, 256, 2, 4, 2>},  // 46
-    {288, 192, 1, 64, launch_big<288, 192, 2, 4, 2>, launch_big<288, 192, 2, 4, 2>, 1},  // 47
-    {288, 128, 1, 64, launch_big<288, 128, 2, 4, 2>, launch_big<288, 128, 2, 4, 2>},  // 48
-    {144, 256, 1, 64, launch_big<144, 256, 1, 8, 2>, launch_big<144, 256, 1, 8, 2>},  // 49
-    {256, 256, 1, 64, launch_big<256, 256, 2, 4, 2>, launch_big<256, 256, 2, 4, 2>},  // 50
-    // the 8-wave kernel's grouped tile order and per-wave staged epilogue on a 4-wave 96 x 64
-    // tile: faster than tile 24 for FC1 / FC2 below 2048 tokens and for every VAE projection
-    {96, 64, 1, 64, launch_big<96, 64, 2, 2, 4>, launch_big<96, 64, 2, 2, 4>},  // 51
-    {64, 64, 1, 64, launch_big<64, 64, 2, 2, 4>, launch_big<64, 64, 2, 2, 4>},    // 52
-    {144, 64, 1, 64, launch_big<144, 64, 3, 2, 4>, launch_big<144, 64, 3, 2, 4>},  // 53: 6 waves
+    // direct-to-LDS, 4 waves: split-K slices of the O projection, QKV + RoPE at 144 / 288 tokens
+    {32, 64, launch_lds<32, 64, 1, 4, 4>},                  // 0: 4 K tiles in flight
+    {32, 64, launch_lds<32, 64, 1, 4, 3>},                  // 1: 3 K tiles in flight
+    // the 8-wave kernel's grouped tile order and per-wave staged epilogue on 4- and 6-wave tiles:
+    // FC1 / FC2 below 2048 tokens and every VAE projection
+    {96, 64, launch_big<96, 64, 2, 2, 4>},                  // 2
+    {64, 64, launch_big<64, 64, 2, 2, 4>},                  // 3
+    {144, 64, launch_big<144, 64, 3, 2, 4>},                // 4: 6 waves
+    // 8-wave large-token tiles (2048+ tokens)
+    {288, 256, launch_big<288, 256, 2, 4, 2>},              // 5
+    {288, 192, launch_big<288, 192, 2, 4, 2>, 1},           // 6
+    {288, 128, launch_big<288, 128, 2, 4, 2>},              // 7
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -587,31 +545,22 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 namespace oasis {
 
-// Tile choice per shape. M is small (288 / 576 tokens) and the weights are streamed
-// once, so the tiles trade L2 re-reads of A and B against enough workgroups to keep
-// all 256 CUs issuing HBM loads.
-// Default tile per shape, from in-situ sweeps of the captured DiT step and frame on MI355X:
-// the direct-to-LDS pipeline with 96 x 64 tiles (4 stages) for the MLP products, the split-K
-// slices and everything at the VAE's 576 tokens, 32 x 64 tiles (3 stages) for the QKV
-// product of the DiT (144 or 288 tokens); 96 x 128 register-ring tiles from 2048 tokens up.
-// From 2048 tokens up, the 8-wave 288-row tiles: 288 x 256 for N = 4096 (16 x 16 tiles at 4608
-// tokens), 288 x 192 for N = 3072 (16 x 16) and 288 x 128 otherwise (with 2 K slices at N = 1024).
 // Default tile per shape, from timings of each projection on MI355X with cold weights:
-//   - 2048+ tokens: the 8-wave tall tiles;
-//   - FC1 (GELU): 64 x 64 (tile 52) at one 144-token frame, 144 x 64 on 6 waves (tile 53)
-//     from 512 tokens (the VAE's 576), else 96 x 64 (tile 51);
-//   - split-K partials: 32 x 64 tiles for short K slices (O: 256 at 144 tokens, 512 at 288),
-//     tile 51 for the longer slices (FC2) and from 320 tokens up;
-//   - other epilogues (QKV + RoPE, plain stores): 32 x 64, tile 52 from 512 tokens.
+//   - 2048+ tokens: the 8-wave tall tiles, the width that fills the last round of 256 workgroups best;
+//   - FC1 (GELU): 64 x 64 (tile 3) at one 144-token frame, 144 x 64 on 6 waves (tile 4) from 512
+//     tokens (the VAE's 576), else 96 x 64 (tile 2);
+//   - split-K partials: 32 x 64 tiles (tile 0) for short K slices (O: 256 at 144 tokens, 512 at 288),
+//     tile 2 for the longer slices (FC2) and from 320 tokens up;
+//   - other epilogues (QKV + RoPE, plain stores): 32 x 64 (tile 1), tile 3 from 512 tokens.
 int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
-  if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 46, 47, 48);
+  if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 5, 6, 7);
   const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
-  if (gelu) return M <= 160 ? 52 : (M >= 512 ? 53 : 51);
+  if (gelu) return M <= 160 ? 3 : (M >= 512 ? 4 : 2);
   if (kind == OASIS_EPI_PARTIAL_F32) {
-    if (M <= 160) return Kslice <= 256 ? 23 : 51;
-    return M <= 320 && Kslice <= 512 ? 23 : 51;
+    if (M <= 160) return Kslice <= 256 ? 0 : 2;
+    return M <= 320 && Kslice <= 512 ? 0 : 2;
   }
-  return M >= 512 ? 52 : 32;
+  return M >= 512 ? 3 : 1;
 }
 
 // Split-K count for the default tile of a large-token split-K product: K slices until the
@@ -644,11 +593,7 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
   const TileCfg& t = kTiles[tile];
   OASIS_REQUIRE(!(t.no_fp8_epi && e.kind == OASIS_EPI_GELU_TANH_FP8), OASIS_ERR_ARG,
                 "gemm: tile config %d cannot run the GELU_TANH_FP8 epilogue", tile);
-  // the prefetch ring needs (K steps per split) % stages == 0; 128-wide configs also need
-  // K % 128 per split, else their one-stage 64-wide twin runs
-  const int64_t ks = K / splits / t.bk;
-  const bool ring = (K / splits) % t.bk == 0 && ks % t.stages == 0;
-  const hipError_t err = (ring ? t.fn : t.fn_single)(A, lda, B, ldb, (int)M, (int)N, (int)K, splits, e, s);
+  const hipError_t err = t.fn(A, lda, B, ldb, (int)M, (int)N, (int)K, splits, e, s);
   if (err != hipSuccess) {
     set_error("gemm launch failed: %s", hipGetErrorString(err));
     return OASIS_ERR_LAUNCH;

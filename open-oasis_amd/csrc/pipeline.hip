@@ -75,7 +75,7 @@ int side_stream(SideStream** out) {
 
 // GEMM plan per projection role: tile configuration (-1 = gemm.hip's default for the
 // shape) and split-K count (0 = chosen from the shape). Tuning override, read once:
-//   OASIS_GEMM_PLAN="qkv:7,o:7:4,fc1:0,fc2:0:4,vqkv:7,vo:7:2,vfc1:0,vfc2:0:2"
+//   OASIS_GEMM_PLAN="qkv:1,o:0:4,fc1:2,fc2:2:4,vqkv:3,vo:2:2,vfc1:4,vfc2:2:2" (tile ids of gemm.hip)
 //   OASIS_ADALN_OVERLAP=1 streams the adaLN projections on a side stream, overlapped with
 //   the sub-blocks (off by default: the cross-stream graph edges cost more than they
 //   hide on MI355X, 2.09 vs 1.90 ms per config-1 step).

@@ -523,7 +523,7 @@ def test_rope_layout_surface(dt, mode):
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(54)))
+@pytest.mark.parametrize("tile", list(range(8)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -536,9 +536,9 @@ def test_gemm_tile_configs(tile):
     assert_close(out, A.float() @ B.float().t(), 0.999999, 1e-4, "tile %d" % tile)
 
 
-@pytest.mark.parametrize("tile", list(range(23, 43)) + [51, 52, 53])
+@pytest.mark.parametrize("tile", list(range(5)))
 def test_gemm_direct_lds_ragged(tile):
-    """The direct-to-LDS configurations (23-42, and 51-53 on the 8-wave kernel's code) on a ragged
+    """The direct-to-LDS configurations (0, 1, and 2-4 on the 8-wave kernel's code) on a ragged
     shape: K = 5 tiles (not a multiple of the stage count), M and N not multiples of the tile,
     GELU epilogue and split-K slices."""
     M, N, K = 300, 520, 320
@@ -558,7 +558,7 @@ def test_gemm_direct_lds_ragged(tile):
     assert_close(part.sum(0), ref, 0.999999, 1e-4, "tile %d split-K x5" % tile)
 
 
-@pytest.mark.parametrize("tile", list(range(46, 51)))
+@pytest.mark.parametrize("tile", list(range(5, 8)))
 def test_gemm_large_token_tiles_ragged(tile):
     """The 8-wave large-token tiles on a ragged shape: M and N not multiples of the tile (the
     last tile row and column are partial), K = 5 tiles, GELU epilogue with bias, split-K x5,

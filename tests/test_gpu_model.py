@@ -69,7 +69,7 @@ def test_temporal_sub_block_config2():
 @pytest.mark.parametrize("kind,T", [("s", 1), ("t", 1), ("s", 4), ("t", 4), ("t", 13)])
 def test_sub_blocks_between_sizes(kind, T):
     """Sub-blocks at the token counts between configs: one 144-token frame (the K/V-cache
-    steps' tile and split choices), 576 tokens (tile 51 with the QKV + RoPE epilogue in both
+    steps' tile and split choices), 576 tokens (tile 2 with the QKV + RoPE epilogue in both
     layouts) and 1872 tokens (the largest count below the 8-wave tall tiles)."""
     c0, c2 = synth.config0(), synth.config2()
     dr = synth.Draw(70 + T)
