@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define OASIS_ABI_VERSION 2
+#define OASIS_ABI_VERSION 3
 #define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
 
 enum {
@@ -563,8 +563,7 @@ int oasis_vae_decode_batch(const oasis_vae_weights_t* w, const oasis_vae_buffers
  *   hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (1 + n_steps rows);
  *   ctx_z: fp32 [P, D] scratch; v_out: fp32 [2P, 64] scratch; latent: fp32 [4P, vae
  *   latent_dim] scratch; frame: fp32 [3, H, W] output. n_steps <= 15.
- * The adaLN projections of all conditioning rows run as one pass before the first step
- * (OASIS_ADALN_OVERLAP=1: on a library-owned side stream, overlapped with the first step).
+ * The adaLN projections of all conditioning rows run as one pass before the first step.
  * kv: NULL runs every step as the T=2 forward. Otherwise (a cache for >= 1 stream) step 0
  * runs at T=2 and stores the context frame's temporal K/V, and steps 1.. run only the
  * current frame at T=1 against that cache (the K/V-cache path of oasis_inference.py:
@@ -581,15 +580,15 @@ int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* bu
  * the device: frame f's context is frame f-1's denoised latent (frame 0: ctx_patches). Per
  * frame: context patch embed and n_steps DDIM steps (K/V cache as in oasis_ddim_frame). The
  * bridges + VAE decodes run after the last frame on `stream`, batched as oasis_video_decode
- * runs them; or, with overlap_decode != 0, one per frame on a library-owned side stream
- * overlapping frame f+1's DiT steps (joined back into `stream` at the end).
+ * runs them. (To overlap the decodes with the next frames' DiT steps, run this with
+ * frames = NULL on one stream and oasis_video_decode on another.)
  *   chunks: fp32 [n_frames, P, 64] noise in, denoised latents out;
  *   t, action: fp32 [n_frames * (1 + n_steps)] and [n_frames * (1 + n_steps), ext_dim_pad]:
  *        frame f's rows at f*(1 + n_steps), row 0 its context frame, row 1 + i step i;
  *   hid/cond/ada: conditioning scratch for n_frames * (1 + n_steps) rows;
  *   frames: fp32 [n_frames, 3, H, W], or NULL for the DiT half only (the chunks are the
  *        output; vbuf and latent may then be NULL; oasis_video_decode is the other half);
- *   latent: scratch as in oasis_video_decode (one latent with overlap_decode);
+ *   latent: scratch as in oasis_video_decode;
  *   other arguments as in oasis_ddim_frame. n_frames <= 64.
  * The calls into one (w, buf) pair must not overlap. (The interactive loop's context roll,
  * oasis_inference.py:2296-2306, with play.py:241-531's per-frame DDIM + decode.) */
@@ -598,8 +597,7 @@ int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* 
                        const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
                        const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
                        const float* coeffs, float* hid, float* cond, float* ada, float* ctx_z,
-                       float* v_out, float* latent, float* frames, int overlap_decode,
-                       oasis_stream_t stream);
+                       float* v_out, float* latent, float* frames, oasis_stream_t stream);
 
 /* The decode half of oasis_video_frames: for f < n_frames, the bridge of chunks[f] (denoised
  * latents fp32 [P, 64], (p,q,c) columns) into latent, then the VAE decode into frames[f] (fp32

@@ -17,7 +17,7 @@ EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32, EPI_GELU_TANH_FP8 = 8, 9
 ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
@@ -140,7 +140,7 @@ SIGNATURES = {
     "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,
                          c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_video_frames": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_i64, c_p, c_p,
-                           c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p],
+                           c_p, c_p, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_dit_precompute_past": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p],
     "oasis_dit_forward_current": [P(DiTWeights), P(DiTBuffers), P(KVCache), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_graph_begin": [c_p],

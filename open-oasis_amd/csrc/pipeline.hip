@@ -38,52 +38,15 @@ int check_launch(const char* what) {
 
 namespace {
 
-// Per-device side stream + events used to overlap the adaLN projections (pure weight
-// streaming, independent of the token path) with the sub-blocks that consume them.
-// Created on first use, kept for the process lifetime; default stream priority.
-struct SideStream {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t ev[OASIS_MAX_SUB + 1] = {};
-};
-
-int side_stream(SideStream** out) {
-  static std::mutex mu;
-  static SideStream table[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    oasis::set_error("side stream: no current device");
-    return OASIS_ERR_LAUNCH;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  SideStream& t = table[dev];
-  if (!t.s) {
-    if (hipStreamCreateWithFlags(&t.s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&t.fork, hipEventDisableTiming) != hipSuccess) {
-      oasis::set_error("side stream: creation failed");
-      return OASIS_ERR_LAUNCH;
-    }
-    for (auto& e : t.ev)
-      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-        oasis::set_error("side stream: event creation failed");
-        return OASIS_ERR_LAUNCH;
-      }
-  }
-  *out = &t;
-  return OASIS_OK;
-}
-
 // GEMM plan per projection role: tile configuration (-1 = gemm.hip's default for the
-// shape) and split-K count (0 = chosen from the shape). Tuning override, read once:
+// shape) and split-K count (0 = chosen from the shape). Tuning override, read once (the only
+// process-wide state besides the per-thread error text and the per-device address of the
+// not-allocating entry point's scratch):
 //   OASIS_GEMM_PLAN="qkv:1,o:0:4,fc1:2,fc2:2:4,vqkv:3,vo:2:2,vfc1:4,vfc2:2:2" (tile ids of gemm.hip)
-//   OASIS_ADALN_OVERLAP=1 streams the adaLN projections on a side stream, overlapped with
-//   the sub-blocks (off by default: the cross-stream graph edges cost more than they
-//   hide on MI355X, 2.09 vs 1.90 ms per config-1 step).
 enum { ROLE_QKV, ROLE_O, ROLE_FC1, ROLE_FC2, ROLE_VQKV, ROLE_VO, ROLE_VFC1, ROLE_VFC2, ROLE_N };
 struct Plan {
   int tile[ROLE_N];
   int splits[ROLE_N];
-  bool overlap;
   bool fused_temporal;  // two-frame temporal windows on temporal_qkv.hip (OASIS_TEMPORAL_FUSED=0: off)
 };
 
@@ -94,7 +57,6 @@ const Plan& plan() {
       q.tile[i] = -1;
       q.splits[i] = 0;
     }
-    q.overlap = false;
     q.fused_temporal = true;
     static const char* names[ROLE_N] = {"qkv", "o", "fc1", "fc2", "vqkv", "vo", "vfc1", "vfc2"};
     if (const char* env = getenv("OASIS_GEMM_PLAN")) {
@@ -117,7 +79,6 @@ const Plan& plan() {
           }
       }
     }
-    if (const char* env = getenv("OASIS_ADALN_OVERLAP")) q.overlap = atoi(env) != 0;
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env) != 0;
     return q;
   }();
@@ -351,7 +312,7 @@ struct KvPass {
 // oasis_inference.py:1218-1352).
 int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B, int64_t T, const float* ada,
                int64_t fs, int64_t j0, int64_t j1, Pending* pend, oasis_stream_t stream,
-               const hipEvent_t* ada_ready = nullptr, const KvPass& kv = KvPass()) {
+               const KvPass& kv = KvPass()) {
   const int64_t D = w->d_model, H = w->n_heads, Dm = w->d_mlp;
   const int64_t P = (int64_t)w->grid_h * w->grid_w;
   const int64_t M = B * T * P;
@@ -386,8 +347,6 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   for (int64_t j = j0; j < j1; ++j) {
     const bool spatial = (j % 2) == 0;
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
-    if (ada_ready && hipStreamWaitEvent(s, ada_ready[j], 0) != hipSuccess)
-      return oasis::check_launch("wait for adaLN rows");
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
@@ -478,10 +437,8 @@ int dit_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64
 // final layer (oasis_inference.py:1497-1521): adaLN(2 chunks) + LN + modulate + linear,
 // with any pending FC2 residual folded into the LN pass
 int dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M, const float* ada, int64_t fs,
-              const Pending& pend, float* v_out, oasis_stream_t stream, hipEvent_t ada_ready = nullptr) {
+              const Pending& pend, float* v_out, oasis_stream_t stream) {
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w;
-  if (ada_ready && hipStreamWaitEvent((hipStream_t)stream, ada_ready, 0) != hipSuccess)
-    return oasis::check_launch("wait for adaLN rows");
   const float* fa = ada + (int64_t)w->n_sub * 6 * D;  // shift, scale_p1
   return oasis::final_layer(buf->x, M, D, buf->partial, pend.n, M * D, pend.bias, pend.gate, fs, P, fa + D, fa, fs,
                             w->final_w, w->final_b, v_out, kLnEps, (hipStream_t)stream);
@@ -490,34 +447,6 @@ int dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int6
 }  // namespace
 
 namespace {
-
-// ada[r, :] = silu(cond[r]) @ ada_w^T + ada_b on the side stream, one event per consumer
-// (sub-block j -> ev[j], final layer -> ev[n_sub]); returns the side-stream table.
-int fork_adaln(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, oasis_stream_t stream,
-               SideStream** out) {
-  const int64_t D = w->d_model, NA = ada_width(w);
-  if (!plan().overlap) {  // all projections in one pass on the caller's stream; no waits needed
-    OASIS_TRY(adaln_rows(w, cond, R, ada, (hipStream_t)stream));
-    *out = nullptr;
-    return OASIS_OK;
-  }
-  SideStream* ss = nullptr;
-  OASIS_TRY(side_stream(&ss));
-  if (hipEventRecord(ss->fork, (hipStream_t)stream) != hipSuccess || hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
-    return oasis::check_launch("adaLN fork");
-  for (int j = 0; j <= w->n_sub; ++j) {
-    const int64_t r0 = (int64_t)j * 6 * D;
-    if (j < w->n_sub)
-      OASIS_TRY(oasis_gemv_bf16(cond, D, R, static_cast<const bf16*>(w->ada_w) + r0 * D, 6 * D, D, w->ada_b + r0,
-                                ada + r0, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, ss->s));
-    else
-      OASIS_TRY(oasis_gemv_f32(cond, D, R, w->final_ada_w, 2 * D, D, w->final_ada_b, ada + r0, NA, OASIS_ACT_SILU,
-                               OASIS_ACT_NONE, 0, ss->s));
-    if (hipEventRecord(ss->ev[j], ss->s) != hipSuccess) return oasis::check_launch("adaLN event");
-  }
-  *out = ss;
-  return OASIS_OK;
-}
 
 }  // namespace
 
@@ -530,13 +459,12 @@ extern "C" int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buff
   const int64_t R = B * T, D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
   OASIS_REQUIRE(R <= 1024, OASIS_ERR_SHAPE, "dit_step: at most 1024 frames per call (got %lld)", (long long)R);
   OASIS_TRY(cond_mlp(w, t, action, R, hid, cond, stream));
-  SideStream* ss = nullptr;
-  OASIS_TRY(fork_adaln(w, cond, R, ada, stream, &ss));
+  OASIS_TRY(adaln_rows(w, cond, R, ada, (hipStream_t)stream));
   OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
                                buf->x, D, stream));
   Pending pend;
-  OASIS_TRY(dit_blocks(w, buf, B, T, ada, NA, 0, w->n_sub, &pend, stream, ss ? ss->ev : nullptr));
-  return dit_final(w, buf, B * T * P, ada, NA, pend, v_out, stream, ss ? ss->ev[w->n_sub] : nullptr);
+  OASIS_TRY(dit_blocks(w, buf, B, T, ada, NA, 0, w->n_sub, &pend, stream));
+  return dit_final(w, buf, B * T * P, ada, NA, pend, v_out, stream);
 }
 
 extern "C" int oasis_dit_sub_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
@@ -598,7 +526,7 @@ extern "C" int oasis_dit_precompute_past(const oasis_dit_weights_t* w, const oas
   KvPass kp;
   OASIS_TRY(kv_args(w, buf, kv, B, ada, &kp, KV_SAVE_T1));
   Pending pend;
-  return dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, nullptr, kp);
+  return dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, kp);
 }
 
 extern "C" int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf,
@@ -608,7 +536,7 @@ extern "C" int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oas
   OASIS_TRY(kv_args(w, buf, kv, B, ada, &kp, KV_USE_T1));
   OASIS_REQUIRE(v_out, OASIS_ERR_NULL, "dit_forward_current: null v_out");
   Pending pend;
-  OASIS_TRY(dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, nullptr, kp));
+  OASIS_TRY(dit_blocks(w, buf, B, 1, ada, ada_fstride, 0, w->n_sub, &pend, stream, kp));
   return dit_final(w, buf, B * (int64_t)w->grid_h * w->grid_w, ada, ada_fstride, pend, v_out, stream);
 }
 
@@ -742,7 +670,7 @@ namespace {
 // generated frame alone at T=1. chunk is updated in place.
 int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, const oasis_kv_cache_t* kv,
                 float* chunk, const float* ctx_z, const float* ada, int64_t n_steps, const float* coeffs,
-                float* v_out, SideStream* ss, oasis_stream_t stream) {
+                float* v_out, oasis_stream_t stream) {
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
   hipStream_t s = (hipStream_t)stream;
   KvPass save, use;
@@ -755,12 +683,11 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     const bool t1 = kv && i > 0;  // K/V cache filled by step 0: the current frame alone
     const float* c = coeffs + 6 * i;
     Pending pend;
-    const bool wait = ss && i == 0;
     if (t1) {
       OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, buf->x, D,
                                    stream));
       const float* ada_cur = ada + (1 + i) * NA;  // the generated frame's rows at step i
-      OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, nullptr, use));
+      OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, use));
       OASIS_TRY(dit_final(w, buf, P, ada_cur, NA, pend, v_out, stream));
       OASIS_TRY(oasis_ddim_update(chunk, v_out, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5], stream));
       continue;
@@ -771,9 +698,8 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
                                  buf->x + P * D, D, stream));
     const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
-    OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, wait ? ss->ev : nullptr,
-                         kv ? save : KvPass()));
-    OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream, wait ? ss->ev[w->n_sub] : nullptr));
+    OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, kv ? save : KvPass()));
+    OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream));
     OASIS_TRY(oasis_ddim_update(chunk, v_out + P * w->patch_dim, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5],
                                 stream));
   }
@@ -808,13 +734,12 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
                 OASIS_ERR_NULL, "ddim_frame: null pointer");
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4;
   // conditioning rows: 0 = context frame, 1 + i = generated frame at step i; one adaLN pass
-  // covers all rows (with the overlap option it streams on the side stream during step 0)
+  // covers all rows
   OASIS_TRY(cond_mlp(w, t, action, 1 + n_steps, hid, cond, stream));
-  SideStream* ss = nullptr;
-  OASIS_TRY(fork_adaln(w, cond, 1 + n_steps, ada, stream, &ss));
+  OASIS_TRY(adaln_rows(w, cond, 1 + n_steps, ada, (hipStream_t)stream));
   OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z,
                                D, stream));
-  OASIS_TRY(frame_steps(w, buf, kv, chunk, ctx_z, ada, n_steps, coeffs, v_out, ss, stream));
+  OASIS_TRY(frame_steps(w, buf, kv, chunk, ctx_z, ada, n_steps, coeffs, v_out, stream));
   OASIS_TRY(oasis_bridge(chunk, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
   return oasis_vae_decode(vw, vbuf, latent, frame, stream);
 }
@@ -824,8 +749,7 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
                                   const oasis_kv_cache_t* kv, int64_t n_frames, float* chunks,
                                   const float* ctx_patches, const float* t, const float* action, int64_t n_steps,
                                   const float* coeffs, float* hid, float* cond, float* ada, float* ctx_z,
-                                  float* v_out, float* latent, float* frames, int overlap_decode,
-                                  oasis_stream_t stream) {
+                                  float* v_out, float* latent, float* frames, oasis_stream_t stream) {
   OASIS_TRY(frame_args(w, buf, vw, n_steps));
   const bool decode = frames != nullptr;  // frames == NULL: the DiT half only
   OASIS_REQUIRE(chunks && ctx_patches && t && action && coeffs && hid && cond && ada && ctx_z && v_out &&
@@ -840,26 +764,16 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
   // every frame's conditioning rows at once: frame f's rows at f*R (context, then step i)
   OASIS_TRY(cond_mlp(w, t, action, n_frames * R, hid, cond, stream));
   OASIS_TRY(adaln_rows(w, cond, n_frames * R, ada, s));
-  SideStream* ss = nullptr;
-  if (overlap_decode && decode) OASIS_TRY(side_stream(&ss));
   for (int64_t f = 0; f < n_frames; ++f) {
     // context = the previous frame's denoised latent (the rolled context window)
     const float* ctx = f == 0 ? ctx_patches : chunks + (f - 1) * fsz;
     OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z, D,
                                  stream));
-    OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out, nullptr,
+    OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out,
                           stream));
-    if (!ss) continue;  // in order: the decodes run after the last frame, batched
-    // bridge + VAE of frame f on the side stream, overlapping frame f + 1's DiT
-    hipEvent_t ev = ss->ev[f % (OASIS_MAX_SUB + 1)];
-    if (hipEventRecord(ev, s) != hipSuccess || hipStreamWaitEvent(ss->s, ev, 0) != hipSuccess)
-      return oasis::check_launch("video_frames fork");
-    OASIS_TRY(oasis_bridge(chunks + f * fsz, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, ss->s));
-    OASIS_TRY(vae_decode(vw, vbuf, 1, latent, frames + f * frame_elems, ss->s));
   }
-  if (ss && (hipEventRecord(ss->fork, ss->s) != hipSuccess || hipStreamWaitEvent(s, ss->fork, 0) != hipSuccess))
-    return oasis::check_launch("video_frames join");
-  if (decode && !ss) OASIS_TRY(decode_chunks(w, vw, vbuf, n_frames, chunks, latent, frames, stream));
+  // the bridges + decodes after the last frame, batched
+  if (decode) OASIS_TRY(decode_chunks(w, vw, vbuf, n_frames, chunks, latent, frames, stream));
   return OASIS_OK;
 }
 

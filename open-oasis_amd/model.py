@@ -622,7 +622,7 @@ class VideoPipeline:
                self.n_frames, L.ptr(self.chunk_bufs[b]), L.ptr(self.ctx_patches), L.ptr(ws.t), L.ptr(ws.act), self.n,
                ctypes.cast(self.coeffs, ctypes.c_void_p), L.ptr(ws.hid), L.ptr(ws.cond),
                L.ptr(ws.ada), L.ptr(self.ctx_z), L.ptr(ws.v_out), L.ptr(self.vws.latent) if decode else None,
-               L.ptr(self.frame_bufs[b]) if decode else None, 0, L.stream_handle(self.stream))
+               L.ptr(self.frame_bufs[b]) if decode else None, L.stream_handle(self.stream))
 
     def _enqueue_decode(self, b):
         L.call("oasis_video_decode", ctypes.byref(self.dit.struct), ctypes.byref(self.vae.struct),
