@@ -511,7 +511,8 @@ def main():
     fc1_ai = fc1_flop / fc1_bytes
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     fc1_gbs = fc1_bytes / (fc1_ms * 1e-3) / 1e9
-    fc1_roofline = {"kernel": "gemm_big_kernel<96,64,2,2,4> (direct-to-LDS bf16 MFMA GEMM), FC1 projection + bias + "
+    fc1_roofline = {"kernel": "gemm_wave_kernel<96,64,2,4,GELU_TANH> (bf16 MFMA GEMM, 4 waves splitting K, each over "
+                              "its own direct-to-LDS ring), FC1 projection + bias + "
                               "tanh-GELU (M=288, N=4096, K=1024), the largest of the step's 128 projections (4 per sub-block; the 16 temporal QKVs run fused with their attention); "
                               "launch i uses sub-block i % 32's weights (cold, as in the step); 100 launches in "
                               "one hipGraph"}

@@ -188,8 +188,9 @@ typedef struct {
 int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                     int64_t N, int64_t K, const oasis_epilogue_t* epi, oasis_stream_t stream);
 
-/* Same with an explicit tile configuration (0..7, the kTiles table of gemm.hip; -1 = default) and
- * split-K count (splits divides K/64; splits > 1 requires OASIS_EPI_PARTIAL_F32).
+/* Same with an explicit tile configuration (0..12, the kTiles table of gemm.hip; -1 = default) and
+ * split-K count (splits divides K/64; splits > 1 requires OASIS_EPI_PARTIAL_F32). The wave-split
+ * tiles 8..12 need K/splits = 256, 512, 1024 or 2048 and refuse OASIS_EPI_GELU_TANH_FP8.
  * No counterpart in the reference: it exposes the tiling for tuning and benchmarks. */
 int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                            int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,

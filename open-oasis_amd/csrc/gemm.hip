@@ -12,6 +12,9 @@
 //   - gemm_big_kernel: the same ring with a grouped tile order and a per-wave staged epilogue, on
 //     4-, 6- and 8-wave tiles: the MLP products, every VAE projection, and the 8-wave 288-row
 //     tiles from 2048 tokens up.
+//   - gemm_wave_kernel: 4 waves split each workgroup's K slice four ways, each over its own LDS
+//     ring with no workgroup barrier in the K loop; the default below 320 tokens (QKV + RoPE, O,
+//     FC1, FC2) and for the VAE's O projection.
 //   - gemm_bf16_kernel: global -> registers -> LDS, for the reference-surface oasis_linear with
 //     its [K, N] weight layout (the weights transposed into LDS).
 // After the K loop the fp32 tile is staged through LDS so each thread handles 8 consecutive
@@ -486,6 +489,222 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
   }
 }
 
+// Wave-split K (below 2048 tokens): the 4 waves of a workgroup share one BM x BN output tile and
+// split its K slice four ways. Each wave stages its own K tiles (global_load_lds into the same
+// swizzled 128-byte rows as above) in a private STG-deep LDS ring and multiplies them, so the K
+// loop waits only on the wave's own loads (no workgroup barrier) and every staged byte is read
+// from LDS once (a 2 x 2 wave grid reads each A and B fragment twice). The four partial tiles are
+// summed through LDS before the epilogue; the bias of each thread's epilogue columns is fetched
+// before the K loop.
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(VM >= 0 && VM <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int BN, int STG, int NK, int KIND>
+__global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__ A, int64_t lda,
+                                                        const bf16* __restrict__ B, int64_t ldb, int M, int N,
+                                                        int K, int splits, Epi e) {
+  constexpr int NW = 4;
+  constexpr int FM = BM / 16, FN = BN / 16;
+  static_assert(FM * 16 == BM && FN * 16 == BN, "tile must be a multiple of 16");
+  static_assert(STG == 1 || STG == 2, "ring depth");
+  constexpr int ROWB = 128;
+  constexpr int NBLK = (BM + BN) / 8;  // 8-row (1 KB) blocks per K tile: one load instruction each
+  static_assert(NBLK * 8 == BM + BN && NBLK <= 63, "whole 8-row blocks within the vmcnt range");
+  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int WAVE_BYTES = STG * STAGE_BYTES;
+  constexpr int PITCH = BN + 4;
+  constexpr int RED_BYTES = NW * BM * PITCH * 4;
+  constexpr int SMEM = NW * WAVE_BYTES > RED_BYTES ? NW * WAVE_BYTES : RED_BYTES;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  constexpr int UPR = BN / 8;                      // 8-column epilogue units per row
+  constexpr int UNITS = BM * UPR;
+  constexpr int UPT = (UNITS + 255) / 256;         // units per thread
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
+  const int mt = pid % Mt;
+  const int rest = pid / Mt;
+  const int split = rest % splits, nt = rest / splits;
+  const int m0 = mt * BM, n0 = nt * BN;
+  constexpr int nk = NK;                           // K tiles per wave: K = 256 NK splits (host-checked)
+  const int kb = (split * NW + wave) * nk * 64;
+  char* ring = smem + wave * WAVE_BYTES;
+
+  // bias of this thread's epilogue columns (bias-less and split-K slices skip it)
+  float bv[UPT][8];
+  // KIND >= 0: the epilogue kind fixed at compile time (equal to e.kind); -1: read from e
+  constexpr bool partial_only = KIND == OASIS_EPI_PARTIAL_F32;
+  const bool has_bias = !partial_only && e.bias && e.kind != OASIS_EPI_PARTIAL_F32;
+#pragma unroll
+  for (int q = 0; q < UPT; ++q) {
+    const int gn = min(n0 + ((tid + q * 256) % UPR) * 8, N - 8);
+    f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (has_bias) {
+      b0 = *reinterpret_cast<const f32x4*>(e.bias + gn);
+      b1 = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bv[q][j] = b0[j];
+      bv[q][j + 4] = b1[j];
+    }
+  }
+
+  // lane's row in each 8-row block: r = 8 blk + lane / 8, K chunk (lane % 8) ^ ((r >> 1) & 7);
+  // the tile index only moves the pointer by a constant, folded into each load's offset
+  const bf16* src[NBLK];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) {
+    const int r = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    src[blk] = r < BM ? A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 8
+                      : B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 8;
+  }
+  auto issue = [&](int kt, int buf) {
+    char* base = ring + buf * STAGE_BYTES;
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) load_lds16(src[blk] + kt * 64, base + blk * 1024);
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, g = lane >> 4;
+  auto compute = [&](int buf) {
+    const char* base = ring + buf * STAGE_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + g;
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = i * 16 + lr;
+        af[i] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = BM + j * 16 + lr;
+        bfr[j] = *reinterpret_cast<const bf16x8*>(base + r * ROWB + ((c ^ ((r >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  // The scheduling barriers keep each tile's loads where they are written: the compiler would
+  // otherwise sink them next to their first use and serialise the ring.
+  issue(0, 0);
+  if (STG == 2 && nk > 1) issue(1, 1);
+#pragma unroll
+  for (int k = 0; k < nk; ++k) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (STG == 2 && k + 1 < nk)
+      wait_vmcnt<NBLK>();  // tile k + 1 may still be in flight
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(STG == 2 ? (k & 1) : 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + STG < nk) issue(k + STG, STG == 2 ? (k & 1) : 0);  // into the buffer just read
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();  // every wave is done with its ring: reuse LDS for the partial tiles
+
+  float* red = reinterpret_cast<float*>(smem);
+  float* mine = red + wave * BM * PITCH;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mine[(i * 16 + g * 4 + r) * PITCH + j * 16 + lr] = acc[i][j][r];
+  __syncthreads();
+
+  // thread -> (row, 8 consecutive columns): coalesced 16- / 32-byte stores
+#pragma unroll
+  for (int q = 0; q < UPT; ++q) {
+    const int u = tid + q * 256;
+    if (UNITS % 256 != 0 && u >= UNITS) break;
+    const int r = u / UPR, c8 = (u % UPR) * 8;
+    const int gm = m0 + r, gn = n0 + c8;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = bv[q][j];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(red + w * BM * PITCH + r * PITCH + c8);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(red + w * BM * PITCH + r * PITCH + c8 + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] += c0[j];
+        v[j + 4] += c1[j];
+      }
+    }
+    if (gm < M && gn < N) {
+      if (partial_only || (KIND < 0 && e.kind == OASIS_EPI_PARTIAL_F32)) {
+        float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+        *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      } else {
+        epilogue8(e, gm, gn, v, nullptr, 0, false, KIND);
+      }
+    }
+  }
+}
+
+// The K loop is unrolled for 1, 2, 4 or 8 K tiles per wave (K / splits = 256, 512, 1024, 2048); the
+// split-K, GELU and QKV + RoPE epilogues of 2 or 4 tiles per wave (the step's and the VAE's
+// projections) get kernels of their own.
+template <int BM, int BN, int STG, int NK>
+void launch_wave_nk(const dim3& grid, const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K,
+                    int splits, const Epi& e, hipStream_t s) {
+  const dim3 block(256);
+  if (NK == 2 || NK == 4) {
+    switch (e.kind) {
+      case OASIS_EPI_PARTIAL_F32:
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_PARTIAL_F32>), grid, block, 0, s, A, lda, B,
+                           ldb, M, N, K, splits, e);
+        return;
+      case OASIS_EPI_GELU_TANH:
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_GELU_TANH>), grid, block, 0, s, A, lda, B, ldb,
+                           M, N, K, splits, e);
+        return;
+      case OASIS_EPI_QKV_ROPE:
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_QKV_ROPE>), grid, block, 0, s, A, lda, B, ldb,
+                           M, N, K, splits, e);
+        return;
+      default:
+        break;
+    }
+  }
+  hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, -1>), grid, block, 0, s, A, lda, B, ldb, M, N, K, splits, e);
+}
+
+template <int BM, int BN, int STG>
+hipError_t launch_wave(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
+                       const Epi& e, hipStream_t s) {
+  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const dim3 grid(Mt * Nt * splits);
+  switch ((K / splits) % 256 == 0 ? K / splits / 256 : 0) {
+    case 1: launch_wave_nk<BM, BN, STG, 1>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 2: launch_wave_nk<BM, BN, STG, 2>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 4: launch_wave_nk<BM, BN, STG, 4>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 8: launch_wave_nk<BM, BN, STG, 8>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    default: return hipErrorInvalidConfiguration;
+  }
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES>
 hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
                       const Epi& e, hipStream_t s) {
@@ -524,6 +743,8 @@ struct TileCfg {
   int bm, bn;
   launch_fn fn;
   int no_fp8_epi = 0;   // 1: its epilogue lanes do not cover aligned 32-column blocks
+  int k_gran = 64;      // each split-K slice must be a multiple of this
+  int k_max = 1 << 30;  // and at most this long
 };
 const TileCfg kTiles[] = {
     // direct-to-LDS, 4 waves: split-K slices of the O projection, QKV + RoPE at 144 / 288 tokens
@@ -538,6 +759,13 @@ const TileCfg kTiles[] = {
     {288, 256, launch_big<288, 256, 2, 4, 2>},              // 5
     {288, 192, launch_big<288, 192, 2, 4, 2>, 1},           // 6
     {288, 128, launch_big<288, 128, 2, 4, 2>},              // 7
+    // wave-split K, 4 waves on one tile, each wave's K tiles in its own 2-deep LDS ring (K slices of
+    // 256 x 1, 2, 4 or 8; not used for the fp8-block GELU epilogue)
+    {96, 64, launch_wave<96, 64, 2>, 1, 256, 2048},                       // 8
+    {48, 32, launch_wave<48, 32, 2>, 1, 256, 2048},                       // 9
+    {48, 64, launch_wave<48, 64, 2>, 1, 256, 2048},                       // 10
+    {64, 64, launch_wave<64, 64, 2>, 1, 256, 2048},                       // 11
+    {32, 64, launch_wave<32, 64, 2>, 1, 256, 2048},                       // 12
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -545,16 +773,28 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 namespace oasis {
 
-// Default tile per shape, from timings of each projection on MI355X with cold weights:
+// Default tile per shape, from timings of each projection on MI355X with cold weights (hipGraphs
+// of 100 launches over rotating weight sets):
 //   - 2048+ tokens: the 8-wave tall tiles, the width that fills the last round of 256 workgroups best;
-//   - FC1 (GELU): 64 x 64 (tile 3) at one 144-token frame, 144 x 64 on 6 waves (tile 4) from 512
-//     tokens (the VAE's 576), else 96 x 64 (tile 2);
-//   - split-K partials: 32 x 64 tiles (tile 0) for short K slices (O: 256 at 144 tokens, 512 at 288),
-//     tile 2 for the longer slices (FC2) and from 320 tokens up;
-//   - other epilogues (QKV + RoPE, plain stores): 32 x 64 (tile 1), tile 3 from 512 tokens.
-int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
+//   - below, where the K slice suits the wave-split kernel (256, 512, 1024 or 2048 long):
+//       FC1 (GELU): 48 x 64 (tile 10) at one 144-token frame, 96 x 64 (tile 8) up to 320 tokens;
+//       split-K partials of K <= 1024 (O): 48 x 32 (tile 9) up to 320 tokens, 48 x 64 (tile 10) above;
+//       split-K partials of longer K (FC2): tile 10 at one frame, tile 8 up to 320 tokens;
+//       other epilogues (QKV + RoPE): 32 x 64 (tile 12) at one frame, 64 x 64 (tile 11) up to 320;
+//   - otherwise the shared-ring kernels: FC1 on 144 x 64 six-wave tiles (tile 4) from 512 tokens (the
+//     VAE's 576) and 96 x 64 (tile 2) else; split-K partials on 32 x 64 (tile 0) for short slices up to
+//     320 tokens and tile 2 else; other epilogues on 32 x 64 (tile 1), 64 x 64 (tile 3) from 512 tokens.
+int auto_tile(int64_t M, int64_t N, int64_t K, int splits, int kind) {
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 5, 6, 7);
+  const int64_t Kslice = K / splits;
+  const bool wave_k = Kslice % 256 == 0 && Kslice <= 2048 && ((Kslice / 256) & (Kslice / 256 - 1)) == 0;
   const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
+  if (wave_k && M <= 320) {
+    if (gelu) return M <= 160 ? 10 : 8;
+    if (kind == OASIS_EPI_PARTIAL_F32) return K <= 1024 ? 9 : (M <= 160 ? 10 : 8);
+    if (kind != OASIS_EPI_GELU_TANH_FP8) return M <= 160 ? 12 : 11;
+  }
+  if (wave_k && kind == OASIS_EPI_PARTIAL_F32 && K <= 1024) return 10;
   if (gelu) return M <= 160 ? 3 : (M >= 512 ? 4 : 2);
   if (kind == OASIS_EPI_PARTIAL_F32) {
     if (M <= 160) return Kslice <= 256 ? 0 : 2;
@@ -566,7 +806,7 @@ int auto_tile(int64_t M, int64_t N, int64_t Kslice, int kind) {
 // Split-K count for the default tile of a large-token split-K product: K slices until the
 // launch has at least 256 workgroups (one per CU), within max_splits and whole 64-wide K tiles.
 int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits) {
-  const TileCfg& t = kTiles[auto_tile(M, N, K, OASIS_EPI_PARTIAL_F32)];
+  const TileCfg& t = kTiles[auto_tile(M, N, K, 1, OASIS_EPI_PARTIAL_F32)];
   const int64_t tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   int s = 1;
   while (tiles * s < 256 && 2 * s <= max_splits && 2 * s <= 8 && (K / 64) % (2 * s) == 0) s *= 2;
@@ -588,11 +828,15 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
                 "gemm: splits=%d must divide K/64=%lld", splits, (long long)(K / BK));
   const Epi e = to_epi(ex);
   if (const int rc = check_epilogue(e, M, N, splits)) return rc;
-  if (tile < 0) tile = auto_tile(M, N, K / splits, e.kind);
+  if (tile < 0) tile = auto_tile(M, N, K, splits, e.kind);
   OASIS_REQUIRE(tile < kNumTiles, OASIS_ERR_ARG, "gemm: tile config %d out of range", tile);
   const TileCfg& t = kTiles[tile];
   OASIS_REQUIRE(!(t.no_fp8_epi && e.kind == OASIS_EPI_GELU_TANH_FP8), OASIS_ERR_ARG,
                 "gemm: tile config %d cannot run the GELU_TANH_FP8 epilogue", tile);
+  OASIS_REQUIRE((K / splits) % t.k_gran == 0 && K / splits <= t.k_max &&
+                    (t.k_gran == 64 || ((K / splits / t.k_gran) & (K / splits / t.k_gran - 1)) == 0),
+                OASIS_ERR_SHAPE, "gemm: tile config %d needs K/splits=%lld to be %s of %d up to %d", tile,
+                (long long)(K / splits), t.k_gran == 64 ? "a multiple" : "a power-of-two multiple", t.k_gran, t.k_max);
   const hipError_t err = t.fn(A, lda, B, ldb, (int)M, (int)N, (int)K, splits, e, s);
   if (err != hipSuccess) {
     set_error("gemm launch failed: %s", hipGetErrorString(err));

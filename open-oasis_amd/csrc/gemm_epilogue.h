@@ -165,10 +165,12 @@ __device__ __forceinline__ void qkv_rope_store(const Epi& e, int64_t m, int n0, 
 }
 
 // Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N). tab / tab_rows:
-// an LDS copy of the QKV rotation tables (see rope_lds_rows), or null.
+// an LDS copy of the QKV rotation tables (see rope_lds_rows), or null. with_bias = false: the
+// caller has already added the bias. kind >= 0: the epilogue kind known at compile time (it must
+// equal e.kind), which drops the other kinds' code.
 __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float* v, const float* tab = nullptr,
-                                          int tab_rows = 0) {
-  if (e.bias) {
+                                          int tab_rows = 0, bool with_bias = true, int kind = -1) {
+  if (with_bias && e.bias) {
     const f32x4 b0 = *reinterpret_cast<const f32x4*>(e.bias + n0);
     const f32x4 b1 = *reinterpret_cast<const f32x4*>(e.bias + n0 + 4);
 #pragma unroll
@@ -177,7 +179,7 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       v[j + 4] += b1[j];
     }
   }
-  switch (e.kind) {
+  switch (kind >= 0 ? kind : e.kind) {
     case OASIS_EPI_STORE_F32: {
       float* d = e.out_f32 + m * e.ld_out + n0;
       *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};

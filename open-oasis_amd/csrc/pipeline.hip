@@ -254,16 +254,14 @@ extern "C" int oasis_dit_conditioning_noalloc(const oasis_dit_weights_t* w, cons
 
 namespace {
 
-// Split-K count for an O / FC2 GEMM (tile 0: 32 x 64): enough workgroups to cover the
-// 256 CUs, each split still a multiple of the 4-deep prefetch ring. From 2048 tokens up the
-// GEMM's own large-token tiles decide.
-// Split-K count of a partial-sum projection (O: K = D, FC2: K = 4D). Below 2048 tokens, from
-// timings on MI355X: O in 4 slices at one 144-token frame and 2 above, FC2 in 8 slices at
-// one frame and 4 above; fewer when max_splits or whole 64-wide K tiles per slice require it.
+// Split-K count of a partial-sum projection (O: K = D, FC2: K = 4D) below 2048 tokens, from timings
+// on MI355X of gemm.hip's default tiles: O in 2 slices at one 144-token frame and whole above (the
+// wave-split tiles fill the CUs without slicing), FC2 in 4; fewer when max_splits or whole 64-wide K
+// tiles per slice require it. From 2048 tokens up the GEMM's own large-token tiles decide.
 int choose_splits(int64_t M, int64_t N, int64_t K, int64_t max_splits) {
   (void)N;
   if (M >= 2048) return oasis::gemm_auto_splits(M, N, K, (int)std::min<int64_t>(max_splits, 8));
-  int s = K > 1024 ? (M <= 160 ? 8 : 4) : (M <= 160 ? 4 : 2);
+  int s = K > 1024 ? 4 : (M <= 160 ? 2 : 1);
   while (s > 1 && (s > max_splits || (K / 64) % s != 0)) s /= 2;
   return s;
 }

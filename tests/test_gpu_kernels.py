@@ -104,13 +104,17 @@ def test_gemm_gated_and_plain_residual():
     assert_close(x, ref + y, 0.999999, 1e-5, "residual")
 
 
-@pytest.mark.parametrize("layout", ["spatial", "temporal", "vae"])
-def test_gemm_qkv_rope(layout):
+@pytest.mark.parametrize("layout,tile", [("spatial", -1), ("temporal", -1), ("vae", -1), ("spatial", 11),
+                                         ("temporal", 11), ("spatial", 12), ("vae", 11)])
+def test_gemm_qkv_rope(layout, tile):
+    """QKV + RoPE + head split into each attention layout: the default tile (K = 256), and the
+    wave-split tiles 11 / 12 with the kernels specialised for this epilogue (K = 1024)."""
     H, D = 4, 256
+    K = 256 if tile < 0 else 1024
     if layout == "vae":
-        B_, T, P, K = 1, 1, 576, 256
+        B_, T, P = 1, 1, 576
     else:
-        B_, T, P, K = 2, 2, 144, 256
+        B_, T, P = (2, 2, 144) if tile < 0 else (1, 2, 144)
     M, N = B_ * T * P, 3 * D
     g = _gen(5)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
@@ -131,7 +135,7 @@ def test_gemm_qkv_rope(layout):
     e = _epi(kind=L.EPI_QKV_ROPE, n_heads=H, bias=dev(bias), q=q, k=k, v=v, rope_cos=dev(cos),
              rope_sinp=dev(sinp), rope_by_frame=int(layout == "temporal"), rows_per_frame=P,
              frames_per_stream=T, s_b=s_b, s_t=s_t, s_p=s_p, s_h=s_h)
-    _gemm(dev(A), dev(W), M, N, K, e)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(A)), K, L.ptr(dev(W)), K, M, N, K, ctypes.byref(e), tile, 1, stream())
     sync()
     y = (A.float() @ W.float().t() + bias).reshape(B_, T, P, 3, H, 64)
     pos_c = cos[torch.arange(T)] if layout == "temporal" else cos
@@ -145,7 +149,7 @@ def test_gemm_qkv_rope(layout):
     rv = y[:, :, :, 2]
     perm = (0, 2, 3, 1, 4) if layout == "temporal" else (0, 1, 3, 2, 4)
     for name, got, ref in (("q", q, rq), ("k", k, rk), ("v", v, rv)):
-        assert_close(got, ref.permute(*perm).contiguous(), 0.99999, 1e-2, "qkv_rope %s %s" % (layout, name))
+        assert_close(got, ref.permute(*perm).contiguous(), 0.99999, 1e-2, "qkv_rope %s tile %d %s" % (layout, tile, name))
 
 
 def test_gemm_unpatchify():
@@ -523,7 +527,7 @@ def test_rope_layout_surface(dt, mode):
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(8)))
+@pytest.mark.parametrize("tile", list(range(13)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
@@ -556,6 +560,47 @@ def test_gemm_direct_lds_ragged(tile):
     ref = A.float() @ B.float().t()
     assert_close(out, torch.nn.functional.gelu(ref + bias, approximate="tanh"), 0.99999, 1e-2, "tile %d gelu" % tile)
     assert_close(part.sum(0), ref, 0.999999, 1e-4, "tile %d split-K x5" % tile)
+
+
+@pytest.mark.parametrize("tile", list(range(8, 13)))
+def test_gemm_wave_tiles_ragged(tile):
+    """The wave-split tiles (8-12: four waves split each K slice, each over its own LDS ring) on a
+    ragged shape (M and N not multiples of the tile) with every K-loop length they unroll: GELU
+    with K = 1024 (4 K tiles per wave, the GELU kernel), split-K x2 of K = 1024 (2 tiles, the
+    split-K kernel), one K = 2048 slice (8 tiles) and K = 256 (1 tile, the generic kernel); K
+    slices that are not 256 x a power of two are refused."""
+    M, N = 300, 520
+    g = _gen(120 + tile)
+    # 4096 columns, so the refused shapes below stay in bounds should a check ever let one through
+    A = torch.randn(M, 4096, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, 4096, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    Ad, Bd = dev(A), dev(B)
+
+    def ref(K):
+        return A[:, :K].float() @ B[:, :K].float().t()
+    out = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+    e = _epi(kind=L.EPI_GELU_TANH, bias=dev(bias), out_bf16=out, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), 4096, L.ptr(Bd), 4096, M, N, 1024, ctypes.byref(e), tile, 1, stream())
+    part = torch.zeros(2, M, N, device="cuda")
+    ep = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part, ld_out=N, split_stride=M * N)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), 4096, L.ptr(Bd), 4096, M, N, 1024, ctypes.byref(ep), tile, 2, stream())
+    part8 = torch.zeros(1, M, N, device="cuda")
+    ep8 = _epi(kind=L.EPI_PARTIAL_F32, out_f32=part8, ld_out=N, split_stride=M * N)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), 4096, L.ptr(Bd), 4096, M, N, 2048, ctypes.byref(ep8), tile, 1, stream())
+    o32 = torch.zeros(M, N, device="cuda")
+    e32 = _epi(kind=L.EPI_STORE_F32, bias=dev(bias), out_f32=o32, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), 4096, L.ptr(Bd), 4096, M, N, 256, ctypes.byref(e32), tile, 1, stream())
+    sync()
+    r1 = ref(1024)
+    assert_close(out, torch.nn.functional.gelu(r1 + bias, approximate="tanh"), 0.99999, 1e-2, "tile %d gelu" % tile)
+    assert_close(part.sum(0), r1, 0.999999, 1e-4, "tile %d split-K x2" % tile)
+    assert_close(part8[0], ref(2048), 0.999999, 1e-4, "tile %d K=2048" % tile)
+    assert_close(o32, ref(256) + bias, 0.999999, 1e-4, "tile %d K=256" % tile)
+    for K, splits in ((320, 1), (768, 1), (4096, 1)):
+        with pytest.raises(L.OasisError):
+            L.call("oasis_gemm_bf16_config", L.ptr(Ad), 4096, L.ptr(Bd), 4096, M, N, K, ctypes.byref(e32), tile,
+                   splits, stream())
 
 
 @pytest.mark.parametrize("tile", list(range(5, 8)))
