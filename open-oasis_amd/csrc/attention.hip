@@ -87,8 +87,12 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
   __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wq = wave % NW, wk = wave / NW;  // query block, key-chunk parity
-  const int bh = blockIdx.y;
-  const int q0 = (blockIdx.x * NW + wq) * 16;
+  // work id -> (head, query block) with a head's query blocks on consecutive ids: xcd_remap puts
+  // them on one XCD, whose L2 then fetches the head's K and V once for all of them
+  const int nqb = gridDim.x;
+  const int wid = xcd_remap(blockIdx.y * nqb + blockIdx.x, nqb * gridDim.y);
+  const int bh = wid / nqb;
+  const int q0 = ((wid - bh * nqb) * NW + wq) * 16;
   const int lr = lane & 15, g = lane >> 4;
   const T* Qb = Q + (int64_t)bh * a.q_bh;
   const T* Kb = K + (int64_t)bh * a.kv_bh;
@@ -264,6 +268,7 @@ void flash_go(dim3 g, const T* q, const T* k, const T* v, T* o, const AttnArgs& 
 template <typename T>
 int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const AttnArgs& a, hipStream_t s) {
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
+  OASIS_REQUIRE((a.Lq / 16 + 1) * n_bh < (1ll << 31), OASIS_ERR_SHAPE, "attention: too many query blocks");
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
   // staging: short sequences (up to 32 or 64 keys: the temporal windows) and whole frames (up
   // to 160 keys, 144 per DiT frame; up to 192) in one chunk; up to 576 keys (the VAE) staged at

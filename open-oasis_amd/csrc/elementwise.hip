@@ -272,30 +272,38 @@ __global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t 
     row[i] = r < rows ? r : -1;
   }
   if (row[0] < 0) return;  // no row of this workgroup exists (nor does its table row, necessarily)
+  // 8 values of T as raw 16-byte vectors (one for bf16, two for fp32), converted at use
+  constexpr int NV = sizeof(T) * 8 / 16;
   for (int t = threadIdx.x; t < D / 8; t += blockDim.x) {
     const int c8 = t * 8, h = c8 >> 6, d0 = c8 & 63;
-    float c[8], s[8], v[RPG][3][8];
+    float c[8], s[8];
+    i32x4 raw[RPG][3][NV];
     ld8<float>(cs + pos * tab_ld + h * tab_hs + d0, c);
     ld8<float>(sn + pos * tab_ld + h * tab_hs + d0, s);
 #pragma unroll
     for (int i = 0; i < RPG; ++i)
       if (row[i] >= 0) {
 #pragma unroll
-        for (int w = 0; w < 3; ++w) ld8<T>(qkv + row[i] * ldq + w * D + c8, v[i][w]);
+        for (int w = 0; w < 3; ++w)
+#pragma unroll
+          for (int u = 0; u < NV; ++u)
+            raw[i][w][u] = reinterpret_cast<const i32x4*>(qkv + row[i] * ldq + w * D + c8)[u];
       }
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
       if (row[i] < 0) break;
       const int64_t f = row[i] / seq, p = row[i] - f * seq;
-      float r[2][8];
+      float v[3][8], r[2][8];
+#pragma unroll
+      for (int w = 0; w < 3; ++w) ld8<T>(reinterpret_cast<const T*>(raw[i][w]), v[w]);
 #pragma unroll
       for (int w = 0; w < 2; ++w)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[w][e] = v[i][w][e] * c[e] + v[i][w][e ^ 1] * s[e];
+        for (int e = 0; e < 8; ++e) r[w][e] = v[w][e] * c[e] + v[w][e ^ 1] * s[e];
       const int64_t off = MODE == 0 ? ((f * H + h) * seq + p) * 64 + d0 : row[i] * D + c8;
       st8<T>(qo + off, r[0]);
       st8<T>(ko + off, r[1]);
-      st8<T>(vo + off, v[i][2]);
+      st8<T>(vo + off, v[2]);
     }
   }
 }

@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
 // rows of A and a few weight slices instead of every row of A.
 // The epilogue stages 16 rows of a wave's tile at a time in LDS owned by that wave alone.
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int GN = 8>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __restrict__ A, int64_t lda,
                                                                const bf16* __restrict__ B, int64_t ldb, int M,
                                                                int N, int K, int splits, Epi e) {
@@ -372,7 +372,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
   constexpr int SMEM = RING > EPI_BYTES ? RING : EPI_BYTES;
   static_assert(SMEM <= 160 * 1024, "LDS");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW <= 63, "vmcnt range");
-  constexpr int GN = 8;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -526,10 +525,13 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  // work id -> (split, n tile, m tile), m fastest and the split outermost: an XCD's contiguous
+  // range of ids covers the M tiles of a few weight slices of one K slice, so its L2 fetches
+  // one K slice of A rather than all of them
   const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
-  const int mt = pid % Mt;
-  const int rest = pid / Mt;
-  const int split = rest % splits, nt = rest / splits;
+  const int split = pid / (Mt * Nt);
+  const int t = pid - split * (Mt * Nt);
+  const int nt = t / Mt, mt = t - nt * Mt;
   const int m0 = mt * BM, n0 = nt * BN;
   constexpr int nk = NK;                           // K tiles per wave: K = 256 NK splits (host-checked)
   const int kb = (split * NW + wave) * nk * 64;
@@ -705,13 +707,13 @@ hipError_t launch_wave(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, i
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int GN = 8>
 hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
                       const Epi& e, hipStream_t s) {
   if ((K / splits) % 64 != 0) return hipErrorInvalidConfiguration;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s, A,
-                     lda, B, ldb, M, N, K, splits, e);
+  hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
+                     A, lda, B, ldb, M, N, K, splits, e);
   return hipGetLastError();
 }
 
@@ -753,7 +755,8 @@ const TileCfg kTiles[] = {
     // the 8-wave kernel's grouped tile order and per-wave staged epilogue on 4- and 6-wave tiles:
     // FC1 / FC2 below 2048 tokens and every VAE projection
     {96, 64, launch_big<96, 64, 2, 2, 4>},                  // 2
-    {64, 64, launch_big<64, 64, 2, 2, 4>},                  // 3
+    {64, 64, launch_big<64, 64, 2, 2, 4, 6>},               // 3: groups of 6 n tiles (576 tokens: an XCD's 54 tiles
+                                                            //    are 6 whole weight slices)
     {144, 64, launch_big<144, 64, 3, 2, 4>},                // 4: 6 waves
     // 8-wave large-token tiles (2048+ tokens)
     {288, 256, launch_big<288, 256, 2, 4, 2>},              // 5

@@ -6,7 +6,6 @@
 
 namespace {
 
-constexpr int NUM_XCD = 8;
 
 
 struct Epi {
@@ -58,11 +57,6 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint64_t magic, int shi
   return (uint32_t)(((uint64_t)n * magic) >> shift);
 }
 
-__device__ __forceinline__ int xcd_remap(int pid, int G) {
-  const int q = G / NUM_XCD, r = G % NUM_XCD;
-  const int xcd = pid % NUM_XCD, local = pid / NUM_XCD;
-  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
-}
 
 // Large-token tile order: pid -> (split, m tile, n tile) with the split outermost, then groups
 // of GN n tiles in which n runs fastest, so consecutive ids (one XCD's share after xcd_remap)

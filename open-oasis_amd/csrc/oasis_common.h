@@ -168,6 +168,18 @@ OASIS_DEV uint32_t pack4_fp8(float a, float b, float c, float d) {
   return (uint32_t)r;
 }
 
+// ---- XCD-aware workgroup order --------------------------------------------
+// MI355X dispatches workgroup i of a launch to XCD i % 8 (each XCD has its own L2). xcd_remap
+// maps the dispatch id to a work id such that every XCD receives a contiguous range of work ids,
+// so work items that share operands (the M tiles of one weight block, the query blocks of one
+// attention head) are fetched into one L2. A bijection on [0, G): it decides locality only.
+constexpr int NUM_XCD = 8;
+OASIS_DEV int xcd_remap(int pid, int G) {
+  const int q = G / NUM_XCD, r = G % NUM_XCD;
+  const int xcd = pid % NUM_XCD, local = pid / NUM_XCD;
+  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
 // ---- MFMA -------------------------------------------------------------------
 // v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8*(l/16)+j] and
 // B[8*(l/16)+j][l%16] (j=0..7) and receives D[4*(l/16)+i][l%16] (i=0..3).
