@@ -47,7 +47,11 @@ enum { ROLE_QKV, ROLE_O, ROLE_FC1, ROLE_FC2, ROLE_VQKV, ROLE_VO, ROLE_VFC1, ROLE
 struct Plan {
   int tile[ROLE_N];
   int splits[ROLE_N];
-  bool fused_temporal;  // two-frame temporal windows on temporal_qkv.hip (OASIS_TEMPORAL_FUSED=0: off)
+  // two-frame temporal windows on temporal_qkv.hip (OASIS_TEMPORAL_FUSED): 0 for none (default:
+  // the wave-split QKV GEMM + temporal attention pair times as fast or faster on MI355X, 1.592
+  // against 1.601 ms per step and 160.9 against 160.6 FPS per frame), 1 for the T = 2 passes,
+  // 2 for every pass
+  int fused_temporal;
 };
 
 const Plan& plan() {
@@ -57,7 +61,7 @@ const Plan& plan() {
       q.tile[i] = -1;
       q.splits[i] = 0;
     }
-    q.fused_temporal = true;
+    q.fused_temporal = 0;
     static const char* names[ROLE_N] = {"qkv", "o", "fc1", "fc2", "vqkv", "vo", "vfc1", "vfc2"};
     if (const char* env = getenv("OASIS_GEMM_PLAN")) {
       std::string str(env);
@@ -79,7 +83,7 @@ const Plan& plan() {
           }
       }
     }
-    if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env) != 0;
+    if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
     return q;
   }();
   return p;
@@ -348,10 +352,11 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
-    // two-frame temporal windows (the T = 2 step, the K/V-cache passes of the frame): QKV,
+    // with OASIS_TEMPORAL_FUSED=1 or 2, two-frame temporal windows (the T = 2 step and the frame's
+    // first, cache-filling pass; with 2 also the current-frame passes against the cache): QKV,
     // RoPE and the causal attention in one kernel
-    if (!spatial && !fp8 && pl.fused_temporal && pl.tile[ROLE_QKV] < 0 && P % 16 == 0 &&
-        ((kv.mode == KV_NONE && T == 2) || kv.mode == KV_SAVE_T2 || kv.mode == KV_USE_T1)) {
+    if (!spatial && !fp8 && pl.fused_temporal > 0 && pl.tile[ROLE_QKV] < 0 && P % 16 == 0 &&
+        ((kv.mode == KV_NONE && T == 2) || kv.mode == KV_SAVE_T2 || (kv.mode == KV_USE_T1 && pl.fused_temporal > 1))) {
       bf16* kcj = kv.mode == KV_NONE ? nullptr : kv.k + (j / 2) * kv.sub_stride;
       bf16* vcj = kv.mode == KV_NONE ? nullptr : kv.v + (j / 2) * kv.sub_stride;
       OASIS_TRY(oasis::temporal_qkv_attention(static_cast<const bf16*>(buf->h), D,
