@@ -68,16 +68,16 @@ __global__ __launch_bounds__(256) void ew_vec_kernel(const T* a, const T* b, con
   const int64_t ng = n / N, stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (int64_t g = t0; g < ng; g += stride) {
-    const V va = reinterpret_cast<const V*>(a)[g];
+    const V va = ld_stream(reinterpret_cast<const V*>(a) + g);
     V vb = va, vc = va, vd = va, r;
     if (OP != EW_SILU) {
-      vb = reinterpret_cast<const V*>(b)[g];
-      vc = reinterpret_cast<const V*>(c)[g];
+      vb = ld_stream(reinterpret_cast<const V*>(b) + g);
+      vc = ld_stream(reinterpret_cast<const V*>(c) + g);
     }
-    if (OP == EW_BIAS_GATED) vd = reinterpret_cast<const V*>(d)[g];
+    if (OP == EW_BIAS_GATED) vd = ld_stream(reinterpret_cast<const V*>(d) + g);
 #pragma unroll
     for (int j = 0; j < N; ++j) r[j] = (T)ew_op<OP>((float)va[j], (float)vb[j], (float)vc[j], (float)vd[j]);
-    reinterpret_cast<V*>(out)[g] = r;
+    st_stream(reinterpret_cast<V*>(out) + g, r);
   }
   for (int64_t i = ng * N + t0; i < n; i += stride) {
     const float vb = OP != EW_SILU ? ld<T>(b, i) : 0.f, vc = OP != EW_SILU ? ld<T>(c, i) : 0.f;
@@ -243,17 +243,19 @@ template <typename T>
 __device__ __forceinline__ void st8(T* p, const float* v);
 template <>
 __device__ __forceinline__ void st8<float>(float* p, const float* v) {
-  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
-  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  st_stream(reinterpret_cast<f32x4*>(p), f32x4{v[0], v[1], v[2], v[3]});
+  st_stream(reinterpret_cast<f32x4*>(p + 4), f32x4{v[4], v[5], v[6], v[7]});
 }
 template <>
 __device__ __forceinline__ void st8<bf16>(bf16* p, const float* v) {
-  *reinterpret_cast<bf16x8*>(p) = pack8(v);
+  st_stream(reinterpret_cast<bf16x8*>(p), pack8(v));
 }
 
 // A workgroup takes up to RPG rows that share one table position (rows
 // (q * pos_mod + pos) * pos_div + rem): thread t owns column group c8 = 8t of Q, K and V, loads its
 // 8 cos / sin values once for all of them, and issues the loads of all its rows before any store.
+// QKV rows are read with streaming loads and Q, K, V written with streaming stores (each byte is
+// touched once). The elementwise kernels above stream their operands the same way.
 constexpr int RPG = 4;
 
 template <typename T, int MODE>
@@ -266,9 +268,10 @@ __global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t 
   int64_t row[RPG];
 #pragma unroll
   for (int i = 0; i < RPG; ++i) {  // the j-th row of this position, j = blockIdx.y * RPG + i (rows: -1 past the end)
-    const int64_t j = (int64_t)blockIdx.y * RPG + i;
-    const int64_t q = j / pos_div, rem = j - q * pos_div;
-    const int64_t r = (q * pos_mod + pos) * pos_div + rem;
+    // 32-bit divisions (the host checks that j, pos_div, seq and rows are below 2^31)
+    const uint32_t j = blockIdx.y * RPG + i;
+    const uint32_t q = j / (uint32_t)pos_div, rem = j - q * (uint32_t)pos_div;
+    const int64_t r = ((int64_t)q * pos_mod + pos) * pos_div + rem;
     row[i] = r < rows ? r : -1;
   }
   if (row[0] < 0) return;  // no row of this workgroup exists (nor does its table row, necessarily)
@@ -287,12 +290,12 @@ __global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t 
         for (int w = 0; w < 3; ++w)
 #pragma unroll
           for (int u = 0; u < NV; ++u)
-            raw[i][w][u] = reinterpret_cast<const i32x4*>(qkv + row[i] * ldq + w * D + c8)[u];
+            raw[i][w][u] = ld_stream(reinterpret_cast<const i32x4*>(qkv + row[i] * ldq + w * D + c8) + u);
       }
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
       if (row[i] < 0) break;
-      const int64_t f = row[i] / seq, p = row[i] - f * seq;
+      const uint32_t f = (uint32_t)row[i] / (uint32_t)seq, p = (uint32_t)row[i] - f * (uint32_t)seq;
       float v[3][8], r[2][8];
 #pragma unroll
       for (int w = 0; w < 3; ++w) ld8<T>(reinterpret_cast<const T*>(raw[i][w]), v[w]);
@@ -300,7 +303,7 @@ __global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t 
       for (int w = 0; w < 2; ++w)
 #pragma unroll
         for (int e = 0; e < 8; ++e) r[w][e] = v[w][e] * c[e] + v[w][e ^ 1] * s[e];
-      const int64_t off = MODE == 0 ? ((f * H + h) * seq + p) * 64 + d0 : row[i] * D + c8;
+      const int64_t off = MODE == 0 ? (((int64_t)f * H + h) * seq + p) * 64 + d0 : row[i] * D + c8;
       st8<T>(qo + off, r[0]);
       st8<T>(ko + off, r[1]);
       st8<T>(vo + off, v[2]);
@@ -427,7 +430,8 @@ extern "C" int oasis_rope_layout(const void* qkv, int64_t ld_qkv, const float* c
   OASIS_REQUIRE(oasis_aligned(16, qkv, q_out, k_out, v_out, cos, sinp) && (ld_qkv * esz) % 16 == 0 && tab_ld % 4 == 0 &&
                     tab_head_stride % 4 == 0,
                 OASIS_ERR_ARG, "rope_layout: pointers, ld_qkv rows and table strides must be 16-byte aligned");
-  OASIS_REQUIRE(rows < (1ll << 31), OASIS_ERR_SHAPE, "rope_layout: too many rows");
+  OASIS_REQUIRE(rows < (1ll << 31) && pos_div < (1ll << 31) && seq < (1ll << 31), OASIS_ERR_SHAPE,
+                "rope_layout: rows, pos_div and seq must be below 2^31");
   hipStream_t s = static_cast<hipStream_t>(stream);
   // rows per table position, then workgroups of up to RPG of them per position
   const int64_t per_pos = ((rows + pos_mod * pos_div - 1) / (pos_mod * pos_div)) * pos_div;

@@ -3,7 +3,7 @@
 //
 // This is pure weight streaming (the adaLN matrices of all sub-blocks are 406 MB of
 // bf16 per DiT step against ~0.8 GFLOP), so the kernel is shaped around HBM:
-//   - W rows are read as 16-byte vectors straight into MFMA A operands
+//   - W rows are read as 16-byte streaming vectors straight into MFMA A operands
 //     (v_mfma_f32_16x16x32_bf16, 16 weight rows x 32 k per instruction), two k-steps
 //     per 128-byte cache line and several k-steps in flight per wave;
 //   - x (16 rows per row group, one or two groups) is staged once per workgroup in LDS as a
@@ -82,8 +82,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
       for (int u = 0; u < UNROLL; ++u) {
         const int kk = k0 + u * KSTEP;
         if (kk < kend) {
-          w[u][0] = *reinterpret_cast<const bf16x8*>(wp + kk);
-          w[u][1] = *reinterpret_cast<const bf16x8*>(wp + kk + 32);
+          w[u][0] = ld_stream(reinterpret_cast<const bf16x8*>(wp + kk));
+          w[u][1] = ld_stream(reinterpret_cast<const bf16x8*>(wp + kk + 32));
         }
       }
 #pragma unroll

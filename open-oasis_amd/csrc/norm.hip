@@ -27,11 +27,11 @@ template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
 template <>
 __device__ __forceinline__ void store4<float>(float* p, const float* v) {
-  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  st_stream(reinterpret_cast<f32x4*>(p), f32x4{v[0], v[1], v[2], v[3]});
 }
 template <>
 __device__ __forceinline__ void store4<bf16>(bf16* p, const float* v) {
-  *reinterpret_cast<bf16x4*>(p) = bf16x4{f2bf(v[0]), f2bf(v[1]), f2bf(v[2]), f2bf(v[3])};
+  st_stream(reinterpret_cast<bf16x4*>(p), bf16x4{f2bf(v[0]), f2bf(v[1]), f2bf(v[2]), f2bf(v[3])});
 }
 
 // mode 0: modulate with per-frame (shift, scale_p1); mode 1: affine (w, b) with row stride.
@@ -87,6 +87,8 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
 
 // The same LayerNorm with 16-byte accesses for D % 512 == 0: lane l holds columns
 // v*512 + 8l .. v*512 + 8l + 7 of each 512-wide chunk v (one 16-byte bf16 vector, or two fp32).
+// bf16 rows are read with streaming loads. Every kernel in this file writes its outputs with
+// streaming stores.
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* v);
 template <>
@@ -96,7 +98,7 @@ __device__ __forceinline__ void load8<float>(const float* p, float* v) {
 }
 template <>
 __device__ __forceinline__ void load8<bf16>(const bf16* p, float* v) {
-  unpack8(*reinterpret_cast<const bf16x8*>(p), v);
+  unpack8(ld_stream(reinterpret_cast<const bf16x8*>(p)), v);
 }
 template <typename T>
 __device__ __forceinline__ void store8(T* p, const float* v);
@@ -107,7 +109,7 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
 }
 template <>
 __device__ __forceinline__ void store8<bf16>(bf16* p, const float* v) {
-  *reinterpret_cast<bf16x8*>(p) = pack8(v);
+  st_stream(reinterpret_cast<bf16x8*>(p), pack8(v));
 }
 
 template <int NV, typename TIn, typename TOut, int MODE>

@@ -99,6 +99,15 @@ OASIS_DEV void unpack8(bf16x8 p, float* v) {
   for (int i = 0; i < 8; ++i) v[i] = bf2f(p[i]);
 }
 
+// ---- streaming accesses -----------------------------------------------------
+// Non-temporal vector loads and stores (the `nt` cache policy): for data a kernel touches once.
+// A streamed store leaves the L2 early instead of waiting, dirty, for the write-back at the
+// kernel's end, so a memory-bound kernel's writes overlap its reads.
+template <typename V>
+OASIS_DEV void st_stream(V* p, V v) { __builtin_nontemporal_store(v, p); }
+template <typename V>
+OASIS_DEV V ld_stream(const V* p) { return __builtin_nontemporal_load(p); }
+
 // ---- wave reductions (64 lanes) ---------------------------------------------
 OASIS_DEV float wave_sum(float v) {
 #pragma unroll

@@ -760,9 +760,8 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
                 OASIS_ERR_NULL, "video_frames: null pointer");
   OASIS_REQUIRE(n_frames > 0 && n_frames <= OASIS_MAX_SUB, OASIS_ERR_ARG, "video_frames: n_frames must be in [1, %d]",
                 OASIS_MAX_SUB);
-  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, C = w->patch_dim / 4, NA = ada_width(w);
+  const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w, NA = ada_width(w);
   const int64_t R = 1 + n_steps, fsz = (int64_t)w->patch_dim * P;
-  const int64_t frame_elems = 3LL * vw->grid_h * vw->patch * vw->grid_w * vw->patch;
   hipStream_t s = (hipStream_t)stream;
   // every frame's conditioning rows at once: frame f's rows at f*R (context, then step i)
   OASIS_TRY(cond_mlp(w, t, action, n_frames * R, hid, cond, stream));
