@@ -443,6 +443,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
     compute(k % STAGES);
   }
   __builtin_amdgcn_s_waitcnt(0);
+
+  // The epilogue gives lane l the 8 columns 8 * ((l + 64 q) % UPR) of its wave's tile in pass q,
+  // for every row: their bias is fetched once, here (a load per stored row would put a memory
+  // round trip into every pass), and lands while the tables and first rows are staged.
+  constexpr int UPR = TN / 8;
+  constexpr int NBQ = (64 % UPR) == 0 ? 1 : 2;  // distinct column sets among the passes (TN <= 64)
+  static_assert(UPR <= 8, "two passes per 16-row group at most");
+  const bool add_bias = e.bias && e.kind != OASIS_EPI_PARTIAL_F32;
+  f32x4 hb[NBQ][2];
+#pragma unroll
+  for (int q = 0; q < NBQ; ++q) {
+    const int gn = min(n0 + wn * TN + ((lane + 64 * q) % UPR) * 8, N - 8);
+    hb[q][0] = hb[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (add_bias) {
+      hb[q][0] = *reinterpret_cast<const f32x4*>(e.bias + gn);
+      hb[q][1] = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
+    }
+  }
   __syncthreads();
 
   // QKV rotation tables to LDS (above the epilogue staging) when they fit
@@ -456,7 +474,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
   // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
   // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
-  constexpr int UPR = TN / 8;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -477,8 +494,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
           *reinterpret_cast<f32x4*>(d) = c0;
           *reinterpret_cast<f32x4*>(d + 4) = c1;
         } else {
-          float v[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows);
+          const bool q1 = NBQ > 1 && u >= 64;
+          const f32x4 b0 = q1 ? hb[NBQ - 1][0] : hb[0][0], b1 = q1 ? hb[NBQ - 1][1] : hb[0][1];
+          float v[8] = {c0[0] + b0[0], c0[1] + b0[1], c0[2] + b0[2], c0[3] + b0[3],
+                        c1[0] + b1[0], c1[1] + b1[1], c1[2] + b1[2], c1[3] + b1[3]};
+          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false);
         }
       }
     }

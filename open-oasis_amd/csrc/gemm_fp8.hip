@@ -52,6 +52,17 @@ __device__ __forceinline__ uint2 quant8(i32x4 raw, int* sbyte) {
                     pack4_fp8(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv));
 }
 
+// v = c * s + b (weight channel scale, then bias) with the product rounded before the sum (no
+// fused multiply-add), the same in every fp8 kernel, so all fp8 tiles give bit-identical outputs.
+__device__ __forceinline__ void scale_bias8(f32x4 c0, f32x4 c1, f32x4 s0, f32x4 s1, f32x4 b0, f32x4 b1, float* v) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = c0[j] * s0[j] + b0[j];
+    v[j + 4] = c1[j] * s1[j] + b1[j];
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, bool AQ>
 __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ Av, int64_t lda,
                                                        const uint8_t* __restrict__ Ascale, int64_t lds,
@@ -212,18 +223,19 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
     const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + r * C_PITCH + c8 + 4);
     const f32x4 s0 = *reinterpret_cast<const f32x4*>(wscale + gn);
     const f32x4 s1 = *reinterpret_cast<const f32x4*>(wscale + gn + 4);
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[j] = c0[j] * s0[j];
-      v[j + 4] = c1[j] * s1[j];
+    f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (e.bias && e.kind != OASIS_EPI_PARTIAL_F32) {
+      b0 = *reinterpret_cast<const f32x4*>(e.bias + gn);
+      b1 = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
     }
+    float v[8];
+    scale_bias8(c0, c1, s0, s1, b0, b1, v);
     if (e.kind == OASIS_EPI_PARTIAL_F32) {
       float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
       *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
       *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
     } else {
-      epilogue8(e, gm, gn, v);
+      epilogue8(e, gm, gn, v, nullptr, 0, false);
     }
   }
 }
@@ -330,6 +342,26 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
     compute(k & 1);
   }
   __builtin_amdgcn_s_waitcnt(0);
+
+  // lane l stores the 8 columns 8 * ((l + 64 q) % UPR) of its wave's tile in pass q, for every
+  // row: their weight scales and bias are fetched once, here, and land while the tables and the
+  // first rows are staged
+  constexpr int UPR = TN / 8;
+  constexpr int NBQ = (64 % UPR) == 0 ? 1 : 2;  // distinct column sets among the passes (TN <= 64)
+  static_assert(UPR <= 8, "two passes per 16-row group at most");
+  const bool add_bias = e.bias && e.kind != OASIS_EPI_PARTIAL_F32;
+  f32x4 hs[NBQ][2], hb[NBQ][2];
+#pragma unroll
+  for (int q = 0; q < NBQ; ++q) {
+    const int gn = min(n0 + wn * TN + ((lane + 64 * q) % UPR) * 8, N - 8);
+    hs[q][0] = *reinterpret_cast<const f32x4*>(wscale + gn);
+    hs[q][1] = *reinterpret_cast<const f32x4*>(wscale + gn + 4);
+    hb[q][0] = hb[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (add_bias) {
+      hb[q][0] = *reinterpret_cast<const f32x4*>(e.bias + gn);
+      hb[q][1] = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
+    }
+  }
   __syncthreads();
 
   // QKV rotation tables to LDS (above the epilogue staging) when they fit
@@ -342,7 +374,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   // lanes 4i..4i+3 cover one aligned 32-column block when TN % 32 == 0 (the host checks it for
   // the GELU_TANH_FP8 epilogue)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
-  constexpr int UPR = TN / 8;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -358,20 +389,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
       if (gm < M && gn < N) {
         const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
         const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(wscale + gn);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(wscale + gn + 4);
+        const bool q1 = NBQ > 1 && u >= 64;
+        const f32x4 s0 = q1 ? hs[NBQ - 1][0] : hs[0][0], s1 = q1 ? hs[NBQ - 1][1] : hs[0][1];
+        const f32x4 b0 = q1 ? hb[NBQ - 1][0] : hb[0][0], b1 = q1 ? hb[NBQ - 1][1] : hb[0][1];
         float v[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = c0[j] * s0[j];
-          v[j + 4] = c1[j] * s1[j];
-        }
+        scale_bias8(c0, c1, s0, s1, b0, b1, v);
         if (e.kind == OASIS_EPI_PARTIAL_F32) {
           float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
           *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
           *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
         } else {
-          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows);
+          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false);
         }
       }
     }
