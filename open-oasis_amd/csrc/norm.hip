@@ -27,11 +27,11 @@ template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
 template <>
 __device__ __forceinline__ void store4<float>(float* p, const float* v) {
-  st_stream(reinterpret_cast<f32x4*>(p), f32x4{v[0], v[1], v[2], v[3]});
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
 }
 template <>
 __device__ __forceinline__ void store4<bf16>(bf16* p, const float* v) {
-  st_stream(reinterpret_cast<bf16x4*>(p), bf16x4{f2bf(v[0]), f2bf(v[1]), f2bf(v[2]), f2bf(v[3])});
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{f2bf(v[0]), f2bf(v[1]), f2bf(v[2]), f2bf(v[3])};
 }
 
 // mode 0: modulate with per-frame (shift, scale_p1); mode 1: affine (w, b) with row stride.
@@ -87,8 +87,9 @@ __global__ __launch_bounds__(256) void ln_kernel(const TIn* __restrict__ x, int6
 
 // The same LayerNorm with 16-byte accesses for D % 512 == 0: lane l holds columns
 // v*512 + 8l .. v*512 + 8l + 7 of each 512-wide chunk v (one 16-byte bf16 vector, or two fp32).
-// bf16 rows are read with streaming loads. Every kernel in this file writes its outputs with
-// streaming stores.
+// Rows are read and written with streaming accesses (this kernel serves the reference-surface
+// LayerNorm and the VAE's first LN; the step's residual + LN kernels below keep plain stores,
+// whose output the next GEMM reads: measured no faster streamed).
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* v);
 template <>
@@ -104,8 +105,8 @@ template <typename T>
 __device__ __forceinline__ void store8(T* p, const float* v);
 template <>
 __device__ __forceinline__ void store8<float>(float* p, const float* v) {
-  store4<float>(p, v);
-  store4<float>(p + 4, v + 4);
+  st_stream(reinterpret_cast<f32x4*>(p), f32x4{v[0], v[1], v[2], v[3]});
+  st_stream(reinterpret_cast<f32x4*>(p + 4), f32x4{v[4], v[5], v[6], v[7]});
 }
 template <>
 __device__ __forceinline__ void store8<bf16>(bf16* p, const float* v) {
