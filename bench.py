@@ -511,11 +511,11 @@ def main():
     fc1_ai = fc1_flop / fc1_bytes
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     fc1_gbs = fc1_bytes / (fc1_ms * 1e-3) / 1e9
-    fc1_roofline = {"kernel": "gemm_wave_kernel<96,64,2,4,GELU_TANH> (bf16 MFMA GEMM, 4 waves splitting K, each over "
-                              "its own direct-to-LDS ring), FC1 projection + bias + "
-                              "tanh-GELU (M=288, N=4096, K=1024), the largest of the step's 128 projections (4 per sub-block; the 16 temporal QKVs run fused with their attention); "
-                              "launch i uses sub-block i % 32's weights (cold, as in the step); 100 launches in "
-                              "one hipGraph"}
+    fc1_roofline = {"kernel": "gemm_wave_kernel<80,64,2,4,GELU_TANH,72> (bf16 MFMA GEMM, 4 waves splitting K, each "
+                              "over its own direct-to-LDS ring; 80-row tiles every 72 rows, 256 workgroups), FC1 "
+                              "projection + bias + tanh-GELU (M=288, N=4096, K=1024), the largest of the step's 128 "
+                              "projections (4 per sub-block); launch i uses sub-block i % 32's weights (cold, as in "
+                              "the step); 100 launches in one hipGraph"}
     if fc1_ai < ridge:
         fc1_roofline.update({"bound": "hbm", "achieved": round(fc1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(fc1_gbs / HBM_PEAK_GBS, 4)})

@@ -521,7 +521,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int BM, int BN, int STG, int NK, int KIND>
+template <int BM, int BN, int STG, int NK, int KIND, int BMS>
 __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__ A, int64_t lda,
                                                         const bf16* __restrict__ B, int64_t ldb, int M, int N,
                                                         int K, int splits, Epi e) {
@@ -538,13 +538,14 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   constexpr int RED_BYTES = NW * BM * PITCH * 4;
   constexpr int SMEM = NW * WAVE_BYTES > RED_BYTES ? NW * WAVE_BYTES : RED_BYTES;
   static_assert(SMEM <= 160 * 1024, "LDS");
+  static_assert(BMS <= BM, "row step within the tile");
   constexpr int UPR = BN / 8;                      // 8-column epilogue units per row
-  constexpr int UNITS = BM * UPR;
+  constexpr int UNITS = BMS * UPR;                 // the tile's first BMS rows are stored
   constexpr int UPT = (UNITS + 255) / 256;         // units per thread
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
   // work id -> (split, n tile, m tile), m fastest and the split outermost: an XCD's contiguous
   // range of ids covers the M tiles of a few weight slices of one K slice, so its L2 fetches
   // one K slice of A rather than all of them
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   const int split = pid / (Mt * Nt);
   const int t = pid - split * (Mt * Nt);
   const int nt = t / Mt, mt = t - nt * Mt;
-  const int m0 = mt * BM, n0 = nt * BN;
+  const int m0 = mt * BMS, n0 = nt * BN;
   constexpr int nk = NK;                           // K tiles per wave: K = 256 NK splits (host-checked)
   const int kb = (split * NW + wave) * nk * 64;
   char* ring = smem + wave * WAVE_BYTES;
@@ -687,41 +688,44 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
 // The K loop is unrolled for 1, 2, 4 or 8 K tiles per wave (K / splits = 256, 512, 1024, 2048); the
 // split-K, GELU and QKV + RoPE epilogues of 2 or 4 tiles per wave (the step's and the VAE's
 // projections) get kernels of their own.
-template <int BM, int BN, int STG, int NK>
+template <int BM, int BN, int STG, int NK, int BMS>
 void launch_wave_nk(const dim3& grid, const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K,
                     int splits, const Epi& e, hipStream_t s) {
   const dim3 block(256);
   if (NK == 2 || NK == 4) {
     switch (e.kind) {
       case OASIS_EPI_PARTIAL_F32:
-        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_PARTIAL_F32>), grid, block, 0, s, A, lda, B,
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_PARTIAL_F32, BMS>), grid, block, 0, s, A, lda, B,
                            ldb, M, N, K, splits, e);
         return;
       case OASIS_EPI_GELU_TANH:
-        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_GELU_TANH>), grid, block, 0, s, A, lda, B, ldb,
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_GELU_TANH, BMS>), grid, block, 0, s, A, lda, B, ldb,
                            M, N, K, splits, e);
         return;
       case OASIS_EPI_QKV_ROPE:
-        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_QKV_ROPE>), grid, block, 0, s, A, lda, B, ldb,
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_QKV_ROPE, BMS>), grid, block, 0, s, A, lda, B, ldb,
                            M, N, K, splits, e);
         return;
       default:
         break;
     }
   }
-  hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, -1>), grid, block, 0, s, A, lda, B, ldb, M, N, K, splits, e);
+  hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, -1, BMS>), grid, block, 0, s, A, lda, B, ldb, M, N, K, splits, e);
 }
 
-template <int BM, int BN, int STG>
+// BMS < BM: tiles start every BMS rows and compute BM (the last BM - BMS rows, which the next tile
+// owns, are not stored), so that a row count such as 288 = 4 x 72 splits into whole 16-row MFMA
+// blocks over more workgroups
+template <int BM, int BN, int STG, int BMS = BM>
 hipError_t launch_wave(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
                        const Epi& e, hipStream_t s) {
-  const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
+  const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
   const dim3 grid(Mt * Nt * splits);
   switch ((K / splits) % 256 == 0 ? K / splits / 256 : 0) {
-    case 1: launch_wave_nk<BM, BN, STG, 1>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
-    case 2: launch_wave_nk<BM, BN, STG, 2>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
-    case 4: launch_wave_nk<BM, BN, STG, 4>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
-    case 8: launch_wave_nk<BM, BN, STG, 8>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 1: launch_wave_nk<BM, BN, STG, 1, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 2: launch_wave_nk<BM, BN, STG, 2, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 4: launch_wave_nk<BM, BN, STG, 4, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
+    case 8: launch_wave_nk<BM, BN, STG, 8, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
     default: return hipErrorInvalidConfiguration;
   }
   return hipGetLastError();
@@ -784,7 +788,9 @@ const TileCfg kTiles[] = {
     {288, 128, launch_big<288, 128, 2, 4, 2>},              // 7
     // wave-split K, 4 waves on one tile, each wave's K tiles in its own 2-deep LDS ring (K slices of
     // 256 x 1, 2, 4 or 8; not used for the fp8-block GELU epilogue)
-    {96, 64, launch_wave<96, 64, 2>, 1, 256, 2048},                       // 8
+    // 8: 80-row tiles every 72 rows: 288 tokens as 4 row blocks, so FC1 (64 weight slices) and FC2
+    // (16 slices x 4 K slices) run 256 workgroups, one per CU, instead of 192 on 96-row tiles
+    {72, 64, launch_wave<80, 64, 2, 72>, 1, 256, 2048},
     {48, 32, launch_wave<48, 32, 2>, 1, 256, 2048},                       // 9
     {48, 64, launch_wave<48, 64, 2>, 1, 256, 2048},                       // 10
     {64, 64, launch_wave<64, 64, 2>, 1, 256, 2048},                       // 11
@@ -800,7 +806,8 @@ namespace oasis {
 // of 100 launches over rotating weight sets):
 //   - 2048+ tokens: the 8-wave tall tiles, the width that fills the last round of 256 workgroups best;
 //   - below, where the K slice suits the wave-split kernel (256, 512, 1024 or 2048 long):
-//       FC1 (GELU): 48 x 64 (tile 10) at one 144-token frame, 96 x 64 (tile 8) up to 320 tokens;
+//       FC1 (GELU): 48 x 64 (tile 10) at one 144-token frame, 80-row tiles every 72 rows x 64
+//       (tile 8) up to 320 tokens (8.51 us at 288 against 9.36 on 96 x 64 tiles);
 //       split-K partials of K <= 1024 (O): 48 x 32 (tile 9) up to 320 tokens, 48 x 64 (tile 10) above;
 //       split-K partials of longer K (FC2): tile 10 at one frame, tile 8 up to 320 tokens;
 //       other epilogues (QKV + RoPE): 32 x 64 (tile 12) at one frame, 64 x 64 (tile 11) up to 320;

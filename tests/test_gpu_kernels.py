@@ -564,8 +564,8 @@ def test_gemm_direct_lds_ragged(tile):
 
 @pytest.mark.parametrize("tile", list(range(8, 13)))
 def test_gemm_wave_tiles_ragged(tile):
-    """The wave-split tiles (8-12: four waves split each K slice, each over its own LDS ring) on a
-    ragged shape (M and N not multiples of the tile) with every K-loop length they unroll: GELU
+    """The wave-split tiles (8-12: four waves split each K slice, each over its own LDS ring; 8
+    computes 80-row tiles every 72 rows) on a ragged shape (M and N not multiples of the tile) with every K-loop length they unroll: GELU
     with K = 1024 (4 K tiles per wave, the GELU kernel), split-K x2 of K = 1024 (2 tiles, the
     split-K kernel), one K = 2048 slice (8 tiles) and K = 256 (1 tile, the generic kernel); K
     slices that are not 256 x a power of two are refused."""
