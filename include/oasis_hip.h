@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define OASIS_ABI_VERSION 3
+#define OASIS_ABI_VERSION 4
 #define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
 
 enum {
@@ -298,6 +298,16 @@ int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64
                     int64_t K, const float* b, float* out, int64_t ld_out, int act_in,
                     int act_out, int accumulate, oasis_stream_t stream);
 
+/* Same product with W in 16-row MFMA tile order: for tile t (rows 16t..16t+15) and each
+ * 32-wide K step s, 64 pieces of 8 bf16 back to back, piece l holding row 16t + (l & 15),
+ * columns 32s + 8(l >> 4) .. +7 (tile t, step s at element offset (t*K/32 + s)*512). Each
+ * wave's weight loads are then 1 KB contiguous. The DiT's stacked adaLN weights (ada_w of
+ * oasis_dit_weights_t) are kept in this order. No counterpart in the reference: a storage
+ * order of the adaLN projections' weights (oasis_inference.py:983-993). */
+int oasis_gemv_bf16_tiled(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N,
+                          int64_t K, const float* b, float* out, int64_t ld_out, int act_in,
+                          int act_out, int accumulate, oasis_stream_t stream);
+
 /* The same product with fp32 weights and fp32 arithmetic throughout:
  * out[r, n] (+)= act_out(sum_k act_in(x[r, k]) W[n, k] + b[n]), W fp32 [N, K] (K % 4 == 0,
  * K <= 4096), R <= 1024. act_in = OASIS_ACT_TEMB: x is fp32 [R, ldx] with one timestep per
@@ -346,7 +356,8 @@ int oasis_vae_unpatchify(const float* patches, float* frame, int64_t gh, int64_t
 /* Device pointers of one DiT ([out, in] weights; biases and tables fp32).
  * Sub-block j = 2*i + (0 spatial | 1 temporal) of block i.
  * ada_w/ada_b (bf16 / fp32) hold every sub-block's adaLN projection back to back: rows
- * [j*6D, (j+1)*6D) for sub-block j, with +1 folded into the bias of each scale chunk.
+ * [j*6D, (j+1)*6D) for sub-block j, with +1 folded into the bias of each scale chunk; ada_w is
+ * stored in the 16-row tile order of oasis_gemv_bf16_tiled.
  * The pieces the reference keeps in fp32 are fp32 here too: the conditioning MLP and action
  * projection (oasis_inference.py:512-520), the patch embed W_rt (1821-1826), and the final
  * layer's adaLN and linear (527-532). The adaLN rows of all consumers go to one buffer of
@@ -360,7 +371,7 @@ typedef struct {
   int patch_dim;             /* 64 = 2*2*16                                        */
   int freq_dim;              /* 256                                                */
   int ext_dim_pad;           /* 64 (25 action dims zero-padded)                    */
-  const void* ada_w;         /* [n_sub*6D, D] bf16                                 */
+  const void* ada_w;         /* [n_sub*6D, D] bf16, 16-row tile order              */
   const float* ada_b;        /* [n_sub*6D]                                         */
   const float* final_ada_w;  /* [2D, D] fp32: shift, scale                         */
   const float* final_ada_b;  /* [2D], +1 folded into the scale half                */

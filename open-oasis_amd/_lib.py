@@ -17,7 +17,7 @@ EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32, EPI_GELU_TANH_FP8 = 8, 9
 ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
@@ -122,6 +122,7 @@ SIGNATURES = {
     "oasis_temporal_qkv_attention": [c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_f,
                                      c_p],
     "oasis_gemv_bf16": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
+    "oasis_gemv_bf16_tiled": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
     "oasis_gemv_f32": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
     "oasis_timestep_embedding": [c_p, c_i64, c_i64, c_p, c_p],
     "oasis_small_linear": [c_p, c_i64, c_i64, c_i64, c_p, c_i, c_i, c_i64, c_p, c_p, c_i64, c_p],

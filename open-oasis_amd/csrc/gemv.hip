@@ -23,7 +23,10 @@ namespace {
 constexpr int KSTEP = 64;   // k per pipeline step (two MFMAs)
 constexpr int UNROLL = 4;   // pipeline steps whose loads are issued together
 
-template <int RG, int KS>
+// TILED: W in 16-row MFMA tile order (for tile t and 32-wide K step s, the 64 lanes' 16-byte
+// pieces back to back, lane l holding row 16t + (l & 15), columns 32s + 8(l >> 4) .. +7), so a
+// wave's load instruction reads 1 KB contiguous; else row-major [N, K].
+template <int RG, int KS, bool TILED>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, int R,
                                                    const bf16* __restrict__ W, int N, int K,
                                                    const float* __restrict__ b, float* __restrict__ out,
@@ -71,7 +74,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     const int tile = tile0 + wave / KS;
     const bool has_tile = tile < tiles;
     if (KS == 1 && !has_tile) continue;  // no barriers to keep in step with
-    const bf16* wp = W + ((int64_t)(has_tile ? tile : 0) * 16 + lr) * K + g * 8;
+    const int tl = has_tile ? tile : 0;
+    // row-major: row 16 tl + lr, columns 8g + kk; tiled: step kk / 32 of tile tl at 512 elements each
+    const bf16* wp = TILED ? W + ((int64_t)tl * (K / 32) * 64 + lane) * 8 : W + ((int64_t)tl * 16 + lr) * K + g * 8;
     f32x4 acc[RG];
 #pragma unroll
     for (int q = 0; q < RG; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -82,8 +87,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
       for (int u = 0; u < UNROLL; ++u) {
         const int kk = k0 + u * KSTEP;
         if (kk < kend) {
-          w[u][0] = ld_stream(reinterpret_cast<const bf16x8*>(wp + kk));
-          w[u][1] = ld_stream(reinterpret_cast<const bf16x8*>(wp + kk + 32));
+          const bf16* p0 = TILED ? wp + (kk / 32) * 512 : wp + kk;
+          const bf16* p1 = TILED ? p0 + 512 : wp + kk + 32;
+          w[u][0] = ld_stream(reinterpret_cast<const bf16x8*>(p0));
+          w[u][1] = ld_stream(reinterpret_cast<const bf16x8*>(p1));
         }
       }
 #pragma unroll
@@ -142,9 +149,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
 
 }  // namespace
 
-extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N, int64_t K,
-                               const float* b, float* out, int64_t ld_out, int act_in, int act_out, int accumulate,
-                               oasis_stream_t stream) {
+namespace {
+
+int gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N, int64_t K, const float* b,
+              float* out, int64_t ld_out, int act_in, int act_out, int accumulate, bool tiled, oasis_stream_t stream) {
   OASIS_REQUIRE(x && W && out, OASIS_ERR_NULL, "gemv: null pointer");
   OASIS_REQUIRE(oasis_aligned(16, W), OASIS_ERR_ARG, "gemv: W must be 16-byte aligned");
   OASIS_REQUIRE(R > 0 && R <= 1024, OASIS_ERR_SHAPE, "gemv: R=%lld must be in [1, 1024]", (long long)R);
@@ -159,8 +167,8 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   // one pass over W per 32 rows (two 16-row groups) while x fits in LDS, else per 16 rows
   const int per_pass = 2 * 32 * (K + 8) * (int64_t)sizeof(bf16) <= 160 * 1024 ? 32 : 16;
   for (int64_t r0 = per_pass; r0 < R; r0 += per_pass) {
-    const int rc = oasis_gemv_bf16(x + r0 * ldx, ldx, R - r0 < per_pass ? R - r0 : per_pass, W, N, K, b,
-                                   out + r0 * ld_out, ld_out, act_in, act_out, accumulate, stream);
+    const int rc = gemv_bf16(x + r0 * ldx, ldx, R - r0 < per_pass ? R - r0 : per_pass, W, N, K, b,
+                             out + r0 * ld_out, ld_out, act_in, act_out, accumulate, tiled, stream);
     if (rc != OASIS_OK) return rc;
   }
   if (R > per_pass) R = per_pass;
@@ -179,7 +187,10 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   int blocks = (tiles + per_block - 1) / per_block;
   blocks = std::min(std::min(blocks, 2048), std::max(1, resident) * 256 * 2);
   const void* fn = nullptr;
-#define OASIS_GEMV_FN(RGV, KSV) if (rg == RGV && ks == KSV) fn = reinterpret_cast<const void*>(&gemv_kernel<RGV, KSV>)
+#define OASIS_GEMV_FN(RGV, KSV)                                                                                   \
+  if (rg == RGV && ks == KSV)                                                                                     \
+  fn = tiled ? reinterpret_cast<const void*>(&gemv_kernel<RGV, KSV, true>)                                        \
+             : reinterpret_cast<const void*>(&gemv_kernel<RGV, KSV, false>)
   OASIS_GEMV_FN(1, 1);
   OASIS_GEMV_FN(1, 2);
   OASIS_GEMV_FN(1, 4);
@@ -198,9 +209,14 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   const bf16* Wb = static_cast<const bf16*>(W);
   const int Ri = (int)R, Ni = (int)N, Ki = (int)K;
 #define OASIS_GEMV_GO(RGV, KSV)                                                                                   \
-  if (rg == RGV && ks == KSV)                                                                                     \
-  hipLaunchKernelGGL((gemv_kernel<RGV, KSV>), dim3(blocks), dim3(256), smem, s, x, ldx, Ri, Wb, Ni, Ki, b, out,   \
-                     ld_out, act_in, act_out, accumulate)
+  if (rg == RGV && ks == KSV) {                                                                                   \
+    if (tiled)                                                                                                    \
+      hipLaunchKernelGGL((gemv_kernel<RGV, KSV, true>), dim3(blocks), dim3(256), smem, s, x, ldx, Ri, Wb, Ni, Ki, \
+                         b, out, ld_out, act_in, act_out, accumulate);                                            \
+    else                                                                                                          \
+      hipLaunchKernelGGL((gemv_kernel<RGV, KSV, false>), dim3(blocks), dim3(256), smem, s, x, ldx, Ri, Wb, Ni,    \
+                         Ki, b, out, ld_out, act_in, act_out, accumulate);                                        \
+  }
   OASIS_GEMV_GO(1, 1);
   OASIS_GEMV_GO(1, 2);
   OASIS_GEMV_GO(1, 4);
@@ -209,6 +225,20 @@ extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const voi
   OASIS_GEMV_GO(2, 4);
 #undef OASIS_GEMV_GO
   return oasis::check_launch("gemv");
+}
+
+}  // namespace
+
+extern "C" int oasis_gemv_bf16(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N, int64_t K,
+                               const float* b, float* out, int64_t ld_out, int act_in, int act_out, int accumulate,
+                               oasis_stream_t stream) {
+  return gemv_bf16(x, ldx, R, W, N, K, b, out, ld_out, act_in, act_out, accumulate, false, stream);
+}
+
+extern "C" int oasis_gemv_bf16_tiled(const float* x, int64_t ldx, int64_t R, const void* W, int64_t N, int64_t K,
+                                     const float* b, float* out, int64_t ld_out, int act_in, int act_out,
+                                     int accumulate, oasis_stream_t stream) {
+  return gemv_bf16(x, ldx, R, W, N, K, b, out, ld_out, act_in, act_out, accumulate, true, stream);
 }
 
 // ---------------------------------------------------------------------------------------

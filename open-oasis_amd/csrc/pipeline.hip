@@ -189,7 +189,8 @@ int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, 
 // final layer's (fp32 weights) at column n_sub*6D
 int adaln_rows(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, hipStream_t s) {
   const int64_t D = w->d_model, NA = ada_width(w), NS = (int64_t)w->n_sub * 6 * D;
-  OASIS_TRY(oasis_gemv_bf16(cond, D, R, w->ada_w, NS, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0, s));
+  OASIS_TRY(oasis_gemv_bf16_tiled(cond, D, R, w->ada_w, NS, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
+                                  s));
   return oasis_gemv_f32(cond, D, R, w->final_ada_w, 2 * D, D, w->final_ada_b, ada + NS, NA, OASIS_ACT_SILU,
                         OASIS_ACT_NONE, 0, s);
 }

@@ -7,8 +7,9 @@ points of liboasis_hip.so on a torch-ROCm stream.
 
 HBM layout (nn.Linear [out, in] weights, fp32 biases/tables):
   - ``ada_w`` (bf16): every sub-block's adaLN projection stacked, [n_sub*6D, D] (403 MB at
-    Oasis-500M). One skinny-GEMM pass over it produces the adaLN rows of all 32 sub-blocks
-    for every conditioning row at once.
+    Oasis-500M), in the 16-row MFMA tile order of ``oasis_gemv_bf16_tiled`` (``tile_rows16``),
+    so each wave of the skinny GEMM streams 1 KB contiguous per load. One pass over it produces
+    the adaLN rows of all 32 sub-blocks for every conditioning row at once.
   - per sub-block (bf16): qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
     contiguous (37.7 MB of the 1.21 GB weight set per sub-block incl. adaLN).
   - fp32, as the reference keeps them (oasis_inference.py:512-532,1821-1826): the
@@ -24,6 +25,21 @@ import torch
 from . import _lib as L
 
 HEAD_DIM = 64
+
+
+def tile_rows16(W):
+    """[N, K] -> the 16-row MFMA tile order of oasis_gemv_bf16_tiled (same shape, [N, K]): for
+    tile t and 32-wide K step s, 64 pieces of 8 values, piece l = row 16t + (l % 16), columns
+    32s + 8(l // 16) .. +7."""
+    N, K = W.shape
+    assert N % 16 == 0 and K % 32 == 0
+    return W.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(N, K).contiguous()
+
+
+def untile_rows16(Wt):
+    """Inverse of tile_rows16."""
+    N, K = Wt.shape
+    return Wt.reshape(N // 16, K // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(N, K).contiguous()
 
 
 def _count(w, pattern):
@@ -114,7 +130,7 @@ class DiT:
                 b[4 * d:5 * d] += 1.0
                 bs.append(b)
         self.ada_width = self.n_sub * 6 * d + 2 * d   # adaLN row width: every sub-block, then the final layer
-        self.ada_w = put(torch.cat([x.to(bf) for x in ws], 0), bf)
+        self.ada_w = put(tile_rows16(torch.cat([x.to(bf) for x in ws], 0)), bf)
         self.ada_b = put(torch.cat(bs, 0), f32)
         del ws, bs
         fb = w["final.ada_b"].float().clone()
@@ -186,6 +202,11 @@ class DiT:
     def weight_bytes(self):
         return sum(t.numel() * t.element_size() for t in self._keep)
 
+    def ada_w_rows(self):
+        """The stacked adaLN weights in row-major [n_sub*6D, D] order (a copy; the device keeps
+        them in tile order)."""
+        return untile_rows16(self.ada_w)
+
     def workspace(self, max_rows, max_cond=16, max_splits=None):
         return DiTWorkspace(self, max_rows, max_cond, max_splits)
 
@@ -213,7 +234,7 @@ class DiT:
         ws.cond[:R].copy_(cond)
         ns = self.n_sub * 6 * self.d
         h = L.stream_handle(stream)
-        L.call("oasis_gemv_bf16", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), ns, self.d,
+        L.call("oasis_gemv_bf16_tiled", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), ns, self.d,
                L.ptr(self.ada_b), L.ptr(ws.ada), self.ada_width, L.ACT_SILU, L.ACT_NONE, 0, h)
         L.call("oasis_gemv_f32", L.ptr(ws.cond), self.d, R, L.ptr(self.final_ada_w), 2 * self.d, self.d,
                L.ptr(self.final_ada_b), ctypes.c_void_p(ws.ada.data_ptr() + 4 * ns), self.ada_width, L.ACT_SILU,

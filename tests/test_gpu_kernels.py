@@ -373,6 +373,12 @@ def test_gemv(R, K, N, act_in, act_out, acc):
         ref = ref + out0.double()
     # x is split into bf16 hi+lo, so the result keeps ~fp32 accuracy
     assert_close(out, ref, 0.9999999, 1e-4, "gemv R=%d K=%d N=%d" % (R, K, N))
+    # the same weights in 16-row tile order give the same bits
+    out_t = dev(out0)
+    L.call("oasis_gemv_bf16_tiled", L.ptr(dev(x)), K, R, L.ptr(dev(pkg.model.tile_rows16(W))), N, K, L.ptr(dev(b)),
+           L.ptr(out_t), N, act_in, act_out, acc, stream())
+    sync()
+    assert torch.equal(out_t, out), "tiled gemv R=%d K=%d N=%d" % (R, K, N)
 
 
 @pytest.mark.parametrize("R,K,N,act_in,act_out,acc", [(2, 1024, 2048, 1, 0, 0), (5, 256, 1024, 2, 1, 0),

@@ -173,7 +173,7 @@ def test_dit_step_adaln_rows_of_every_consumer(c1):
     step.run()
     torch.cuda.synchronize()
     cond = step.ws.cond[:2].double().cpu()
-    W = torch.cat([dit.ada_w.double().cpu(), dit.final_ada_w.double().cpu()])
+    W = torch.cat([dit.ada_w_rows().double().cpu(), dit.final_ada_w.double().cpu()])
     B_ = torch.cat([dit.ada_b.double().cpu(), dit.final_ada_b.double().cpu()])
     ref = torch.nn.functional.silu(cond) @ W.t() + B_
     got = step.ws.ada[:2].double().cpu()

@@ -59,7 +59,7 @@ def test_dit_packing_adaln_rows():
     assert dit.ada_width == 4 * 6 * 128 + 2 * 128 and dit.ada_w.shape == (4 * 6 * 128, 128)
     assert dit.ada_w.dtype == torch.bfloat16 and dit.final_ada_w.dtype == torch.float32
     cond = torch.randn(3, 128, generator=torch.Generator().manual_seed(1))
-    rows = oracle.silu(cond) @ dit.ada_w.float().t() + dit.ada_b
+    rows = oracle.silu(cond) @ dit.ada_w_rows().float().t() + dit.ada_b
     for j in range(4):  # sub-block j: blocks.(j//2).(s|t), chunks shift, scale+1, gate, shift, scale+1, gate
         p = "blocks.%d.%s." % (j // 2, "st"[j % 2])
         ref = oracle.silu(cond) @ w[p + "ada_w"].float().t() + w[p + "ada_b"]
@@ -73,6 +73,23 @@ def test_dit_packing_adaln_rows():
     fin = oracle.silu(cond) @ dit.final_ada_w.t() + dit.final_ada_b
     assert torch.allclose(fin[:, :128], ref[:, :128], atol=1e-4)
     assert torch.allclose(fin[:, 128:], ref[:, 128:] + 1.0, atol=1e-4)
+
+
+def test_tile_rows16_layout():
+    """The 16-row MFMA tile order of the adaLN stack (oasis_gemv_bf16_tiled): piece l of tile t,
+    K step s is row 16t + (l % 16), columns 32s + 8(l // 16) .. +7, at element (t*K/32 + s)*512 +
+    8l; untile_rows16 inverts it."""
+    N, K = 48, 96
+    W = torch.arange(N * K, dtype=torch.float32).reshape(N, K)
+    T = M.tile_rows16(W)
+    assert T.shape == (N, K) and torch.equal(M.untile_rows16(T), W)
+    flat = T.reshape(-1)
+    for t in range(N // 16):
+        for s_ in range(K // 32):
+            for l in (0, 5, 16, 37, 63):
+                off = (t * (K // 32) + s_) * 512 + 8 * l
+                r, c = 16 * t + l % 16, 32 * s_ + 8 * (l // 16)
+                assert torch.equal(flat[off:off + 8], W[r, c:c + 8]), (t, s_, l)
 
 
 def test_dit_packing_patch_embed_and_action_pad():
