@@ -662,8 +662,9 @@ def main():
                                  "single-stream hipGraphs on two streams, batch k's decodes (launched once its DDIM "
                                  "steps are done) overlapping batch k+1's DDIM steps")
         out["play_workload"] = ("interactive loop (PlaySession): one config-3 frame per action, host-synchronised "
-                                "per frame; noise drawn on the device, conditioning rows written, frame graph "
-                                "replayed, context rolled on the device, frame [360,640,3] in [0,1] returned")
+                                "per frame; one hipGraph per frame holding the noise draw (Philox on the device), "
+                                "the DDIM steps and decode, the [360,640,3] conversion to [0,1] and the context "
+                                "roll; action rows uploaded when they change, the frame copied out")
         out["frame_workload"] = ("config3: 4 DDIM v-prediction steps (t=999,749,499,249, cosine alphas) "
                                  "over the DiT (step 1 at T=2 storing the context frame's temporal K/V, steps "
                                  "2-4 on the generated frame at T=1 against that cache; frame_fps_all_t2: every "

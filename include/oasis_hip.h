@@ -349,6 +349,19 @@ int oasis_bridge(const float* chunk, float* latent, int64_t gh, int64_t gw, int6
 int oasis_vae_unpatchify(const float* patches, float* frame, int64_t gh, int64_t gw,
                          int64_t ps, oasis_stream_t stream);
 
+/* out[i] = clamp(z_i, -clamp_abs, clamp_abs), i < n, z_i N(0, 1) draws (Philox4x32-10 under key
+ * seed, counter block (i / 4, *counter), Box-Muller); copy, if not NULL, gets the same values.
+ * *counter (device memory) is then incremented, so a captured graph draws new noise on every
+ * replay. The interactive loop's per-frame noise (play.py:466-472, torch.randn clamped to +-20),
+ * drawn inside the frame graph. */
+int oasis_noise_normal(float* out, float* copy, int64_t n, uint64_t seed, uint32_t* counter,
+                       float clamp_abs, oasis_stream_t stream);
+
+/* [C, H, W] frame in [-1, 1] -> [H, W, C] in [0, 1]: (x + 1) / 2, clamped. The interactive loop's
+ * frame for display (play.py:476-480). */
+int oasis_frame_hwc(const float* frame, float* out, int64_t C, int64_t H, int64_t W,
+                    oasis_stream_t stream);
+
 /* ======================================================================
  * Composite entry points: the DiT step, the VAE decoder and the DDIM frame.
  * ==================================================================== */

@@ -125,6 +125,8 @@ SIGNATURES = {
     "oasis_gemv_bf16_tiled": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
     "oasis_gemv_f32": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],
     "oasis_timestep_embedding": [c_p, c_i64, c_i64, c_p, c_p],
+    "oasis_noise_normal": [c_p, c_p, c_i64, ctypes.c_uint64, c_p, c_f, c_p],
+    "oasis_frame_hwc": [c_p, c_p, c_i64, c_i64, c_i64, c_p],
     "oasis_small_linear": [c_p, c_i64, c_i64, c_i64, c_p, c_i, c_i, c_i64, c_p, c_p, c_i64, c_p],
     "oasis_ddim_update": [c_p, c_p, c_i64, c_f, c_f, c_f, c_f, c_f, c_f, c_p],
     "oasis_bridge": [c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],

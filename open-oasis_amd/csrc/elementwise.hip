@@ -155,6 +155,68 @@ __global__ void unpatchify_kernel(const float* patches, float* frame, int gh, in
   }
 }
 
+// Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+// SC 2011): ten rounds of two 32 x 32 -> 64-bit products mixed with the key, the key bumped by
+// the two Weyl constants between rounds. A counter-based generator: output i depends only on
+// (key, counter), so every lane draws its own numbers with no state.
+OASIS_DEV void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)M0 * c[0], p1 = (uint64_t)M1 * c[2];
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0, hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0;
+    c[1] = lo1;
+    c[2] = n2;
+    c[3] = lo0;
+    k0 += W0;
+    k1 += W1;
+  }
+}
+
+// out[i] = clamp(N(0, 1) draw, -lim, lim) for i < n (and copy[i] the same when copy is set): one
+// workgroup; draw i comes from Philox block (i / 4, *counter) under key (k0, k1) through the
+// Box-Muller transform of its uniforms (2j, 2j+1) in (0, 1). *counter is then bumped, so a graph
+// replaying this kernel draws fresh numbers every replay.
+__global__ __launch_bounds__(256) void noise_kernel(float* __restrict__ out, float* __restrict__ copy, int64_t n,
+                                                    uint32_t k0, uint32_t k1, uint32_t* __restrict__ counter,
+                                                    float lim) {
+  const uint32_t frame = counter[0];
+  for (int64_t q = threadIdx.x; q * 4 < n; q += blockDim.x) {
+    uint32_t x[4] = {(uint32_t)q, (uint32_t)(q >> 32), frame, 0u};
+    philox4x32_10(x, k0, k1);
+    float z[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float u1 = ((float)x[2 * j] + 0.5f) * 2.3283064365386963e-10f;  // (0, 1): 2^-32 steps
+      const float u2 = ((float)x[2 * j + 1] + 0.5f) * 2.3283064365386963e-10f;
+      const float r = sqrtf(-2.0f * logf(u1));
+      float sn, cs;
+      sincosf(6.283185307179586f * u2, &sn, &cs);
+      z[2 * j] = r * cs;
+      z[2 * j + 1] = r * sn;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = 4 * q + j;
+      if (i < n) {
+        const float v = fminf(fmaxf(z[j], -lim), lim);
+        out[i] = v;
+        if (copy) copy[i] = v;
+      }
+    }
+  }
+  __syncthreads();  // every lane has read the counter
+  if (threadIdx.x == 0) counter[0] = frame + 1u;
+}
+
+// CHW frame in [-1, 1] -> HWC in [0, 1]: out[(y*W + x)*C + c] = clamp((frame[(c*H + y)*W + x] + 1) / 2)
+__global__ void frame_hwc_kernel(const float* __restrict__ frame, float* __restrict__ out, int C, int64_t HW) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < HW; i += (int64_t)gridDim.x * blockDim.x)
+    for (int c = 0; c < C; ++c) out[i * C + c] = fminf(fmaxf((frame[c * HW + i] + 1.0f) * 0.5f, 0.0f), 1.0f);
+}
+
 __global__ void temb_kernel(const float* t, int64_t R, int half, float* out) {
   const int64_t n = R * half;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -364,6 +426,26 @@ extern "C" int oasis_vae_unpatchify(const float* patches, float* frame, int64_t 
   hipLaunchKernelGGL(unpatchify_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), patches,
                      frame, (int)gh, (int)gw, (int)ps);
   return oasis::check_launch("vae_unpatchify");
+}
+
+extern "C" int oasis_noise_normal(float* out, float* copy, int64_t n, uint64_t seed, uint32_t* counter,
+                                  float clamp_abs, oasis_stream_t stream) {
+  OASIS_REQUIRE(out && counter, OASIS_ERR_NULL, "noise_normal: null pointer");
+  OASIS_REQUIRE(n > 0 && n <= (1ll << 34), OASIS_ERR_SHAPE, "noise_normal: n must be in [1, 2^34]");
+  OASIS_REQUIRE(clamp_abs > 0.0f, OASIS_ERR_ARG, "noise_normal: clamp_abs must be positive");
+  hipLaunchKernelGGL(noise_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), out, copy, n,
+                     (uint32_t)seed, (uint32_t)(seed >> 32), counter, clamp_abs);
+  return oasis::check_launch("noise_normal");
+}
+
+extern "C" int oasis_frame_hwc(const float* frame, float* out, int64_t C, int64_t H, int64_t W,
+                               oasis_stream_t stream) {
+  OASIS_REQUIRE(frame && out, OASIS_ERR_NULL, "frame_hwc: null pointer");
+  OASIS_REQUIRE(C > 0 && C <= 16 && H > 0 && W > 0, OASIS_ERR_SHAPE, "frame_hwc: bad shape");
+  const int64_t HW = H * W;
+  hipLaunchKernelGGL(frame_hwc_kernel, dim3(ew_grid(HW)), dim3(256), 0, static_cast<hipStream_t>(stream), frame, out,
+                     (int)C, HW);
+  return oasis::check_launch("frame_hwc");
 }
 
 extern "C" int oasis_timestep_embedding(const float* t, int64_t R, int64_t dim, float* out, oasis_stream_t stream) {

@@ -6,7 +6,9 @@
   the count to [1, 12] (play.py:55-56,103-108) and resets the context to the prompt and the
   frame index to 0, as the reference does.
 - Each frame draws fresh noise, N(0, 1) clamped to +-noise_abs_max (play.py:466-472). Patchify
-  is a permutation of iid noise, so it is drawn directly in patch space, on the device.
+  is a permutation of iid noise, so it is drawn directly in patch space, on the device, by a
+  counter-based generator (`oasis_noise_normal`: Philox4x32-10 keyed by the session's seed, its
+  frame counter in device memory) inside the frame's graph.
 - The context is the previous frame's denoised latent. Its conditioning is at
   stabilization_level - 1 with the previous frame's action (play.py:486-496); the first context
   is the prompt with the prompt action. After frame index k (k > 0, k % reset_every == 0) the
@@ -15,12 +17,17 @@
   `hold` frames after a release (read_action, play.py:80-100).
 - Everything stays on the device. The context moves device-to-device. The frame comes back as
   [H, W, 3] in [0, 1], that is (x + 1) / 2 of the decoder's clamped output (play.py:476-480).
+- One hipGraph per step count holds the whole frame: the noise draw, the DDIM steps and the
+  decode, the [H, W, 3] conversion (`oasis_frame_hwc`) and the context roll. Per frame the host
+  launches it, uploads the action rows when they change, and copies the frame out.
 """
+import ctypes
 import time
 
 import torch
 
-from .model import FramePipeline
+from . import _lib as L
+from .model import FramePipeline, Graph
 from .schedule import ddim_steps as ddim_schedule
 from .schedule import sigmoid_alphas_cumprod
 
@@ -96,9 +103,14 @@ class PlaySession:
         self.prompt_action = (torch.zeros(e) if prompt_action is None else
                               torch.as_tensor(prompt_action, dtype=torch.float32).reshape(e).clone())
         self.hold = ActionHold(e, hold)
-        self.gen = torch.Generator(device=dev)
-        self.gen.manual_seed(seed)
+        # the noise generator's key and its frame counter (bumped on the device by every draw)
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        self.counter = torch.zeros(1, dtype=torch.int32, device=dev)
+        P = dit.P
+        self.noise_buf = torch.zeros(P, dit.patch_dim, device=dev) if keep_noise else None
+        self.img_buf = torch.zeros(vae.frame_shape[1], vae.frame_shape[2], vae.frame_shape[0], device=dev)
         self.pipelines = {}
+        self.graphs = {}
         # action rows go up through a pinned buffer; the event guards its reuse
         self.act_host = torch.zeros(1 + MAX_DDIM_STEPS, dit.ext_pad, pin_memory=True)
         self.act_copied = torch.cuda.Event()
@@ -115,9 +127,21 @@ class PlaySession:
             t_rows = torch.tensor([self.ctx_t] + [float(t) for t, _ in fp.steps], dtype=torch.float32)
             with torch.cuda.stream(self.stream):
                 fp.ws.t[:1 + n].copy_(t_rows)
-            fp.capture()
             self.pipelines[n] = fp
+            self.graphs[n] = Graph(lambda: self._enqueue(fp), self.stream)
         return fp
+
+    def _enqueue(self, fp):
+        """One frame on self.stream: noise into fp.chunk, the frame, its [H, W, 3] copy, and the
+        context roll (this frame's denoised latent is the next context)."""
+        h = L.stream_handle(self.stream)
+        L.call("oasis_noise_normal", L.ptr(fp.chunk), L.ptr(self.noise_buf) if self.noise_buf is not None else None,
+               fp.chunk.numel(), ctypes.c_uint64(self.seed), L.ptr(self.counter), self.noise_abs_max, h)
+        fp.enqueue()
+        C, H, W = self.vae.frame_shape
+        L.call("oasis_frame_hwc", L.ptr(fp.vws.frame), L.ptr(self.img_buf), C, H, W, h)
+        with torch.cuda.stream(self.stream):
+            fp.ctx_patches.copy_(fp.chunk)
 
     def set_ddim_steps(self, n):
         """Switch to n DDIM steps per frame (clamped to [1, 12]); resets the context to the
@@ -154,17 +178,15 @@ class PlaySession:
             rows[0, :e] = self.ctx_action
             rows[1:, :e] = a
             self.rows_key = key
-        with torch.cuda.stream(self.stream):
-            fp.chunk.normal_(generator=self.gen).clamp_(-self.noise_abs_max, self.noise_abs_max)
-            if self.keep_noise:
-                self.last_noise = fp.chunk.clone()
-            if upload:
+        if upload:
+            with torch.cuda.stream(self.stream):
                 fp.ws.act[:R].copy_(rows, non_blocking=True)
                 self.act_copied.record(self.stream)
-        fp.graph.launch()
+        self.graphs[n].launch()
         with torch.cuda.stream(self.stream):
-            img = ((fp.vws.frame + 1.0) * 0.5).clamp_(0.0, 1.0).permute(1, 2, 0).contiguous()
-            fp.ctx_patches.copy_(fp.chunk)  # this frame's denoised latent is the next context
+            img = self.img_buf.clone()
+            if self.keep_noise:
+                self.last_noise = self.noise_buf.clone()
         self.ctx_action = a.clone()
         cur = torch.cuda.current_stream(self.device)
         img.record_stream(cur)

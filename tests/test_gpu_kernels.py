@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import L, assert_close, bf, cuda, pkg, stream, sync
+from helpers import L, assert_close, bf, cuda, noise_reference, pkg, stream, sync
 
 pytestmark = pytest.mark.gpu
 
@@ -700,3 +700,31 @@ def test_residual_ln(np_, mode):
         assert_close(y, oracle.layer_norm(xr) * ada[f, D:2 * D] + ada[f, :D], 0.99999, 1e-2, "ln modulate")
     elif mode == "affine":
         assert_close(y, oracle.layer_norm(xr, w_aff, b_aff), 0.99999, 1e-2, "ln affine")
+
+
+# ---------------------------------------------------------------- interactive-loop helpers
+def test_noise_normal_and_frame_hwc():
+    """oasis_noise_normal against the host Philox + Box-Muller (ragged n, the copy, the clamp, the
+    counter bump: every call draws anew), and oasis_frame_hwc against torch."""
+    n, seed = 9216 + 3, 0x1234_5678_9ABC
+    out = torch.zeros(n, device="cuda")
+    cp = torch.zeros(n, device="cuda")
+    ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    draws = []
+    for frame in range(3):
+        L.call("oasis_noise_normal", L.ptr(out), L.ptr(cp), n, ctypes.c_uint64(seed), L.ptr(ctr), 20.0, stream())
+        sync()
+        got = out.cpu().double().numpy()
+        ref = noise_reference(n, seed, frame, 20.0)
+        assert abs(got - ref).max() < 1e-4, (frame, abs(got - ref).max())
+        assert torch.equal(out, cp) and int(ctr.item()) == frame + 1
+        draws.append(got)
+    assert not (draws[0] == draws[1]).all()
+    L.call("oasis_noise_normal", L.ptr(out), None, n, ctypes.c_uint64(seed), L.ptr(ctr), 0.5, stream())
+    sync()
+    assert out.abs().max().item() <= 0.5 and abs(out.cpu().double().numpy() - noise_reference(n, seed, 3, 0.5)).max() < 1e-4
+    frame = torch.randn(3, 7, 11, generator=_gen(77)) * 1.3
+    hwc = torch.zeros(7, 11, 3, device="cuda")
+    L.call("oasis_frame_hwc", L.ptr(dev(frame)), L.ptr(hwc), 3, 7, 11, stream())
+    sync()
+    assert torch.equal(hwc.cpu(), ((frame + 1.0) * 0.5).clamp(0.0, 1.0).permute(1, 2, 0))

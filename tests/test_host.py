@@ -1,10 +1,11 @@
 """Host-side logic on the CPU: schedules and DDIM coefficients, the RoPE tables and the
 weight packing the device kernels consume (laid out on device='cpu' here), and the
 determinism of the synthetic inputs."""
+import numpy as np
 import torch
 
 import oracle
-from helpers import pkg
+from helpers import noise_reference, philox4x32_10, pkg
 
 M = pkg.model
 S = pkg.schedule
@@ -73,6 +74,23 @@ def test_dit_packing_adaln_rows():
     fin = oracle.silu(cond) @ dit.final_ada_w.t() + dit.final_ada_b
     assert torch.allclose(fin[:, :128], ref[:, :128], atol=1e-4)
     assert torch.allclose(fin[:, 128:], ref[:, 128:] + 1.0, atol=1e-4)
+
+
+def test_philox_known_answers_and_noise_reference():
+    """The host Philox4x32-10 the device noise is checked against reproduces the published
+    known-answer vectors of the Random123 distribution (counter, key -> output), and its
+    Box-Muller draws have the moments of N(0, 1)."""
+    kat = [((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+           ((0xffffffff,) * 4, (0xffffffff,) * 2, (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+           ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+            (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1))]
+    for ctr, key, want in kat:
+        got = philox4x32_10(np.array([ctr], dtype=np.uint32), key)[0]
+        assert tuple(int(v) for v in got) == want
+    z = noise_reference(200000, 5, 0, 20.0)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+    assert not np.array_equal(noise_reference(64, 5, 0, 20.0), noise_reference(64, 5, 1, 20.0))
+    assert np.abs(noise_reference(4096, 5, 2, 0.5)).max() <= 0.5
 
 
 def test_tile_rows16_layout():
