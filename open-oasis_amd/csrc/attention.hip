@@ -63,8 +63,13 @@ struct AttnArgs {
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
 // sequence once, with no barrier in the key loop) and consumed in KC-key chunks.
-// V^T is built from 8x8 blocks: a thread loads 8 key rows x 8 dims, transposes them in
-// registers and writes 8 16-byte LDS rows.
+// V^T is built from 8x8 blocks: a thread loads 8 key rows x 8 dims and transposes them in
+// registers. Each V^T row (one head dim) holds its keys in k-slot order: within a 32-key
+// block, position 8g + j holds the key that k-slot j of lane group g multiplies in the P V
+// product (key 4g + j for j < 4, 16 + 4g + j - 4 for j >= 4), so a V fragment is one
+// 16-byte LDS read. The 16-byte units of a row are XOR-swizzled by (row >> 3) & 7 within
+// each 64-key group: the 8-byte staging writes of 8 dims x the same keys (rows 8 apart) and
+// the fragment reads of 8 consecutive rows then fall in distinct LDS banks.
 // KSPLIT = 2: two waves per 16-query block, each taking every other key chunk (two waves
 // per SIMD, half the serial softmax chain each); their running (max, sum, output) states
 // are merged through LDS at the end.
@@ -76,7 +81,7 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
   static_assert(KS % KC == 0 && KC % 32 == 0 && KS % 8 == 0, "chunking");
   static_assert(KSPLIT == 1 || KSPLIT == 2, "key split");
   static_assert(KSPLIT == 1 || KS * KPITCH * 2 >= NW * 64 * 18 * 4, "merge slots fit in the K staging");
-  constexpr int VPITCH = KS + 8;
+  constexpr int VPITCH = (KS + 63) / 64 * 64 + 8;  // whole 64-key swizzle groups, +8 against bank repeats
   constexpr int KT = KC / 16;   // 16-key tiles per chunk
   constexpr int NT = NW * KSPLIT * 64;
   constexpr int KCH = KS * 8;             // 16-byte K chunks per stage
@@ -137,12 +142,16 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
         const int b = tid + u * NT;
         if (b < VBL) {
           const int kb = b >> 3, db = b & 7;
+          // keys 8kb..8kb+3 go to k-slot positions p0..p0+3, keys 8kb+4..8kb+7 to p0+8..p0+11;
+          // rows db*8..db*8+7 share the swizzle db
+          const int p0 = (kb >> 2) * 32 + 16 * (kb & 1) + 4 * ((kb >> 1) & 1);
+          const int e0 = (((p0 >> 3) ^ db) << 3) + (p0 & 7);
+          const int e1 = ((((p0 >> 3) + 1) ^ db) << 3) + (p0 & 7);
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            bf16x8 t;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) t[r] = vv[u][r][j];
-            *reinterpret_cast<bf16x8*>(Vt + (db * 8 + j) * VPITCH + kb * 8) = t;
+            bf16* row = Vt + (db * 8 + j) * VPITCH;
+            *reinterpret_cast<bf16x4*>(row + e0) = bf16x4{vv[u][0][j], vv[u][1][j], vv[u][2][j], vv[u][3][j]};
+            *reinterpret_cast<bf16x4*>(row + e1) = bf16x4{vv[u][4][j], vv[u][5][j], vv[u][6][j], vv[u][7][j]};
           }
         }
       }
@@ -208,10 +217,8 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
       }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const bf16* vp = Vt + (dt * 16 + lr) * VPITCH + kl + kc * 32 + 4 * g;
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vp);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vp + 16);
-        const bf16x8 va = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const int row = dt * 16 + lr, unit = ((kl + kc * 32) >> 3) + g;
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(Vt + row * VPITCH + ((unit ^ ((row >> 3) & 7)) << 3));
         o[dt] = mfma16(va, pb, o[dt]);
       }
     }
