@@ -544,7 +544,8 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   constexpr int UPT = (UNITS + 255) / 256;         // units per thread
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index read back as a scalar, so that the addresses built from it stay in SGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
   // work id -> (split, n tile, m tile), m fastest and the split outermost: an XCD's contiguous
   // range of ids covers the M tiles of a few weight slices of one K slice, so its L2 fetches
@@ -578,20 +579,24 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
     }
   }
 
-  // lane's row in each 8-row block: r = 8 blk + lane / 8, K chunk (lane % 8) ^ ((r >> 1) & 7);
-  // the tile index only moves the pointer by a constant, folded into each load's offset
-  const bf16* src[NBLK];
+  // lane's row in each 8-row block: r = 8 blk + lane / 8, K chunk (lane % 8) ^ ((r >> 1) & 7).
+  // Loads are buffer loads: a scalar base (the tile's first A row / weight row at this wave's K
+  // slice), the K tile as a scalar offset and a 32-bit per-lane byte offset, below BM (BN) rows of
+  // lda (ldb).
+  const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(A + (int64_t)m0 * lda + kb);
+  const __amdgpu_buffer_rsrc_t Brs = buffer_rsrc(B + (int64_t)n0 * ldb + kb);
+  uint32_t off[NBLK];
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) {
     const int r = blk * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    src[blk] = r < BM ? A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 8
-                      : B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 8;
+    off[blk] = r < BM ? (uint32_t)(((int64_t)(min(m0 + r, M - 1) - m0) * lda + c * 8) * 2)
+                      : (uint32_t)(((int64_t)(min(n0 + r - BM, N - 1) - n0) * ldb + c * 8) * 2);
   }
   auto issue = [&](int kt, int buf) {
     char* base = ring + buf * STAGE_BYTES;
 #pragma unroll
-    for (int blk = 0; blk < NBLK; ++blk) load_lds16(src[blk] + kt * 64, base + blk * 1024);
+    for (int blk = 0; blk < NBLK; ++blk) buffer_load_lds16(blk < BM / 8 ? Ars : Brs, off[blk], kt * 128, base + blk * 1024);
   };
 
   f32x4 acc[FM][FN];
