@@ -235,7 +235,8 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index read back as a scalar, so that the load bases built from it stay in SGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
   const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
@@ -247,24 +248,27 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
   const int kb = split * nk * 64;
 
   // this lane's source in each of its LPW blocks: row r = 8 * blk + lane / 8 of the A|B stack,
-  // slot lane % 8 holds K chunk (lane % 8) ^ ((r >> 1) & 7)
-  const bf16* src[LPW];
+  // slot lane % 8 holds K chunk (lane % 8) ^ ((r >> 1) & 7); buffer loads from the tile's first
+  // A row / weight row (scalar base, K tile as scalar offset, 32-bit lane offset)
+  const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(A + (int64_t)m0 * lda + kb);
+  const __amdgpu_buffer_rsrc_t Brs = buffer_rsrc(B + (int64_t)n0 * ldb + kb);
+  uint32_t off[LPW];
   int dst[LPW];
+  bool from_a[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const int blk = min(wave * LPW + u, NBLK - 1);
     const int r = blk * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (r < BM)
-      src[u] = A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 8;
-    else
-      src[u] = B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 8;
+    from_a[u] = blk * 8 < BM;  // wave-uniform: BM is a multiple of 8
+    off[u] = from_a[u] ? (uint32_t)(((int64_t)(min(m0 + r, M - 1) - m0) * lda + c * 8) * 2)
+                       : (uint32_t)(((int64_t)(min(n0 + r - BM, N - 1) - n0) * ldb + c * 8) * 2);
     dst[u] = blk * 1024;
   }
   auto issue = [&](int kt, int buf) {
     char* base = smem + buf * STAGE_BYTES;
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * 64, base + dst[u]);
+    for (int u = 0; u < LPW; ++u) buffer_load_lds16(from_a[u] ? Ars : Brs, off[u], kt * 128, base + dst[u]);
   };
 
   f32x4 acc[FM][FN];

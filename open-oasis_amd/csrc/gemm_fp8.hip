@@ -270,7 +270,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   constexpr int GN = 8;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index read back as a scalar, so that the load bases built from it stay in SGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
   int split, mt, nt;
@@ -279,17 +280,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   const int nk = K / BK8 / splits;
   const int kb = split * nk * BK8;
 
-  const uint8_t* src[LPW];
+  // buffer loads: the tile's first A row / weight row as the scalar base, the K tile as a scalar
+  // offset, a 32-bit lane offset below BM (BN) rows of lda (ldb) bytes
+  const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(A + (int64_t)m0 * lda + kb);
+  const __amdgpu_buffer_rsrc_t Brs = buffer_rsrc(B + (int64_t)n0 * ldb + kb);
+  uint32_t off[LPW];
   int dst[LPW];
+  bool from_a[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const int blk = min(wave * LPW + u, NBLK - 1);
     const int r = blk * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (r < BM)
-      src[u] = A + (int64_t)min(m0 + r, M - 1) * lda + kb + c * 16;
-    else
-      src[u] = B + (int64_t)min(n0 + r - BM, N - 1) * ldb + kb + c * 16;
+    from_a[u] = blk * 8 < BM;  // wave-uniform: BM is a multiple of 8
+    off[u] = from_a[u] ? (uint32_t)((int64_t)(min(m0 + r, M - 1) - m0) * lda + c * 16)
+                       : (uint32_t)((int64_t)(min(n0 + r - BM, N - 1) - n0) * ldb + c * 16);
     dst[u] = blk * 1024;
   }
   // scale word of A row wave*64 + lane (rows past the tile load a clamped row, never read)
@@ -297,7 +302,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   auto issue = [&](int kt, int buf) {
     char* base = smem + buf * STAGE;
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * BK8, base + dst[u]);
+    for (int u = 0; u < LPW; ++u) buffer_load_lds16(from_a[u] ? Ars : Brs, off[u], kt * BK8, base + dst[u]);
     if (wave < SWAVES) load_lds4(ssrc + kt * (BK8 / 32), base + DATA + wave * 256);
   };
 
