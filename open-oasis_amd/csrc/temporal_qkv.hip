@@ -86,7 +86,8 @@ __global__ __launch_bounds__(WM * WN * 64) void tqkv_kernel(TqkvArgs a) {
   static_assert((STAGES - 2) * LPW <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index read back as a scalar, so that the load bases built from it stay in SGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
   // position groups run fastest, so one XCD's consecutive workgroups share a few heads' weights
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -94,25 +95,31 @@ __global__ __launch_bounds__(WM * WN * 64) void tqkv_kernel(TqkvArgs a) {
   const int h = rest % a.H, b = rest / a.H;
   const int64_t m_base = ((int64_t)b * a.T) * a.P + pg * 16;  // row of (frame f, position i): m_base + f P + i
 
-  const bf16* src[LPW];
+  // buffer loads: scalar bases (the group's first A row, head h's first q weight row), the K tile
+  // as a scalar offset, 32-bit lane offsets (T frames of P rows of A; the q, k, v row blocks of W)
+  const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(a.A + m_base * a.lda);
+  const __amdgpu_buffer_rsrc_t Wrs = buffer_rsrc(a.W + (int64_t)h * 64 * a.D);
+  uint32_t off[LPW];
   int dst[LPW];
+  bool from_a[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const int blk = min(wave * LPW + u, NBLK - 1);
     const int r = blk * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (r < BM) {
-      src[u] = a.A + (m_base + (int64_t)(r >> 4) * a.P + (r & 15)) * a.lda + c * 8;
+    from_a[u] = blk * 8 < BM;  // wave-uniform: BM is a multiple of 16
+    if (from_a[u]) {
+      off[u] = (uint32_t)((((int64_t)(r >> 4) * a.P + (r & 15)) * a.lda + c * 8) * 2);
     } else {
       const int cc = r - BM;  // q, k, v rows of head h
-      src[u] = a.W + ((int64_t)(cc >> 6) * a.D + h * 64 + (cc & 63)) * a.D + c * 8;
+      off[u] = (uint32_t)((((int64_t)(cc >> 6) * a.D + (cc & 63)) * a.D + c * 8) * 2);
     }
     dst[u] = blk * 1024;
   }
   auto issue = [&](int kt, int buf) {
     char* base = smem + buf * STAGE_BYTES;
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) load_lds16(src[u] + (int64_t)kt * 64, base + dst[u]);
+    for (int u = 0; u < LPW; ++u) buffer_load_lds16(from_a[u] ? Ars : Wrs, off[u], kt * 128, base + dst[u]);
   };
 
   f32x4 acc[FM][FN];
