@@ -54,7 +54,7 @@ def _event_ms(fn, stream, n, graph=None):
 # HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
 # scaled by what the same counter reads for a plain device copy of known size.
-TRAFFIC = {"fc1": 15644192, "gemv": 405114403, "fc1_4608_bf16": 90742080, "fc1_4608_fp8": 46778930}
+TRAFFIC = {"fc1": 15619781, "gemv": 405115017, "fc1_4608_bf16": 90722144, "fc1_4608_fp8": 46773862}
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100, graph=True):

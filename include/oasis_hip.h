@@ -184,7 +184,7 @@ typedef struct {
 } oasis_epilogue_t;
 
 /* acc[M,N] = A[M,K] @ B[N,K]^T (bf16 in, fp32 accumulate) followed by the epilogue.
- * K % 64 == 0, N % 8 == 0. */
+ * K % 64 == 0, N % 8 == 0, lda and ldb below 2^22 elements. */
 int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                     int64_t N, int64_t K, const oasis_epilogue_t* epi, oasis_stream_t stream);
 
@@ -199,7 +199,7 @@ int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ld
 /* fp8 weight GEMM: acc[M,N] = A[M,K] @ (Bq[N,K] * w_scale[N])^T, then the epilogue.
  * A bf16 (quantized per 32-wide K block to e4m3 with a power-of-two scale inside the kernel),
  * Bq OCP fp8 e4m3 bytes, w_scale fp32 per output channel. K % 128 == 0, N % 8 == 0,
- * lda % 8 == 0, ldb % 16 == 0. tile: 0..4 (gemm_fp8.hip's kTiles8), -1 = default;
+ * lda % 8 == 0, ldb % 16 == 0, both below 2^22. tile: 0..4 (gemm_fp8.hip's kTiles8), -1 = default;
  * splits divides K/128 (> 1 requires OASIS_EPI_PARTIAL_F32).
  * No counterpart in the reference: it has no sub-fp32 weight path (the config-4 serving
  * case of the build's benchmark plan). */

@@ -868,6 +868,8 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
   OASIS_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K, OASIS_ERR_SHAPE,
                 "gemm: lda/ldb must be >= K and multiples of 8");
   OASIS_REQUIRE(M < (1ll << 31) && N < (1ll << 31), OASIS_ERR_SHAPE, "gemm: M/N too large");
+  // the kernels address a tile's rows by 32-bit byte offsets from its first row
+  OASIS_REQUIRE(lda < (1ll << 22) && ldb < (1ll << 22), OASIS_ERR_SHAPE, "gemm: lda/ldb must be below 2^22");
   OASIS_REQUIRE(splits >= 1 && (K / BK) % splits == 0, OASIS_ERR_SHAPE,
                 "gemm: splits=%d must divide K/64=%lld", splits, (long long)(K / BK));
   const Epi e = to_epi(ex);

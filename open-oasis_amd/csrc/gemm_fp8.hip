@@ -536,6 +536,8 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
   OASIS_REQUIRE(N % 8 == 0, OASIS_ERR_SHAPE, "gemm_fp8: N=%lld must be a multiple of 8", (long long)N);
   OASIS_REQUIRE(lda % 8 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K, OASIS_ERR_SHAPE,
                 "gemm_fp8: need lda %% 8 == 0, ldb %% 16 == 0, both >= K");
+  // the kernels address a tile's rows by 32-bit byte offsets from its first row
+  OASIS_REQUIRE(lda < (1ll << 22) && ldb < (1ll << 22), OASIS_ERR_SHAPE, "gemm_fp8: lda/ldb must be below 2^22");
   OASIS_REQUIRE(splits >= 1 && (K / BK8) % splits == 0, OASIS_ERR_SHAPE, "gemm_fp8: splits=%d must divide K/128",
                 splits);
   const Epi e = to_epi(ex);

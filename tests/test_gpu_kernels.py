@@ -172,6 +172,10 @@ def test_gemm_rejects_bad_shapes():
     out = torch.zeros(4, 8, device="cuda")
     with pytest.raises(L.OasisError, match="multiple of 64"):
         _gemm(A, A, 4, 8, 96, _epi(kind=L.EPI_STORE_F32, out_f32=out, ld_out=8))
+    # rows are addressed by 32-bit byte offsets from a tile's first row: leading dimensions of
+    # 2^22 elements or more are refused before any launch (the pointers are never dereferenced)
+    with pytest.raises(L.OasisError, match="below 2\\^22"):
+        _gemm(A, A, 4, 8, 64, _epi(kind=L.EPI_STORE_F32, out_f32=out, ld_out=8), lda=1 << 22)
 
 
 @pytest.mark.parametrize("layout", [0, 1])
