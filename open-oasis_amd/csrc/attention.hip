@@ -183,8 +183,7 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_xor32(max_xor16(mx));
     const float m_new = fmaxf(m, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m - m_use);
@@ -196,8 +195,7 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
         s[kt][i] = __builtin_amdgcn_exp2f(s[kt][i] - m_use);
         ps += s[kt][i];
       }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = sum_xor32(sum_xor16(ps));
     lsum = lsum * alpha + ps;
     m = m_new;
 #pragma unroll
@@ -345,11 +343,8 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
       d10 += bf2f(q1[i]) * bf2f(k0[i]);
       d11 += bf2f(q1[i]) * bf2f(k1[i]);
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      d10 += __shfl_xor(d10, o, 16);
-      d11 += __shfl_xor(d11, o, 16);
-    }
+    d10 = row16_sum(d10);
+    d11 = row16_sum(d11);
     (void)q0;
     const float x0 = d10 * scale_log2, x1 = d11 * scale_log2;
     const float mx = fmaxf(x0, x1);
@@ -372,10 +367,7 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     for (int s = 0; s <= t; ++s) {
       const bf16x4 kv4 = *reinterpret_cast<const bf16x4*>(k + base + s * 64);
       float dot = qv[0] * bf2f(kv4[0]) + qv[1] * bf2f(kv4[1]) + qv[2] * bf2f(kv4[2]) + qv[3] * bf2f(kv4[3]);
-      dot += __shfl_xor(dot, 1, 16);
-      dot += __shfl_xor(dot, 2, 16);
-      dot += __shfl_xor(dot, 4, 16);
-      dot += __shfl_xor(dot, 8, 16);
+      dot = row16_sum(dot);
       const float x = dot * scale_log2;
       const float m_new = fmaxf(m, x);
       const float alpha = exp2f(m - m_new);

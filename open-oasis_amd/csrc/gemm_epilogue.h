@@ -266,8 +266,7 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
         v[j] = gelu_tanh(v[j]);
         amax = fmaxf(amax, fabsf(v[j]));
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      amax = quad_max(amax);
       const int sb = fp8_block_scale(amax);
       const float inv = fp8_block_inv(sb);
       *reinterpret_cast<uint2*>(e.out_fp8 + m * e.ld_out + n0) =

@@ -43,8 +43,7 @@ __device__ __forceinline__ uint2 quant8(i32x4 raw, int* sbyte) {
     v[j] = (float)h[j];
     amax = fmaxf(amax, fabsf(v[j]));
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = quad_max(amax);
   const int sb = fp8_block_scale(amax);
   const float inv = fp8_block_inv(sb);
   *sbyte = sb;

@@ -133,18 +133,23 @@ __global__ __launch_bounds__(256) void ln8_kernel(const TIn* __restrict__ x, int
   }
   float v[NV][8], av[NV][8], bv[NV][8];
 #pragma unroll
-  for (int c = 0; c < NV; ++c) {
-    const int k = c * 512 + lane * 8;
-    load8<TIn>(x + row * D + k, v[c]);
-    load8<float>(a + k, av[c]);
-    load8<float>(b + k, bv[c]);
-  }
+  for (int c = 0; c < NV; ++c) load8<TIn>(x + row * D + c * 512 + lane * 8, v[c]);
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c)
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += v[c][j];
   const float mean = wave_sum(s) * (1.0f / D);
+  // the affine rows (4x the row's bytes, mostly L2 hits) are fetched once the row is in: issued
+  // with the row, they queue ahead of the other waves' row loads and delay the HBM reads
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int k = c * 512 + lane * 8;
+    load8<float>(a + k, av[c]);
+    load8<float>(b + k, bv[c]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < NV; ++c)
@@ -261,9 +266,7 @@ __global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restric
     for (int j = 0; j < W; ++j) o[j] = v[c][j] * rstd * av[c][j] + cv[c][j];
     if (W == 4 && y8) {
       float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      amax = oct_max(amax);
       const int sb = fp8_block_scale(amax);
       const float inv = fp8_block_inv(sb);
       *reinterpret_cast<uint32_t*>(y8 + row * D + k) = pack4_fp8(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
@@ -348,9 +351,7 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
     for (int j = 0; j < 4; ++j) o[j] = v[c][j] * rstd * av[c][j] + cv[c][j];
     if (y8) {
       float amax = fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3])));
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+      amax = oct_max(amax);
       const int sb = fp8_block_scale(amax);
       const float inv = fp8_block_inv(sb);
       *reinterpret_cast<uint32_t*>(y8 + row * D + k) = pack4_fp8(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);

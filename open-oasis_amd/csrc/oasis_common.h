@@ -108,18 +108,75 @@ OASIS_DEV void st_stream(V* p, V v) { __builtin_nontemporal_store(v, p); }
 template <typename V>
 OASIS_DEV V ld_stream(const V* p) { return __builtin_nontemporal_load(p); }
 
-// ---- wave reductions (64 lanes) ---------------------------------------------
-OASIS_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// ---- cross-lane reductions without LDS --------------------------------------
+// DPP moves within 16-lane rows and the gfx950 row / half-wave swaps are one VALU instruction
+// each, where __shfl_xor is an LDS permute (ds_bpermute) with an LDS round trip: a 64-lane sum
+// takes ~110 ns against ~260 ns in a dependent chain. Every lane pairs with a partner that pairs
+// back (l ^ 1, l ^ 2, 7 - l and 15 - l within rows, l ^ 16, l ^ 32) and a + b == b + a exactly,
+// so all lanes of a group end with bit-identical results. All lanes of the group must be active.
+template <int CTRL>
+OASIS_DEV float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7 - i within each 8 lanes
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15 - i within each 16 lanes
+
+// v_permlane16_swap (rows 0 <-> 1 and 2 <-> 3 between the two registers) and v_permlane32_swap
+// (lanes 0-31 <-> 32-63), as inline asm with both registers read and written: this compiler's
+// builtins return the second register's new value as the first's. Two wait states on each side.
+OASIS_DEV void swap_rows16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+OASIS_DEV void swap_halves32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+// v op v[lane ^ 16] and v op v[lane ^ 32]: after the swap of two copies of v, a holds the even
+// row's (lower half's) value and b the odd row's (upper half's) in every lane
+OASIS_DEV float sum_xor16(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  return a + b;
+}
+OASIS_DEV float max_xor16(float v) {
+  float a = v, b = v;
+  swap_rows16(a, b);
+  return fmaxf(a, b);
+}
+OASIS_DEV float sum_xor32(float v) {
+  float a = v, b = v;
+  swap_halves32(a, b);
+  return a + b;
+}
+OASIS_DEV float max_xor32(float v) {
+  float a = v, b = v;
+  swap_halves32(a, b);
+  return fmaxf(a, b);
+}
+// over aligned groups of 4, 8 and 16 lanes
+OASIS_DEV float quad_max(float v) {
+  v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
+  return fmaxf(v, dpp_mov<DPP_XOR2>(v));
+}
+OASIS_DEV float oct_max(float v) {
+  v = quad_max(v);
+  return fmaxf(v, dpp_mov<DPP_HALF_MIRROR>(v));
+}
+OASIS_DEV float row16_sum(float v) {
+  v += dpp_mov<DPP_XOR1>(v);
+  v += dpp_mov<DPP_XOR2>(v);
+  v += dpp_mov<DPP_HALF_MIRROR>(v);
+  return v + dpp_mov<DPP_MIRROR>(v);
+}
+OASIS_DEV float row16_max(float v) {
+  v = oct_max(v);
+  return fmaxf(v, dpp_mov<DPP_MIRROR>(v));
 }
 
-OASIS_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+// ---- wave reductions (64 lanes) ---------------------------------------------
+OASIS_DEV float wave_sum(float v) { return sum_xor32(sum_xor16(row16_sum(v))); }
+OASIS_DEV float wave_max(float v) { return max_xor32(max_xor16(row16_max(v))); }
 
 // Sums of N values (N a power of two, 2..64) across the 64 lanes at once, v[i] holding this
 // lane's part of value i. Recursive halving: at each level every lane keeps the half of its

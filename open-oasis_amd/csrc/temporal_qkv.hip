@@ -219,11 +219,8 @@ __global__ __launch_bounds__(WM * WN * 64) void tqkv_kernel(TqkvArgs a) {
     d10 += q1[j] * k0[j];
     d11 += q1[j] * k1[j];
   }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    d10 += __shfl_xor(d10, o, 16);
-    d11 += __shfl_xor(d11, o, 16);
-  }
+  d10 = row16_sum(d10);
+  d11 = row16_sum(d11);
   const float x0 = d10 * a.scale_log2, x1 = d11 * a.scale_log2;
   const float mx = fmaxf(x0, x1);
   const float p0 = exp2f(x0 - mx), p1 = exp2f(x1 - mx);
