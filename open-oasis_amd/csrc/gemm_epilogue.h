@@ -104,14 +104,8 @@ __device__ __forceinline__ void load_lds4(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, reinterpret_cast<uint32_t*>(lds), 4, 0, 0);
 }
 
-// The same from a buffer: a scalar base (rsrc, made from a wave-uniform pointer) plus a 32-bit
-// per-lane byte offset voff and a scalar byte offset soff. These loads move ~1.35x the bytes per
-// cycle of loads with 64-bit per-lane addresses (measured from L2 with 4 waves per CU: 41 against
-// 31 bytes per clock per CU).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
-  // raw buffer (stride 0), every 32-bit offset in range, 32-bit data format
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0xffffffff, 0x00020000);
-}
+// The same from a buffer (buffer_rsrc): a 32-bit per-lane byte offset voff and a scalar byte
+// offset soff.
 __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff, void* lds) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }

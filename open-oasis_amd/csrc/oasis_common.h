@@ -108,6 +108,16 @@ OASIS_DEV void st_stream(V* p, V v) { __builtin_nontemporal_store(v, p); }
 template <typename V>
 OASIS_DEV V ld_stream(const V* p) { return __builtin_nontemporal_load(p); }
 
+// ---- buffer loads -----------------------------------------------------------
+// A scalar base (the buffer resource, made from a wave-uniform pointer) plus a 32-bit per-lane
+// byte offset voff and a scalar byte offset soff: such loads move ~1.35x the bytes per cycle of
+// loads with 64-bit per-lane addresses (measured from L2 with 4 waves per CU: 41 against 31 bytes
+// per clock per CU).
+OASIS_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  // raw buffer (stride 0), every 32-bit offset in range, 32-bit data format
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0xffffffff, 0x00020000);
+}
+
 // ---- cross-lane reductions without LDS --------------------------------------
 // DPP moves within 16-lane rows and the gfx950 row / half-wave swaps are one VALU instruction
 // each, where __shfl_xor is an LDS permute (ds_bpermute) with an LDS round trip: a 64-lane sum
