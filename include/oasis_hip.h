@@ -397,7 +397,7 @@ typedef struct {
   const float* fc2_b[OASIS_MAX_SUB];
   const float* final_w;      /* [64, D] fp32                                       */
   const float* final_b;
-  const float* xemb_w;       /* [D, 64] fp32 patch embed, columns in (p, q, c) order */
+  const float* xemb_w;       /* [64, D] fp32 patch embed (K-major), rows in (p, q, c) order */
   const float* xemb_b;
   const float* temb_w0;      /* [D, 256] fp32                                      */
   const float* temb_b0;

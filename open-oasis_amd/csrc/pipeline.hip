@@ -464,7 +464,7 @@ extern "C" int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buff
   OASIS_REQUIRE(R <= 1024, OASIS_ERR_SHAPE, "dit_step: at most 1024 frames per call (got %lld)", (long long)R);
   OASIS_TRY(cond_mlp(w, t, action, R, hid, cond, stream));
   OASIS_TRY(adaln_rows(w, cond, R, ada, (hipStream_t)stream));
-  OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
+  OASIS_TRY(oasis_small_linear(patches, w->patch_dim, B * T * P, w->patch_dim, w->xemb_w, OASIS_F32, 1, D, w->xemb_b,
                                buf->x, D, stream));
   Pending pend;
   OASIS_TRY(dit_blocks(w, buf, B, T, ada, NA, 0, w->n_sub, &pend, stream));
@@ -688,7 +688,7 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     const float* c = coeffs + 6 * i;
     Pending pend;
     if (t1) {
-      OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, buf->x, D,
+      OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 1, D, w->xemb_b, buf->x, D,
                                    stream));
       const float* ada_cur = ada + (1 + i) * NA;  // the generated frame's rows at step i
       OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, use));
@@ -699,7 +699,7 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
     // z = [context frame; patch-embedded chunk] (oasis_inference.py:1911-1913)
     if (hipMemcpyAsync(buf->x, ctx_z, P * D * sizeof(float), hipMemcpyDeviceToDevice, s) != hipSuccess)
       return oasis::check_launch("ddim_frame context copy");
-    OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b,
+    OASIS_TRY(oasis_small_linear(chunk, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 1, D, w->xemb_b,
                                  buf->x + P * D, D, stream));
     const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
     OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, kv ? save : KvPass()));
@@ -741,7 +741,7 @@ extern "C" int oasis_ddim_frame(const oasis_dit_weights_t* w, const oasis_dit_bu
   // covers all rows
   OASIS_TRY(cond_mlp(w, t, action, 1 + n_steps, hid, cond, stream));
   OASIS_TRY(adaln_rows(w, cond, 1 + n_steps, ada, (hipStream_t)stream));
-  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z,
+  OASIS_TRY(oasis_small_linear(ctx_patches, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 1, D, w->xemb_b, ctx_z,
                                D, stream));
   OASIS_TRY(frame_steps(w, buf, kv, chunk, ctx_z, ada, n_steps, coeffs, v_out, stream));
   OASIS_TRY(oasis_bridge(chunk, latent, w->grid_h, w->grid_w, C, vw->latent_dim, kInvScaling, stream));
@@ -770,7 +770,7 @@ extern "C" int oasis_video_frames(const oasis_dit_weights_t* w, const oasis_dit_
   for (int64_t f = 0; f < n_frames; ++f) {
     // context = the previous frame's denoised latent (the rolled context window)
     const float* ctx = f == 0 ? ctx_patches : chunks + (f - 1) * fsz;
-    OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 0, D, w->xemb_b, ctx_z, D,
+    OASIS_TRY(oasis_small_linear(ctx, w->patch_dim, P, w->patch_dim, w->xemb_w, OASIS_F32, 1, D, w->xemb_b, ctx_z, D,
                                  stream));
     OASIS_TRY(frame_steps(w, buf, kv, chunks + f * fsz, ctx_z, ada + f * R * NA, n_steps, coeffs, v_out,
                           stream));

@@ -175,9 +175,10 @@ class DiT:
             torch.cuda.synchronize(dev)
         S.final_w = put(w["final.w"], f32).data_ptr()
         S.final_b = put(w["final.b"], f32).data_ptr()
-        # patch embed: conv [D, C, 2, 2] -> [D, (p, q, c)], W_rt^T (oasis_inference.py:1821-1826)
+        # patch embed: conv [D, C, 2, 2] -> [(p, q, c), D], W_rt (oasis_inference.py:1821-1826), stored
+        # K-major so that the lanes computing consecutive outputs read consecutive weights
         cw = w["x_emb.w"]
-        S.xemb_w = put(cw.float().permute(0, 2, 3, 1).reshape(d, -1), f32).data_ptr()
+        S.xemb_w = put(cw.float().permute(0, 2, 3, 1).reshape(d, -1).t().contiguous(), f32).data_ptr()
         S.xemb_b = put(w["x_emb.b"], f32).data_ptr()
         S.temb_w0 = put(w["t_emb.w0"], f32).data_ptr()
         S.temb_b0 = put(w["t_emb.b0"], f32).data_ptr()
@@ -245,7 +246,7 @@ class DiT:
         """out[M, D] = patches[M, 64] @ W_rt + b (patches in (p, q, c) column order)."""
         M = patches.shape[0]
         L.call("oasis_small_linear", L.ptr(patches), self.patch_dim, M, self.patch_dim,
-               ctypes.c_void_p(self.struct.xemb_w), L.F32, 0, self.d, ctypes.c_void_p(self.struct.xemb_b),
+               ctypes.c_void_p(self.struct.xemb_w), L.F32, 1, self.d, ctypes.c_void_p(self.struct.xemb_b),
                L.ptr(out), self.d, L.stream_handle(stream))
 
     def sub_blocks_inplace(self, ws, B, T, ada, ada_fstride, j0, j1, stream=None):

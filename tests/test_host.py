@@ -116,8 +116,8 @@ def test_dit_packing_patch_embed_and_action_pad():
     lat = torch.randn(2, 16, 18, 32, generator=torch.Generator().manual_seed(2))
     patches = oracle.patchify_to_output_space(lat)                  # [2, 144, 64], (p, q, c) columns
     xw = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.xemb_w)]
-    assert xw.dtype == torch.float32 and xw.shape == (128, 64)  # the reference's fp32 W_rt^T (1821-1826)
-    got = patches @ xw.t() + w["x_emb.b"]
+    assert xw.dtype == torch.float32 and xw.shape == (64, 128)  # the reference's fp32 W_rt, K-major (1821-1826)
+    got = patches @ xw + w["x_emb.b"]
     ref = oracle.patch_embed(lat, {k: v.float() for k, v in w.items()})
     assert torch.allclose(got, ref, atol=1e-5 * ref.abs().max().item())
     cw = dit._keep[[t.data_ptr() for t in dit._keep].index(dit.struct.cond_w)]
