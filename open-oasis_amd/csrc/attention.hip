@@ -37,6 +37,19 @@ __device__ __forceinline__ bf16x8 load8_bf16<float>(const float* p) {
   return pack8(v);
 }
 
+// 8 consecutive K / V elements at element offset e of a (frame, head) block: bf16 blocks through a
+// buffer resource (scalar base, 32-bit lane offset), which stages faster than 64-bit addresses
+template <typename T>
+__device__ __forceinline__ bf16x8 load8_kv(__amdgpu_buffer_rsrc_t r, const T* base, int e);
+template <>
+__device__ __forceinline__ bf16x8 load8_kv<bf16>(__amdgpu_buffer_rsrc_t r, const bf16*, int e) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)e * 2, 0, 0));
+}
+template <>
+__device__ __forceinline__ bf16x8 load8_kv<float>(__amdgpu_buffer_rsrc_t, const float* base, int e) {
+  return load8_bf16<float>(base + e);
+}
+
 template <typename T>
 __device__ __forceinline__ void store4(T* p, float a, float b, float c, float d);
 template <>
@@ -114,6 +127,7 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const __amdgpu_buffer_rsrc_t Krs = buffer_rsrc(Kb), Vrs = buffer_rsrc(Vb);  // bf16 blocks: Lk * 128 bytes
   for (int ks0 = 0; ks0 < a.Lk; ks0 += KS) {
     __syncthreads();
     {
@@ -122,15 +136,14 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
 #pragma unroll
       for (int u = 0; u < KPER; ++u) {
         const int c = min(tid + u * NT, KCH - 1);
-        kv[u] = load8_bf16<T>(Kb + (int64_t)min(ks0 + (c >> 3), a.Lk - 1) * 64 + (c & 7) * 8);
+        kv[u] = load8_kv<T>(Krs, Kb, min(ks0 + (c >> 3), a.Lk - 1) * 64 + (c & 7) * 8);
       }
 #pragma unroll
       for (int u = 0; u < VPER; ++u) {
         const int b = min(tid + u * NT, VBL - 1);
         const int kb = b >> 3, db = b & 7;
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
-          vv[u][r] = load8_bf16<T>(Vb + (int64_t)min(ks0 + kb * 8 + r, a.Lk - 1) * 64 + db * 8);
+        for (int r = 0; r < 8; ++r) vv[u][r] = load8_kv<T>(Vrs, Vb, min(ks0 + kb * 8 + r, a.Lk - 1) * 64 + db * 8);
       }
 #pragma unroll
       for (int u = 0; u < KPER; ++u) {
@@ -275,6 +288,8 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
   OASIS_REQUIRE(n_bh > 0 && n_bh <= 65535, OASIS_ERR_SHAPE, "attention: bad head count %lld", (long long)n_bh);
   OASIS_REQUIRE((a.Lq / 16 + 1) * n_bh < (1ll << 31), OASIS_ERR_SHAPE, "attention: too many query blocks");
   OASIS_REQUIRE(a.Lq > 0 && a.Lk > 0, OASIS_ERR_SHAPE, "attention: empty sequence");
+  // K and V rows are addressed by 32-bit offsets within a (frame, head) block
+  OASIS_REQUIRE(a.Lk < (1 << 24), OASIS_ERR_SHAPE, "attention: Lk=%d must be below 2^24", a.Lk);
   // staging: short sequences (up to 32 or 64 keys: the temporal windows) and whole frames (up
   // to 160 keys, 144 per DiT frame; up to 192) in one chunk; up to 576 keys (the VAE) staged at
   // once (158 KB of LDS) and consumed in 64-key chunks by two waves per query block; longer
