@@ -26,11 +26,12 @@ constexpr int UNROLL = 4;   // pipeline steps whose loads are issued together
 // TILED: W in 16-row MFMA tile order (for tile t and 32-wide K step s, the 64 lanes' 16-byte
 // pieces back to back, lane l holding row 16t + (l & 15), columns 32s + 8(l >> 4) .. +7), so a
 // wave's load instruction reads 1 KB contiguous; else row-major [N, K].
+// block / nblocks: this workgroup's index among the nblocks that share the tiles
 template <int RG, int KS, bool TILED>
-__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, int R,
-                                                   const bf16* __restrict__ W, int N, int K,
-                                                   const float* __restrict__ b, float* __restrict__ out,
-                                                   int64_t ld_out, int act_in, int act_out, int accumulate) {
+__device__ __forceinline__ void gemv_tiles(const float* __restrict__ x, int64_t ldx, int R, const bf16* __restrict__ W,
+                                           int N, int K, const float* __restrict__ b, float* __restrict__ out,
+                                           int64_t ld_out, int act_in, int act_out, int accumulate, int block,
+                                           int nblocks) {
   static_assert(KS == 1 || KS == 2 || KS == 4, "waves per tile");
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   const int pitch = K + 8;  // bf16 elements per LDS row
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   const int lane = threadIdx.x & 63, lr = lane & 15, g = lane >> 4, wave = threadIdx.x >> 6;
   // KS waves per tile, each over K / KS (a multiple of KSTEP)
   const int tiles_per_block = (blockDim.x >> 6) / KS;
-  const int waves_total = gridDim.x * tiles_per_block;
+  const int waves_total = nblocks * tiles_per_block;
   const int tiles = N >> 4;
   const int kpart = wave % KS, kq = K / KS;
   // row group q covers conditioning rows 16q..16q+15; lanes whose row is >= R feed zeros to the
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   for (int j = 0; j < 8; ++j) zero[j] = f2bf(0.f);
   // KS > 1: every wave of the workgroup runs the same number of iterations (one tile per
   // workgroup per iteration), so the barriers of the reduction below are uniform
-  for (int tile0 = blockIdx.x * tiles_per_block; tile0 < tiles; tile0 += waves_total) {
+  for (int tile0 = block * tiles_per_block; tile0 < tiles; tile0 += waves_total) {
     const int tile = tile0 + wave / KS;
     const bool has_tile = tile < tiles;
     if (KS == 1 && !has_tile) continue;  // no barriers to keep in step with
@@ -145,6 +146,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
       for (int i = 0; i < 4; ++i) o[i] = v[i];
     }
   }
+}
+
+template <int RG, int KS, bool TILED>
+__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, int R,
+                                                   const bf16* __restrict__ W, int N, int K,
+                                                   const float* __restrict__ b, float* __restrict__ out,
+                                                   int64_t ld_out, int act_in, int act_out, int accumulate) {
+  gemv_tiles<RG, KS, TILED>(x, ldx, R, W, N, K, b, out, ld_out, act_in, act_out, accumulate, blockIdx.x, gridDim.x);
 }
 
 }  // namespace
@@ -262,15 +271,15 @@ constexpr int F32_CH = 4;    // 256-wide K chunks of a weight row held in regist
 // workgroup stages x, so the HBM latency overlaps the staging; longer rows take further groups of
 // 1024 columns. The multiplied row can be two inputs side by side: columns [0, K1) from x and
 // [K1, K) from x2 (K1 = K without a second input).
-__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ x, int64_t ldx, int K1,
-                                                       const float* __restrict__ x2, int64_t ldx2, int R,
-                                                       const float* __restrict__ W, int N, int K,
-                                                       const float* __restrict__ b, float* __restrict__ out,
-                                                       int64_t ld_out, int act_in, int act_out, int accumulate) {
+__device__ __forceinline__ void gemv_f32_rows(const float* __restrict__ x, int64_t ldx, int K1,
+                                              const float* __restrict__ x2, int64_t ldx2, int R,
+                                              const float* __restrict__ W, int N, int K,
+                                              const float* __restrict__ b, float* __restrict__ out, int64_t ld_out,
+                                              int act_in, int act_out, int accumulate, int block) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  float* xs = reinterpret_cast<float*>(smem_raw);  // [F32_RP][K]
+  float* xs = reinterpret_cast<float*>(smem_raw);  // [R][K], R <= F32_RP
   const int lane = threadIdx.x & 63;
-  const int64_t n0 = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * F32_NU;
+  const int64_t n0 = ((int64_t)block * (blockDim.x >> 6) + (threadIdx.x >> 6)) * F32_NU;
   auto load_group = [&](int kb, f32x4 (&w)[F32_NU][F32_CH]) {
 #pragma unroll
     for (int u = 0; u < F32_NU; ++u)
@@ -360,7 +369,57 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
   }
 }
 
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ x, int64_t ldx, int K1,
+                                                       const float* __restrict__ x2, int64_t ldx2, int R,
+                                                       const float* __restrict__ W, int N, int K,
+                                                       const float* __restrict__ b, float* __restrict__ out,
+                                                       int64_t ld_out, int act_in, int act_out, int accumulate) {
+  gemv_f32_rows(x, ldx, K1, x2, ldx2, R, W, N, K, b, out, ld_out, act_in, act_out, accumulate, blockIdx.x);
+}
+
+// The two adaLN projections of a step's conditioning rows in one launch: workgroups [0, nb32) run
+// the final layer's fp32 rows (gemv_f32_rows), the rest the sub-blocks' bf16 rows in MFMA tile
+// order (gemv_tiles, one wave per 16-row tile). Both read the same rows x (SiLU applied), write
+// into one output with row stride ld_out, and stage at most R * (K + 8) * 4 bytes of LDS.
+__global__ __launch_bounds__(256) void gemv_adaln_pair_kernel(const float* __restrict__ x, int64_t ldx, int R,
+                                                              const bf16* __restrict__ W16, int N16,
+                                                              const float* __restrict__ b16, float* __restrict__ out16,
+                                                              const float* __restrict__ W32, int N32,
+                                                              const float* __restrict__ b32, float* __restrict__ out32,
+                                                              int K, int64_t ld_out, int nb32) {
+  if ((int)blockIdx.x < nb32)
+    gemv_f32_rows(x, ldx, K, nullptr, 0, R, W32, N32, K, b32, out32, ld_out, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
+                  blockIdx.x);
+  else
+    gemv_tiles<1, 1, true>(x, ldx, R, W16, N16, K, b16, out16, ld_out, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
+                           blockIdx.x - nb32, gridDim.x - nb32);
+}
+
 namespace oasis {
+
+// out16[r, :N16] = W16 silu(x_r) + b16 (bf16 weights in 16-row tile order) and
+// out32[r, :N32] = W32 silu(x_r) + b32 (fp32 weights) for R <= 8 rows in one launch. Returns 1
+// without launching when the shapes are outside what the pair kernel covers.
+int gemv_adaln_pair(const float* x, int64_t ldx, int64_t R, const void* W16, int64_t N16, const float* b16,
+                    float* out16, const float* W32, int64_t N32, const float* b32, float* out32, int64_t K,
+                    int64_t ld_out, hipStream_t s) {
+  if (!x || !W16 || !W32 || !out16 || !out32 || !oasis_aligned(16, W16, W32, x) || R < 1 || R > F32_RP ||
+      K % KSTEP != 0 || K > 1024 || ldx < K || ldx % 4 != 0 || N16 % 16 != 0 || N16 / 16 < 512 ||
+      N16 >= (1ll << 31) || N32 < 1 || N32 >= (1ll << 31) || ld_out < N16 || ld_out % 4 != 0)
+    return 1;
+  // the bf16 part's grid as gemv_bf16 sizes it for one row group and one wave per tile
+  const size_t smem = 2 * (size_t)R * (size_t)(K + 8) * sizeof(bf16) > (size_t)R * K * sizeof(float)
+                          ? 2 * (size_t)R * (size_t)(K + 8) * sizeof(bf16)
+                          : (size_t)R * K * sizeof(float);
+  const int resident = (int)std::min<size_t>(8, (160 * 1024) / smem);
+  const int tiles = (int)(N16 / 16);
+  const int nb16 = std::min(std::min((tiles + 3) / 4, 2048), std::max(1, resident) * 256 * 2);
+  const int nb32 = (int)((N32 + 4 * F32_NU - 1) / (4 * F32_NU));
+  hipLaunchKernelGGL(gemv_adaln_pair_kernel, dim3((unsigned)(nb32 + nb16)), dim3(256), smem, s, x, ldx, (int)R,
+                     static_cast<const bf16*>(W16), (int)N16, b16, out16, W32, (int)N32, b32, out32, (int)K, ld_out,
+                     nb32);
+  return check_launch("gemv_adaln_pair");
+}
 
 int gemv_f32_cat(const float* x, int64_t ldx, int64_t K1, const float* x2, int64_t ldx2, int64_t R, const float* W,
                  int64_t N, int64_t K, const float* b, float* out, int64_t ld_out, int act_in, int act_out,

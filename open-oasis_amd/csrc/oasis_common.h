@@ -53,6 +53,12 @@ int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_part
 int gemv_f32_cat(const float* x, int64_t ldx, int64_t K1, const float* x2, int64_t ldx2, int64_t R, const float* W,
                  int64_t N, int64_t K, const float* b, float* out, int64_t ld_out, int act_in, int act_out,
                  int accumulate, hipStream_t s);
+// Both adaLN projections of R <= 8 rows in one launch: W16 bf16 in 16-row tile order and W32
+// fp32, each applied to silu(x) (gemv.hip). Returns 1, launching nothing, for shapes it does not
+// cover (the caller then runs oasis_gemv_bf16_tiled and oasis_gemv_f32).
+int gemv_adaln_pair(const float* x, int64_t ldx, int64_t R, const void* W16, int64_t N16, const float* b16,
+                    float* out16, const float* W32, int64_t N32, const float* b32, float* out32, int64_t K,
+                    int64_t ld_out, hipStream_t s);
 // Causal temporal attention (attention.hip); q_frame >= 0 computes only that query frame of
 // each group and writes it as a single frame: out [B*P, n_heads*64].
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,

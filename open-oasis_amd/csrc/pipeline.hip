@@ -189,6 +189,10 @@ int cond_mlp(const oasis_dit_weights_t* w, const float* t, const float* action, 
 // final layer's (fp32 weights) at column n_sub*6D
 int adaln_rows(const oasis_dit_weights_t* w, const float* cond, int64_t R, float* ada, hipStream_t s) {
   const int64_t D = w->d_model, NA = ada_width(w), NS = (int64_t)w->n_sub * 6 * D;
+  // up to 8 rows (a step, a frame): one launch for both
+  const int pair = oasis::gemv_adaln_pair(cond, D, R, w->ada_w, NS, w->ada_b, ada, w->final_ada_w, 2 * D,
+                                          w->final_ada_b, ada + NS, D, NA, s);
+  if (pair != 1) return pair;
   OASIS_TRY(oasis_gemv_bf16_tiled(cond, D, R, w->ada_w, NS, D, w->ada_b, ada, NA, OASIS_ACT_SILU, OASIS_ACT_NONE, 0,
                                   s));
   return oasis_gemv_f32(cond, D, R, w->final_ada_w, 2 * D, D, w->final_ada_b, ada + NS, NA, OASIS_ACT_SILU,
