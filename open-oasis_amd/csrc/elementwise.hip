@@ -118,14 +118,9 @@ int ew_launch(const void* a, const void* b, const void* c, const void* d, void* 
   return oasis::check_launch(what);
 }
 
-__global__ void ddim_kernel(float* chunk, const float* v, int64_t n, float c0, float c1, float c2, float c3,
-                            float c4, float c5) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const float x = chunk[i];
-    const float x0 = c0 * x - c1 * v[i];
-    const float eps = (c2 * x - x0) * c3;
-    chunk[i] = c4 * x0 + c5 * eps;
-  }
+__global__ void ddim_kernel(float* chunk, const float* v, int64_t n, DdimCoeffs k) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    chunk[i] = ddim_step(chunk[i], v[i], k);
 }
 
 // latent row r = (h*2+p)*(2gw) + (w*2+q), col c  <-  chunk row h*gw+w, col (p*2+q)*C + c
@@ -403,8 +398,8 @@ extern "C" int oasis_ddim_update(float* chunk, const float* v, int64_t n, float 
   OASIS_REQUIRE(chunk && v, OASIS_ERR_NULL, "ddim_update: null pointer");
   OASIS_REQUIRE(n >= 0, OASIS_ERR_SHAPE, "ddim_update: negative n");
   if (n == 0) return OASIS_OK;
-  hipLaunchKernelGGL(ddim_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), chunk, v, n,
-                     c0, c1, c2, c3, c4, c5);
+  const DdimCoeffs k = {{c0, c1, c2, c3, c4, c5}};
+  hipLaunchKernelGGL(ddim_kernel, dim3(ew_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), chunk, v, n, k);
   return oasis::check_launch("ddim_update");
 }
 

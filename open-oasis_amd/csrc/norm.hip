@@ -379,7 +379,9 @@ __global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x,
                                                           const float* __restrict__ scale_p1,
                                                           const float* __restrict__ shift, int64_t ada_fs,
                                                           const float* __restrict__ W, const float* __restrict__ fb,
-                                                          float* __restrict__ v_out, float eps) {
+                                                          float* __restrict__ v_out, float eps,
+                                                          float* __restrict__ chunk, int64_t chunk_row0,
+                                                          DdimCoeffs ddim) {
   constexpr int D = NC * 256;
   constexpr int RB = 4;     // rows per workgroup (one wave each in phase 1)
   constexpr int NW = 8;     // outputs per wave (32 per workgroup, two workgroups per row block)
@@ -497,17 +499,26 @@ __global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x,
   const int idx = lane >> 1, u = idx / RB, r = idx % RB;
   const int64_t row = m0 + r;
   const int n = nbase + u;
-  if ((lane & 1) == 0 && row < M) v_out[row * 64 + n] = total + (fb ? fb[n] : 0.f);
+  if ((lane & 1) == 0 && row < M) {
+    const float vo = total + (fb ? fb[n] : 0.f);
+    v_out[row * 64 + n] = vo;
+    // the fused DDIM step: rows from chunk_row0 on are the denoised frame, chunk [., 64]
+    if (chunk && row >= chunk_row0) {
+      float* cp = chunk + (row - chunk_row0) * 64 + n;
+      *cp = ddim_step(*cp, vo, ddim);
+    }
+  }
 }
 
 template <int NC>
 hipError_t final_layer_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* scale_p1, const float* shift,
-                          int64_t afs, const float* W, const float* fb, float* v_out, float eps, hipStream_t s) {
+                          int64_t afs, const float* W, const float* fb, float* v_out, float eps, float* chunk,
+                          int64_t chunk_row0, const DdimCoeffs& dc, hipStream_t s) {
   const dim3 grid((unsigned)(2 * ((M + 3) / 4))), block(256);  // 4 rows x 2 output halves per row block
 #define OASIS_FIN(NPV)                                                                                            \
   hipLaunchKernelGGL((final_layer_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, scale_p1, \
-                     shift, afs, W, fb, v_out, eps)
+                     shift, afs, W, fb, v_out, eps, chunk, chunk_row0, dc)
   switch (np) {
     case 0: OASIS_FIN(0); break;
     case 1: OASIS_FIN(1); break;
@@ -659,8 +670,12 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
 int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* scale_p1,
                 const float* shift, int64_t ada_fstride, const float* W, const float* b, float* v_out, float eps,
-                hipStream_t s) {
+                hipStream_t s, float* chunk, int64_t chunk_row0, const float* ddim) {
   OASIS_REQUIRE(x && scale_p1 && shift && W && v_out, OASIS_ERR_NULL, "final_layer: null pointer");
+  OASIS_REQUIRE(!chunk || (ddim && chunk_row0 >= 0 && chunk_row0 < M), OASIS_ERR_ARG,
+                "final_layer: the fused DDIM update needs its coefficients and a first row in [0, M)");
+  DdimCoeffs dc = {};
+  if (chunk) memcpy(dc.c, ddim, sizeof(dc.c));
   OASIS_REQUIRE(oasis_aligned(16, x, partial, bias, gate, scale_p1, shift, W), OASIS_ERR_ARG,
                 "final_layer: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "final_layer: bad M/rows_per_frame");
@@ -668,10 +683,10 @@ int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_part
   OASIS_REQUIRE(n_partials <= 1 || partial_stride >= M * D, OASIS_ERR_ARG, "final_layer: partial_stride too small");
   hipError_t e;
   switch (D) {
-    case 256: e = final_layer_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
-    case 512: e = final_layer_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
-    case 1024: e = final_layer_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
-    case 2048: e = final_layer_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, s); break;
+    case 256: e = final_layer_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, chunk, chunk_row0, dc, s); break;
+    case 512: e = final_layer_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, chunk, chunk_row0, dc, s); break;
+    case 1024: e = final_layer_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, chunk, chunk_row0, dc, s); break;
+    case 2048: e = final_layer_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, scale_p1, shift, ada_fstride, W, b, v_out, eps, chunk, chunk_row0, dc, s); break;
     default:
       set_error("final_layer: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
       return OASIS_ERR_SHAPE;

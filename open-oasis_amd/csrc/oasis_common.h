@@ -43,11 +43,13 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
                 hipStream_t s);
 // The DiT's final layer in fp32 (norm.hip): the pending residual (n_partials split-K slices +
 // bias, gated), LN, modulate with the frame's (scale_p1, shift) rows, then v_out[M, 64] =
-// h @ W^T + b with W fp32 [64, D].
+// h @ W^T + b with W fp32 [64, D]. With chunk set, rows chunk_row0.. also take one DDIM step of
+// chunk [M - chunk_row0, 64] with those v rows (ddim: host array of the 6 coefficients, in
+// oasis_ddim_update order).
 int final_layer(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* scale_p1,
                 const float* shift, int64_t ada_fstride, const float* W, const float* b, float* v_out, float eps,
-                hipStream_t s);
+                hipStream_t s, float* chunk = nullptr, int64_t chunk_row0 = 0, const float* ddim = nullptr);
 // oasis_gemv_f32 whose multiplied row is two inputs side by side: columns [0, K1) from x
 // [R, ldx] and [K1, K) from x2 [R, ldx2] (gemv.hip).
 int gemv_f32_cat(const float* x, int64_t ldx, int64_t K1, const float* x2, int64_t ldx2, int64_t R, const float* W,
@@ -188,6 +190,18 @@ OASIS_DEV float row16_sum(float v) {
 OASIS_DEV float row16_max(float v) {
   v = oct_max(v);
   return fmaxf(v, dpp_mov<DPP_MIRROR>(v));
+}
+
+// One DDIM step of a latent element x with predicted v (oasis_inference.py:1919-1931):
+// x0 = c0 x - c1 v, eps = (c2 x - x0) c3, returns c4 x0 + c5 eps. The stand-alone update and
+// the final layer's fused update share it, so both round the same way.
+struct DdimCoeffs {
+  float c[6];
+};
+OASIS_DEV float ddim_step(float x, float v, const DdimCoeffs& k) {
+  const float x0 = k.c[0] * x - k.c[1] * v;
+  const float eps = (k.c[2] * x - x0) * k.c[3];
+  return k.c[4] * x0 + k.c[5] * eps;
 }
 
 // ---- wave reductions (64 lanes) ---------------------------------------------

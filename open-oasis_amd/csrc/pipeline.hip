@@ -443,13 +443,15 @@ int dit_args(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64
 }
 
 // final layer (oasis_inference.py:1497-1521): adaLN(2 chunks) + LN + modulate + linear,
-// with any pending FC2 residual folded into the LN pass
+// with any pending FC2 residual folded into the LN pass. With chunk set, the DDIM update of
+// chunk from the v rows chunk_row0.. (oasis_inference.py:1919-1931) runs in the same launch.
 int dit_final(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M, const float* ada, int64_t fs,
-              const Pending& pend, float* v_out, oasis_stream_t stream) {
+              const Pending& pend, float* v_out, oasis_stream_t stream, float* chunk = nullptr,
+              int64_t chunk_row0 = 0, const float* ddim = nullptr) {
   const int64_t D = w->d_model, P = (int64_t)w->grid_h * w->grid_w;
   const float* fa = ada + (int64_t)w->n_sub * 6 * D;  // shift, scale_p1
   return oasis::final_layer(buf->x, M, D, buf->partial, pend.n, M * D, pend.bias, pend.gate, fs, P, fa + D, fa, fs,
-                            w->final_w, w->final_b, v_out, kLnEps, (hipStream_t)stream);
+                            w->final_w, w->final_b, v_out, kLnEps, (hipStream_t)stream, chunk, chunk_row0, ddim);
 }
 
 }  // namespace
@@ -696,8 +698,7 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
                                    stream));
       const float* ada_cur = ada + (1 + i) * NA;  // the generated frame's rows at step i
       OASIS_TRY(dit_blocks(w, buf, 1, 1, ada_cur, NA, 0, w->n_sub, &pend, stream, use));
-      OASIS_TRY(dit_final(w, buf, P, ada_cur, NA, pend, v_out, stream));
-      OASIS_TRY(oasis_ddim_update(chunk, v_out, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5], stream));
+      OASIS_TRY(dit_final(w, buf, P, ada_cur, NA, pend, v_out, stream, chunk, 0, c));
       continue;
     }
     // z = [context frame; patch-embedded chunk] (oasis_inference.py:1911-1913)
@@ -707,9 +708,7 @@ int frame_steps(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, co
                                  buf->x + P * D, D, stream));
     const int64_t fs = (1 + i) * NA;  // frame 0 -> ada row 0, frame 1 -> ada row 1 + i
     OASIS_TRY(dit_blocks(w, buf, 1, 2, ada, fs, 0, w->n_sub, &pend, stream, kv ? save : KvPass()));
-    OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream));
-    OASIS_TRY(oasis_ddim_update(chunk, v_out + P * w->patch_dim, P * w->patch_dim, c[0], c[1], c[2], c[3], c[4], c[5],
-                                stream));
+    OASIS_TRY(dit_final(w, buf, 2 * P, ada, fs, pend, v_out, stream, chunk, P, c));
   }
   return OASIS_OK;
 }

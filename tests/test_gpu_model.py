@@ -286,6 +286,31 @@ def test_ddim_frame_config3(c3):
     assert cc >= COS_STEP and cf >= COS_STEP, (cc, cf)
 
 
+def test_frame_ddim_update_fused_into_the_final_layer(c3):
+    """The frame's DDIM update runs inside the final layer's launch; on a one-step frame it gives
+    the chunk the stand-alone oasis_ddim_update gives from the same noise and v rows, bit for bit
+    (with and without the K/V cache)."""
+    c, dit, vae = c3
+    ac = pkg.schedule.cosine_alphas_cumprod()
+    steps = c["steps"][:1]
+    noise = cuda(oracle.patchify_to_output_space(c["x_T"])[0])
+    ctx = cuda(oracle.patchify_to_output_space(c["ctx_latent"])[0])
+    coeffs = pkg.schedule.ddim_coefficients(ac, steps)
+    P = dit.P
+    for kv in (False, True):
+        fp = pkg.FramePipeline(dit, vae, steps, ac, kv_cache=kv)
+        fp.set_inputs(noise, ctx, c["ctx_t"], cuda(c["ctx_action"]), cuda(c["gen_action"]))
+        fp.run()
+        torch.cuda.synchronize()
+        v = fp.ws.v_out[P:2 * P].clone()   # the generated frame's v rows of the T=2 step
+        want = noise.clone()
+        pkg._lib.call("oasis_ddim_update", pkg._lib.ptr(want), pkg._lib.ptr(v), want.numel(),
+                      *[ctypes.c_float(z) for z in coeffs], pkg._lib.stream_handle())
+        torch.cuda.synchronize()
+        assert torch.equal(fp.chunk, want), "fused DDIM update differs (kv_cache=%s)" % kv
+        assert not torch.equal(fp.chunk, noise)
+
+
 def test_dit_from_an_upstream_checkpoint_steps_identically(tmp_path):
     """A DiT built from an upstream-named safetensors checkpoint (checkpoint.load_dit) runs the
     same step, bit for bit, as one built from the weight dict it was written from."""
