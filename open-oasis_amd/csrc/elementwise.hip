@@ -312,8 +312,11 @@ __device__ __forceinline__ void st8<bf16>(bf16* p, const float* v) {
 // (q * pos_mod + pos) * pos_div + rem): thread t owns column group c8 = 8t of Q, K and V, loads its
 // 8 cos / sin values once for all of them, and issues the loads of all its rows before any store.
 // QKV rows are read with streaming loads and Q, K, V written with streaming stores (each byte is
-// touched once). The elementwise kernels above stream their operands the same way.
-constexpr int RPG = 4;
+// touched once). The elementwise kernels above stream their operands the same way. One row per
+// workgroup times fastest (4608 rows: 12.9 us against 12.9 with 2 rows, 13.4 with 4 and 17.5 with
+// 8; 288 rows: 2.55 against 2.86 and 3.11 us): more, smaller workgroups spread the rows' loads and
+// stores over more waves.
+constexpr int RPG = 1;
 
 template <typename T, int MODE>
 __global__ __launch_bounds__(256) void rope_layout_kernel(const T* qkv, int64_t ldq, const float* cs, const float* sn,
