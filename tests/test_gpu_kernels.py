@@ -536,6 +536,32 @@ def test_rope_layout_surface(dt, mode):
     assert torch.equal(vo.float().cpu(), layout(x[:, :, 2]))
 
 
+@pytest.mark.parametrize("H,T", [(16, 5), (4, 3), (2, 21), (40, 2)])
+def test_rope_layout_shared_positions(H, T):
+    """T frames of 144 positions over one [144, D] table (pos_mod = 144, the layout the bench
+    times): the rows of a position share its table row, one workgroup each; with H = 40 the 320
+    column groups of a row stride over 256 threads. bf16, both output layouts."""
+    P, D = 144, H * 64
+    g = _gen(29 + H)
+    qkv = torch.randn(T * P, 3 * D, generator=g).to(torch.bfloat16)
+    cs, sn = torch.randn(P, D, generator=g), torch.randn(P, D, generator=g)
+    x = qkv.float().reshape(T, P, 3, H, 64)
+    c4 = cs.reshape(1, P, H, 64).expand(T, P, H, 64)
+    s4 = sn.reshape(1, P, H, 64).expand(T, P, H, 64)
+    for mode in (0, 1):
+        qo, ko, vo = (torch.zeros(T * P * H, 64, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+        L.call("oasis_rope_layout", L.ptr(dev(qkv)), 3 * D, L.ptr(dev(cs)), L.ptr(dev(sn)), D, 64, 1, P,
+               L.ptr(qo), L.ptr(ko), L.ptr(vo), T * P, P, H, 64, mode, L.BF16, stream())
+        sync()
+
+        def layout(t):   # [T, P, H, 64] -> the output layout of the mode
+            return t.permute(0, 2, 1, 3).reshape(-1, 64) if mode == 0 else t.reshape(-1, 64)
+        for i, (name, got) in enumerate((("q", qo), ("k", ko))):
+            ref = layout(oracle.apply_rope_swap(x[:, :, i], c4, s4))
+            assert_close(got.float(), ref, 0.99999, 8e-3, "rope_layout H=%d T=%d %s mode %d" % (H, T, name, mode))
+        assert torch.equal(vo.float().cpu(), layout(x[:, :, 2])), (H, T, mode)
+
+
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
 @pytest.mark.parametrize("tile", list(range(13)))
 def test_gemm_tile_configs(tile):
