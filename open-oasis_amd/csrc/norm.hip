@@ -363,17 +363,19 @@ __global__ __launch_bounds__(256) void residual_ln_kernel(float* __restrict__ x,
 }
 
 // The DiT's final layer in one launch, fp32 end to end as the reference keeps it
-// (oasis_inference.py:1497-1521). A workgroup takes RB = 4 rows and half of the 64 outputs:
+// (oasis_inference.py:1497-1521). A workgroup of 8 waves takes RB = 4 rows and all 64 outputs:
 //   x[m] += g * (sum_s partial[s][m] + bias)                 (NP > 0: the pending FC2 residual)
 //   h[m]  = LN(x[m]) * scale_p1[f(m)] + shift[f(m)]          (fp32, kept in LDS)
 //   v[m, n] = sum_k h[m, k] W[n, k] + b[n]                    (W fp32 [64, D])
-// Phase 1 gives each wave one row (the row in registers, two wave reductions); the workgroup of
-// output half 0 writes x back. Phase 2: wave w owns 8 outputs, read as whole weight rows (lane l
-// holds columns 4l..4l+3 of each 256-wide chunk, so each load instruction reads 1 KB of one row);
-// the first 4 rows' loads are issued before phase 1. Each lane multiplies its columns against the
-// 4 h rows (held in registers), and every (output, row) dot product is reduced across the wave.
+// Phase 1 gives waves 0-3 one row each (the row in registers, two wave reductions); that wave
+// also writes the updated row back, and no other workgroup reads the row, so the read of x and
+// its write-back cannot interleave across workgroups. Phase 2: wave w owns 8 outputs, read as
+// whole weight rows (lane l holds columns 4l..4l+3 of each 256-wide chunk, so each load
+// instruction reads 1 KB of one row); the first NU rows' loads are issued before phase 1. Each
+// lane multiplies its columns against the 4 h rows, and every (output, row) dot product is
+// reduced across the wave.
 template <int NC, int NP>
-__global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
+__global__ __launch_bounds__(512) void final_layer_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
                                                           int64_t pstride, const float* __restrict__ bias,
                                                           const float* __restrict__ gate, int64_t gate_fs, int64_t rpf,
                                                           const float* __restrict__ scale_p1,
@@ -384,20 +386,19 @@ __global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x,
                                                           DdimCoeffs ddim) {
   constexpr int D = NC * 256;
   constexpr int RB = 4;     // rows per workgroup (one wave each in phase 1)
-  constexpr int NW = 8;     // outputs per wave (32 per workgroup, two workgroups per row block)
+  constexpr int NW = 8;     // outputs per wave (8 waves: all 64)
   constexpr int NU = NC <= 4 ? 4 : 2;  // weight rows in registers at once
   __shared__ __attribute__((aligned(16))) float hs[RB][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = blockIdx.x & 1;
-  const int64_t m0 = (int64_t)(blockIdx.x >> 1) * RB;
-  const int nbase = half * 32 + wave * NW;
+  const int64_t m0 = (int64_t)blockIdx.x * RB;
+  const int nbase = wave * NW;
   f32x4 w[NU][NC];
 #pragma unroll
   for (int u = 0; u < NU; ++u)
 #pragma unroll
     for (int c = 0; c < NC; ++c) w[u][c] = *reinterpret_cast<const f32x4*>(W + (int64_t)(nbase + u) * D + c * 256 + 4 * lane);
-  // ---- phase 1: residual + LN + modulate of row m0 + wave
-  {
+  // ---- phase 1: residual + LN + modulate of row m0 + wave (waves 0..RB-1)
+  if (wave < RB) {
     const int rr = wave;
     const int64_t row = m0 + rr;
     if (row >= M) {
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(256) void final_layer_kernel(float* __restrict__ x,
             for (int p = 0; p < NP; ++p) acc += pv[p][c][j];
             v[c][j] += gv[c][j] * acc;
           }
-          if (half == 0) store4<float>(xr + c * 256 + lane * 4, v[c]);
+          store4<float>(xr + c * 256 + lane * 4, v[c]);
         }
       }
       float s = 0.f;
@@ -515,7 +516,7 @@ hipError_t final_layer_np(int np, float* x, int64_t M, const float* part, int64_
                           const float* gate, int64_t gfs, int64_t rpf, const float* scale_p1, const float* shift,
                           int64_t afs, const float* W, const float* fb, float* v_out, float eps, float* chunk,
                           int64_t chunk_row0, const DdimCoeffs& dc, hipStream_t s) {
-  const dim3 grid((unsigned)(2 * ((M + 3) / 4))), block(256);  // 4 rows x 2 output halves per row block
+  const dim3 grid((unsigned)((M + 3) / 4)), block(512);  // 4 rows and all 64 outputs per workgroup
 #define OASIS_FIN(NPV)                                                                                            \
   hipLaunchKernelGGL((final_layer_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, scale_p1, \
                      shift, afs, W, fb, v_out, eps, chunk, chunk_row0, dc)

@@ -459,6 +459,8 @@ class DiTStep:
         self.ws = dit.workspace(self.M, max_cond=max(16, B * T))
         self.patches = torch.zeros(self.M, dit.patch_dim, device=dit.device)
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dit.device)
+        # the buffers were zero-filled on the allocating stream: work on self.stream follows that
+        self.stream.wait_stream(torch.cuda.current_stream(dit.device))
         self.graph = None
 
     def set_inputs(self, patches, t, actions):
@@ -517,6 +519,8 @@ class FramePipeline:
         self.ctx_z = torch.zeros(P, dit.d, device=dev)
         self.coeffs = (ctypes.c_float * (6 * self.n))(*ddim_coefficients(alphas_cumprod, self.steps))
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
+        # the buffers were zero-filled on the allocating stream: work on self.stream follows that
+        self.stream.wait_stream(torch.cuda.current_stream(dev))
         self.graph = None
 
     def set_inputs(self, noise_patches, ctx_patches, ctx_t, ctx_action, gen_action):
@@ -601,6 +605,10 @@ class VideoPipeline:
         self.coeffs = (ctypes.c_float * (6 * self.n))(*ddim_coefficients(alphas_cumprod, self.steps))
         self.stream = stream if stream is not None else torch.cuda.Stream(device=dev)
         self.decode_stream = torch.cuda.Stream(device=dev) if overlap_decode else None
+        # the buffers were zero-filled on the allocating stream: work on the others follows that
+        for st in (self.stream, self.decode_stream):
+            if st is not None:
+                st.wait_stream(torch.cuda.current_stream(dev))
         self.graph = None
         self.graphs, self.decode_graphs = [], []
         self._ev_dit = [torch.cuda.Event() for _ in range(nb)]

@@ -311,6 +311,39 @@ def test_frame_ddim_update_fused_into_the_final_layer(c3):
         assert not torch.equal(fp.chunk, noise)
 
 
+@pytest.mark.parametrize("B,T", [(8, 4), (1, 2)])
+def test_final_layer_with_pending_residual_matches_residual_ln_then_final(B, T):
+    """oasis_dit_forward folds the last FC2's split-K partials (bias + gated residual) into the
+    final layer's launch. At 4608 rows (config 4's batch, more workgroups than run at once) and at
+    288 rows it leaves x bit-equal to oasis_dit_sub_blocks (which applies that residual with
+    oasis_residual_ln), and its v rows equal oasis_dit_final's on that x: every row's residual is
+    added once, whatever order the workgroups run in."""
+    dr = synth.Draw(57)
+    w = synth.dit_weights(dr, n_blocks=1)
+    dit = pkg.DiT(w, "cuda", t_max=max(T, 2))
+    M, D = B * T * dit.P, dit.d
+    ws = dit.workspace(M, max_cond=B * T)
+    ada = dit.adaln_from_cond(cuda(dr.normal(B * T, D)), ws)
+    x0 = cuda(dr.normal(M, D))
+    ws.x[:M].copy_(x0)
+    v_fused = torch.zeros(M, 64, device="cuda")
+    dit.forward_inplace(ws, B, T, ada, dit.ada_width, v_fused)
+    torch.cuda.synchronize()
+    x_fused = ws.x[:M].clone()
+    ws.x[:M].copy_(x0)
+    dit.sub_blocks_inplace(ws, B, T, ada, dit.ada_width, 0, dit.n_sub)
+    v_sep = torch.zeros(M, 64, device="cuda")
+    L = pkg._lib
+    L.call("oasis_dit_final", ctypes.byref(dit.struct), ctypes.byref(ws.struct), M, L.ptr(ada), dit.ada_width,
+           L.ptr(v_sep), L.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(x_fused, ws.x[:M]), "residual applied differently (B=%d, T=%d)" % (B, T)
+    e = _rel(v_fused, v_sep)
+    print("final layer with pending residual, M=%d: v rel %.2e, bit-equal %s"
+          % (M, e, torch.equal(v_fused, v_sep)), flush=True)
+    assert e < 1e-6, e
+
+
 def test_dit_from_an_upstream_checkpoint_steps_identically(tmp_path):
     """A DiT built from an upstream-named safetensors checkpoint (checkpoint.load_dit) runs the
     same step, bit for bit, as one built from the weight dict it was written from."""

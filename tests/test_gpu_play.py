@@ -77,10 +77,12 @@ def test_session_ddim_switch_resets_and_reuses_graphs():
     fp2 = s.fp
     assert not torch.equal(fp2.ctx_patches, s.prompt)  # context rolled
     s.set_ddim_steps(3)
+    s.stream.synchronize()  # the reset copies run on the session's stream
     assert s.ddim_steps == 3 and s.frame_index == 0 and s.fp is not fp2
     assert torch.equal(s.fp.ctx_patches, s.prompt)
     s.frame(a)
     s.set_ddim_steps(2)
+    s.stream.synchronize()
     assert s.fp is fp2 and torch.equal(fp2.ctx_patches, s.prompt)
     s.set_ddim_steps(0)
     assert s.ddim_steps == 1
