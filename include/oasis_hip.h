@@ -482,10 +482,10 @@ int oasis_dit_forward(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* b
 /* One full DiT denoising step for B streams of T frames (B*T <= 1024): conditioning MLP
  * (t fp32 [B*T], action fp32 [B*T, ext_dim_pad]), patch embed of patches fp32 [B*T*P, 64]
  * into buf->x, every sub-block and the final layer; v_out fp32 [B*T*P, 64].
- * hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The
- * adaLN projections of all sub-blocks run as one pass over the stacked adaLN weights before
- * the first sub-block (with OASIS_ADALN_OVERLAP=1 in the environment: on a library-owned
- * side stream, each sub-block waiting only for its own rows).
+ * hid/cond/ada: conditioning scratch as in oasis_dit_conditioning (B*T rows). The adaLN
+ * rows of every consumer (the sub-blocks' bf16 stack and the final layer's fp32 rows) come
+ * from one pass over the stacked adaLN weights before the first sub-block (one launch for up
+ * to 8 conditioning rows).
  * (dit_forward_device with compute_cond_for_frame, oasis_inference.py:1406-1526.) */
 int oasis_dit_step(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t B,
                    int64_t T, const float* t, const float* action, const float* patches,
@@ -577,6 +577,14 @@ int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* bu
  * batches the decodes of several frames or streams.) */
 int oasis_vae_decode_batch(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
                            const float* latents, float* frames, oasis_stream_t stream);
+
+/* B latents fp32 [B, L, latent_dim] -> the predictor's rows pred_out fp32 [B*L, ld_pred]
+ * (ld_pred >= 3*patch^2; columns from 3*patch^2 on are not written): acc + bias, unclamped,
+ * before any unpatchify. This is what the reference's vae_decode_forward returns
+ * (vae_scr["pred_out"], oasis_inference.py:1546-1618) and vae_decode_device reads back
+ * (oasis_inference.py:1620-1634) for the host-side vae_unpatchify. */
+int oasis_vae_decode_patches(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
+                             const float* latents, float* pred_out, int64_t ld_pred, oasis_stream_t stream);
 
 /* One generated frame at T=2: conditioning, n_steps DDIM v-prediction steps, then bridge +
  * VAE decode.

@@ -138,6 +138,7 @@ SIGNATURES = {
     "oasis_dit_final": [P(DiTWeights), P(DiTBuffers), c_i64, c_p, c_i64, c_p, c_p],
     "oasis_vae_decode": [P(VAEWeights), P(VAEBuffers), c_p, c_p, c_p],
     "oasis_vae_decode_batch": [P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_p],
+    "oasis_vae_decode_patches": [P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_i64, c_p],
     "oasis_video_decode": [P(DiTWeights), P(VAEWeights), P(VAEBuffers), c_i64, c_p, c_p, c_p, c_p],
     "oasis_dit_step": [P(DiTWeights), P(DiTBuffers), c_i64, c_i64, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p],
     "oasis_ddim_frame": [P(DiTWeights), P(DiTBuffers), P(VAEWeights), P(VAEBuffers), P(KVCache), c_p, c_p, c_p,

@@ -553,10 +553,15 @@ extern "C" int oasis_dit_forward_current(const oasis_dit_weights_t* w, const oas
 namespace {
 
 // vae_decode_forward (oasis_inference.py:1546-1618) + vae_unpatchify for B latents at once: every
-// projection runs over B*L tokens, the attention per latent (B frames of L tokens).
+// projection runs over B*L tokens, the attention per latent (B frames of L tokens). With pred set,
+// the predictor writes its plain rows (acc + bias, unclamped: vae_decode_forward's pred_out) to
+// pred[B*L, ld_pred] instead of the unpatchified frames.
 int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B, const float* latent,
-               float* frame, oasis_stream_t stream) {
-  OASIS_REQUIRE(w && buf && latent && frame, OASIS_ERR_NULL, "vae_decode: null pointer");
+               float* frame, oasis_stream_t stream, float* pred = nullptr, int64_t ld_pred = 0) {
+  OASIS_REQUIRE(w && buf && latent && (frame || pred), OASIS_ERR_NULL, "vae_decode: null pointer");
+  OASIS_REQUIRE(!pred || ld_pred >= 3LL * w->patch * w->patch, OASIS_ERR_ARG,
+                "vae_decode: ld_pred=%lld is below the predictor's %lld columns", (long long)ld_pred,
+                3LL * w->patch * w->patch);
   OASIS_REQUIRE(w->depth > 0 && w->depth <= OASIS_MAX_SUB && w->n_heads > 0 && w->d_model == w->n_heads * 64,
                 OASIS_ERR_SHAPE, "vae_decode: bad depth/heads/d_model");
   OASIS_REQUIRE(buf->x && buf->h && buf->q && buf->k && buf->v && buf->attn && buf->mlp && buf->partial,
@@ -626,15 +631,21 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
   }
   OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->norm_w, w->norm_b,
                               0, buf->h, kLnEps, stream));
-  oasis_epilogue_t pred = epi_zero();
-  pred.kind = OASIS_EPI_UNPATCHIFY;
-  pred.bias = w->pred_b;
-  pred.out_f32 = frame;
-  pred.rows_per_frame = Lf;
-  pred.unpatch_grid_w = w->grid_w;
-  pred.unpatch_patch = w->patch;
-  pred.unpatch_channels = 3;
-  return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->pred_w, D, L, 3LL * w->patch * w->patch, D, pred,
+  oasis_epilogue_t pe = epi_zero();
+  pe.bias = w->pred_b;
+  if (pred) {
+    pe.kind = OASIS_EPI_STORE_F32;
+    pe.out_f32 = pred;
+    pe.ld_out = ld_pred;
+  } else {
+    pe.kind = OASIS_EPI_UNPATCHIFY;
+    pe.out_f32 = frame;
+    pe.rows_per_frame = Lf;
+    pe.unpatch_grid_w = w->grid_w;
+    pe.unpatch_patch = w->patch;
+    pe.unpatch_channels = 3;
+  }
+  return oasis::gemm_launch((const bf16*)buf->h, D, (const bf16*)w->pred_w, D, L, 3LL * w->patch * w->patch, D, pe,
                             s);
 }
 
@@ -642,12 +653,21 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
 
 extern "C" int oasis_vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, const float* latent,
                                 float* frame, oasis_stream_t stream) {
+  OASIS_REQUIRE(frame, OASIS_ERR_NULL, "vae_decode: null frame");
   return vae_decode(w, buf, 1, latent, frame, stream);
 }
 
 extern "C" int oasis_vae_decode_batch(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
                                       const float* latents, float* frames, oasis_stream_t stream) {
+  OASIS_REQUIRE(frames, OASIS_ERR_NULL, "vae_decode_batch: null frames");
   return vae_decode(w, buf, B, latents, frames, stream);
+}
+
+extern "C" int oasis_vae_decode_patches(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int64_t B,
+                                        const float* latents, float* pred_out, int64_t ld_pred,
+                                        oasis_stream_t stream) {
+  OASIS_REQUIRE(pred_out, OASIS_ERR_NULL, "vae_decode_patches: null pred_out");
+  return vae_decode(w, buf, B, latents, nullptr, stream, pred_out, ld_pred);
 }
 
 namespace {

@@ -179,47 +179,139 @@ linear_k32 = make_linear_kernel(32)
 layernorm_d1024 = make_layernorm_kernel(32)
 
 
+def padded_rows(rows):
+    """Rows per frame in the reference's TILE layout: 144 -> 160 (N_PATCH_PAD,
+    oasis_inference.py:103)."""
+    return -(-rows // TILE) * TILE
+
+
+def _surface_workspace(dev, scr, T):
+    """The DiTWorkspace a reference-named composite call runs in: scr when it is one (the
+    caller's buffers), else one kept on dev and replaced only when T frames do not fit, so calls
+    in sequence allocate nothing (the reference's composite calls never allocate,
+    oasis_inference.py:1546-1549; a call that grows it must not be inside a graph capture)."""
+    M = T * dev.P
+    if isinstance(scr, DiTWorkspace):
+        if scr.max_rows < M or scr.max_cond < T:
+            raise L.OasisError("dit_forward", -2, "workspace holds %d rows / %d cond rows, the call needs %d / %d"
+                               % (scr.max_rows, scr.max_cond, M, T))
+        return scr
+    ws = getattr(dev, "_surface_ws", None)
+    if ws is None or ws.max_rows < M or ws.max_cond < T:
+        ws = dev._surface_ws = dev.workspace(M, max_cond=max(16, T))
+    return ws
+
+
+def _padded_v(ws, dev, T):
+    """ws's v rows in the padded layout [T*160, 64]: frame t's 144 rows at t*160, the 16 pad
+    rows after them zero (written once here and never again)."""
+    Pp = padded_rows(dev.P)
+    vp = getattr(ws, "v_pad", None)
+    if vp is None or vp.shape[0] < T * Pp:
+        vp = ws.v_pad = torch.zeros(max(ws.max_rows // dev.P, T) * Pp, dev.patch_dim, device=dev.device)
+    return vp[:T * Pp]
+
+
 def dit_forward_device(z_cur, cond_list, dev, scr=None, tt_device=None, scaler=None, mean_scale=None,
                        profile_step=False):
     """DiT forward (oasis_inference.py:1438-1526).
 
-    z_cur: [T*P, D] fp32 device tensor of embedded tokens; cond_list: T conditioning
-    vectors (pre-SiLU; [D] or the reference's row-expanded [32, D]) or a [T, D] tensor;
-    dev: a ``DiT``; scr: an optional ``DiTWorkspace``. Returns v [T*P, 64] fp32 (a view
-    of the workspace, valid until the next call with it).
+    z_cur: embedded tokens, fp32 (or bf16) device tensor, either the reference's padded
+    layout [T*160, D] (SEQ = N_PATCH_PAD*T, oasis_inference.py:1445: frame t's 144 tokens at
+    row t*160, the 16 pad rows after them ignored) or packed [T*144, D].
+    cond_list: T conditioning vectors (pre-SiLU; [D] or the reference's row-expanded [32, D])
+    or a [T, D] tensor. dev: a ``DiT``. scr: a ``DiTWorkspace``, or anything else (the
+    reference's scratch dict): then a workspace kept on dev is used.
+    Returns v fp32 in the layout z_cur came in: [T*160, 64] with the pad rows zero, so that
+    ddim_step_fn's slice at gen_start = (T-1)*160 works unchanged (oasis_inference.py:1915-
+    1918), or [T*144, 64]. The result is a view of the workspace, valid until its next call.
+    Nothing is allocated once the workspace exists (the inputs are copied into it). Spatial
+    attention runs over the 144 tokens of each frame (the reference also lets the 16 pad keys
+    into every softmax, with logit 0).
     """
     assert isinstance(dev, DiT)
-    if isinstance(cond_list, (list, tuple)):
-        cond = torch.stack([c.reshape(-1, c.shape[-1])[0] for c in cond_list])
+    D, P = dev.d, dev.P
+    T = len(cond_list) if isinstance(cond_list, (list, tuple)) else cond_list.shape[0]
+    rows = z_cur.numel() // D
+    Pp = padded_rows(P)
+    if rows == T * P:
+        padded = False
+    elif rows == T * Pp:
+        padded = True
     else:
-        cond = cond_list
-    T = cond.shape[0]
-    M = z_cur.numel() // dev.d
-    if M != T * dev.P:
-        raise L.OasisError("dit_forward", -2, "z_cur has %d rows, expected T*P = %d" % (M, T * dev.P))
-    ws = scr if isinstance(scr, DiTWorkspace) else dev.workspace(M, max_cond=max(16, T))
-    ada = dev.adaln_from_cond(cond.float(), ws)
-    ws.x[:M].copy_(z_cur.reshape(M, dev.d))
+        raise L.OasisError("dit_forward", -2, "z_cur has %d rows; expected T*%d (padded) or T*%d for T=%d"
+                           % (rows, Pp, P, T))
+    ws = _surface_workspace(dev, scr, T)
+    for t in range(T):
+        c = cond_list[t]
+        ws.cond[t].copy_(c.reshape(-1, D)[0])
+    ada = dev.adaln_inplace(T, ws)
+    z = z_cur.reshape(rows, D)
+    if padded:
+        ws.x[:T * P].view(T, P, D).copy_(z.view(T, Pp, D)[:, :P])
+    else:
+        ws.x[:T * P].copy_(z)
     dev.forward_inplace(ws, 1, T, ada, dev.ada_width, ws.v_out)
-    return ws.v_out[:M]
+    if not padded:
+        return ws.v_out[:T * P]
+    out = _padded_v(ws, dev, T)
+    out.view(T, Pp, -1)[:, :P].copy_(ws.v_out[:T * P].view(T, P, -1))
+    return out
 
 
 dit_forward = dit_forward_device
 
 
-def vae_decode_forward(vae_dev, vae_scr, scaler=None, mean_scale=None):
-    """VAE decode of vae_scr.latent into vae_scr.frame (oasis_inference.py:1546-1618, with
-    the unpatchify and clamp of 1636-1645 / 2292 fused into the predictor)."""
-    assert isinstance(vae_dev, VAE) and isinstance(vae_scr, VAEWorkspace)
-    vae_dev.decode_inplace(vae_scr.latent, vae_scr.frame, vae_scr)
-    return vae_scr.frame
+def _vae_workspace(vae_dev, vae_scr):
+    if isinstance(vae_scr, VAEWorkspace):
+        return vae_scr
+    ws = getattr(vae_dev, "_surface_ws", None)
+    if ws is None:
+        ws = vae_dev._surface_ws = vae_dev.workspace()
+    return ws
+
+
+def vae_decode_forward(vae_dev, vae_scr, scaler=None, mean_scale=None, fused_frame=False):
+    """VAE decode of vae_scr.latent[:L] (the reference's vae_input), oasis_inference.py:1546-1618.
+
+    Returns vae_scr.pred_out, fp32 [L, 1216] as the reference returns vae_scr["pred_out"]: the
+    predictor's rows, unclamped, columns 1200.. zero (TILE padding). fused_frame=True runs the
+    fast path instead: vae_unpatchify and the clamp (oasis_inference.py:1636-1645,2292) fused
+    into the predictor, returning vae_scr.frame [3, 360, 640] in [-1, 1].
+    """
+    assert isinstance(vae_dev, VAE)
+    ws = _vae_workspace(vae_dev, vae_scr)
+    if fused_frame:
+        vae_dev.decode_inplace(ws.latent, ws.frame, ws)
+        return ws.frame
+    vae_dev.decode_patches(ws.latent[:vae_dev.L], ws.pred_out, ws)
+    return ws.pred_out
+
+
+def vae_decode_device(z_flat, vae_dev, vae_scr=None, tt_device=None, scaler=None, mean_scale=None):
+    """z_flat [L, C] (C <= latent_dim; already divided by the scaling factor) -> the predictor's
+    rows as a host fp32 tensor [L, 1200] (oasis_inference.py:1620-1634): the latent is
+    zero-padded to latent_dim columns in the workspace, decoded, and read back without the
+    TILE padding, ready for the reference's host-side vae_unpatchify."""
+    assert isinstance(vae_dev, VAE)
+    ws = _vae_workspace(vae_dev, vae_scr)
+    z = z_flat.reshape(vae_dev.L, -1)
+    c = z.shape[1]
+    if c > vae_dev.latent_dim:
+        raise L.OasisError("vae_decode_device", -2, "z_flat has %d columns, the decoder takes %d"
+                           % (c, vae_dev.latent_dim))
+    lat = ws.latent[:vae_dev.L]
+    lat[:, c:].zero_()
+    lat[:, :c].copy_(z)
+    pred = vae_decode_forward(vae_dev, ws)
+    return pred[:, :vae_dev.patch_dim].cpu()
 
 
 def vae_decode(latent, vae_dev, vae_scr=None):
-    """latent [L, latent_dim] fp32 -> frame [3, H, W] in [-1, 1]."""
-    ws = vae_scr if vae_scr is not None else vae_dev.workspace()
-    ws.latent.copy_(latent.reshape(ws.latent.shape))
-    return vae_decode_forward(vae_dev, ws)
+    """latent [L, latent_dim] fp32 -> frame [3, H, W] in [-1, 1] (the fused fast path)."""
+    ws = _vae_workspace(vae_dev, vae_scr)
+    ws.latent[:vae_dev.L].copy_(latent.reshape(vae_dev.L, -1))
+    return vae_decode_forward(vae_dev, ws, fused_frame=True)
 
 
 def attention_scale(head_dim=64):

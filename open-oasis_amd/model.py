@@ -233,6 +233,10 @@ class DiT:
         computed on the host, oasis_inference.py:1406-1427)."""
         R = cond.shape[0]
         ws.cond[:R].copy_(cond)
+        return self.adaln_inplace(R, ws, stream)
+
+    def adaln_inplace(self, R, ws, stream=None):
+        """ada rows from the pre-SiLU cond rows already in ws.cond[:R] (nothing allocated)."""
         ns = self.n_sub * 6 * self.d
         h = L.stream_handle(stream)
         L.call("oasis_gemv_bf16_tiled", L.ptr(ws.cond), self.d, R, L.ptr(self.ada_w), ns, self.d,
@@ -370,6 +374,7 @@ class VAE:
         self.struct = S
         self._keep = keep
         self.frame_shape = (3, grid[0] * patch, grid[1] * patch)
+        self.patch_dim = 3 * patch * patch
 
     @property
     def weight_bytes(self):
@@ -387,6 +392,16 @@ class VAE:
         B = latents.shape[0]
         L.call("oasis_vae_decode_batch", ctypes.byref(self.struct), ctypes.byref(ws.struct), B,
                L.ptr(latents), L.ptr(frames), L.stream_handle(stream))
+
+    def decode_patches(self, latents, pred_out, ws, stream=None):
+        """B latents [B*L, latent_dim] -> the predictor's unclamped rows pred_out [B*L, ld]
+        (ld >= patch_dim; vae_decode_forward's pred_out, oasis_inference.py:1546-1618)."""
+        rows = latents.numel() // self.latent_dim
+        if rows % self.L or pred_out.shape[0] < rows or pred_out.shape[-1] < self.patch_dim:
+            raise L.OasisError("vae_decode_patches", -2, "latents of %d rows / pred_out %s do not fit L=%d, "
+                               "patch_dim=%d" % (rows, tuple(pred_out.shape), self.L, self.patch_dim))
+        L.call("oasis_vae_decode_patches", ctypes.byref(self.struct), ctypes.byref(ws.struct), rows // self.L,
+               L.ptr(latents), L.ptr(pred_out), pred_out.stride(0), L.stream_handle(stream))
 
 
 class VAEWorkspace:
@@ -407,6 +422,9 @@ class VAEWorkspace:
         self.partial = torch.zeros(self.max_splits, n, d, device=dev)
         self.latent = torch.zeros(n, vae.latent_dim, device=dev)
         self.frame = torch.zeros(*vae.frame_shape, device=dev)
+        # the predictor's rows as the reference keeps them (pred_out, TILE-padded columns that
+        # stay zero: 1200 -> 1216), for the reference-named vae_decode_forward
+        self.pred_out = torch.zeros(vae.L, -(-vae.patch_dim // 32) * 32, device=dev)
         S = L.VAEBuffers()
         S.max_rows = n
         for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
@@ -596,6 +614,9 @@ class VideoPipeline:
         self.ws = dit.workspace(2 * P, max_cond=max(16, R))
         # the decodes of a batch run batched: the VAE workspace holds all n_frames latents
         self.vws = vae.workspace(max_frames=n_frames)
+        # oasis_video_frames / oasis_video_decode write as many latents into the latent scratch as
+        # the VAE workspace's rows hold (max_rows / L); the scratch must have that many rows
+        assert self.vws.latent.shape[0] >= self.vws.struct.max_rows, "latent scratch below the VAE workspace"
         self.kv = KVCache(dit, 1) if kv_cache else None
         nb = 2 if overlap_decode else 1
         self.chunk_bufs = [torch.zeros(n_frames, P, dit.patch_dim, device=dev) for _ in range(nb)]

@@ -221,6 +221,43 @@ def test_dit_forward_surface_reduced():
     assert_close(v, ref, COS_SUB, REL_SUB, "dit_forward surface (2 blocks, D=256)")
 
 
+def test_dit_forward_device_takes_the_reference_padded_layout(c1):
+    """dit_forward_device on the reference's SEQ = 160*T rows (oasis_inference.py:1445): z_cur
+    [320, D] holds each frame's 144 tokens at row 160*t and junk in the 16 pad rows; cond_list
+    holds the reference's row-expanded [32, D] vectors; scr is the reference's scratch dict. The
+    result [320, 64], sliced at gen_start = 160 as ddim_step_fn slices it (oasis_inference.py:
+    1915-1918), gives the generated frame's v (config 1, against the oracle) with its pad rows
+    zero. The packed [288, D] layout gives the same rows bit for bit, and the calls share one
+    workspace."""
+    c, dit = c1
+    K = pkg.kernels
+    D, P = dit.d, dit.P
+    z = oracle.patch_embed(c["latent"][0], c["w"])                     # [2, 144, D]
+    cond = oracle.conditioning(c["t"], c["actions"], c["w"])           # [2, D]
+    ref = oracle.dit_forward(z, cond, c["w"])                          # [2, 144, 64]
+    zp = synth.Draw(33).normal(2, 160, D) * 1e3
+    zp[:, :P] = z
+    conds = [cuda(cond[t].expand(32, D).contiguous()) for t in range(2)]
+    scr = {}
+    out = K.dit_forward_device(cuda(zp.reshape(320, D)), conds, dit, scr, None, None, None)
+    torch.cuda.synchronize()
+    ws = dit._surface_ws
+    assert out.shape == (320, 64)
+    v_dev = out[160:320]                                               # ddim_step_fn's slice
+    assert torch.count_nonzero(v_dev[P:]) == 0 and torch.count_nonzero(out[P:160]) == 0
+    for t, rows in ((0, out[:P]), (1, v_dev[:P])):
+        cos, rel = metrics(rows, ref[t])
+        print("padded dit_forward_device frame %d: cos=%.6f rel=%.3e" % (t, cos, rel), flush=True)
+        assert cos >= COS_STEP, (t, cos)
+    padded = out.clone()
+    packed = K.dit_forward_device(cuda(z.reshape(2 * P, D)), conds, dit, scr)
+    torch.cuda.synchronize()
+    assert torch.equal(packed[:P], padded[:P]) and torch.equal(packed[P:], padded[160:160 + P])
+    assert dit._surface_ws is ws
+    with pytest.raises(pkg._lib.OasisError, match="rows"):
+        K.dit_forward_device(cuda(zp.reshape(320, D)[:300]), conds, dit, scr)
+
+
 @pytest.fixture(scope="module")
 def c3():
     c = synth.config3()
@@ -237,6 +274,34 @@ def test_vae_decode_config3(c3):
     cos, rel = metrics(frame, ref)
     print("config3 VAE decode: cos=%.6f max_rel=%.3e" % (cos, rel), flush=True)
     assert cos >= COS_STEP and rel <= 5e-2, (cos, rel)
+
+
+def test_vae_decode_forward_returns_pred_out(c3):
+    """vae_decode_forward returns the reference's pred_out (oasis_inference.py:1546-1618): the
+    predictor's rows, unclamped, [576, 1216] with zero TILE-padding columns; vae_decode_device
+    (oasis_inference.py:1620-1634) pads a [576, 16] latent to the decoder's width and reads
+    back [576, 1200] on the host. Both match the oracle's predictor rows, and unpatchified and
+    clamped they give the fused fast path's frame."""
+    c, _, vae = c3
+    K = pkg.kernels
+    ws = vae.workspace()
+    ws.latent.copy_(cuda(c["vae_latent"]))
+    pred = K.vae_decode_forward(vae, ws, None, None)
+    torch.cuda.synchronize()
+    ref = oracle.vae_decode(c["vae_latent"], c["vw"])                  # [576, 1200]
+    assert pred.shape == (576, 1216) and torch.count_nonzero(pred[:, 1200:]) == 0
+    assert_close(pred[:, :1200], ref, COS_STEP, 5e-2, "vae_decode_forward pred_out vs oracle")
+    frame = K.vae_decode_forward(vae, ws, fused_frame=True).clone()
+    torch.cuda.synchronize()
+    assert_close(oracle.vae_unpatchify(pred[:, :1200].cpu()), frame, 0.99999, 1e-3,
+                 "unpatchified pred_out vs the fused frame")
+    # the reference's 16-channel latent, zero-padded on the device
+    z16 = c["vae_latent"][:, :16].contiguous()
+    lat32 = torch.zeros(576, 32)
+    lat32[:, :16] = z16
+    host = K.vae_decode_device(cuda(z16), vae, ws, None, None, None)
+    assert host.device.type == "cpu" and host.shape == (576, 1200)
+    assert_close(host, oracle.vae_decode(lat32, c["vw"]), COS_STEP, 5e-2, "vae_decode_device vs oracle")
 
 
 @pytest.mark.parametrize("B", [3, 8])
