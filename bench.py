@@ -114,8 +114,7 @@ def probe(pkg, n=10):
     c1 = pkg.synth.config1()
     dit = pkg.DiT(c1["w"], "cuda")
     step = pkg.DiTStep(dit, B=1, T=2)
-    import oracle
-    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    patches = pkg.patchify_latent(c1["latent"][0]).reshape(-1, 64)
     step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
     step.run()
     torch.cuda.synchronize()
@@ -163,11 +162,10 @@ def kernel_probe(pkg, n=10):
     each), the bandwidth kernels of `bandwidth_kernels` (n + 1 launches each), and n plain 256 MiB
     device copies (the calibration kernel)."""
     import torch
-    import oracle
     c1 = pkg.synth.config1()
     dit = pkg.DiT(c1["w"], "cuda")
     step = pkg.DiTStep(dit, B=1, T=2)
-    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    patches = pkg.patchify_latent(c1["latent"][0]).reshape(-1, 64)
     step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
     for _ in range(2):
         step.run()
@@ -204,7 +202,7 @@ def _graph_step_ms(step, steps, warmup):
     return 1e3 * (time.perf_counter() - t0) / steps
 
 
-def config4(pkg, oracle, steps, warmup):
+def config4(pkg, steps, warmup):
     """Config 4: 8 independent streams x T=4 frames (4608 tokens) per DiT step, QKV/O/FC1/FC2
     on e4m3 weights, against the same batch on bf16 weights. A generated frame needs 4 DDIM
     steps, so DiT frames/s = 8 streams / (4 x step time); with the decodes, frames/s =
@@ -212,7 +210,7 @@ def config4(pkg, oracle, steps, warmup):
     import torch
     c = pkg.synth.config4()
     B, T = 8, 4
-    patches = oracle.patchify_to_output_space(c["latent"].reshape(B * T, 16, 18, 32)).reshape(-1, 64).cuda()
+    patches = pkg.patchify_latent(c["latent"].reshape(B * T, 16, 18, 32)).reshape(-1, 64).cuda()
     res = {"workload": "config4: 8 streams x T=4 (4608 tokens), 16 blocks, D=1024; QKV/O/FC1/FC2 weights "
                        "e4m3 with per-channel fp32 scales, activations in e4m3 blocks of 32 with power-of-two "
                        "scales (written by the LN / GELU producers) on the block-scaled fp8 MFMA; "
@@ -484,14 +482,13 @@ def main():
     if args.probe_kernels:
         kernel_probe(pkg)
         return
-    import oracle
     synth = pkg.synth
 
     # ---------------- config 1: the DiT step ----------------
     c1 = synth.config1()
     dit = pkg.DiT(c1["w"], "cuda")
     step = pkg.DiTStep(dit, B=1, T=2)
-    patches = oracle.patchify_to_output_space(c1["latent"][0]).reshape(-1, 64)
+    patches = pkg.patchify_latent(c1["latent"][0]).reshape(-1, 64)
     step.set_inputs(patches.cuda(), c1["t"].cuda(), c1["actions"].cuda())
     step.capture()
     for _ in range(args.warmup):
@@ -570,8 +567,8 @@ def main():
         dit3 = pkg.DiT(c3["w"], "cuda")
         vae3 = pkg.VAE(c3["vw"], "cuda")
         fp = pkg.FramePipeline(dit3, vae3, c3["steps"], pkg.schedule.cosine_alphas_cumprod())
-        noise = oracle.patchify_to_output_space(c3["x_T"])[0]
-        ctx = oracle.patchify_to_output_space(c3["ctx_latent"])[0]
+        noise = pkg.patchify_latent(c3["x_T"])[0]
+        ctx = pkg.patchify_latent(c3["ctx_latent"])[0]
         fp.set_inputs(noise.cuda(), ctx.cuda(), c3["ctx_t"], c3["ctx_action"].cuda(), c3["gen_action"].cuda())
         fp.capture()
         for _ in range(max(3, args.warmup // 4)):
@@ -675,9 +672,10 @@ def main():
         fp = dit3 = vae3 = None  # release the config-3 model before loading configs 2 and 4
         torch.cuda.empty_cache()
         out["config2"] = config2(pkg)
-        out["config4"] = config4(pkg, oracle, max(10, args.steps // 4), max(3, args.warmup // 4))
+        out["config4"] = config4(pkg, max(10, args.steps // 4), max(3, args.warmup // 4))
 
     if not args.no_cpu_baseline:
+        import oracle  # the CPU baseline's leg only: the GPU path above never touches it
         out["cpu_baseline"] = cpu_baseline(c1, oracle, pkg)
     print(json.dumps(out), flush=True)
 

@@ -40,11 +40,14 @@ FPS_WINDOW = 10                          # frames in the rolling FPS figure (pla
 
 
 def patchify_latent(latent, patch=2):
-    """[C, H, W] latent -> [(H/p)(W/p), p*p*C] patch rows with columns ordered (p, q, c), the
-    reference's patchify_to_output_space (oasis_inference.py:958-963)."""
-    C, H, W = latent.shape
-    x = latent.reshape(C, H // patch, patch, W // patch, patch).permute(1, 3, 2, 4, 0)
-    return x.reshape((H // patch) * (W // patch), patch * patch * C)
+    """[..., C, H, W] latent -> [..., (H/p)(W/p), p*p*C] patch rows with columns ordered
+    (p, q, c), the reference's patchify_to_output_space (oasis_inference.py:958-963); leading
+    dims (frames, streams) are kept."""
+    *lead, C, H, W = latent.shape
+    n = len(lead)
+    x = latent.reshape(*lead, C, H // patch, patch, W // patch, patch)
+    x = x.permute(*range(n), n + 1, n + 3, n + 2, n + 4, n)
+    return x.reshape(*lead, (H // patch) * (W // patch), patch * patch * C)
 
 
 class ActionHold:

@@ -32,6 +32,11 @@ def test_patchify_latent_matches_the_oracle_layout():
     got = play.patchify_latent(lat)
     assert got.shape == (144, 64)
     assert torch.equal(got, oracle.patchify_to_output_space(lat[None])[0])
+    # leading dims (streams, frames) are kept
+    lat4 = torch.randn(2, 3, 16, 18, 32, generator=g)
+    got4 = play.patchify_latent(lat4)
+    assert got4.shape == (2, 3, 144, 64)
+    assert torch.equal(got4, oracle.patchify_to_output_space(lat4.reshape(6, 16, 18, 32)).reshape(2, 3, 144, 64))
 
 
 def test_session_rejects_a_batch_of_prompts():
