@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define OASIS_ABI_VERSION 4
+#define OASIS_ABI_VERSION 5
 #define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
 
 enum {
@@ -146,11 +146,20 @@ enum {
                                  frame f (rows_per_frame each) to out_f32 + f*3*H*W     */
   OASIS_EPI_PARTIAL_F32 = 8,  /* split-K slice s: out_f32[s*split_stride + m*ld_out + n] = acc
                                  (no bias; summed by oasis_residual_ln)                */
-  OASIS_EPI_GELU_TANH_FP8 = 9 /* g = gelu_tanh(acc + bias) as fp8 activation blocks:
+  OASIS_EPI_GELU_TANH_FP8 = 9,/* g = gelu_tanh(acc + bias) as fp8 activation blocks:
                                  out_fp8[m*ld_out + n] = e4m3(g / 2^e) and
                                  out_scale[m*ld_scale + n/32] = e + 127 per 32 columns
                                  (N % 32 == 0); the A operand of oasis_gemm_fp8_a8     */
+  OASIS_EPI_GELU_TANH_FRAG = 10 /* gelu_tanh(acc + bias) into out_bf16 in MFMA fragment order
+                                 (below) as a matrix of ld_out columns (ld_out % 32 == 0):
+                                 the A operand of oasis_gemm_bf16_frag                  */
 };
+
+/* MFMA fragment order of a bf16 matrix X [R, C] (R % 16 == 0, C % 32 == 0): R/16 x C/32
+ * blocks of 512 elements, block (rb, s) at element (rb*C/32 + s)*512; within a block 64
+ * pieces of 8 elements, piece l = X[16*rb + l%16][32*s + 8*(l/16) .. +7]: the operand lane l
+ * of v_mfma_f32_16x16x32_bf16 takes, so a wave reads a block as one contiguous 1 KB load.
+ * (The 16-row tile order of oasis_gemv_bf16_tiled is the same layout.) */
 
 /* Row m is token p of frame f = m / rows_per_frame (p = m % rows_per_frame);
  * frame f is frame t = f % frames_per_stream of stream b = f / frames_per_stream. */
@@ -195,6 +204,16 @@ int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, int6
 int oasis_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                            int64_t N, int64_t K, const oasis_epilogue_t* epi, int tile, int splits,
                            oasis_stream_t stream);
+
+/* acc[M,N] = A[M,K] @ B[N,K]^T with both operands in MFMA fragment order: A [a_rows, K] (a_rows
+ * >= M rounded up to the tile: 48 rows for M <= 160, else 80; rows past M are read and their
+ * results dropped), B [N, K]. Each workgroup's 8 waves split its K slice, every load issued
+ * before the first MFMA, the partial tiles summed through LDS. M % 16 == 0, M <= 320,
+ * N % 16 == 0, K % 256 == 0 and K/splits one of 256, 512, 1024 (splits > 1 requires
+ * OASIS_EPI_PARTIAL_F32). Any epilogue but UNPATCHIFY and GELU_TANH_FP8.
+ * No counterpart in the reference: it is the DiT projections' kernel at one or two frames. */
+int oasis_gemm_bf16_frag(const void* A, int64_t a_rows, const void* B, int64_t M, int64_t N, int64_t K,
+                         const oasis_epilogue_t* epi, int splits, oasis_stream_t stream);
 
 /* fp8 weight GEMM: acc[M,N] = A[M,K] @ (Bq[N,K] * w_scale[N])^T, then the epilogue.
  * A bf16 (quantized per 32-wide K block to e4m3 with a power-of-two scale inside the kernel),
@@ -417,6 +436,17 @@ typedef struct {
   const float* out_s[OASIS_MAX_SUB];
   const float* fc1_s[OASIS_MAX_SUB];
   const float* fc2_s[OASIS_MAX_SUB];
+  /* OASIS_WEIGHTS_BF16 only, optional, per role: the projection weights once more in MFMA
+   * fragment order (see above). A forward pass of at most 320 tokens (a multiple of 48), with
+   * frag_rows in the buffers, keeps the operand of each role the library's plan picks for its
+   * size (by default O's and FC2's up to 160 tokens, O's above; OASIS_FRAG="m1[,m2]" sets the
+   * masks, bits 1 QKV, 2 O, 4 FC1, 8 FC2) in fragment order and runs that projection on
+   * oasis_gemm_bf16_frag, when every sub-block of the pass has that role's weights here. NULL
+   * keeps the role on the row-major weights. */
+  const void* qkv_wf[OASIS_MAX_SUB];
+  const void* out_wf[OASIS_MAX_SUB];
+  const void* fc1_wf[OASIS_MAX_SUB];
+  const void* fc2_wf[OASIS_MAX_SUB];
 } oasis_dit_weights_t;
 
 /* Activation workspace for up to max_rows = B*T*P tokens (caller-allocated). */
@@ -437,6 +467,10 @@ typedef struct {
   void* act8_scale;  /* [max_rows, D/32] e8m0                                       */
   void* mlp8;        /* [max_rows, Dm] e4m3: GELU(FC1) output                       */
   void* mlp8_scale;  /* [max_rows, Dm/32] e8m0                                      */
+  /* rows h, attn and mlp hold (>= max_rows), for the fragment-order passes (0: none). A pass of
+   * M <= 320 tokens needs M rounded up to a multiple of 48, and also of 80 when M > 160 (the
+   * 80-row tiles of the wide products). */
+  int64_t frag_rows;
 } oasis_dit_buffers_t;
 
 /* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action) in fp32, then

@@ -15,9 +15,9 @@ MAX_SUB = 64
 
 EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
-EPI_PARTIAL_F32, EPI_GELU_TANH_FP8 = 8, 9
+EPI_PARTIAL_F32, EPI_GELU_TANH_FP8, EPI_GELU_TANH_FRAG = 8, 9, 10
 ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
@@ -60,13 +60,14 @@ class DiTWeights(ctypes.Structure):
         ("s_cos", c_p), ("s_sinp", c_p), ("t_cos", c_p), ("t_sinp", c_p), ("t_max", c_i),
         ("weight_format", c_i), ("qkv_s", c_p * MAX_SUB), ("out_s", c_p * MAX_SUB), ("fc1_s", c_p * MAX_SUB),
         ("fc2_s", c_p * MAX_SUB),
+        ("qkv_wf", c_p * MAX_SUB), ("out_wf", c_p * MAX_SUB), ("fc1_wf", c_p * MAX_SUB), ("fc2_wf", c_p * MAX_SUB),
     ]
 
 
 class DiTBuffers(ctypes.Structure):
     _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p),
                 ("attn", c_p), ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64),
-                ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p)]
+                ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p), ("frag_rows", c_i64)]
 
 
 class KVCache(ctypes.Structure):
@@ -108,6 +109,7 @@ SIGNATURES = {
     "oasis_sdpa": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p, c_i, c_i, c_p],
     "oasis_gemm_bf16": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_p],
     "oasis_gemm_bf16_config": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
+    "oasis_gemm_bf16_frag": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_p],
     "oasis_gemm_fp8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_quantize_fp8_rows": [c_p, c_i64, c_i64, c_p, c_p, c_p],
     "oasis_gemm_fp8_a8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i,

@@ -72,6 +72,9 @@ struct AttnArgs {
   // (f / f_inner) * o_sfo + (f % f_inner) * o_sf + h * o_sh + i * o_si + d
   int f_inner;
   int64_t o_sfo, o_sf, o_sh, o_si;
+  // > 0: the output is a token-major [rows, frag_ks * 32] matrix stored in MFMA fragment order
+  // (bf16): the row-major offset above names the element
+  int frag_ks = 0;
 };
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
@@ -262,11 +265,13 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
   const float inv = 1.0f / lsum;
   const int f = bh / a.H, h = bh - f * a.H;
   const int fo = f / a.f_inner, fi = f - fo * a.f_inner;
-  T* op = O + fo * a.o_sfo + fi * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
+  const int64_t off = fo * a.o_sfo + fi * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
+  const int64_t ocols = (int64_t)a.frag_ks * 32, orow = a.frag_ks ? off / ocols : 0;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const int d = dt * 16 + 4 * g;
-    store4<T>(op + d, o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+    T* dst = a.frag_ks ? O + frag_index(orow, off - orow * ocols + d, a.frag_ks) : O + off + d;
+    store4<T>(dst, o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
   }
 }
 
@@ -333,10 +338,12 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
   return oasis::check_launch("attention");
 }
 
-// q,k,v: [B][P][H][T][64] bf16; out: token-major [(b*T + t)*P + p][h*64 + d]
+// q,k,v: [B][P][H][T][64] bf16; out: token-major [(b*T + t)*P + p][h*64 + d], row-major or
+// (fks = 2H) in MFMA fragment order
 __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                        const bf16* __restrict__ v, bf16* __restrict__ out,
-                                                       int64_t G, int T, int P, int H, float scale_log2, int qf) {
+                                                       int64_t G, int T, int P, int H, float scale_log2, int qf,
+                                                       int fks) {
   const int64_t grp = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int j = threadIdx.x & 15;
   if (grp >= G) return;  // whole 16-lane groups exit together; no cross-group shuffles
@@ -366,8 +373,10 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     const float p0 = exp2f(x0 - mx), p1 = exp2f(x1 - mx);
     const float inv = 1.0f / (p0 + p1);
     const int T_out = qf < 0 ? T : 1;
-    bf16* dst0 = out + (b * T_out * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
-    bf16* dst1 = qf < 0 ? dst0 + (int64_t)P * H * 64 : dst0;
+    const int64_t row0 = b * T_out * P + p, row1 = qf < 0 ? row0 + P : row0;
+    const int col = h * 64 + j * 4;
+    bf16* dst0 = fks ? out + frag_index(row0, col, fks) : out + row0 * (int64_t)(H * 64) + col;
+    bf16* dst1 = fks ? out + frag_index(row1, col, fks) : out + row1 * (int64_t)(H * 64) + col;
     if (qf <= 0) *reinterpret_cast<bf16x4*>(dst0) = v0;
     if (qf == 0) return;
     *reinterpret_cast<bf16x4*>(dst1) =
@@ -395,7 +404,8 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     }
     const float inv = 1.0f / l;
     const int64_t frame = qf < 0 ? b * T + t : b;
-    bf16* dst = out + (frame * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
+    bf16* dst = fks ? out + frag_index(frame * P + p, h * 64 + j * 4, fks)
+                    : out + (frame * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
     *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(acc[0] * inv), f2bf(acc[1] * inv), f2bf(acc[2] * inv),
                                               f2bf(acc[3] * inv)};
   }
@@ -403,9 +413,13 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
 
 }  // namespace
 
-extern "C" int oasis_attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
-                               int64_t n_heads, float scale, oasis_stream_t stream) {
+namespace {
+
+int attention_impl(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
+                   int64_t n_heads, float scale, hipStream_t stream, bool out_frag) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "attention: null pointer");
+  OASIS_REQUIRE(!out_frag || (n_frames * L) % 16 == 0, OASIS_ERR_SHAPE,
+                "attention: a fragment-order output needs a multiple of 16 rows");
   OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "attention: pointers must be 16-byte aligned");
   OASIS_REQUIRE(n_frames > 0 && L > 0 && n_heads > 0 && L < (1 << 30), OASIS_ERR_SHAPE, "attention: bad shape");
   AttnArgs a;
@@ -420,8 +434,16 @@ extern "C" int oasis_attention(const void* q, const void* k, const void* v, void
   a.o_sf = L * n_heads * 64;
   a.o_sh = 64;
   a.o_si = n_heads * 64;
+  a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
   return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                            static_cast<bf16*>(out), n_frames * n_heads, a, static_cast<hipStream_t>(stream));
+                            static_cast<bf16*>(out), n_frames * n_heads, a, stream);
+}
+
+}  // namespace
+
+extern "C" int oasis_attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
+                               int64_t n_heads, float scale, oasis_stream_t stream) {
+  return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, static_cast<hipStream_t>(stream), false);
 }
 
 extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out, int64_t n_heads_total, int64_t sq,
@@ -458,9 +480,16 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
 
 namespace oasis {
 
+int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
+                   int64_t n_heads, float scale, hipStream_t stream) {
+  return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, stream, true);
+}
+
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
-                       int64_t n_heads, float scale, int q_frame, hipStream_t stream) {
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
+  OASIS_REQUIRE(!out_frag || (B * (q_frame < 0 ? T : 1) * P) % 16 == 0, OASIS_ERR_SHAPE,
+                "temporal_attention: a fragment-order output needs a multiple of 16 rows");
   OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "temporal_attention: pointers must be 16-byte aligned");
   OASIS_REQUIRE(B > 0 && T > 0 && P > 0 && n_heads > 0 && T <= 4096, OASIS_ERR_SHAPE,
                 "temporal_attention: bad shape");
@@ -482,12 +511,14 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
     a.o_sf = n_heads * 64;
     a.o_sh = 64;
     a.o_si = P * n_heads * 64;
+    a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
     return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                               static_cast<bf16*>(out), G, a, stream);
   }
   hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0, stream,
                      static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                     static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame);
+                     static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame,
+                     out_frag ? (int)(n_heads * 2) : 0);
   return check_launch("temporal_attention");
 }
 

@@ -25,6 +25,8 @@
 // same XCD; the weight block is then fetched from HBM once into that XCD's L2.
 #include <string.h>
 
+#include <algorithm>
+
 #include "gemm_epilogue.h"
 
 namespace {
@@ -699,6 +701,154 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   }
 }
 
+// Fragment-order GEMM (at most 320 tokens): A [a_rows, K] and B [N, K] both in MFMA fragment order
+// (each 16-row x 32-k block is the 64 lanes' 16-byte operands back to back), so every operand load is
+// one wave reading 1 KB contiguous straight into the MFMA's registers: no LDS staging, and the whole
+// K slice of a wave in flight at once. A workgroup of 8 waves owns one FM x FN block tile (16-row,
+// 16-column blocks) and splits its K slice eight ways (SPW 32-wide k-steps per wave); the 8 partial
+// tiles are summed through LDS (16-byte column groups XOR-swizzled by (row >> 2) & 3, which spreads
+// a wave's 4-row accumulator groups over the banks), then the bias and the epilogue. Tiles are
+// ordered with the split outermost, then n, then m, as in gemm_wave_kernel. Rows past M (the last
+// tile's rounding) are read and their results dropped.
+template <int FM, int FN, int SPW, int KIND>
+__global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
+                                                        int M, int N, int K, int splits, Epi e) {
+  constexpr int NW = 8, TM = FM * 16, TN = FN * 16;
+  __shared__ __attribute__((aligned(16))) float red[NW * TM * TN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int Mt = (M + TM - 1) / TM, Nt = N / TN;
+  const int ks = K / 32;  // k-steps per 16-row block
+  const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
+  const int split = pid / (Mt * Nt);
+  const int t = pid - split * (Mt * Nt);
+  const int nt = t / Mt, mt = t - nt * Mt;
+  const int s0 = (split * NW + wave) * SPW;  // this wave's first k-step
+  // buffer loads: the wave's first A / B block as the scalar base, 32-bit lane offsets
+  const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(A + ((int64_t)mt * FM * ks + s0) * 512);
+  const __amdgpu_buffer_rsrc_t Brs = buffer_rsrc(B + ((int64_t)nt * FN * ks + s0) * 512);
+  i32x4 a[SPW][FM], b[SPW][FN];
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      a[s][i] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(Ars, ((i * ks + s) * 64 + lane) * 16, 0, 0));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b[s][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(Brs, ((j * ks + s) * 64 + lane) * 16, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = mfma16(__builtin_bit_cast(bf16x8, a[s][i]), __builtin_bit_cast(bf16x8, b[s][j]), acc[i][j]);
+  const int lr = lane & 15, g = lane >> 4;
+  float* mine = red + wave * (TM * TN);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = i * 16 + g * 4 + r, col = j * 16 + lr;
+        mine[row * TN + ((((col >> 2) ^ ((row >> 2) & 3)) << 2) | (col & 3))] = acc[i][j][r];
+      }
+  __syncthreads();
+  constexpr bool partial_only = KIND == OASIS_EPI_PARTIAL_F32;
+  const bool is_partial = partial_only || (KIND < 0 && e.kind == OASIS_EPI_PARTIAL_F32);
+  constexpr int UNITS = TM * TN / 8;
+  for (int u = tid; u < UNITS; u += NW * 64) {
+    const int r = u / (TN / 8), c8 = (u - r * (TN / 8)) * 8;
+    const int gm = mt * TM + r, gn = nt * TN + c8;
+    if (gm >= M) continue;
+    f32x4 s0v = f32x4{0.f, 0.f, 0.f, 0.f}, s1v = s0v;
+    if (!is_partial && e.bias) {
+      s0v = *reinterpret_cast<const f32x4*>(e.bias + gn);
+      s1v = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
+    }
+    const int q0 = ((c8 >> 2) ^ ((r >> 2) & 3)) << 2, q1 = (((c8 >> 2) + 1) ^ ((r >> 2) & 3)) << 2;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + r * TN + q0);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + r * TN + q1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s0v[j] += c0[j];
+        s1v[j] += c1[j];
+      }
+    }
+    if (is_partial) {
+      float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
+      *reinterpret_cast<f32x4*>(d) = s0v;
+      *reinterpret_cast<f32x4*>(d + 4) = s1v;
+    } else {
+      float v[8] = {s0v[0], s0v[1], s0v[2], s0v[3], s1v[0], s1v[1], s1v[2], s1v[3]};
+      epilogue8(e, gm, gn, v, nullptr, 0, false, KIND);
+    }
+  }
+}
+
+// the DiT's projections at one and two frames get kernels with the epilogue fixed at compile time
+template <int FM, int FN, int SPW, int KIND>
+constexpr bool frag_special() {
+  return SPW == 4 && ((KIND == OASIS_EPI_QKV_ROPE && FN == 3) || (KIND == OASIS_EPI_GELU_TANH_FRAG && FN == 4) ||
+                      (KIND == OASIS_EPI_PARTIAL_F32 && (FN == 4 || (FM == 3 && FN <= 2))));
+}
+
+template <int FM, int FN, int SPW, int KIND>
+bool try_frag(const dim3& g, const bf16* A, const bf16* B, int M, int N, int K, int splits, const Epi& e,
+              hipStream_t s) {
+  if constexpr (frag_special<FM, FN, SPW, KIND>()) {
+    if (e.kind == KIND) {
+      hipLaunchKernelGGL((gemm_frag_kernel<FM, FN, SPW, KIND>), g, dim3(512), 0, s, A, B, M, N, K, splits, e);
+      return true;
+    }
+  }
+  return false;
+}
+
+template <int FM, int FN, int SPW>
+void launch_frag3(const bf16* A, const bf16* B, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
+  const int Mt = (M + FM * 16 - 1) / (FM * 16), Nt = N / (FN * 16);
+  const dim3 g(Mt * Nt * splits);
+  if (try_frag<FM, FN, SPW, OASIS_EPI_PARTIAL_F32>(g, A, B, M, N, K, splits, e, s) ||
+      try_frag<FM, FN, SPW, OASIS_EPI_GELU_TANH_FRAG>(g, A, B, M, N, K, splits, e, s) ||
+      try_frag<FM, FN, SPW, OASIS_EPI_QKV_ROPE>(g, A, B, M, N, K, splits, e, s))
+    return;
+  hipLaunchKernelGGL((gemm_frag_kernel<FM, FN, SPW, -1>), g, dim3(512), 0, s, A, B, M, N, K, splits, e);
+}
+
+template <int FM, int FN>
+void launch_frag2(int spw, const bf16* A, const bf16* B, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
+  if (spw == 1) launch_frag3<FM, FN, 1>(A, B, M, N, K, splits, e, s);
+  else if (spw == 2) launch_frag3<FM, FN, 2>(A, B, M, N, K, splits, e, s);
+  else launch_frag3<FM, FN, 4>(A, B, M, N, K, splits, e, s);
+}
+
+// Tile of a fragment-order product, from timings of the DiT's projections at 144 and 288 tokens
+// (hipGraphs of 100 launches over 32 weight copies): 80-row tiles (5 blocks) for the wide products
+// over two frames (FC1, QKV and FC2's split-K slices), 48-row tiles (3 blocks) at one frame and
+// for the unsplit O projection; then the widest n tile that still gives 256 workgroups (80-row
+// tiles) or 192 (48-row tiles).
+void frag_tile(int64_t M, int64_t N, int splits, int& fm, int& fn) {
+  fm = (M <= 160 || (N <= 1024 && splits == 1)) ? 3 : 5;
+  const int64_t mt = (M + fm * 16 - 1) / (fm * 16);
+  const int64_t want = fm == 5 ? 256 : 192;
+  fn = 0;
+  for (int c = 4; c >= 1; --c)
+    if (N % (16 * c) == 0 && (fn == 0 || mt * (N / (16 * c)) * splits >= want)) {
+      fn = c;
+      if (mt * (N / (16 * c)) * splits >= want) break;
+    }
+}
+
 // The K loop is unrolled for 1, 2, 4 or 8 K tiles per wave (K / splits = 256, 512, 1024, 2048); the
 // split-K, GELU and QKV + RoPE epilogues of 2 or 4 tiles per wave (the step's and the VAE's
 // projections) get kernels of their own.
@@ -715,6 +865,10 @@ void launch_wave_nk(const dim3& grid, const bf16* A, int64_t lda, const bf16* B,
       case OASIS_EPI_GELU_TANH:
         hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_GELU_TANH, BMS>), grid, block, 0, s, A, lda, B, ldb,
                            M, N, K, splits, e);
+        return;
+      case OASIS_EPI_GELU_TANH_FRAG:
+        hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_GELU_TANH_FRAG, BMS>), grid, block, 0, s, A, lda, B,
+                           ldb, M, N, K, splits, e);
         return;
       case OASIS_EPI_QKV_ROPE:
         hipLaunchKernelGGL((gemm_wave_kernel<BM, BN, STG, NK, OASIS_EPI_QKV_ROPE, BMS>), grid, block, 0, s, A, lda, B, ldb,
@@ -832,7 +986,7 @@ int auto_tile(int64_t M, int64_t N, int64_t K, int splits, int kind) {
   if (M >= 2048) return large_token_tile(M, N, kind != OASIS_EPI_GELU_TANH_FP8, 5, 6, 7);
   const int64_t Kslice = K / splits;
   const bool wave_k = Kslice % 256 == 0 && Kslice <= 2048 && ((Kslice / 256) & (Kslice / 256 - 1)) == 0;
-  const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF;
+  const bool gelu = kind == OASIS_EPI_GELU_TANH || kind == OASIS_EPI_GELU_ERF || kind == OASIS_EPI_GELU_TANH_FRAG;
   if (wave_k && M <= 320) {
     if (gelu) return M <= 160 ? 10 : 8;
     if (kind == OASIS_EPI_PARTIAL_F32) return K <= 1024 ? 9 : (M <= 160 ? 10 : 8);
@@ -891,6 +1045,51 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
   return OASIS_OK;
 }
 
+int64_t gemm_frag_rows(int64_t M) {
+  const int64_t r48 = (M + 47) / 48 * 48, r80 = (M + 79) / 80 * 80;
+  return M <= 160 ? r48 : std::max(r48, r80);
+}
+
+int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, int64_t N, int64_t K,
+                     const oasis_epilogue_t& ex, int splits, hipStream_t s) {
+  OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm_frag: null operand");
+  OASIS_REQUIRE(aligned16(A) && aligned16(B), OASIS_ERR_ARG, "gemm_frag: A and B must be 16-byte aligned");
+  OASIS_REQUIRE(M > 0 && M <= 320 && M % 16 == 0, OASIS_ERR_SHAPE,
+                "gemm_frag: M=%lld must be a multiple of 16 up to 320", (long long)M);
+  OASIS_REQUIRE(N > 0 && N % 16 == 0 && N < (1ll << 24), OASIS_ERR_SHAPE, "gemm_frag: N=%lld must be a multiple of 16",
+                (long long)N);
+  OASIS_REQUIRE(splits >= 1 && K > 0 && K % splits == 0, OASIS_ERR_SHAPE, "gemm_frag: splits=%d must divide K",
+                splits);
+  const int64_t slice = K / splits;
+  OASIS_REQUIRE(slice == 256 || slice == 512 || slice == 1024, OASIS_ERR_SHAPE,
+                "gemm_frag: K/splits=%lld must be 256, 512 or 1024", (long long)slice);
+  const Epi e = to_epi(ex);
+  if (const int rc = check_epilogue(e, M, N, splits)) return rc;
+  OASIS_REQUIRE(e.kind != OASIS_EPI_UNPATCHIFY && e.kind != OASIS_EPI_GELU_TANH_FP8, OASIS_ERR_ARG,
+                "gemm_frag: epilogue kind %d is not supported", e.kind);
+  int fm, fn;
+  frag_tile(M, N, splits, fm, fn);
+  const int64_t rows = (M + fm * 16 - 1) / (fm * 16) * (fm * 16);
+  OASIS_REQUIRE(a_rows >= rows, OASIS_ERR_SHAPE, "gemm_frag: A holds %lld rows, the %d-row tiles read %lld",
+                (long long)a_rows, fm * 16, (long long)rows);
+  // block offsets are 32-bit byte offsets from a wave's first block
+  OASIS_REQUIRE((int64_t)fm * K * 32 < (1ll << 31) && (int64_t)fn * K * 32 < (1ll << 31), OASIS_ERR_SHAPE,
+                "gemm_frag: K too large");
+  const int spw = (int)(slice / 256);
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+#define OASIS_FRAG(FM_, FN_) \
+  if (fm == FM_ && fn == FN_) launch_frag2<FM_, FN_>(spw, A, B, Mi, Ni, Ki, splits, e, s)
+  OASIS_FRAG(5, 4); else OASIS_FRAG(5, 3); else OASIS_FRAG(5, 2); else OASIS_FRAG(5, 1);
+  else OASIS_FRAG(3, 4); else OASIS_FRAG(3, 3); else OASIS_FRAG(3, 2); else OASIS_FRAG(3, 1);
+#undef OASIS_FRAG
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("gemm_frag launch failed: %s", hipGetErrorString(err));
+    return OASIS_ERR_LAUNCH;
+  }
+  return OASIS_OK;
+}
+
 // Default tile choice. M is small (288 / 576 tokens) and the weights are streamed once,
 // so the tiles trade L2 re-reads of A and B against enough workgroups (and K-tiles in
 // flight per workgroup) to keep all 256 CUs issuing HBM loads.
@@ -944,4 +1143,11 @@ extern "C" int oasis_gemm_bf16(const void* A, int64_t lda, const void* B, int64_
   OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm: null epilogue");
   return oasis::gemm_launch(static_cast<const bf16*>(A), lda, static_cast<const bf16*>(B), ldb, M, N,
                             K, *epi, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_gemm_bf16_frag(const void* A, int64_t a_rows, const void* B, int64_t M, int64_t N, int64_t K,
+                                    const oasis_epilogue_t* epi, int splits, oasis_stream_t stream) {
+  OASIS_REQUIRE(epi, OASIS_ERR_NULL, "gemm_frag: null epilogue");
+  return oasis::gemm_frag_launch(static_cast<const bf16*>(A), a_rows, static_cast<const bf16*>(B), M, N, K, *epi,
+                                 splits, static_cast<hipStream_t>(stream));
 }

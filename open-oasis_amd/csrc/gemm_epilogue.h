@@ -252,6 +252,12 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
       }
       break;
     }
+    case OASIS_EPI_GELU_TANH_FRAG: {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = gelu_tanh(v[j]);
+      store8_bf16(e.out_bf16 + frag_index(m, n0, e.ld_out >> 5), v);
+      break;
+    }
     case OASIS_EPI_GELU_TANH_FP8: {
       // the 4 threads of one 32-column block are lanes 4i..4i+3 of the caller's loop
       float amax = 0.f;
@@ -361,6 +367,10 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
     case OASIS_EPI_GELU_ERF:
       OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 8 == 0, OASIS_ERR_ARG,
                     "gemm: bf16 epilogue needs out_bf16 and ld_out >= N (multiple of 8)");
+      break;
+    case OASIS_EPI_GELU_TANH_FRAG:
+      OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 32 == 0 && M % 16 == 0, OASIS_ERR_ARG,
+                    "gemm: GELU_TANH_FRAG needs out_bf16, ld_out >= N (multiple of 32) and M %% 16 == 0");
       break;
     case OASIS_EPI_GELU_TANH_FP8:
       OASIS_REQUIRE(e.out_fp8 && e.out_scale && N % 32 == 0 && e.ld_out >= N && e.ld_out % 8 == 0 &&

@@ -174,8 +174,9 @@ __global__ __launch_bounds__(256) void ln8_kernel(const TIn* __restrict__ x, int
 // block reductions:
 //   x[m] += g * (sum_s partial[s][m] + bias)          (NP > 0; g = gate[f(m)] or 1)
 //   y[m]  = LN(x[m]) * a + b                           (a, b: modulate rows or affine)
-// y is bf16, or (y8 != nullptr, D >= 1024) fp8 activation blocks: e4m3 bytes y8[m, :] and
-// one e8m0 scale per 32 columns in ys[m, :] (8 consecutive threads share a block).
+// y is bf16, row-major or (yf) in MFMA fragment order, or (y8 != nullptr, D >= 1024) fp8
+// activation blocks: e4m3 bytes y8[m, :] and one e8m0 scale per 32 columns in ys[m, :] (8
+// consecutive threads share a block).
 template <int VPT, int NP>
 __global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restrict__ x, int64_t M, const float* __restrict__ part,
                                                           int64_t pstride, const float* __restrict__ bias,
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restric
                                                           int64_t rpf, const float* __restrict__ la,
                                                           const float* __restrict__ lb, int64_t ln_fs,
                                                           bf16* __restrict__ y, uint8_t* __restrict__ y8,
-                                                          uint8_t* __restrict__ ys, float eps) {
+                                                          uint8_t* __restrict__ ys, float eps, int yf) {
   constexpr int D = VPT * 256;
   constexpr int NC = VPT / 4 > 0 ? VPT / 4 : 1;   // 4-float groups per thread
   constexpr int W = VPT < 4 ? VPT : 4;            // floats per group
@@ -272,10 +273,10 @@ __global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restric
       *reinterpret_cast<uint32_t*>(y8 + row * D + k) = pack4_fp8(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
       if ((tid & 7) == 0) ys[row * (D / 32) + k / 32] = (uint8_t)sb;
     } else if (W == 4) {
-      store4<bf16>(yr + k, o);
+      store4<bf16>(yf ? y + frag_index(row, k, D / 32) : yr + k, o);
     } else {
 #pragma unroll
-      for (int j = 0; j < W; ++j) yr[k + j] = f2bf(o[j]);
+      for (int j = 0; j < W; ++j) (yf ? y[frag_index(row, k + j, D / 32)] : yr[k + j]) = f2bf(o[j]);
     }
   }
 }
@@ -536,7 +537,7 @@ hipError_t final_layer_np(int np, float* x, int64_t M, const float* part, int64_
 template <int NC>
 hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
-                          bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s) {
+                          bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s, int yf) {
   // few rows: a 256-thread workgroup per row (VPT = NC floats per thread); many: a wave per row
   const bool wave_rows = M >= 2048;
   const dim3 grid((unsigned)(wave_rows ? (M + 3) / 4 : M)), block(256);
@@ -546,7 +547,7 @@ hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_
                        lb, lfs, y, y8, ys, eps);                                                                \
   else                                                                                                          \
     hipLaunchKernelGGL((residual_ln_block_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, \
-                       la, lb, lfs, y, y8, ys, eps)
+                       la, lb, lfs, y, y8, ys, eps, yf)
   switch (np) {
     case 0: OASIS_RLN(0); break;
     case 1: OASIS_RLN(1); break;
@@ -637,8 +638,10 @@ namespace oasis {
 int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
-                hipStream_t s) {
+                hipStream_t s, bool y_frag) {
   OASIS_REQUIRE(x, OASIS_ERR_NULL, "residual_ln: null x");
+  OASIS_REQUIRE(!y_frag || (M < 2048 && M % 16 == 0 && !y8), OASIS_ERR_ARG,
+                "residual_ln: a fragment-order output needs M < 2048, M %% 16 == 0 and a bf16 output");
   OASIS_REQUIRE(oasis_aligned(16, x, partial, bias, gate, ln_a, ln_b, y_bf16, y8), OASIS_ERR_ARG,
                 "residual_ln: pointers must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && M < (1ll << 31) && rows_per_frame > 0, OASIS_ERR_SHAPE, "residual_ln: bad M/rows_per_frame");
@@ -649,10 +652,10 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
   bf16* y = static_cast<bf16*>(y_bf16);
   hipError_t e;
   switch (D) {
-    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
-    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
-    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
-    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s); break;
+    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0); break;
+    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0); break;
+    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0); break;
+    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0); break;
     default:
       set_error("residual_ln: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
       return OASIS_ERR_SHAPE;

@@ -25,6 +25,12 @@ int check_launch(const char* what);
 // acc = A[M,K] @ B[N,K]^T with the given epilogue (gemm.hip).
 int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                 const oasis_epilogue_t& epi, hipStream_t s);
+// both operands in MFMA fragment order (A with a_rows >= M rows), M <= 320 (gemm.hip)
+int gemm_frag_launch(const __bf16* A, int64_t a_rows, const __bf16* B, int64_t M, int64_t N, int64_t K,
+                     const oasis_epilogue_t& epi, int splits, hipStream_t s);
+// rows of A any fragment-order product of M rows may read (its row tiles rounded up: 48 rows at
+// most 160 tokens, 48 or 80 above)
+int64_t gemm_frag_rows(int64_t M);
 // explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
 int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                     const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
@@ -37,10 +43,11 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
                     int splits, hipStream_t s);
 // oasis_residual_ln with an optional fp8-block LN output (y8 e4m3 [M, D], y8_scale e8m0
 // [M, D/32]) in place of the bf16 one (norm.hip).
+// y_frag: the bf16 output in MFMA fragment order (below 2048 rows).
 int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
-                hipStream_t s);
+                hipStream_t s, bool y_frag = false);
 // The DiT's final layer in fp32 (norm.hip): the pending residual (n_partials split-K slices +
 // bias, gated), LN, modulate with the frame's (scale_p1, shift) rows, then v_out[M, 64] =
 // h @ W^T + b with W fp32 [64, D]. With chunk set, rows chunk_row0.. also take one DDIM step of
@@ -63,8 +70,12 @@ int gemv_adaln_pair(const float* x, int64_t ldx, int64_t R, const void* W16, int
                     int64_t ld_out, hipStream_t s);
 // Causal temporal attention (attention.hip); q_frame >= 0 computes only that query frame of
 // each group and writes it as a single frame: out [B*P, n_heads*64].
+// out_frag: out in MFMA fragment order (as a [rows, n_heads*64] matrix).
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
-                       int64_t n_heads, float scale, int q_frame, hipStream_t stream);
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag = false);
+// oasis_attention (heads-first q/k/v per frame, token-major out) with out in fragment order.
+int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
+                   int64_t n_heads, float scale, hipStream_t stream);
 // QKV projection + temporal RoPE + causal attention of a two-frame temporal window in one
 // kernel (temporal_qkv.hip). A: LN output [B*T*P, lda]; W: QKV weight [3D, D] (D = 64 H);
 // out: attention output [B*T*P, D]. T = 2: both frames (kc / vc, optional, receive both frames'
@@ -105,6 +116,14 @@ OASIS_DEV bf16x8 pack8(const float* v) {
 OASIS_DEV void unpack8(bf16x8 p, float* v) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = bf2f(p[i]);
+}
+
+// ---- MFMA fragment order ------------------------------------------------------
+// Element (m, c) of a bf16 matrix of ks * 32 columns stored in fragment order: block (m / 16,
+// c / 32) of 512 elements, piece (m % 16) + 16 ((c / 8) % 4) of 8, element c % 8. A run of 4 or 8
+// columns starting at a multiple of 4 or 8 stays inside one piece.
+OASIS_DEV int64_t frag_index(int64_t m, int64_t c, int64_t ks) {
+  return ((((m >> 4) * ks + (c >> 5)) * 64 + (m & 15) + ((c >> 3) & 3) * 16) << 3) + (c & 7);
 }
 
 // ---- streaming accesses -----------------------------------------------------

@@ -52,7 +52,17 @@ struct Plan {
   // against 1.601 ms per step and 160.9 against 160.6 FPS per frame), 1 for the T = 2 passes,
   // 2 for every pass
   int fused_temporal;
+  // which operands are kept in MFMA fragment order, with their projection on gemm_frag: a mask of
+  // the FRAG_* bits for passes of at most 160 tokens (frag1) and of 161 to 320 (frag2). OASIS_FRAG
+  // = "frag1[,frag2]" (0 for none). The defaults are the fastest masks on MI355X with cold weights
+  // (the K/V-cache frame 5.960 ms against 5.985 with none, the T = 2 step 1.4728 against 1.4786):
+  // O and FC2 at one frame, O alone at two; every other mask measured slower.
+  int frag1, frag2;
 };
+
+// Fragment-order operands, one bit each: the LN output QKV reads, the attention output O reads,
+// the LN output FC1 reads, and FC1's GELU output FC2 reads.
+enum { FRAG_QKV = 1, FRAG_O = 2, FRAG_FC1 = 4, FRAG_FC2 = 8, FRAG_ALL = 15 };
 
 const Plan& plan() {
   static Plan p = [] {
@@ -84,6 +94,14 @@ const Plan& plan() {
       }
     }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
+    q.frag1 = FRAG_O | FRAG_FC2;
+    q.frag2 = FRAG_O;
+    if (const char* env = getenv("OASIS_FRAG")) {
+      int a = 0, b = 0;
+      const int n = sscanf(env, "%d,%d", &a, &b);
+      if (n >= 1) q.frag1 = q.frag2 = a & FRAG_ALL;
+      if (n == 2) q.frag2 = b & FRAG_ALL;
+    }
     return q;
   }();
   return p;
@@ -313,6 +331,39 @@ struct KvPass {
   int mode = KV_NONE;
 };
 
+// The FRAG_* operands a pass of M tokens over sub-blocks [j0, j1) keeps in fragment order: the
+// plan's mask for its size, narrowed to the roles whose fragment-order weights every sub-block has.
+// None without bf16 weights, past 320 tokens or whole 48-row tiles, without the rounded-up rows in
+// the buffers, with a per-role tile override or the fused temporal kernel (those read row-major
+// operands), or at a model width the kernel's K slices do not cover (D <= 1024; FC2 in slices of
+// 1024 or less).
+int frag_mask(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int64_t M, int64_t j0, int64_t j1,
+              int fc2_splits) {
+  const Plan& pl = plan();
+  int m = M <= 160 ? pl.frag1 : pl.frag2;
+  if (!m || pl.fused_temporal > 0 || w->weight_format != OASIS_WEIGHTS_BF16) return 0;
+  for (int r = 0; r < ROLE_N; ++r)
+    if (pl.tile[r] >= 0 || pl.splits[r] > 0) return 0;
+  const int64_t D = w->d_model, Dm = w->d_mlp;
+  if (M > 320 || M % 48 != 0 || buf->frag_rows < oasis::gemm_frag_rows(M)) return 0;
+  if (!(D == 256 || D == 512 || D == 1024)) return 0;
+  const int64_t sl = fc2_splits >= 1 && Dm % fc2_splits == 0 ? Dm / fc2_splits : 0;
+  if (!(sl == 256 || sl == 512 || sl == 1024)) m &= ~FRAG_FC2;
+  for (int64_t j = j0; j < j1; ++j) {
+    if (!w->qkv_wf[j]) m &= ~FRAG_QKV;
+    if (!w->out_wf[j]) m &= ~FRAG_O;
+    if (!w->fc1_wf[j]) m &= ~FRAG_FC1;
+    if (!w->fc2_wf[j]) m &= ~FRAG_FC2;
+  }
+  return m;
+}
+
+// FC2's split-K count on the fragment-order GEMM: slices of 1024 (4 at d_mlp = 4096)
+int frag_fc2_splits(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf) {
+  int s = (int)std::max<int64_t>(1, w->d_mlp / 1024);
+  return s <= buf->max_splits ? s : -1;
+}
+
 // run_sub_block (oasis_inference.py:995-1215) for sub-blocks [j0, j1); sub-block j is
 // spatial for even j. The FC2 residual of the last sub-block is left pending. With a
 // K/V-cache pass the temporal sub-blocks read and write the cache (run_sub_block_t1,
@@ -327,8 +378,17 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   const Plan& pl = plan();
   const int so = pl.splits[ROLE_O] > 0 ? std::min<int>(pl.splits[ROLE_O], buf->max_splits)
                                        : choose_splits(M, D, D, buf->max_splits);
-  const int sf = pl.splits[ROLE_FC2] > 0 ? std::min<int>(pl.splits[ROLE_FC2], buf->max_splits)
-                                         : choose_splits(M, D, Dm, buf->max_splits);
+  int sf = pl.splits[ROLE_FC2] > 0 ? std::min<int>(pl.splits[ROLE_FC2], buf->max_splits)
+                                   : choose_splits(M, D, Dm, buf->max_splits);
+  // fragment order (the FRAG_* bits of the plan): the producer of each chosen operand (residual_ln,
+  // the attention kernels, FC1's GELU epilogue) writes it in MFMA fragment order and its projection
+  // runs on gemm_frag (O unsplit, FC2 in slices of 1024)
+  const int sf_frag = frag_fc2_splits(w, buf);
+  const int fg = frag_mask(w, buf, M, j0, j1, sf_frag);
+  const bool f_qkv = fg & FRAG_QKV, f_o = fg & FRAG_O, f_fc1 = fg & FRAG_FC1, f_fc2 = fg & FRAG_FC2;
+  const int so_use = f_o ? 1 : so;
+  if (f_fc2) sf = sf_frag;
+  const int64_t FR = buf->frag_rows;
 
   oasis_epilogue_t qkv = epi_zero();
   qkv.kind = OASIS_EPI_QKV_ROPE;
@@ -337,7 +397,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   qkv.frames_per_stream = T;
   const bool fp8 = w->weight_format == OASIS_WEIGHTS_FP8;
   oasis_epilogue_t gelu = epi_zero();
-  gelu.kind = fp8 ? OASIS_EPI_GELU_TANH_FP8 : OASIS_EPI_GELU_TANH;
+  gelu.kind = fp8 ? OASIS_EPI_GELU_TANH_FP8 : (f_fc2 ? OASIS_EPI_GELU_TANH_FRAG : OASIS_EPI_GELU_TANH);
   gelu.out_bf16 = buf->mlp;
   gelu.out_fp8 = buf->mlp8;
   gelu.out_scale = buf->mlp8_scale;
@@ -356,7 +416,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
-                                 fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
+                                 fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv));
     // with OASIS_TEMPORAL_FUSED=1 or 2, two-frame temporal windows (the T = 2 step and the frame's
     // first, cache-filling pass; with 2 also the current-frame passes against the cache): QKV,
     // RoPE and the causal attention in one kernel
@@ -407,23 +467,37 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
         qkv.rope_sinp = w->t_sinp + slot * 64;
         qkv.rope_by_frame = 1;
       }
-      OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
-                     s));
-      if (spatial)
+      if (f_qkv)
+        OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->qkv_wf[j], M, 3 * D, D, qkv, 1, s));
+      else
+        OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
+                       s));
+      if (spatial && f_o)
+        OASIS_TRY(oasis::attention_frag(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s));
+      else if (spatial)
         OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
       else if (kv.mode == KV_NONE)
-        OASIS_TRY(oasis_temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, stream));
+        OASIS_TRY(oasis::temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, -1, s, f_o));
       else
-        OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s));
+        OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s, f_o));
     }
     if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     // O projection as split-K partials; bias + gated residual + LN + modulate fused after
-    OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
-    OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
-                                 a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s));
+    if (f_o)
+      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use, s));
+    else
+      OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
+    OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
+                                 a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
     gelu.bias = w->fc1_b[j];
-    OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
-    OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
+    if (f_fc1)
+      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
+    else
+      OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+    if (f_fc2)
+      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->mlp, FR, (const bf16*)w->fc2_wf[j], M, D, Dm, part, sf, s));
+    else
+      OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
     pend->bias = w->fc2_b[j];
     pend->gate = a + 5 * D;
     pend->n = sf;

@@ -12,6 +12,9 @@ HBM layout (nn.Linear [out, in] weights, fp32 biases/tables):
     the adaLN rows of all 32 sub-blocks for every conditioning row at once.
   - per sub-block (bf16): qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
     contiguous (37.7 MB of the 1.21 GB weight set per sub-block incl. adaLN).
+  - per sub-block (bf16), for the passes of at most 320 tokens: out_w and fc2_w once more in
+    the MFMA fragment order of ``tile_rows16`` (``DiT(frag=...)`` picks the roles; 335 MB at
+    Oasis-500M for the default two).
   - fp32, as the reference keeps them (oasis_inference.py:512-532,1821-1826): the
     conditioning MLP and action projection (zero-padded to 64 inputs), the patch embed
     [D, 64] in (p, q, c) column order, the final layer's adaLN [2D, D] and linear [64, D].
@@ -34,6 +37,17 @@ def tile_rows16(W):
     N, K = W.shape
     assert N % 16 == 0 and K % 32 == 0
     return W.reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(N, K).contiguous()
+
+
+FRAG_ROLES_ALL = ("qkv", "out", "fc1", "fc2")
+FRAG_ROLES_DEFAULT = ("out", "fc2")
+
+
+def frag_rows(m):
+    """Rows of h, attn and mlp a fragment-order pass of m tokens reads: m rounded up to its row
+    tiles (48 rows up to 160 tokens; 48 or 80 above)."""
+    r48, r80 = -(-m // 48) * 48, -(-m // 80) * 80
+    return r48 if m <= 160 else max(r48, r80)
 
 
 def untile_rows16(Wt):
@@ -89,10 +103,19 @@ class DiT:
     the sub-blocks' adaLN stays bf16, and conditioning, patch embed and the final layer
     fp32, in both modes."""
 
-    def __init__(self, w, device="cuda", grid=(9, 16), t_max=32, weights="bf16"):
+    def __init__(self, w, device="cuda", grid=(9, 16), t_max=32, weights="bf16", frag=True):
         if weights not in ("bf16", "fp8"):
             raise ValueError("weights must be 'bf16' or 'fp8'")
         self.weights = weights
+        # bf16: projection weights also in MFMA fragment order (tile_rows16) for the passes of at
+        # most 320 tokens (the step, the K/V-cache passes), for the roles whose operands those passes
+        # keep in that order (OASIS_FRAG in the library; the default uses O and FC2). frag: True for
+        # those two, False for none, or an iterable of "qkv", "out", "fc1", "fc2".
+        roles = FRAG_ROLES_DEFAULT if frag is True else (() if not frag else tuple(frag))
+        if any(r not in FRAG_ROLES_ALL for r in roles):
+            raise ValueError("frag roles must be among %s" % (FRAG_ROLES_ALL,))
+        self.frag_roles = roles if weights == "bf16" else ()
+        self.frag = bool(self.frag_roles)
         self.device = torch.device(device)
         dev = self.device
         self.d = d = w["t_emb.w2"].shape[0]
@@ -112,6 +135,7 @@ class DiT:
         self.t_max = t_max
         bf = torch.bfloat16
         keep = []
+        frag_keep = []
 
         def put(t, dtype):
             x = t.to(device=dev, dtype=dtype).contiguous()
@@ -171,6 +195,10 @@ class DiT:
             S.fc1_b[j] = put(w[p + "fc1_b"], torch.float32).data_ptr()
             S.fc2_w[j], S.fc2_s[j] = proj(w[p + "fc2_w"])
             S.fc2_b[j] = put(w[p + "fc2_b"], torch.float32).data_ptr()
+            for r in self.frag_roles:   # second copies: not in keep, so not in weight_bytes
+                wf = tile_rows16(w[p + r + "_w"].to(device=dev, dtype=bf))
+                frag_keep.append(wf)
+                getattr(S, r + "_wf")[j] = wf.data_ptr()
         if fp8:
             torch.cuda.synchronize(dev)
         S.final_w = put(w["final.w"], f32).data_ptr()
@@ -198,10 +226,16 @@ class DiT:
         S.t_max = t_max
         self.struct = S
         self._keep = keep
+        self._frag_keep = frag_keep
 
     @property
     def weight_bytes(self):
+        """Bytes of one copy of every weight (what a forward pass reads); the fragment-order
+        second copies are frag_weight_bytes."""
         return sum(t.numel() * t.element_size() for t in self._keep)
+
+    def frag_weight_bytes(self):
+        return sum(t.numel() * t.element_size() for t in self._frag_keep)
 
     def ada_w_rows(self):
         """The stacked adaLN weights in row-major [n_sub*6D, D] order (a copy; the device keeps
@@ -297,13 +331,15 @@ class DiTWorkspace:
         if max_splits is None:
             max_splits = 8 if max_rows <= 640 else 2
         self.max_rows, self.max_cond = max_rows, max_cond
+        # h, attn and mlp hold the rows a fragment-order pass rounds up to (dit.frag)
+        fr = max(max_rows, frag_rows(min(max_rows, 320))) if dit.frag else max_rows
         self.x = torch.zeros(max_rows, d, device=dev)
-        self.h = torch.zeros(max_rows, d, device=dev, dtype=bf)
+        self.h = torch.zeros(fr, d, device=dev, dtype=bf)
         self.q = torch.zeros(max_rows, d, device=dev, dtype=bf)
         self.k = torch.zeros(max_rows, d, device=dev, dtype=bf)
         self.v = torch.zeros(max_rows, d, device=dev, dtype=bf)
-        self.attn = torch.zeros(max_rows, d, device=dev, dtype=bf)
-        self.mlp = torch.zeros(max_rows, dit.d_mlp, device=dev, dtype=bf)
+        self.attn = torch.zeros(fr, d, device=dev, dtype=bf)
+        self.mlp = torch.zeros(fr, dit.d_mlp, device=dev, dtype=bf)
         self.max_splits = max_splits
         self.partial = torch.zeros(max_splits, max_rows, d, device=dev)
         self.v_out = torch.zeros(max_rows, dit.patch_dim, device=dev)
@@ -317,6 +353,7 @@ class DiTWorkspace:
         for name in ("x", "h", "q", "k", "v", "attn", "mlp", "partial"):
             setattr(S, name, getattr(self, name).data_ptr())
         S.max_splits = max_splits
+        S.frag_rows = fr if dit.frag else 0
         if dit.weights == "fp8":  # fp8 activation blocks: e4m3 bytes + one e8m0 scale per 32 columns
             u8 = torch.uint8
             self.act8 = torch.zeros(max_rows, d, device=dev, dtype=u8)
