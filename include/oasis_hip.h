@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define OASIS_ABI_VERSION 5
+#define OASIS_ABI_VERSION 6
 #define OASIS_MAX_SUB 64 /* max sub-blocks (2 per DiT block) in one model */
 
 enum {
@@ -150,9 +150,24 @@ enum {
                                  out_fp8[m*ld_out + n] = e4m3(g / 2^e) and
                                  out_scale[m*ld_scale + n/32] = e + 127 per 32 columns
                                  (N % 32 == 0); the A operand of oasis_gemm_fp8_a8     */
-  OASIS_EPI_GELU_TANH_FRAG = 10 /* gelu_tanh(acc + bias) into out_bf16 in MFMA fragment order
+  OASIS_EPI_GELU_TANH_FRAG = 10,/* gelu_tanh(acc + bias) into out_bf16 in MFMA fragment order
                                  (below) as a matrix of ld_out columns (ld_out % 32 == 0):
                                  the A operand of oasis_gemm_bf16_frag                  */
+  /* The pair below carries a LayerNorm + modulate from one product into the next, so that
+   * (with f = f(m), s = mod_scale[f], t = mod_shift[f])
+   *   GELU_TANH_LN(GATED_RES_LN(...)) = gelu_tanh((LN(x_new) * s + t) @ B^T + bias)
+   * without the normalised rows ever being formed. oasis_gemm_bf16_frag only.            */
+  OASIS_EPI_GATED_RES_LN = 11,/* x = out_f32[m, n] += gate[f, n] * (acc + bias[n]) (N % 32 == 0);
+                                 y = x - ln_center[m]; out_bf16 (fragment order, ld_out
+                                 columns) = y * mod_scale[f, n]; ln_stats[m][n/16] =
+                                 (sum of y, sum of y^2) over those 16 columns; ln_mod rows
+                                 2f, 2f + 1 = bf16(mod_scale[f]), bf16(mod_shift[f]) for the
+                                 frames f < ceil(M / rows_per_frame) <= 8                  */
+  OASIS_EPI_GELU_TANH_LN = 12 /* A = a GATED_RES_LN output over K = its N (K <= 1024, one
+                                 split): gelu_tanh(r (acc - mu c1[f, n]) + c2[f, n] + bias[n])
+                                 with mu, r = 1/sqrt(var + ln_eps) from ln_stats[m][0..K/16),
+                                 c1 and c2 = ln_mod rows 2f and 2f + 1 @ B^T; into out_bf16,
+                                 in fragment order when out_frag                          */
 };
 
 /* MFMA fragment order of a bf16 matrix X [R, C] (R % 16 == 0, C % 32 == 0): R/16 x C/32
@@ -190,6 +205,13 @@ typedef struct {
   void* out_fp8;            /* GELU_TANH_FP8: e4m3 bytes, row stride ld_out         */
   void* out_scale;          /* GELU_TANH_FP8: e8m0 block scales, row stride ld_scale */
   int64_t ld_scale;
+  const float* mod_scale;   /* GATED_RES_LN: modulate scale (+1) row of frame f at mod_scale + f*gate_fstride */
+  const float* mod_shift;   /* GATED_RES_LN: modulate shift rows, the same stride     */
+  const float* ln_center;   /* GATED_RES_LN: [M], subtracted before the statistics    */
+  float* ln_stats;          /* *_LN: [M][N/16][2] (GATED_RES_LN's N = GELU_TANH_LN's K) */
+  void* ln_mod;             /* *_LN: bf16 [16, N] in fragment order (rows 2f, 2f + 1)  */
+  float ln_eps;             /* GELU_TANH_LN                                           */
+  int out_frag;             /* GELU_TANH_LN: out_bf16 in fragment order              */
 } oasis_epilogue_t;
 
 /* acc[M,N] = A[M,K] @ B[N,K]^T (bf16 in, fp32 accumulate) followed by the epilogue.
@@ -471,6 +493,12 @@ typedef struct {
    * M <= 320 tokens needs M rounded up to a multiple of 48, and also of 80 when M > 160 (the
    * 80-row tiles of the wide products). */
   int64_t frag_rows;
+  /* the LayerNorm after O carried into FC1 (GATED_RES_LN / GELU_TANH_LN), optional:
+   * ln_mean [max_rows] fp32 (the LN before QKV's row means), ln_stats [max_rows, D/16, 2] fp32,
+   * ln_mod [16, D] bf16 */
+  float* ln_mean;
+  float* ln_stats;
+  void* ln_mod;
 } oasis_dit_buffers_t;
 
 /* Conditioning for R frames: cond = MLP(timestep_embedding(t)) + ext(action) in fp32, then

@@ -16,8 +16,9 @@ MAX_SUB = 64
 EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32, EPI_GELU_TANH_FP8, EPI_GELU_TANH_FRAG = 8, 9, 10
+EPI_GATED_RES_LN, EPI_GELU_TANH_LN = 11, 12
 ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
 
 
@@ -44,6 +45,9 @@ class Epilogue(ctypes.Structure):
         ("s_b", c_i64), ("s_t", c_i64), ("s_p", c_i64), ("s_h", c_i64),
         ("unpatch_patch", c_i), ("unpatch_channels", c_i), ("split_stride", c_i64),
         ("out_fp8", c_p), ("out_scale", c_p), ("ld_scale", c_i64),
+        ("mod_scale", c_p), ("mod_shift", c_p), ("ln_center", c_p), ("ln_stats", c_p), ("ln_mod", c_p),
+        ("ln_eps", c_f),
+        ("out_frag", c_i),
     ]
 
 
@@ -67,7 +71,8 @@ class DiTWeights(ctypes.Structure):
 class DiTBuffers(ctypes.Structure):
     _fields_ = [("max_rows", c_i64), ("x", c_p), ("h", c_p), ("q", c_p), ("k", c_p), ("v", c_p),
                 ("attn", c_p), ("mlp", c_p), ("partial", c_p), ("max_splits", c_i64),
-                ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p), ("frag_rows", c_i64)]
+                ("act8", c_p), ("act8_scale", c_p), ("mlp8", c_p), ("mlp8_scale", c_p), ("frag_rows", c_i64),
+                ("ln_mean", c_p), ("ln_stats", c_p), ("ln_mod", c_p)]
 
 
 class KVCache(ctypes.Structure):

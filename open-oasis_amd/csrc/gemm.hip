@@ -710,11 +710,32 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
 // a wave's 4-row accumulator groups over the banks), then the bias and the epilogue. Tiles are
 // ordered with the split outermost, then n, then m, as in gemm_wave_kernel. Rows past M (the last
 // tile's rounding) are read and their results dropped.
+//
+// The LayerNorm + modulate carried from O into FC1:
+//  - GATED_RES_LN (O): one epilogue unit per thread, its x, gate, scale and centre fetched before
+//    the MFMAs. x += gate * (acc + bias); with y = x - centre it writes y * s (fragment order), the
+//    per-16-column sums of y and y^2 (the 2 threads of a 16-column group are lanes 2i, 2i + 1),
+//    and, from the threads of rows m < frames, bf16 s and t of frame m as rows 2m and 2m + 1 of
+//    the 16-row modulate block.
+//  - GELU_TANH_LN (FC1, A = y * s) finishes it from the identity
+//      (LN(x) * s + t) @ B^T = r * ((y * s) @ B^T - mu * (s @ B^T)) + t @ B^T,
+//    mu and r = 1/sqrt(var + eps) being y's row mean and inverse deviation (var(y) = var(x)). The
+//    modulate block is one more A block, so s @ B^T and t @ B^T of every frame come out of the same
+//    MFMAs; each row's statistics are 32 lanes' loads summed by a 32-lane reduction. To leave LDS
+//    for the modulate-block rows the 8 partial tiles are summed in two rounds: waves 4-7 hand
+//    theirs to waves 0-3 as 16-byte lane-major stores, which add them and store the swizzled sums.
 template <int FM, int FN, int SPW, int KIND>
 __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
                                                         int M, int N, int K, int splits, Epi e) {
   constexpr int NW = 8, TM = FM * 16, TN = FN * 16;
-  __shared__ __attribute__((aligned(16))) float red[NW * TM * TN];
+  constexpr bool LN = KIND == OASIS_EPI_GELU_TANH_LN;
+  constexpr bool RES = KIND == OASIS_EPI_GATED_RES_LN;
+  constexpr int UNITS = TM * TN / 8;
+  static_assert(!RES || UNITS <= NW * 64, "GATED_RES_LN: one unit per thread");
+  constexpr int SLOTS = LN ? NW / 2 : NW;  // partial tiles held in LDS at once
+  constexpr int ST = LN ? (TM * 32 + NW * 64 - 1) / (NW * 64) : 1;  // statistics loads per thread
+  __shared__ __attribute__((aligned(16))) float red[SLOTS * TM * TN];
+  __shared__ __attribute__((aligned(16))) float lnbuf[LN ? NW * FN * 256 + 16 * TN + TM * 2 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + TM - 1) / TM, Nt = N / TN;
   const int ks = K / 32;  // k-steps per 16-row block
@@ -723,10 +744,12 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
   const int t = pid - split * (Mt * Nt);
   const int nt = t / Mt, mt = t - nt * Mt;
   const int s0 = (split * NW + wave) * SPW;  // this wave's first k-step
+  const int lr = lane & 15, g = lane >> 4;
+  const int vrows = LN ? 2 * ((int)fast_div((uint32_t)(M - 1), e.rpf_magic, e.rpf_shift) + 1) : 0;
   // buffer loads: the wave's first A / B block as the scalar base, 32-bit lane offsets
   const __amdgpu_buffer_rsrc_t Ars = buffer_rsrc(A + ((int64_t)mt * FM * ks + s0) * 512);
   const __amdgpu_buffer_rsrc_t Brs = buffer_rsrc(B + ((int64_t)nt * FN * ks + s0) * 512);
-  i32x4 a[SPW][FM], b[SPW][FN];
+  i32x4 a[SPW][FM], b[SPW][FN], vb[LN ? SPW : 1];
 #pragma unroll
   for (int s = 0; s < SPW; ++s) {
 #pragma unroll
@@ -735,35 +758,236 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
 #pragma unroll
     for (int j = 0; j < FN; ++j)
       b[s][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(Brs, ((j * ks + s) * 64 + lane) * 16, 0, 0));
+    if constexpr (LN) {
+      // only the lanes of rows 2f, 2f + 1 of the pass's frames (lane & 15 < vrows) fetch
+      const __amdgpu_buffer_rsrc_t Vrs = buffer_rsrc(e.ln_mod + (int64_t)s0 * 512);
+      vb[s] = lr < vrows ? __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(Vrs, (s * 64 + lane) * 16, 0, 0))
+                         : i32x4{0, 0, 0, 0};
+    }
+  }
+  // LN: this thread's piece of the tile rows' statistics (32 lanes per row, two groups each)
+  f32x4 st[ST];
+  if constexpr (LN) {
+    const int kg = K / 16;
+#pragma unroll
+    for (int q = 0; q < ST; ++q) {
+      const int u = tid + q * NW * 64, r = u >> 5, c = (u & 31) * 2;
+      const int gm = mt * TM + r;
+      st[q] = (r < TM && gm < M && c < kg) ? *reinterpret_cast<const f32x4*>(e.ln_stats + ((int64_t)gm * kg + c) * 2)
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // GATED_RES_LN: this thread's unit (row r, columns c8..c8 + 7) and its operands
+  const int ur = tid / (TN / 8), uc8 = (tid - ur * (TN / 8)) * 8;
+  const int um = mt * TM + ur, un = nt * TN + uc8;
+  const bool unit_on = RES && tid < UNITS && um < M;
+  const int ufr = RES ? (int)fast_div((uint32_t)um, e.rpf_magic, e.rpf_shift) : 0;
+  const int nfr = RES ? (int)fast_div((uint32_t)(M - 1), e.rpf_magic, e.rpf_shift) + 1 : 0;
+  f32x4 ux[2], ug[2], us[2], ums[2], umt[2];
+  float uctr = 0.f;
+  if constexpr (RES) {
+    if (unit_on) {
+      const float* xp = e.out_f32 + (int64_t)um * e.ld_out + un;
+      const float* gp = e.gate + (int64_t)ufr * e.gate_fstride + un;
+      const float* sp = e.mod_scale + (int64_t)ufr * e.gate_fstride + un;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ux[h] = *reinterpret_cast<const f32x4*>(xp + 4 * h);
+        ug[h] = *reinterpret_cast<const f32x4*>(gp + 4 * h);
+        us[h] = *reinterpret_cast<const f32x4*>(sp + 4 * h);
+      }
+      uctr = e.ln_center[um];
+      if (um < nfr) {  // row m also carries frame m's modulate rows into the modulate block
+        const float* msp = e.mod_scale + (int64_t)um * e.gate_fstride + un;
+        const float* mtp = e.mod_shift + (int64_t)um * e.gate_fstride + un;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          ums[h] = *reinterpret_cast<const f32x4*>(msp + 4 * h);
+          umt[h] = *reinterpret_cast<const f32x4*>(mtp + 4 * h);
+        }
+      }
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA
-  f32x4 acc[FM][FN];
+  f32x4 acc[FM][FN], accv[LN ? FN : 1];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < SPW; ++s)
+  for (int j = 0; j < (LN ? FN : 1); ++j) accv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SPW; ++s) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         acc[i][j] = mfma16(__builtin_bit_cast(bf16x8, a[s][i]), __builtin_bit_cast(bf16x8, b[s][j]), acc[i][j]);
-  const int lr = lane & 15, g = lane >> 4;
+    if constexpr (LN) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        accv[j] = mfma16(__builtin_bit_cast(bf16x8, vb[s]), __builtin_bit_cast(bf16x8, b[s][j]), accv[j]);
+    }
+  }
+  auto slot_at = [&](float* base, int i, int j, int r) -> float* {
+    const int row = i * 16 + g * 4 + r, col = j * 16 + lr;
+    return base + row * TN + ((((col >> 2) ^ ((row >> 2) & 3)) << 2) | (col & 3));
+  };
+  if constexpr (LN) {
+    float* vred = lnbuf;                 // [NW][FN][64 lanes][4]: each wave's modulate-block rows
+    float* vsum = vred + NW * FN * 256;  // [16][TN]
+    float* rowst = vsum + 16 * TN;       // [TM] (mu, r)
+    // each row's mean and 1/deviation: 32 lanes' (sum, sum of squares) pairs
+    const float inv_k = 1.0f / (float)K;
+#pragma unroll
+    for (int q = 0; q < ST; ++q) {
+      const float sy = sum_xor16(row16_sum(st[q][0] + st[q][2])), sq = sum_xor16(row16_sum(st[q][1] + st[q][3]));
+      const int r = (tid + q * NW * 64) >> 5;
+      if ((lane & 31) == 0 && r < TM) {
+        const float mu = sy * inv_k;
+        rowst[r * 2] = mu;
+        rowst[r * 2 + 1] = rsqrtf(fmaxf(sq * inv_k - mu * mu, 0.f) + e.ln_eps);
+      }
+    }
+    // round 1: waves 4-7 park their partial tiles, lane-major; every wave its modulate-block rows
+    if (wave >= NW / 2) {
+      float* mine = red + (wave - NW / 2) * (TM * TN);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(mine + ((i * FN + j) * 64 + lane) * 4) = acc[i][j];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(vred + ((wave * FN + j) * 64 + lane) * 4) = accv[j];
+    __syncthreads();
+    if (wave < NW / 2) {
+      // round 2: waves 0-3 add the parked tile of wave + 4 (every read of it precedes this wave's
+      // first write, LDS keeping a wave's operations in order) and store the sums swizzled
+      float* slot = red + wave * (TM * TN);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const f32x4 p = *reinterpret_cast<const f32x4*>(slot + ((i * FN + j) * 64 + lane) * 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] += p[r];
+        }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) *slot_at(slot, i, j, r) = acc[i][j][r];
+    } else {
+      // meanwhile waves 4-7 sum the modulate-block rows over the waves: element (row, col) sits at
+      // lane (row / 4) * 16 + col % 16, register row % 4 of block col / 16
+      for (int u = tid - (NW / 2) * 64; u < 16 * TN; u += (NW / 2) * 64) {
+        const int row = u / TN, col = u - row * TN;
+        const int off = ((col >> 4) * 64 + (row >> 2) * 16 + (col & 15)) * 4 + (row & 3);
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += vred[w * FN * 256 + off];
+        vsum[u] = sum;
+      }
+    }
+    __syncthreads();
+    for (int u = tid; u < UNITS; u += NW * 64) {
+      const int r = u / (TN / 8), c8 = (u - r * (TN / 8)) * 8;
+      const int gm = mt * TM + r, gn = nt * TN + c8;
+      if (gm >= M) continue;
+      const int q0 = ((c8 >> 2) ^ ((r >> 2) & 3)) << 2, q1 = (((c8 >> 2) + 1) ^ ((r >> 2) & 3)) << 2;
+      f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0;
+#pragma unroll
+      for (int w = 0; w < SLOTS; ++w) {
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + r * TN + q0);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + r * TN + q1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a0[q] += c0[q];
+          a1[q] += c1[q];
+        }
+      }
+      const int fr = (int)fast_div((uint32_t)gm, e.rpf_magic, e.rpf_shift);
+      const float mu = rowst[r * 2], rr = rowst[r * 2 + 1];
+      const f32x4* c1p = reinterpret_cast<const f32x4*>(vsum + (2 * fr) * TN + c8);
+      const f32x4* c2p = reinterpret_cast<const f32x4*>(vsum + (2 * fr + 1) * TN + c8);
+      const f32x4 c10 = c1p[0], c11 = c1p[1], c20 = c2p[0], c21 = c2p[1];
+      f32x4 b0 = f32x4{0.f, 0.f, 0.f, 0.f}, b1 = b0;
+      if (e.bias) {
+        b0 = *reinterpret_cast<const f32x4*>(e.bias + gn);
+        b1 = *reinterpret_cast<const f32x4*>(e.bias + gn + 4);
+      }
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = gelu_tanh(rr * (a0[q] - mu * c10[q]) + c20[q] + b0[q]);
+        v[q + 4] = gelu_tanh(rr * (a1[q] - mu * c11[q]) + c21[q] + b1[q]);
+      }
+      store8_bf16(e.out_bf16 + (e.out_frag ? frag_index(gm, gn, e.ld_out >> 5) : (int64_t)gm * e.ld_out + gn), v);
+    }
+    return;
+  }
   float* mine = red + wave * (TM * TN);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = i * 16 + g * 4 + r, col = j * 16 + lr;
-        mine[row * TN + ((((col >> 2) ^ ((row >> 2) & 3)) << 2) | (col & 3))] = acc[i][j][r];
-      }
+      for (int r = 0; r < 4; ++r) *slot_at(mine, i, j, r) = acc[i][j][r];
   __syncthreads();
+  if constexpr (RES) {
+    if (tid >= UNITS || um >= M) return;  // a 16-column group's two threads leave together
+    const int q0 = ((uc8 >> 2) ^ ((ur >> 2) & 3)) << 2, q1 = (((uc8 >> 2) + 1) ^ ((ur >> 2) & 3)) << 2;
+    f32x4 s0v = f32x4{0.f, 0.f, 0.f, 0.f}, s1v = s0v;
+    if (e.bias) {
+      s0v = *reinterpret_cast<const f32x4*>(e.bias + un);
+      s1v = *reinterpret_cast<const f32x4*>(e.bias + un + 4);
+    }
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + ur * TN + q0);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(red + w * (TM * TN) + ur * TN + q1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s0v[q] += c0[q];
+        s1v[q] += c1[q];
+      }
+    }
+    float v[8], sy = 0.f, sq = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ux[0][q] += ug[0][q] * s0v[q];
+      ux[1][q] += ug[1][q] * s1v[q];
+      const float y0 = ux[0][q] - uctr, y1 = ux[1][q] - uctr;
+      sy += y0 + y1;
+      sq += y0 * y0 + y1 * y1;
+      v[q] = y0 * us[0][q];
+      v[q + 4] = y1 * us[1][q];
+    }
+    float* xp = e.out_f32 + (int64_t)um * e.ld_out + un;
+    *reinterpret_cast<f32x4*>(xp) = ux[0];
+    *reinterpret_cast<f32x4*>(xp + 4) = ux[1];
+    store8_bf16(e.out_bf16 + frag_index(um, un, e.ld_out >> 5), v);
+    sy += dpp_mov<DPP_XOR1>(sy);  // the 16-column group's pair of threads
+    sq += dpp_mov<DPP_XOR1>(sq);
+    if ((uc8 & 15) == 0)
+      *reinterpret_cast<float2*>(e.ln_stats + ((int64_t)um * (e.ld_out >> 4) + (un >> 4)) * 2) = make_float2(sy, sq);
+    if (um < nfr) {
+      float ms[8], mt8[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ms[q] = ums[0][q];
+        ms[q + 4] = ums[1][q];
+        mt8[q] = umt[0][q];
+        mt8[q + 4] = umt[1][q];
+      }
+      store8_bf16(e.ln_mod + frag_index(2 * um, un, e.ld_out >> 5), ms);
+      store8_bf16(e.ln_mod + frag_index(2 * um + 1, un, e.ld_out >> 5), mt8);
+    }
+    return;
+  }
   constexpr bool partial_only = KIND == OASIS_EPI_PARTIAL_F32;
   const bool is_partial = partial_only || (KIND < 0 && e.kind == OASIS_EPI_PARTIAL_F32);
-  constexpr int UNITS = TM * TN / 8;
   for (int u = tid; u < UNITS; u += NW * 64) {
     const int r = u / (TN / 8), c8 = (u - r * (TN / 8)) * 8;
     const int gm = mt * TM + r, gn = nt * TN + c8;
@@ -796,8 +1020,12 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
 }
 
 // the DiT's projections at one and two frames get kernels with the epilogue fixed at compile time
+// (the two LN kinds exist only in these kernels: GELU_TANH_LN on tiles 4 blocks wide, GATED_RES_LN
+// on 48-row tiles)
 template <int FM, int FN, int SPW, int KIND>
 constexpr bool frag_special() {
+  if (KIND == OASIS_EPI_GELU_TANH_LN) return FN == 4;
+  if (KIND == OASIS_EPI_GATED_RES_LN) return FM == 3 && FN != 3;
   return SPW == 4 && ((KIND == OASIS_EPI_QKV_ROPE && FN == 3) || (KIND == OASIS_EPI_GELU_TANH_FRAG && FN == 4) ||
                       (KIND == OASIS_EPI_PARTIAL_F32 && (FN == 4 || (FM == 3 && FN <= 2))));
 }
@@ -820,7 +1048,9 @@ void launch_frag3(const bf16* A, const bf16* B, int M, int N, int K, int splits,
   const dim3 g(Mt * Nt * splits);
   if (try_frag<FM, FN, SPW, OASIS_EPI_PARTIAL_F32>(g, A, B, M, N, K, splits, e, s) ||
       try_frag<FM, FN, SPW, OASIS_EPI_GELU_TANH_FRAG>(g, A, B, M, N, K, splits, e, s) ||
-      try_frag<FM, FN, SPW, OASIS_EPI_QKV_ROPE>(g, A, B, M, N, K, splits, e, s))
+      try_frag<FM, FN, SPW, OASIS_EPI_QKV_ROPE>(g, A, B, M, N, K, splits, e, s) ||
+      try_frag<FM, FN, SPW, OASIS_EPI_GATED_RES_LN>(g, A, B, M, N, K, splits, e, s) ||
+      try_frag<FM, FN, SPW, OASIS_EPI_GELU_TANH_LN>(g, A, B, M, N, K, splits, e, s))
     return;
   hipLaunchKernelGGL((gemm_frag_kernel<FM, FN, SPW, -1>), g, dim3(512), 0, s, A, B, M, N, K, splits, e);
 }
@@ -836,17 +1066,23 @@ void launch_frag2(int spw, const bf16* A, const bf16* B, int M, int N, int K, in
 // (hipGraphs of 100 launches over 32 weight copies): 80-row tiles (5 blocks) for the wide products
 // over two frames (FC1, QKV and FC2's split-K slices), 48-row tiles (3 blocks) at one frame and
 // for the unsplit O projection; then the widest n tile that still gives 256 workgroups (80-row
-// tiles) or 192 (48-row tiles).
-void frag_tile(int64_t M, int64_t N, int splits, int& fm, int& fn) {
+// tiles) or 192 (48-row tiles). GELU_TANH_LN tiles are 4 blocks wide, GATED_RES_LN ones 1, 2 or 4.
+void frag_tile(int64_t M, int64_t N, int splits, int kind, int& fm, int& fn) {
   fm = (M <= 160 || (N <= 1024 && splits == 1)) ? 3 : 5;
   const int64_t mt = (M + fm * 16 - 1) / (fm * 16);
   const int64_t want = fm == 5 ? 256 : 192;
   fn = 0;
-  for (int c = 4; c >= 1; --c)
+  if (kind == OASIS_EPI_GELU_TANH_LN) {
+    fn = N % 64 == 0 ? 4 : 0;
+    return;
+  }
+  for (int c = 4; c >= 1; --c) {
+    if (kind == OASIS_EPI_GATED_RES_LN && c == 3) continue;
     if (N % (16 * c) == 0 && (fn == 0 || mt * (N / (16 * c)) * splits >= want)) {
       fn = c;
       if (mt * (N / (16 * c)) * splits >= want) break;
     }
+  }
 }
 
 // The K loop is unrolled for 1, 2, 4 or 8 K tiles per wave (K / splits = 256, 512, 1024, 2048); the
@@ -1015,6 +1251,8 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
                     const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
   OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm: null operand");
   OASIS_REQUIRE(aligned16(A) && aligned16(B), OASIS_ERR_ARG, "gemm: A and B must be 16-byte aligned");
+  OASIS_REQUIRE(ex.kind != OASIS_EPI_GATED_RES_LN && ex.kind != OASIS_EPI_GELU_TANH_LN, OASIS_ERR_ARG,
+                "gemm: epilogue kind %d runs on oasis_gemm_bf16_frag only", ex.kind);
   OASIS_REQUIRE(M > 0 && N > 0 && K > 0, OASIS_ERR_SHAPE, "gemm: empty shape M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
   OASIS_REQUIRE(K % BK == 0, OASIS_ERR_SHAPE, "gemm: K=%lld must be a multiple of 64", (long long)K);
@@ -1068,7 +1306,11 @@ int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, in
   OASIS_REQUIRE(e.kind != OASIS_EPI_UNPATCHIFY && e.kind != OASIS_EPI_GELU_TANH_FP8, OASIS_ERR_ARG,
                 "gemm_frag: epilogue kind %d is not supported", e.kind);
   int fm, fn;
-  frag_tile(M, N, splits, fm, fn);
+  frag_tile(M, N, splits, e.kind, fm, fn);
+  OASIS_REQUIRE(fn > 0, OASIS_ERR_SHAPE, "gemm_frag: N=%lld has no tile for epilogue kind %d (GELU_TANH_LN needs "
+                "N %% 64 == 0)", (long long)N, e.kind);
+  OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES_LN || fm == 3, OASIS_ERR_SHAPE,
+                "gemm_frag: GATED_RES_LN needs N <= 1024 and one split");
   const int64_t rows = (M + fm * 16 - 1) / (fm * 16) * (fm * 16);
   OASIS_REQUIRE(a_rows >= rows, OASIS_ERR_SHAPE, "gemm_frag: A holds %lld rows, the %d-row tiles read %lld",
                 (long long)a_rows, fm * 16, (long long)rows);

@@ -33,6 +33,13 @@ struct Epi {
   uint8_t* out_fp8;
   uint8_t* out_scale;
   int64_t ld_scale;
+  const float* mod_scale;
+  const float* mod_shift;
+  const float* ln_center;
+  float* ln_stats;
+  bf16* ln_mod;
+  float ln_eps;
+  int out_frag;
   // n / rows_per_frame and n / frames_per_stream as (n * magic) >> shift (see DivMagic)
   uint64_t rpf_magic, fps_magic;
   int rpf_shift, fps_shift;
@@ -334,6 +341,13 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.out_fp8 = static_cast<uint8_t*>(x.out_fp8);
   e.out_scale = static_cast<uint8_t*>(x.out_scale);
   e.ld_scale = x.ld_scale;
+  e.mod_scale = x.mod_scale;
+  e.mod_shift = x.mod_shift;
+  e.ln_center = x.ln_center;
+  e.ln_stats = x.ln_stats;
+  e.ln_mod = static_cast<bf16*>(x.ln_mod);
+  e.ln_eps = x.ln_eps;
+  e.out_frag = x.out_frag;
   return e;
 }
 
@@ -371,6 +385,32 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
     case OASIS_EPI_GELU_TANH_FRAG:
       OASIS_REQUIRE(e.out_bf16 && e.ld_out >= N && e.ld_out % 32 == 0 && M % 16 == 0, OASIS_ERR_ARG,
                     "gemm: GELU_TANH_FRAG needs out_bf16, ld_out >= N (multiple of 32) and M %% 16 == 0");
+      break;
+    case OASIS_EPI_GATED_RES_LN:
+      OASIS_REQUIRE(e.rows_per_frame < (1ll << 31), OASIS_ERR_SHAPE, "gemm: rows_per_frame too large");
+      OASIS_REQUIRE(e.out_f32 && e.out_bf16 && e.gate && e.mod_scale && e.mod_shift && e.ln_center && e.ln_stats &&
+                        e.ln_mod,
+                    OASIS_ERR_NULL, "gemm: GATED_RES_LN needs out_f32, out_bf16, gate, mod_scale, mod_shift, "
+                                    "ln_center, ln_stats and ln_mod");
+      OASIS_REQUIRE(aligned16(e.mod_scale) && aligned16(e.mod_shift) && aligned16(e.ln_mod) &&
+                        ((uintptr_t)e.ln_stats & 7) == 0,
+                    OASIS_ERR_ARG, "gemm: mod_scale, mod_shift and ln_mod must be 16-byte and ln_stats 8-byte aligned");
+      OASIS_REQUIRE(e.ld_out == N && N % 32 == 0 && M % 16 == 0 && e.gate_fstride % 4 == 0, OASIS_ERR_ARG,
+                    "gemm: GATED_RES_LN needs ld_out == N (a multiple of 32), M %% 16 == 0 and gate_fstride %% 4 == 0");
+      OASIS_REQUIRE((M + e.rows_per_frame - 1) / e.rows_per_frame <= 8, OASIS_ERR_SHAPE,
+                    "gemm: GATED_RES_LN covers at most 8 frames");
+      break;
+    case OASIS_EPI_GELU_TANH_LN:
+      OASIS_REQUIRE(e.rows_per_frame < (1ll << 31), OASIS_ERR_SHAPE, "gemm: rows_per_frame too large");
+      OASIS_REQUIRE(e.out_bf16 && e.ln_stats && e.ln_mod, OASIS_ERR_NULL,
+                    "gemm: GELU_TANH_LN needs out_bf16, ln_stats and ln_mod");
+      OASIS_REQUIRE(aligned16(e.ln_stats) && aligned16(e.ln_mod), OASIS_ERR_ARG,
+                    "gemm: ln_stats and ln_mod must be 16-byte aligned");
+      OASIS_REQUIRE(e.ld_out >= N && e.ld_out % (e.out_frag ? 32 : 8) == 0 && M % 16 == 0 && e.ln_eps >= 0.f,
+                    OASIS_ERR_ARG, "gemm: GELU_TANH_LN needs ld_out >= N (a multiple of 32 in fragment order, "
+                                   "else 8), M %% 16 == 0 and ln_eps >= 0");
+      OASIS_REQUIRE((M + e.rows_per_frame - 1) / e.rows_per_frame <= 8, OASIS_ERR_SHAPE,
+                    "gemm: GELU_TANH_LN covers at most 8 frames");
       break;
     case OASIS_EPI_GELU_TANH_FP8:
       OASIS_REQUIRE(e.out_fp8 && e.out_scale && N % 32 == 0 && e.ld_out >= N && e.ld_out % 8 == 0 &&

@@ -525,6 +525,8 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
                     int splits, hipStream_t s) {
   const bool aq = A_scale != nullptr;
   OASIS_REQUIRE(A && B && w_scale, OASIS_ERR_NULL, "gemm_fp8: null operand");
+  OASIS_REQUIRE(ex.kind != OASIS_EPI_GATED_RES_LN && ex.kind != OASIS_EPI_GELU_TANH_LN, OASIS_ERR_ARG,
+                "gemm_fp8: epilogue kind %d runs on oasis_gemm_bf16_frag only", ex.kind);
   OASIS_REQUIRE(aligned16(A) && aligned16(B) && aligned16(w_scale) && (reinterpret_cast<uintptr_t>(A_scale) & 3) == 0,
                 OASIS_ERR_ARG, "gemm_fp8: A, B and w_scale must be 16-byte aligned, A_scale 4-byte aligned");
   OASIS_REQUIRE(!aq || (lds >= K / 32 && lds % 4 == 0 && lda % 16 == 0), OASIS_ERR_SHAPE,

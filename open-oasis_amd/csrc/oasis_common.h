@@ -43,11 +43,12 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
                     int splits, hipStream_t s);
 // oasis_residual_ln with an optional fp8-block LN output (y8 e4m3 [M, D], y8_scale e8m0
 // [M, D/32]) in place of the bf16 one (norm.hip).
-// y_frag: the bf16 output in MFMA fragment order (below 2048 rows).
+// y_frag: the bf16 output in MFMA fragment order (below 2048 rows). mean_out: each row's mean
+// (after the residual), [M] fp32 (below 2048 rows, with an LN output).
 int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
-                hipStream_t s, bool y_frag = false);
+                hipStream_t s, bool y_frag = false, float* mean_out = nullptr);
 // The DiT's final layer in fp32 (norm.hip): the pending residual (n_partials split-K slices +
 // bias, gated), LN, modulate with the frame's (scale_p1, shift) rows, then v_out[M, 64] =
 // h @ W^T + b with W fp32 [64, D]. With chunk set, rows chunk_row0.. also take one DDIM step of
@@ -195,6 +196,11 @@ OASIS_DEV float max_xor32(float v) {
 OASIS_DEV float quad_max(float v) {
   v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
   return fmaxf(v, dpp_mov<DPP_XOR2>(v));
+}
+// sum over the 4 lanes of a quad (every lane of the quad gets the same value)
+OASIS_DEV float quad_sum(float v) {
+  v += dpp_mov<DPP_XOR1>(v);
+  return v + dpp_mov<DPP_XOR2>(v);
 }
 OASIS_DEV float oct_max(float v) {
   v = quad_max(v);

@@ -61,8 +61,10 @@ struct Plan {
 };
 
 // Fragment-order operands, one bit each: the LN output QKV reads, the attention output O reads,
-// the LN output FC1 reads, and FC1's GELU output FC2 reads.
-enum { FRAG_QKV = 1, FRAG_O = 2, FRAG_FC1 = 4, FRAG_FC2 = 8, FRAG_ALL = 15 };
+// the LN output FC1 reads, and FC1's GELU output FC2 reads. FRAG_LN (with FRAG_O) carries the
+// LayerNorm + modulate after O into FC1 (GATED_RES_LN / GELU_TANH_LN): one residual_ln launch
+// fewer per sub-block, FC1 on gemm_frag whatever FRAG_FC1 says.
+enum { FRAG_QKV = 1, FRAG_O = 2, FRAG_FC1 = 4, FRAG_FC2 = 8, FRAG_LN = 16, FRAG_ALL = 31 };
 
 const Plan& plan() {
   static Plan p = [] {
@@ -94,8 +96,8 @@ const Plan& plan() {
       }
     }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
-    q.frag1 = FRAG_O | FRAG_FC2;
-    q.frag2 = FRAG_O;
+    q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
+    q.frag2 = FRAG_O | FRAG_LN;
     if (const char* env = getenv("OASIS_FRAG")) {
       int a = 0, b = 0;
       const int n = sscanf(env, "%d,%d", &a, &b);
@@ -352,9 +354,14 @@ int frag_mask(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int6
   for (int64_t j = j0; j < j1; ++j) {
     if (!w->qkv_wf[j]) m &= ~FRAG_QKV;
     if (!w->out_wf[j]) m &= ~FRAG_O;
-    if (!w->fc1_wf[j]) m &= ~FRAG_FC1;
+    if (!w->fc1_wf[j]) m &= ~(FRAG_FC1 | FRAG_LN);
     if (!w->fc2_wf[j]) m &= ~FRAG_FC2;
   }
+  // the carried LayerNorm: O on gemm_frag, the statistics buffers, FC1 tiles 64 columns wide, at
+  // most 8 frames (the modulate block's 16 rows)
+  const int64_t P = (int64_t)w->grid_h * w->grid_w;
+  if (!(m & FRAG_O) || !buf->ln_mean || !buf->ln_stats || !buf->ln_mod || Dm % 64 != 0 || (M + P - 1) / P > 8)
+    m &= ~FRAG_LN;
   return m;
 }
 
@@ -386,6 +393,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   const int sf_frag = frag_fc2_splits(w, buf);
   const int fg = frag_mask(w, buf, M, j0, j1, sf_frag);
   const bool f_qkv = fg & FRAG_QKV, f_o = fg & FRAG_O, f_fc1 = fg & FRAG_FC1, f_fc2 = fg & FRAG_FC2;
+  const bool f_ln = fg & FRAG_LN;
   const int so_use = f_o ? 1 : so;
   if (f_fc2) sf = sf_frag;
   const int64_t FR = buf->frag_rows;
@@ -416,7 +424,8 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
-                                 fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv));
+                                 fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
+                                 f_ln ? buf->ln_mean : nullptr));
     // with OASIS_TEMPORAL_FUSED=1 or 2, two-frame temporal windows (the T = 2 step and the frame's
     // first, cache-filling pass; with 2 also the current-frame passes against the cache): QKV,
     // RoPE and the causal attention in one kernel
@@ -482,18 +491,49 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
         OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s, f_o));
     }
     if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
-    // O projection as split-K partials; bias + gated residual + LN + modulate fused after
-    if (f_o)
-      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use, s));
-    else
-      OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
-    OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
-                                 a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
     gelu.bias = w->fc1_b[j];
-    if (f_fc1)
-      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
-    else
-      OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+    if (f_ln) {
+      // O + bias + gated residual into x in the epilogue, which also leaves FC1 the centred rows
+      // times the modulate scale (fragment order, in h) and their per-32-column sums; FC1 finishes
+      // the LayerNorm + modulate (the identity at gemm_frag_kernel)
+      oasis_epilogue_t o = epi_zero();
+      o.kind = OASIS_EPI_GATED_RES_LN;
+      o.bias = w->out_b[j];
+      o.out_f32 = buf->x;
+      o.out_bf16 = buf->h;
+      o.ld_out = D;
+      o.gate = a + 2 * D;
+      o.gate_fstride = fs;
+      o.rows_per_frame = P;
+      o.mod_scale = a + 4 * D;
+      o.mod_shift = a + 3 * D;
+      o.ln_center = buf->ln_mean;
+      o.ln_stats = buf->ln_stats;
+      o.ln_mod = buf->ln_mod;
+      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, o, 1, s));
+      oasis_epilogue_t f1 = gelu;
+      f1.kind = OASIS_EPI_GELU_TANH_LN;
+      f1.rows_per_frame = P;
+      f1.ln_stats = buf->ln_stats;
+      f1.ln_mod = buf->ln_mod;
+      f1.ln_eps = kLnEps;
+      f1.out_frag = f_fc2 ? 1 : 0;
+      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, f1, 1, s));
+    } else {
+      // O projection as split-K partials; bias + gated residual + LN + modulate fused after
+      if (f_o)
+        OASIS_TRY(
+            oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use, s));
+      else
+        OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
+      OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
+                                   a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
+      if (f_fc1)
+        OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
+      else
+        OASIS_TRY(
+            proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+    }
     if (f_fc2)
       OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->mlp, FR, (const bf16*)w->fc2_wf[j], M, D, Dm, part, sf, s));
     else

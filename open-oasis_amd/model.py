@@ -12,9 +12,9 @@ HBM layout (nn.Linear [out, in] weights, fp32 biases/tables):
     the adaLN rows of all 32 sub-blocks for every conditioning row at once.
   - per sub-block (bf16): qkv_w [3D, D], out_w [D, D], fc1_w [Dm, D], fc2_w [D, Dm], each
     contiguous (37.7 MB of the 1.21 GB weight set per sub-block incl. adaLN).
-  - per sub-block (bf16), for the passes of at most 320 tokens: out_w and fc2_w once more in
-    the MFMA fragment order of ``tile_rows16`` (``DiT(frag=...)`` picks the roles; 335 MB at
-    Oasis-500M for the default two).
+  - per sub-block (bf16), for the passes of at most 320 tokens: out_w, fc1_w and fc2_w once
+    more in the MFMA fragment order of ``tile_rows16`` (``DiT(frag=...)`` picks the roles; 604 MB
+    at Oasis-500M for the default three).
   - fp32, as the reference keeps them (oasis_inference.py:512-532,1821-1826): the
     conditioning MLP and action projection (zero-padded to 64 inputs), the patch embed
     [D, 64] in (p, q, c) column order, the final layer's adaLN [2D, D] and linear [64, D].
@@ -40,7 +40,7 @@ def tile_rows16(W):
 
 
 FRAG_ROLES_ALL = ("qkv", "out", "fc1", "fc2")
-FRAG_ROLES_DEFAULT = ("out", "fc2")
+FRAG_ROLES_DEFAULT = ("out", "fc1", "fc2")
 
 
 def frag_rows(m):
@@ -109,8 +109,9 @@ class DiT:
         self.weights = weights
         # bf16: projection weights also in MFMA fragment order (tile_rows16) for the passes of at
         # most 320 tokens (the step, the K/V-cache passes), for the roles whose operands those passes
-        # keep in that order (OASIS_FRAG in the library; the default uses O and FC2). frag: True for
-        # those two, False for none, or an iterable of "qkv", "out", "fc1", "fc2".
+        # keep in that order (OASIS_FRAG in the library; by default O, FC1 with the LayerNorm after
+        # O carried into it, and FC2 at one frame). frag: True for those three, False for none, or
+        # an iterable of "qkv", "out", "fc1", "fc2".
         roles = FRAG_ROLES_DEFAULT if frag is True else (() if not frag else tuple(frag))
         if any(r not in FRAG_ROLES_ALL for r in roles):
             raise ValueError("frag roles must be among %s" % (FRAG_ROLES_ALL,))
@@ -354,6 +355,11 @@ class DiTWorkspace:
             setattr(S, name, getattr(self, name).data_ptr())
         S.max_splits = max_splits
         S.frag_rows = fr if dit.frag else 0
+        if "fc1" in dit.frag_roles:   # the LayerNorm after O carried into FC1: row means and statistics
+            self.ln_mean = torch.zeros(max_rows, device=dev)
+            self.ln_stats = torch.zeros(max_rows, d // 16, 2, device=dev)
+            self.ln_mod = torch.zeros(16, d, device=dev, dtype=bf)
+            S.ln_mean, S.ln_stats, S.ln_mod = self.ln_mean.data_ptr(), self.ln_stats.data_ptr(), self.ln_mod.data_ptr()
         if dit.weights == "fp8":  # fp8 activation blocks: e4m3 bytes + one e8m0 scale per 32 columns
             u8 = torch.uint8
             self.act8 = torch.zeros(max_rows, d, device=dev, dtype=u8)

@@ -125,6 +125,120 @@ def test_frag_gemm_rejects_what_it_does_not_cover():
         L.call("oasis_gemm_bf16_frag", L.ptr(A), 320, L.ptr(W), 288, 4096, 1024, ctypes.byref(e), 8, h)
 
 
+def _ln_inputs(M, D, T, g):
+    """x, the LN-before-QKV row means it is centred by (of a nearby x), and per-frame gate /
+    scale / shift rows at a frame stride wider than D (as in the adaLN table)."""
+    x = torch.randn(M, D, generator=g) * 2 + torch.randn(M, 1, generator=g)
+    center = x.mean(1) + torch.randn(M, generator=g) * 0.05
+    fs = 6 * D
+    ada = torch.randn(T, fs, generator=g) * 0.5
+    ada[:, D:2 * D] += 1.0     # scale + 1
+    return x, center, ada, fs
+
+
+def _frame_rows(ada, off, D, P, M):
+    """[M, D]: row m takes frame m // P's row of ada at column offset off."""
+    return ada[:, off:off + D].repeat_interleave(P, 0)[:M]
+
+
+@pytest.mark.parametrize("M", [144, 288])
+def test_gated_res_ln_epilogue(M):
+    """O with GATED_RES_LN: x += gate * (acc + bias); h = bf16((x - centre) * scale) in fragment
+    order; per-16-column (sum, sum of squares) of x - centre; the modulate block."""
+    D, P = 1024, 144
+    T = (M + P - 1) // P
+    g = torch.Generator().manual_seed(M + 7)
+    A = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    W = (torch.randn(D, D, generator=g) * 0.03).to(torch.bfloat16)
+    bias = torch.randn(D, generator=g) * 0.1
+    x, center, ada, fs = _ln_inputs(M, D, T, g)
+    gate_off, scale_off, shift_off = 2 * D, D, 0
+    rows = M_.frag_rows(M)
+    xd, cd, adad, bd = cuda(x), cuda(center), cuda(ada), cuda(bias)
+    h = torch.full((rows, D), float("nan"), device="cuda", dtype=torch.bfloat16)
+    stats = torch.full((M, D // 16, 2), float("nan"), device="cuda")
+    mod = torch.full((16, D), float("nan"), device="cuda", dtype=torch.bfloat16)
+    Af, Wf = _frag(cuda(A), rows), M_.tile_rows16(cuda(W))
+    e = _epi(kind=L.EPI_GATED_RES_LN, bias=bd.data_ptr(), out_f32=xd.data_ptr(), out_bf16=h.data_ptr(), ld_out=D,
+             gate=adad.data_ptr() + gate_off * 4, gate_fstride=fs, rows_per_frame=P,
+             mod_scale=adad.data_ptr() + scale_off * 4, mod_shift=adad.data_ptr() + shift_off * 4,
+             ln_center=cd.data_ptr(), ln_stats=stats.data_ptr(), ln_mod=mod.data_ptr())
+    L.call("oasis_gemm_bf16_frag", L.ptr(Af), rows, L.ptr(Wf), M, D, D, ctypes.byref(e), 1, L.stream_handle())
+    torch.cuda.synchronize()
+    gate, scale = _frame_rows(ada, gate_off, D, P, M), _frame_rows(ada, scale_off, D, P, M)
+    x_ref = x.double() + gate.double() * (A.double() @ W.double().t() + bias.double())
+    assert_close(xd.cpu(), x_ref, 0.9999999, 1e-5, "GATED_RES_LN x M=%d" % M)
+    # h and the statistics from the kernel's own x: the same fp32 operations, so h is the
+    # correctly rounded bf16 of (x - centre) * scale
+    xg = xd.cpu()
+    y = xg - center[:, None]
+    h_ref = (y * scale).to(torch.bfloat16)
+    hg = M_.untile_rows16(h)[:M].cpu()
+    assert torch.equal(hg, h_ref), (hg.float() - h_ref.float()).abs().max().item()
+    st_ref = torch.stack([y.double().reshape(M, D // 16, 16).sum(-1), (y.double() ** 2).reshape(M, D // 16, 16).sum(-1)], -1)
+    assert_close(stats.cpu(), st_ref, 0.9999999, 1e-5, "GATED_RES_LN statistics M=%d" % M)
+    # the modulate block: rows 2f, 2f + 1 = bf16 scale, shift of frame f (the rest untouched)
+    mb = M_.untile_rows16(mod).cpu()
+    for f in range(T):
+        assert torch.equal(mb[2 * f], ada[f, scale_off:scale_off + D].to(torch.bfloat16))
+        assert torch.equal(mb[2 * f + 1], ada[f, shift_off:shift_off + D].to(torch.bfloat16))
+    assert torch.isnan(mb[2 * T:].float()).all()
+
+
+@pytest.mark.parametrize("M,out_frag", [(144, 1), (288, 0), (288, 1)])
+def test_gelu_tanh_ln_epilogue(M, out_frag):
+    """FC1 with GELU_TANH_LN on the output of GATED_RES_LN (y * scale, the statistics and the
+    modulate block) equals gelu(LN(x) * scale + shift) @ W^T + bias: against that in fp64, and
+    against the unfused order (bf16 LN output, then the GEMM)."""
+    D, Dm, P = 1024, 4096, 144
+    T = (M + P - 1) // P
+    g = torch.Generator().manual_seed(M + 11 + out_frag)
+    x, center, ada, fs = _ln_inputs(M, D, T, g)
+    W = (torch.randn(Dm, D, generator=g) * 0.03).to(torch.bfloat16)
+    bias = torch.randn(Dm, generator=g) * 0.1
+    scale_off, shift_off = D, 0
+    scale, shift = _frame_rows(ada, scale_off, D, P, M), _frame_rows(ada, shift_off, D, P, M)
+    y = x - center[:, None]
+    ys = (y * scale).to(torch.bfloat16)
+    stats = torch.stack([y.reshape(M, D // 16, 16).sum(-1), (y * y).reshape(M, D // 16, 16).sum(-1)], -1)
+    rows = M_.frag_rows(M)
+    sd, bd = cuda(stats), cuda(bias)
+    mod = torch.zeros(16, D)
+    for f in range(T):
+        mod[2 * f], mod[2 * f + 1] = ada[f, scale_off:scale_off + D], ada[f, shift_off:shift_off + D]
+    modd = M_.tile_rows16(cuda(mod, torch.bfloat16))
+    out = torch.full((rows if out_frag else M, Dm), float("nan"), device="cuda", dtype=torch.bfloat16)
+    e = _epi(kind=L.EPI_GELU_TANH_LN, bias=bd.data_ptr(), out_bf16=out.data_ptr(), ld_out=Dm, rows_per_frame=P,
+             ln_stats=sd.data_ptr(), ln_mod=modd.data_ptr(), ln_eps=1e-6, out_frag=out_frag)
+    A, Wf = _frag(cuda(ys), rows), M_.tile_rows16(cuda(W))
+    L.call("oasis_gemm_bf16_frag", L.ptr(A), rows, L.ptr(Wf), M, Dm, D, ctypes.byref(e), 1, L.stream_handle())
+    torch.cuda.synchronize()
+    got = (M_.untile_rows16(out)[:M] if out_frag else out).cpu()
+    ln = (x.double() - x.double().mean(1, keepdim=True)) / torch.sqrt(x.double().var(1, unbiased=False, keepdim=True) + 1e-6)
+    hm = ln * scale.double() + shift.double()
+    ref = oracle.gelu_tanh(hm @ W.double().t() + bias.double())
+    assert_close(got, ref, 0.99999, 1e-2, "GELU_TANH_LN M=%d vs fp64" % M)
+    unfused = oracle.gelu_tanh(hm.to(torch.bfloat16).double() @ W.double().t() + bias.double())
+    assert_close(got, unfused, 0.99999, 1e-2, "GELU_TANH_LN M=%d vs the unfused order" % M)
+
+
+def test_ln_kinds_rejected_where_unsupported():
+    M, D = 288, 1024
+    A = torch.zeros(320, D, device="cuda", dtype=torch.bfloat16)
+    W = torch.zeros(4096, D, device="cuda", dtype=torch.bfloat16)
+    buf = torch.zeros(M * 4096 * 2, device="cuda")
+    e = _epi(kind=L.EPI_GELU_TANH_LN, out_bf16=buf.data_ptr(), ld_out=4096, ln_mod=buf.data_ptr(),
+             ln_stats=buf.data_ptr(), rows_per_frame=16, ln_eps=1e-6)
+    h = L.stream_handle()
+    with pytest.raises(L.OasisError, match="frag only"):
+        L.call("oasis_gemm_bf16", L.ptr(A), D, L.ptr(W), D, M, 4096, D, ctypes.byref(e), h)
+    with pytest.raises(L.OasisError, match="8 frames"):        # the modulate block holds 8 frames
+        L.call("oasis_gemm_bf16_frag", L.ptr(A), 320, L.ptr(W), M, 4096, D, ctypes.byref(e), 1, h)
+    e.rows_per_frame = 144
+    with pytest.raises(L.OasisError, match="PARTIAL_F32"):     # one split only
+        L.call("oasis_gemm_bf16_frag", L.ptr(A), 320, L.ptr(W), M, 4096, D, ctypes.byref(e), 2, h)
+
+
 @pytest.fixture(scope="module")
 def dits():
     dr = pkg.synth.Draw(43)
