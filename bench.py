@@ -54,32 +54,52 @@ def _event_ms(fn, stream, n, graph=None):
 # HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
 # scaled by what the same counter reads for a plain device copy of known size.
-TRAFFIC = {"fc1": 15619781, "gemv": 405115017, "fc1_4608_bf16": 90722144, "fc1_4608_fp8": 46773862}
+TRAFFIC = {"fc1_ln": 17448619, "fc1_row": 15622976, "gemv": 405109129, "fc1_4608_bf16": 90723174,
+           "fc1_4608_fp8": 46798391}
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100, graph=True):
-    """The FC1 projection alone (same buffers, same tile choice as in the step), timed with HIP
-    events on the step stream. Launch i uses the weights of sub-block i % 32: as in the step, each
-    launch reads weights that 31 launches (268 MB of other weights, more than the 256 MB
-    memory-side cache) have passed over since their last use, so they come from HBM."""
+    """The FC1 projection alone, as the step runs it at 288 tokens (the same kernel, buffers and
+    tile: with the library's default plan FC1 with the carried LayerNorm on the fragment-order
+    weights), timed with HIP events on the step stream. Launch i uses the weights of sub-block
+    i % 32: as in the step, each launch reads weights that 31 launches (268 MB of other weights,
+    more than the 256 MB memory-side cache) have passed over since their last use, so they come
+    from HBM. Returns (ms, flop, algorithmic bytes, kind)."""
     L = pkg._lib
-    M, D, Dm = 288, dit.d, dit.d_mlp
+    M, D, Dm, P = 288, dit.d, dit.d_mlp, dit.P
     S, n_sub = dit.struct, dit.n_sub
+    plan = L.frag_plan(M)
+    ln = bool(plan & L.FRAG_LN and plan & L.FRAG_O) and "fc1" in dit.frag_roles and hasattr(ws, "ln_mod")
+    frag = ln or (bool(plan & L.FRAG_FC1) and "fc1" in dit.frag_roles)
+    out_frag = 1 if plan & L.FRAG_FC2 and "fc2" in dit.frag_roles else 0
+    F = (M + P - 1) // P
+    rows = ws.struct.frag_rows
     eps = []
     for j in range(n_sub):
         e = L.Epilogue()
-        e.kind, e.bias, e.out_bf16, e.ld_out = L.EPI_GELU_TANH, S.fc1_b[j], ws.mlp.data_ptr(), Dm
-        eps.append((ctypes.c_void_p(S.fc1_w[j]), e))
+        e.bias, e.out_bf16, e.ld_out = S.fc1_b[j], ws.mlp.data_ptr(), Dm
+        if ln:
+            e.kind, e.rows_per_frame, e.ln_eps, e.out_frag = L.EPI_GELU_TANH_LN, P, 1e-6, out_frag
+            e.ln_stats, e.ln_mod = ws.ln_stats.data_ptr(), ws.ln_mod.data_ptr()
+        else:
+            e.kind = L.EPI_GELU_TANH_FRAG if out_frag and frag else L.EPI_GELU_TANH
+        eps.append((ctypes.c_void_p(S.fc1_wf[j] if frag else S.fc1_w[j]), e))
     A, it = L.ptr(ws.h), [0]
 
     def fc1():
         B, e = eps[it[0] % n_sub]
         it[0] += 1
-        L.call("oasis_gemm_bf16", A, D, B, D, M, Dm, D, ctypes.byref(e), L.stream_handle(stream))
+        if frag:
+            L.call("oasis_gemm_bf16_frag", A, rows, B, M, Dm, D, ctypes.byref(e), 1, L.stream_handle(stream))
+        else:
+            L.call("oasis_gemm_bf16", A, D, B, D, M, Dm, D, ctypes.byref(e), L.stream_handle(stream))
     ms = _event_ms(fc1, stream, n, pkg.Graph if graph else None)
     flop = 2 * M * D * Dm
     nbytes = M * D * 2 + Dm * D * 2 + Dm * 4 + M * Dm * 2   # A, W, bias, out (bf16)
-    return ms, flop, nbytes
+    if ln:   # the row statistics (16-column sums) and the frames' modulate rows
+        nbytes += M * (D // 16) * 8 + 2 * F * D * 2
+    kind = "ln" if ln else ("frag" if frag else "row")
+    return ms, flop, nbytes, kind
 
 
 def _gemv_timing(pkg, dit, ws, stream, R=2, n=50, graph=True):
@@ -506,7 +526,7 @@ def main():
     ms_step_gpu = ev0.elapsed_time(ev1) / args.steps
 
     ws = step.ws
-    fc1_ms, fc1_flop, fc1_bytes = _fc1_timing(pkg, dit, ws, step.stream)
+    fc1_ms, fc1_flop, fc1_bytes, fc1_kind = _fc1_timing(pkg, dit, ws, step.stream)
     ada_ms, ada_bytes = _gemv_timing(pkg, dit, ws, step.stream)
     fc1_tflops = fc1_flop / (fc1_ms * 1e-3) / 1e12
     ada_gbs = ada_bytes / (ada_ms * 1e-3) / 1e9
@@ -517,18 +537,25 @@ def main():
     fc1_ai = fc1_flop / fc1_bytes
     ridge = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     fc1_gbs = fc1_bytes / (fc1_ms * 1e-3) / 1e9
-    fc1_roofline = {"kernel": "gemm_wave_kernel<80,64,2,4,GELU_TANH,72> (bf16 MFMA GEMM, 4 waves splitting K, each "
-                              "over its own direct-to-LDS ring; 80-row tiles every 72 rows, 256 workgroups), FC1 "
-                              "projection + bias + tanh-GELU (M=288, N=4096, K=1024), the largest of the step's 128 "
-                              "projections (4 per sub-block); launch i uses sub-block i % 32's weights (cold, as in "
-                              "the step); 100 launches in one hipGraph"}
+    fc1_desc = {
+        "ln": "gemm_frag_kernel<5,4,4,GELU_TANH_LN> (bf16 MFMA GEMM on fragment-order operands, 1 KB per wave load "
+              "straight into registers, 8 waves splitting K; 80 x 64 tiles, 256 workgroups), FC1 projection + the "
+              "LayerNorm + modulate carried from O (row statistics, modulate rows as one more MFMA block) + bias + "
+              "tanh-GELU (M=288, N=4096, K=1024)",
+        "frag": "gemm_frag_kernel<5,4,4,GELU_TANH> (bf16 MFMA GEMM on fragment-order operands, 8 waves splitting K; "
+                "80 x 64 tiles, 256 workgroups), FC1 projection + bias + tanh-GELU (M=288, N=4096, K=1024)",
+        "row": "gemm_wave_kernel<80,64,2,4,GELU_TANH,72> (bf16 MFMA GEMM, 4 waves splitting K, each over its own "
+               "direct-to-LDS ring; 80-row tiles every 72 rows, 256 workgroups), FC1 projection + bias + tanh-GELU "
+               "(M=288, N=4096, K=1024)"}[fc1_kind]
+    fc1_roofline = {"kernel": fc1_desc + ", the step's longest kernel (32 launches per step); launch i uses sub-block "
+                              "i % 32's weights (cold, as in the step); 100 launches in one hipGraph"}
     if fc1_ai < ridge:
         fc1_roofline.update({"bound": "hbm", "achieved": round(fc1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(fc1_gbs / HBM_PEAK_GBS, 4)})
     else:
         fc1_roofline.update({"bound": "mfma", "achieved": round(fc1_tflops, 1), "peak": BF16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(fc1_tflops / BF16_PEAK_TFLOPS, 4)})
-    fc1_roofline.update({"traffic": TRAFFIC.get("fc1"), "avg_launch_ms": round(fc1_ms, 5),
+    fc1_roofline.update({"traffic": TRAFFIC.get("fc1_" + fc1_kind), "avg_launch_ms": round(fc1_ms, 5),
                          "algorithmic_flop": fc1_flop, "algorithmic_bytes": fc1_bytes,
                          "arithmetic_intensity": round(fc1_ai, 1), "ridge_flop_per_byte": round(ridge, 1),
                          "mfma_tflops": round(fc1_tflops, 1), "mfma_frac": round(fc1_tflops / BF16_PEAK_TFLOPS, 4)})

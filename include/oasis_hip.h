@@ -47,6 +47,12 @@ int oasis_abi_version(void);
  * No counterpart in the reference (its kernels take ttnn tensors). */
 int64_t oasis_abi_struct_size(int which);
 
+/* The fragment-order plan (OASIS_FRAG) for DiT forward passes of `rows` tokens: a mask of 1 QKV,
+ * 2 O, 4 FC1, 8 FC2 (whose operand is kept in MFMA fragment order) and 16 (the LayerNorm after O
+ * carried into FC1), before a pass narrows it to the weights and buffers it has; 0 above 320 rows.
+ * No counterpart in the reference (a tuning query, for benchmarks and tests). */
+int oasis_dit_frag_plan(int64_t rows);
+
 /* ======================================================================
  * Reference kernel surface (destination passing: inputs first, outputs last).
  * Elementwise kernels take flat tensors of n elements, all of one dtype.

@@ -17,6 +17,7 @@ EPI_STORE_F32, EPI_STORE_BF16, EPI_GELU_TANH, EPI_GELU_ERF = 0, 1, 2, 3
 EPI_GATED_RES, EPI_RESIDUAL, EPI_QKV_ROPE, EPI_UNPATCHIFY = 4, 5, 6, 7
 EPI_PARTIAL_F32, EPI_GELU_TANH_FP8, EPI_GELU_TANH_FRAG = 8, 9, 10
 EPI_GATED_RES_LN, EPI_GELU_TANH_LN = 11, 12
+FRAG_QKV, FRAG_O, FRAG_FC1, FRAG_FC2, FRAG_LN = 1, 2, 4, 8, 16
 ACT_NONE, ACT_SILU, ACT_TEMB = 0, 1, 2
 ABI_VERSION = 6
 WEIGHTS_BF16, WEIGHTS_FP8 = 0, 1
@@ -115,6 +116,7 @@ SIGNATURES = {
     "oasis_gemm_bf16": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_p],
     "oasis_gemm_bf16_config": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_gemm_bf16_frag": [c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_p],
+    "oasis_dit_frag_plan": [c_i64],
     "oasis_gemm_fp8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i, c_p],
     "oasis_quantize_fp8_rows": [c_p, c_i64, c_i64, c_p, c_p, c_p],
     "oasis_gemm_fp8_a8": [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, P(Epilogue), c_i, c_i,
@@ -212,6 +214,11 @@ def call(name, *args):
     if rc != OASIS_OK:
         raise OasisError(name, rc, h.oasis_last_error().decode(errors="replace"))
     return rc
+
+
+def frag_plan(rows):
+    """The library's fragment-order mask (FRAG_* bits) for DiT passes of `rows` tokens."""
+    return lib().oasis_dit_frag_plan(rows)
 
 
 def ptr(t):

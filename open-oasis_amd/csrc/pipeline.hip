@@ -120,6 +120,11 @@ const Plan& plan() {
 extern "C" const char* oasis_last_error(void) { return oasis::g_err; }
 extern "C" int oasis_abi_version(void) { return OASIS_ABI_VERSION; }
 
+extern "C" int oasis_dit_frag_plan(int64_t rows) {
+  if (rows <= 0 || rows > 320) return 0;
+  return rows <= 160 ? plan().frag1 : plan().frag2;
+}
+
 extern "C" int64_t oasis_abi_struct_size(int which) {
   switch (which) {
     case 0: return sizeof(oasis_epilogue_t);
