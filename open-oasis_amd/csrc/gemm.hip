@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(const bf16* __restrict__ 
 // rows of A and a few weight slices instead of every row of A.
 // The epilogue stages 16 rows of a wave's tile at a time in LDS owned by that wave alone.
 
-template <int BM, int BN, int WM, int WN, int STAGES, int GN = 8>
+template <int BM, int BN, int WM, int WN, int STAGES, int GN = 8, int KIND = -1>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __restrict__ A, int64_t lda,
                                                                const bf16* __restrict__ B, int64_t ldb, int M,
                                                                int N, int K, int splits, Epi e) {
@@ -482,6 +482,36 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
     __syncthreads();
   }
 
+  // QKV + RoPE + head split: what a lane's columns decide (q, k or v; head; dimension; rotated or
+  // not) is fixed for the whole tile, so it is worked out once per pass here, leaving each row its
+  // frame / position split and a 32-bit offset (the host checks that q, k and v offsets fit)
+  constexpr bool QKV = KIND == OASIS_EPI_QKV_ROPE;
+  constexpr int NPASS = (16 * UPR + 63) / 64;  // passes of the 64 lanes over a 16-row group
+  bf16* qb[NPASS];
+  int qcol[NPASS], qd0[NPASS];
+  bool qrot[NPASS];
+  uint32_t qp[NPASS], qt[NPASS], qs[NPASS];  // pass q's row in group i: position, frame in stream, stream
+  const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
+  if constexpr (QKV) {
+    const int D = e.n_heads * 64;
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+      const int gn = n0 + wn * TN + ((lane + 64 * q) % UPR) * 8;
+      const int which = (gn >= D) + (gn >= 2 * D);
+      const int nn = gn - which * D;
+      qb[q] = which == 0 ? e.q : (which == 1 ? e.k : e.v);
+      qd0[q] = nn & 63;
+      qcol[q] = (nn >> 6) * (int)e.s_h + qd0[q];
+      qrot[q] = which < 2;
+      // group 0's row; later groups step it by 16 rows
+      const uint32_t gm = (uint32_t)(m0 + wm * TM + (lane + 64 * q) / UPR);
+      const uint32_t f = fast_div(gm, e.rpf_magic, e.rpf_shift);
+      qp[q] = gm - f * rpf;
+      qs[q] = fast_div(f, e.fps_magic, e.fps_shift);
+      qt[q] = f - qs[q] * fps;
+    }
+  }
+
   // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
   // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
@@ -500,7 +530,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
       const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
       const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
       if (gm < M && gn < N) {
-        if (e.kind == OASIS_EPI_PARTIAL_F32) {
+        if (KIND == OASIS_EPI_PARTIAL_F32 || (KIND < 0 && e.kind == OASIS_EPI_PARTIAL_F32)) {
           float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
           *reinterpret_cast<f32x4*>(d) = c0;
           *reinterpret_cast<f32x4*>(d + 4) = c1;
@@ -509,7 +539,42 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
           const f32x4 b0 = q1 ? hb[NBQ - 1][0] : hb[0][0], b1 = q1 ? hb[NBQ - 1][1] : hb[0][1];
           float v[8] = {c0[0] + b0[0], c0[1] + b0[1], c0[2] + b0[2], c0[3] + b0[3],
                         c1[0] + b1[0], c1[1] + b1[1], c1[2] + b1[2], c1[3] + b1[3]};
-          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false);
+          if constexpr (QKV) {
+            const int qi = u >> 6;
+            const uint32_t p = qp[qi], t = qt[qi], bb = qs[qi];
+            if (qrot[qi]) {
+              const uint32_t pos = e.rope_by_frame ? t : p;
+              const float* cp = tab_rows ? tab + pos * ROPE_TP + qd0[qi] : e.rope_cos + pos * 64 + qd0[qi];
+              const float* sp = tab_rows ? tab + (tab_rows + pos) * ROPE_TP + qd0[qi] : e.rope_sinp + pos * 64 + qd0[qi];
+              const f32x4 cs0 = *reinterpret_cast<const f32x4*>(cp), cs1 = *reinterpret_cast<const f32x4*>(cp + 4);
+              const f32x4 sn0 = *reinterpret_cast<const f32x4*>(sp), sn1 = *reinterpret_cast<const f32x4*>(sp + 4);
+              float rv[8];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                rv[j] = v[j] * cs0[j] + v[j ^ 1] * sn0[j];
+                rv[j + 4] = v[j + 4] * cs1[j] + v[(j + 4) ^ 1] * sn1[j];
+              }
+#pragma unroll
+              for (int j = 0; j < 8; ++j) v[j] = rv[j];
+            }
+            const uint32_t off = bb * (uint32_t)e.s_b + t * (uint32_t)e.s_t + p * (uint32_t)e.s_p + (uint32_t)qcol[qi];
+            store8_bf16(qb[qi] + off, v);
+          } else {
+            epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false, KIND);
+          }
+        }
+      }
+    }
+    if constexpr (QKV) {
+#pragma unroll
+      for (int q = 0; q < NPASS; ++q) {
+        qp[q] += 16;
+        while (qp[q] >= rpf) {
+          qp[q] -= rpf;
+          if (++qt[q] == fps) {
+            qt[q] = 0;
+            ++qs[q];
+          }
         }
       }
     }
@@ -1140,8 +1205,25 @@ hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, in
                       const Epi& e, hipStream_t s) {
   if ((K / splits) % 64 != 0) return hipErrorInvalidConfiguration;
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
-                     A, lda, B, ldb, M, N, K, splits, e);
+  const dim3 grid(Mt * Nt * splits), block(WM * WN * 64);
+  // the projections' epilogues get kernels of their own (the rest read the kind at run time)
+  switch (e.kind) {
+    case OASIS_EPI_QKV_ROPE:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_QKV_ROPE>), grid, block, 0, s, A, lda, B,
+                         ldb, M, N, K, splits, e);
+      break;
+    case OASIS_EPI_GELU_TANH:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_GELU_TANH>), grid, block, 0, s, A, lda,
+                         B, ldb, M, N, K, splits, e);
+      break;
+    case OASIS_EPI_PARTIAL_F32:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_PARTIAL_F32>), grid, block, 0, s, A,
+                         lda, B, ldb, M, N, K, splits, e);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN>), grid, block, 0, s, A, lda, B, ldb, M, N, K,
+                         splits, e);
+  }
   return hipGetLastError();
 }
 

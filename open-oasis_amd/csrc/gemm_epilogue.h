@@ -8,6 +8,9 @@ namespace {
 
 
 
+// pitch (floats) of a position's row in the LDS copy of the QKV rotation tables (rope_to_lds)
+constexpr int ROPE_TP = 68;
+
 struct Epi {
   int kind;
   int n_heads;
@@ -136,8 +139,8 @@ __device__ __forceinline__ void qkv_rope_tables(const Epi& e, int64_t m, int n0,
   const uint32_t f = fast_div((uint32_t)m, e.rpf_magic, e.rpf_shift), p = (uint32_t)m - f * rpf;
   const uint32_t t = f - fast_div(f, e.fps_magic, e.fps_shift) * fps;
   const uint32_t pos = e.rope_by_frame ? t : p;
-  const float* cp = tab ? tab + pos * 64 + d0 : e.rope_cos + pos * 64 + d0;
-  const float* sp = tab ? tab + (tab_rows + pos) * 64 + d0 : e.rope_sinp + pos * 64 + d0;
+  const float* cp = tab ? tab + pos * ROPE_TP + d0 : e.rope_cos + pos * 64 + d0;
+  const float* sp = tab ? tab + (tab_rows + pos) * ROPE_TP + d0 : e.rope_sinp + pos * 64 + d0;
   const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp);
   const f32x4 c1 = *reinterpret_cast<const f32x4*>(cp + 4);
   const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp);
@@ -288,22 +291,26 @@ __device__ __forceinline__ void epilogue8(const Epi& e, int64_t m, int n0, float
 }
 
 // Rows of the QKV rotation tables a large-token workgroup copies to LDS for its epilogue (the
-// cos rows, then the sin rows; 512 bytes per position): the positions of a frame for the
+// cos rows, then the sin rows, each row ROPE_TP floats apart): the positions of a frame for the
 // spatial tables, the frames of a stream for the temporal ones. 0 when the tables do not fit
-// in tab_bytes (the epilogue then reads them from global memory).
+// in tab_bytes (the epilogue then reads them from global memory). The 4-float pad puts the same
+// dimension of consecutive positions 4 banks apart: a pass of the epilogue reads ~11 rows' tables
+// at the same few dimensions, which a 64-float pitch sends to the same banks.
 __device__ __forceinline__ int rope_lds_rows(const Epi& e, int M, int tab_bytes) {
   if (e.kind != OASIS_EPI_QKV_ROPE) return 0;
   // only positions some row m < M reaches: m % rows_per_frame, or its frame's index in the stream
   const int64_t frames = (M + e.rows_per_frame - 1) / e.rows_per_frame;
   const int64_t rows = e.rope_by_frame ? min(e.frames_per_stream, frames) : min(e.rows_per_frame, (int64_t)M);
-  return rows * 512 <= tab_bytes ? (int)rows : 0;
+  return rows * 2 * ROPE_TP * 4 <= tab_bytes ? (int)rows : 0;
 }
 // Workgroup-wide copy of those rows into tab (all threads of the workgroup call it).
 __device__ __forceinline__ void rope_to_lds(const Epi& e, float* tab, int rows, int tid, int nthreads) {
   const int chunks = rows * 16;  // 16-byte chunks per table
   for (int i = tid; i < 2 * chunks; i += nthreads) {
-    const float* src = i < chunks ? e.rope_cos + i * 4 : e.rope_sinp + (i - chunks) * 4;
-    *reinterpret_cast<f32x4*>(tab + i * 4) = *reinterpret_cast<const f32x4*>(src);
+    const int sel = i >= chunks, j = i - sel * chunks;
+    const float* src = (sel ? e.rope_sinp : e.rope_cos) + j * 4;
+    *reinterpret_cast<f32x4*>(tab + (sel * rows + (j >> 4)) * ROPE_TP + (j & 15) * 4) =
+        *reinterpret_cast<const f32x4*>(src);
   }
 }
 
@@ -425,6 +432,15 @@ int check_epilogue(const Epi& e, int64_t M, int64_t N, int splits) {
                     "gemm: QKV_ROPE needs q/k/v and rope tables");
       OASIS_REQUIRE(e.n_heads > 0 && N == 3LL * e.n_heads * 64, OASIS_ERR_SHAPE,
                     "gemm: QKV_ROPE needs N == 3*n_heads*64");
+      {
+        // the kernels address q, k and v with 32-bit element offsets
+        const int64_t fr = (M + e.rows_per_frame - 1) / e.rows_per_frame;
+        const int64_t streams = (fr + e.frames_per_stream - 1) / e.frames_per_stream;
+        const int64_t last = (streams - 1) * e.s_b + (min(fr, e.frames_per_stream) - 1) * e.s_t +
+                             (min(M, e.rows_per_frame) - 1) * e.s_p + (e.n_heads - 1) * e.s_h + 64;
+        OASIS_REQUIRE(e.s_b >= 0 && e.s_t >= 0 && e.s_p >= 0 && e.s_h >= 0 && last < (1ll << 31), OASIS_ERR_SHAPE,
+                      "gemm: QKV_ROPE offsets must be below 2^31 elements");
+      }
       break;
     case OASIS_EPI_UNPATCHIFY:
       OASIS_REQUIRE(e.out_f32 && e.unpatch_patch > 0 && e.unpatch_grid_w > 0, OASIS_ERR_ARG,

@@ -105,16 +105,20 @@ def test_gemm_gated_and_plain_residual():
 
 
 @pytest.mark.parametrize("layout,tile", [("spatial", -1), ("temporal", -1), ("vae", -1), ("spatial", 11),
-                                         ("temporal", 11), ("spatial", 12), ("vae", 11)])
+                                         ("temporal", 11), ("spatial", 12), ("vae", 11), ("spatial", 5),
+                                         ("temporal", 5), ("temporal", 6), ("spatial", 6), ("temporal", 7),
+                                         ("vae", 6)])
 def test_gemm_qkv_rope(layout, tile):
-    """QKV + RoPE + head split into each attention layout: the default tile (K = 256), and the
-    wave-split tiles 11 / 12 with the kernels specialised for this epilogue (K = 1024)."""
+    """QKV + RoPE + head split into each attention layout: the default tile (K = 256), the
+    wave-split tiles 11 / 12 with the kernels specialised for this epilogue (K = 1024), and the
+    large-token tiles 5-7 (288 x 256 / 192 / 128; their epilogue steps each lane's row through
+    positions, frames and streams 16 rows at a time, here over two streams of two frames)."""
     H, D = 4, 256
     K = 256 if tile < 0 else 1024
     if layout == "vae":
-        B_, T, P = 1, 1, 576
+        B_, T, P = (1, 1, 576) if tile < 5 else (1, 2, 576)
     else:
-        B_, T, P = (2, 2, 144) if tile < 0 else (1, 2, 144)
+        B_, T, P = (2, 2, 144) if tile < 0 or tile >= 5 else (1, 2, 144)
     M, N = B_ * T * P, 3 * D
     g = _gen(5)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
