@@ -96,8 +96,9 @@ def _fc1_timing(pkg, dit, ws, stream, n=100, graph=True):
     ms = _event_ms(fc1, stream, n, pkg.Graph if graph else None)
     flop = 2 * M * D * Dm
     nbytes = M * D * 2 + Dm * D * 2 + Dm * 4 + M * Dm * 2   # A, W, bias, out (bf16)
-    if ln:   # the row statistics (16-column sums) and the frames' modulate rows
-        nbytes += M * (D // 16) * 8 + 2 * F * D * 2
+    if ln:   # the row statistics (sums over 32-column groups at 288 tokens) and the frames' modulate rows
+        G = 32 if M > 160 else 16
+        nbytes += M * (D // G) * 8 + 2 * F * D * 2
     kind = "ln" if ln else ("frag" if frag else "row")
     return ms, flop, nbytes, kind
 

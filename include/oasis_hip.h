@@ -165,13 +165,14 @@ enum {
    * without the normalised rows ever being formed. oasis_gemm_bf16_frag only.            */
   OASIS_EPI_GATED_RES_LN = 11,/* x = out_f32[m, n] += gate[f, n] * (acc + bias[n]) (N % 32 == 0);
                                  y = x - ln_center[m]; out_bf16 (fragment order, ld_out
-                                 columns) = y * mod_scale[f, n]; ln_stats[m][n/16] =
-                                 (sum of y, sum of y^2) over those 16 columns; ln_mod rows
+                                 columns) = y * mod_scale[f, n]; ln_stats[m][n/G] = (sum of
+                                 y, sum of y^2) over groups of G columns (G = 32 when its
+                                 tiles are 32 columns wide or more, else 16); ln_mod rows
                                  2f, 2f + 1 = bf16(mod_scale[f]), bf16(mod_shift[f]) for the
                                  frames f < ceil(M / rows_per_frame) <= 8                  */
   OASIS_EPI_GELU_TANH_LN = 12 /* A = a GATED_RES_LN output over K = its N (K <= 1024, one
                                  split): gelu_tanh(r (acc - mu c1[f, n]) + c2[f, n] + bias[n])
-                                 with mu, r = 1/sqrt(var + ln_eps) from ln_stats[m][0..K/16),
+                                 with mu, r = 1/sqrt(var + ln_eps) from ln_stats[m][0..K/G),
                                  c1 and c2 = ln_mod rows 2f and 2f + 1 @ B^T; into out_bf16,
                                  in fragment order when out_frag                          */
 };
@@ -214,7 +215,8 @@ typedef struct {
   const float* mod_scale;   /* GATED_RES_LN: modulate scale (+1) row of frame f at mod_scale + f*gate_fstride */
   const float* mod_shift;   /* GATED_RES_LN: modulate shift rows, the same stride     */
   const float* ln_center;   /* GATED_RES_LN: [M], subtracted before the statistics    */
-  float* ln_stats;          /* *_LN: [M][N/16][2] (GATED_RES_LN's N = GELU_TANH_LN's K) */
+  float* ln_stats;          /* *_LN: [M][N/G][2], G 16 or 32 (GATED_RES_LN's N = GELU_TANH_LN's K;
+                               [M][N/16][2] always holds them) */
   void* ln_mod;             /* *_LN: bf16 [16, N] in fragment order (rows 2f, 2f + 1)  */
   float ln_eps;             /* GELU_TANH_LN                                           */
   int out_frag;             /* GELU_TANH_LN: out_bf16 in fragment order              */

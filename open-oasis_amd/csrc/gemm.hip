@@ -798,7 +798,7 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
   constexpr int UNITS = TM * TN / 8;
   static_assert(!RES || UNITS <= NW * 64, "GATED_RES_LN: one unit per thread");
   constexpr int SLOTS = LN ? NW / 2 : NW;  // partial tiles held in LDS at once
-  constexpr int ST = LN ? (TM * 32 + NW * 64 - 1) / (NW * 64) : 1;  // statistics loads per thread
+  constexpr int ST = LN ? (TM * 32 + NW * 64 - 1) / (NW * 64) : 1;  // statistics loads per thread (at most)
   __shared__ __attribute__((aligned(16))) float red[SLOTS * TM * TN];
   __shared__ __attribute__((aligned(16))) float lnbuf[LN ? NW * FN * 256 + 16 * TN + TM * 2 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -830,13 +830,15 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
                          : i32x4{0, 0, 0, 0};
     }
   }
-  // LN: this thread's piece of the tile rows' statistics (32 lanes per row, two groups each)
+  // LN: this thread's piece of the tile rows' statistics (K / ln_group groups a row, two per lane:
+  // 16 or 32 lanes a row)
   f32x4 st[ST];
+  const int lpr_log = LN ? (e.ln_group == 32 ? 4 : 5) : 5;  // log2 of the lanes per row
   if constexpr (LN) {
-    const int kg = K / 16;
+    const int kg = K / e.ln_group;
 #pragma unroll
     for (int q = 0; q < ST; ++q) {
-      const int u = tid + q * NW * 64, r = u >> 5, c = (u & 31) * 2;
+      const int u = tid + q * NW * 64, r = u >> lpr_log, c = (u & ((1 << lpr_log) - 1)) * 2;
       const int gm = mt * TM + r;
       st[q] = (r < TM && gm < M && c < kg) ? *reinterpret_cast<const f32x4*>(e.ln_stats + ((int64_t)gm * kg + c) * 2)
                                           : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -902,13 +904,17 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
     float* vred = lnbuf;                 // [NW][FN][64 lanes][4]: each wave's modulate-block rows
     float* vsum = vred + NW * FN * 256;  // [16][TN]
     float* rowst = vsum + 16 * TN;       // [TM] (mu, r)
-    // each row's mean and 1/deviation: 32 lanes' (sum, sum of squares) pairs
+    // each row's mean and 1/deviation: its lanes' (sum, sum of squares) pairs
     const float inv_k = 1.0f / (float)K;
 #pragma unroll
     for (int q = 0; q < ST; ++q) {
-      const float sy = sum_xor16(row16_sum(st[q][0] + st[q][2])), sq = sum_xor16(row16_sum(st[q][1] + st[q][3]));
-      const int r = (tid + q * NW * 64) >> 5;
-      if ((lane & 31) == 0 && r < TM) {
+      float sy = row16_sum(st[q][0] + st[q][2]), sq = row16_sum(st[q][1] + st[q][3]);
+      if (lpr_log == 5) {
+        sy = sum_xor16(sy);
+        sq = sum_xor16(sq);
+      }
+      const int r = (tid + q * NW * 64) >> lpr_log;
+      if ((lane & ((1 << lpr_log) - 1)) == 0 && r < TM) {
         const float mu = sy * inv_k;
         rowst[r * 2] = mu;
         rowst[r * 2 + 1] = rsqrtf(fmaxf(sq * inv_k - mu * mu, 0.f) + e.ln_eps);
@@ -1033,10 +1039,16 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
     *reinterpret_cast<f32x4*>(xp) = ux[0];
     *reinterpret_cast<f32x4*>(xp + 4) = ux[1];
     store8_bf16(e.out_bf16 + frag_index(um, un, e.ld_out >> 5), v);
-    sy += dpp_mov<DPP_XOR1>(sy);  // the 16-column group's pair of threads
+    // the statistics group's threads: a pair (16 columns) on 16-column tiles, else a quad (32)
+    constexpr int G = TN >= 32 ? 32 : 16;
+    sy += dpp_mov<DPP_XOR1>(sy);
     sq += dpp_mov<DPP_XOR1>(sq);
-    if ((uc8 & 15) == 0)
-      *reinterpret_cast<float2*>(e.ln_stats + ((int64_t)um * (e.ld_out >> 4) + (un >> 4)) * 2) = make_float2(sy, sq);
+    if (G == 32) {
+      sy += dpp_mov<DPP_XOR2>(sy);
+      sq += dpp_mov<DPP_XOR2>(sq);
+    }
+    if ((uc8 & (G - 1)) == 0)
+      *reinterpret_cast<float2*>(e.ln_stats + ((int64_t)um * (e.ld_out / G) + un / G) * 2) = make_float2(sy, sq);
     if (um < nfr) {
       float ms[8], mt8[8];
 #pragma unroll
@@ -1389,6 +1401,15 @@ int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, in
                 "gemm_frag: epilogue kind %d is not supported", e.kind);
   int fm, fn;
   frag_tile(M, N, splits, e.kind, fm, fn);
+  // the statistics' group width: GATED_RES_LN sums whole 32-column groups on tiles at least 32
+  // columns wide, else 16-column ones; GELU_TANH_LN derives the same from M and its K (= O's N)
+  Epi eg = e;
+  if (e.kind == OASIS_EPI_GATED_RES_LN) eg.ln_group = fn >= 2 ? 32 : 16;
+  if (e.kind == OASIS_EPI_GELU_TANH_LN) {
+    int om, on;
+    frag_tile(M, K, 1, OASIS_EPI_GATED_RES_LN, om, on);
+    eg.ln_group = on >= 2 ? 32 : 16;
+  }
   OASIS_REQUIRE(fn > 0, OASIS_ERR_SHAPE, "gemm_frag: N=%lld has no tile for epilogue kind %d (GELU_TANH_LN needs "
                 "N %% 64 == 0)", (long long)N, e.kind);
   OASIS_REQUIRE(e.kind != OASIS_EPI_GATED_RES_LN || fm == 3, OASIS_ERR_SHAPE,
@@ -1402,7 +1423,7 @@ int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, in
   const int spw = (int)(slice / 256);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
 #define OASIS_FRAG(FM_, FN_) \
-  if (fm == FM_ && fn == FN_) launch_frag2<FM_, FN_>(spw, A, B, Mi, Ni, Ki, splits, e, s)
+  if (fm == FM_ && fn == FN_) launch_frag2<FM_, FN_>(spw, A, B, Mi, Ni, Ki, splits, eg, s)
   OASIS_FRAG(5, 4); else OASIS_FRAG(5, 3); else OASIS_FRAG(5, 2); else OASIS_FRAG(5, 1);
   else OASIS_FRAG(3, 4); else OASIS_FRAG(3, 3); else OASIS_FRAG(3, 2); else OASIS_FRAG(3, 1);
 #undef OASIS_FRAG

@@ -43,6 +43,7 @@ struct Epi {
   bf16* ln_mod;
   float ln_eps;
   int out_frag;
+  int ln_group;  // *_LN: columns per statistics group (16 or 32), set by the fragment-order launcher
   // n / rows_per_frame and n / frames_per_stream as (n * magic) >> shift (see DivMagic)
   uint64_t rpf_magic, fps_magic;
   int rpf_shift, fps_shift;
@@ -355,6 +356,7 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.ln_mod = static_cast<bf16*>(x.ln_mod);
   e.ln_eps = x.ln_eps;
   e.out_frag = x.out_frag;
+  e.ln_group = 16;
   return e;
 }
 

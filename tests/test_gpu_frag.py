@@ -136,6 +136,12 @@ def _ln_inputs(M, D, T, g):
     return x, center, ada, fs
 
 
+def _stat_cols(M):
+    """Columns per statistics group of the carried LayerNorm at D = 1024: O's fragment-order tiles
+    are 32 columns wide above 160 rows (then 32-column groups), 16 at one frame."""
+    return 32 if M > 160 else 16
+
+
 def _frame_rows(ada, off, D, P, M):
     """[M, D]: row m takes frame m // P's row of ada at column offset off."""
     return ada[:, off:off + D].repeat_interleave(P, 0)[:M]
@@ -144,7 +150,7 @@ def _frame_rows(ada, off, D, P, M):
 @pytest.mark.parametrize("M", [144, 288])
 def test_gated_res_ln_epilogue(M):
     """O with GATED_RES_LN: x += gate * (acc + bias); h = bf16((x - centre) * scale) in fragment
-    order; per-16-column (sum, sum of squares) of x - centre; the modulate block."""
+    order; per-group (16 or 32 columns) sums of x - centre and its squares; the modulate block."""
     D, P = 1024, 144
     T = (M + P - 1) // P
     g = torch.Generator().manual_seed(M + 7)
@@ -156,7 +162,8 @@ def test_gated_res_ln_epilogue(M):
     rows = M_.frag_rows(M)
     xd, cd, adad, bd = cuda(x), cuda(center), cuda(ada), cuda(bias)
     h = torch.full((rows, D), float("nan"), device="cuda", dtype=torch.bfloat16)
-    stats = torch.full((M, D // 16, 2), float("nan"), device="cuda")
+    G = _stat_cols(M)
+    stats = torch.full((M, D // G, 2), float("nan"), device="cuda")
     mod = torch.full((16, D), float("nan"), device="cuda", dtype=torch.bfloat16)
     Af, Wf = _frag(cuda(A), rows), M_.tile_rows16(cuda(W))
     e = _epi(kind=L.EPI_GATED_RES_LN, bias=bd.data_ptr(), out_f32=xd.data_ptr(), out_bf16=h.data_ptr(), ld_out=D,
@@ -175,7 +182,7 @@ def test_gated_res_ln_epilogue(M):
     h_ref = (y * scale).to(torch.bfloat16)
     hg = M_.untile_rows16(h)[:M].cpu()
     assert torch.equal(hg, h_ref), (hg.float() - h_ref.float()).abs().max().item()
-    st_ref = torch.stack([y.double().reshape(M, D // 16, 16).sum(-1), (y.double() ** 2).reshape(M, D // 16, 16).sum(-1)], -1)
+    st_ref = torch.stack([y.double().reshape(M, D // G, G).sum(-1), (y.double() ** 2).reshape(M, D // G, G).sum(-1)], -1)
     assert_close(stats.cpu(), st_ref, 0.9999999, 1e-5, "GATED_RES_LN statistics M=%d" % M)
     # the modulate block: rows 2f, 2f + 1 = bf16 scale, shift of frame f (the rest untouched)
     mb = M_.untile_rows16(mod).cpu()
@@ -200,7 +207,8 @@ def test_gelu_tanh_ln_epilogue(M, out_frag):
     scale, shift = _frame_rows(ada, scale_off, D, P, M), _frame_rows(ada, shift_off, D, P, M)
     y = x - center[:, None]
     ys = (y * scale).to(torch.bfloat16)
-    stats = torch.stack([y.reshape(M, D // 16, 16).sum(-1), (y * y).reshape(M, D // 16, 16).sum(-1)], -1)
+    G = _stat_cols(M)
+    stats = torch.stack([y.reshape(M, D // G, G).sum(-1), (y * y).reshape(M, D // G, G).sum(-1)], -1)
     rows = M_.frag_rows(M)
     sd, bd = cuda(stats), cuda(bias)
     mod = torch.zeros(16, D)
