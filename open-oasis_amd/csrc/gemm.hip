@@ -623,13 +623,21 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   // the wave index read back as a scalar, so that the addresses built from it stay in SGPRs
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
-  // work id -> (split, n tile, m tile), m fastest and the split outermost: an XCD's contiguous
-  // range of ids covers the M tiles of a few weight slices of one K slice, so its L2 fetches
-  // one K slice of A rather than all of them
+  // work id -> (split, n tile, m tile), the split outermost: an XCD's contiguous range of ids
+  // covers one K slice of A rather than all of them. Up to 7 row tiles m runs fastest (the ids
+  // cover all rows of a few weight slices); from 8 (576 tokens and up) in groups of 4 weight
+  // slices, so that an XCD's share is a block of rows x 4 slices and its L2 fetches part of A
+  // (the VAE's O: 6 x 4 tiles per XCD instead of 12 x 2)
   const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
-  const int split = pid / (Mt * Nt);
-  const int t = pid - split * (Mt * Nt);
-  const int nt = t / Mt, mt = t - nt * Mt;
+  int split, mt, nt;
+  if (Mt >= 8) {
+    grouped_tile(pid, Mt, Nt, 4, split, mt, nt);
+  } else {
+    split = pid / (Mt * Nt);
+    const int t = pid - split * (Mt * Nt);
+    nt = t / Mt;
+    mt = t - nt * Mt;
+  }
   const int m0 = mt * BMS, n0 = nt * BN;
   constexpr int nk = NK;                           // K tiles per wave: K = 256 NK splits (host-checked)
   const int kb = (split * NW + wave) * nk * 64;
