@@ -805,10 +805,14 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
   constexpr bool RES = KIND == OASIS_EPI_GATED_RES_LN;
   constexpr int UNITS = TM * TN / 8;
   static_assert(!RES || UNITS <= NW * 64, "GATED_RES_LN: one unit per thread");
-  constexpr int SLOTS = LN ? NW / 2 : NW;  // partial tiles held in LDS at once
+  // LN: the modulate-block rows and row statistics beside the partial tiles; when the 8 partial
+  // tiles and those do not fit in LDS together (80-row tiles), the tiles are summed in two rounds
+  constexpr int LNF = LN ? NW * FN * 256 + 16 * TN + TM * 2 : 1;
+  constexpr bool TWO_ROUND = LN && (NW * TM * TN + LNF) * 4 > 160 * 1024;
+  constexpr int SLOTS = TWO_ROUND ? NW / 2 : NW;  // partial tiles held in LDS at once
   constexpr int ST = LN ? (TM * 32 + NW * 64 - 1) / (NW * 64) : 1;  // statistics loads per thread (at most)
   __shared__ __attribute__((aligned(16))) float red[SLOTS * TM * TN];
-  __shared__ __attribute__((aligned(16))) float lnbuf[LN ? NW * FN * 256 + 16 * TN + TM * 2 : 1];
+  __shared__ __attribute__((aligned(16))) float lnbuf[LNF];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + TM - 1) / TM, Nt = N / TN;
   const int ks = K / 32;  // k-steps per 16-row block
@@ -928,6 +932,33 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
         rowst[r * 2 + 1] = rsqrtf(fmaxf(sq * inv_k - mu * mu, 0.f) + e.ln_eps);
       }
     }
+    // element (row, col) of a wave's modulate-block rows sits at lane (row / 4) * 16 + col % 16,
+    // register row % 4 of block col / 16
+    auto sum_vrows = [&](int first, int stride) {
+      for (int u = first; u < 16 * TN; u += stride) {
+        const int row = u / TN, col = u - row * TN;
+        const int off = ((col >> 4) * 64 + (row >> 2) * 16 + (col & 15)) * 4 + (row & 3);
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += vred[w * FN * 256 + off];
+        vsum[u] = sum;
+      }
+    };
+    if constexpr (!TWO_ROUND) {
+      // every wave stores its partial tile swizzled and its modulate-block rows; then all sum the rows
+      float* mine = red + wave * (TM * TN);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) *slot_at(mine, i, j, r) = acc[i][j][r];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(vred + ((wave * FN + j) * 64 + lane) * 4) = accv[j];
+      __syncthreads();
+      sum_vrows(tid, NW * 64);
+      __syncthreads();
+    } else {
     // round 1: waves 4-7 park their partial tiles, lane-major; every wave its modulate-block rows
     if (wave >= NW / 2) {
       float* mine = red + (wave - NW / 2) * (TM * TN);
@@ -958,18 +989,10 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
 #pragma unroll
           for (int r = 0; r < 4; ++r) *slot_at(slot, i, j, r) = acc[i][j][r];
     } else {
-      // meanwhile waves 4-7 sum the modulate-block rows over the waves: element (row, col) sits at
-      // lane (row / 4) * 16 + col % 16, register row % 4 of block col / 16
-      for (int u = tid - (NW / 2) * 64; u < 16 * TN; u += (NW / 2) * 64) {
-        const int row = u / TN, col = u - row * TN;
-        const int off = ((col >> 4) * 64 + (row >> 2) * 16 + (col & 15)) * 4 + (row & 3);
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) sum += vred[w * FN * 256 + off];
-        vsum[u] = sum;
-      }
+      sum_vrows(tid - (NW / 2) * 64, (NW / 2) * 64);  // meanwhile waves 4-7 sum the modulate-block rows
     }
     __syncthreads();
+    }
     for (int u = tid; u < UNITS; u += NW * 64) {
       const int r = u / (TN / 8), c8 = (u - r * (TN / 8)) * 8;
       const int gm = mt * TM + r, gn = nt * TN + c8;
