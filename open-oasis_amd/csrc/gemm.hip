@@ -482,35 +482,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
     __syncthreads();
   }
 
-  // QKV + RoPE + head split: what a lane's columns decide (q, k or v; head; dimension; rotated or
-  // not) is fixed for the whole tile, so it is worked out once per pass here, leaving each row its
-  // frame / position split and a 32-bit offset (the host checks that q, k and v offsets fit)
+  // QKV + RoPE + head split: the lane's column decisions once, its rows stepped per group
   constexpr bool QKV = KIND == OASIS_EPI_QKV_ROPE;
-  constexpr int NPASS = (16 * UPR + 63) / 64;  // passes of the 64 lanes over a 16-row group
-  bf16* qb[NPASS];
-  int qcol[NPASS], qd0[NPASS];
-  bool qrot[NPASS];
-  uint32_t qp[NPASS], qt[NPASS], qs[NPASS];  // pass q's row in group i: position, frame in stream, stream
-  const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
-  if constexpr (QKV) {
-    const int D = e.n_heads * 64;
-#pragma unroll
-    for (int q = 0; q < NPASS; ++q) {
-      const int gn = n0 + wn * TN + ((lane + 64 * q) % UPR) * 8;
-      const int which = (gn >= D) + (gn >= 2 * D);
-      const int nn = gn - which * D;
-      qb[q] = which == 0 ? e.q : (which == 1 ? e.k : e.v);
-      qd0[q] = nn & 63;
-      qcol[q] = (nn >> 6) * (int)e.s_h + qd0[q];
-      qrot[q] = which < 2;
-      // group 0's row; later groups step it by 16 rows
-      const uint32_t gm = (uint32_t)(m0 + wm * TM + (lane + 64 * q) / UPR);
-      const uint32_t f = fast_div(gm, e.rpf_magic, e.rpf_shift);
-      qp[q] = gm - f * rpf;
-      qs[q] = fast_div(f, e.fps_magic, e.fps_shift);
-      qt[q] = f - qs[q] * fps;
-    }
-  }
+  QkvRows<(16 * UPR + 63) / 64> qkv;
+  if constexpr (QKV) qkv.init(e, lane, UPR, n0 + wn * TN, m0 + wm * TM);
 
   // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
   // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
@@ -540,44 +515,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
           float v[8] = {c0[0] + b0[0], c0[1] + b0[1], c0[2] + b0[2], c0[3] + b0[3],
                         c1[0] + b1[0], c1[1] + b1[1], c1[2] + b1[2], c1[3] + b1[3]};
           if constexpr (QKV) {
-            const int qi = u >> 6;
-            const uint32_t p = qp[qi], t = qt[qi], bb = qs[qi];
-            if (qrot[qi]) {
-              const uint32_t pos = e.rope_by_frame ? t : p;
-              const float* cp = tab_rows ? tab + pos * ROPE_TP + qd0[qi] : e.rope_cos + pos * 64 + qd0[qi];
-              const float* sp = tab_rows ? tab + (tab_rows + pos) * ROPE_TP + qd0[qi] : e.rope_sinp + pos * 64 + qd0[qi];
-              const f32x4 cs0 = *reinterpret_cast<const f32x4*>(cp), cs1 = *reinterpret_cast<const f32x4*>(cp + 4);
-              const f32x4 sn0 = *reinterpret_cast<const f32x4*>(sp), sn1 = *reinterpret_cast<const f32x4*>(sp + 4);
-              float rv[8];
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                rv[j] = v[j] * cs0[j] + v[j ^ 1] * sn0[j];
-                rv[j + 4] = v[j + 4] * cs1[j] + v[(j + 4) ^ 1] * sn1[j];
-              }
-#pragma unroll
-              for (int j = 0; j < 8; ++j) v[j] = rv[j];
-            }
-            const uint32_t off = bb * (uint32_t)e.s_b + t * (uint32_t)e.s_t + p * (uint32_t)e.s_p + (uint32_t)qcol[qi];
-            store8_bf16(qb[qi] + off, v);
+            qkv.store(e, u >> 6, v, tab, tab_rows);
           } else {
             epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false, KIND);
           }
         }
       }
     }
-    if constexpr (QKV) {
-#pragma unroll
-      for (int q = 0; q < NPASS; ++q) {
-        qp[q] += 16;
-        while (qp[q] >= rpf) {
-          qp[q] -= rpf;
-          if (++qt[q] == fps) {
-            qt[q] = 0;
-            ++qs[q];
-          }
-        }
-      }
-    }
+    if constexpr (QKV) qkv.advance(e);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

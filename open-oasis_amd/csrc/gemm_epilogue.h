@@ -155,6 +155,16 @@ __device__ __forceinline__ void qkv_rope_tables(const Epi& e, int64_t m, int n0,
   }
 }
 
+// The rotation of 8 consecutive values: v[j] = v[j] c[j] + v[j ^ 1] s[j], one fused multiply-add
+// each, written out so that every QKV epilogue rounds alike
+__device__ __forceinline__ void rope_rotate8(float* v, const float* c, const float* sn) {
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = __builtin_fmaf(v[j], c[j], v[j ^ 1] * sn[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = r[j];
+}
+
 __device__ __forceinline__ void qkv_rope_store(const Epi& e, int64_t m, int n0, float* v, const float* c,
                                                const float* sn) {
   const int D = e.n_heads * 64;
@@ -164,16 +174,85 @@ __device__ __forceinline__ void qkv_rope_store(const Epi& e, int64_t m, int n0, 
   const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
   const uint32_t f = fast_div((uint32_t)m, e.rpf_magic, e.rpf_shift), p = (uint32_t)m - f * rpf;
   const uint32_t b = fast_div(f, e.fps_magic, e.fps_shift), t = f - b * fps;
-  if (which < 2) {
-    float r[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = v[j] * c[j] + v[j ^ 1] * sn[j];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = r[j];
-  }
+  if (which < 2) rope_rotate8(v, c, sn);
   bf16* base = which == 0 ? e.q : (which == 1 ? e.k : e.v);
   store8_bf16(base + (int64_t)b * e.s_b + (int64_t)t * e.s_t + (int64_t)p * e.s_p + (int64_t)h * e.s_h + d0, v);
 }
+
+// QKV + RoPE + head split in the large-token kernels' per-wave epilogue, where lane l takes the 8
+// columns ((l + 64 q) % upr) * 8 of row (l + 64 q) / upr of every 16-row group in pass q. What a
+// lane's columns decide (q, k or v; head; dimension; rotated or not) is worked out once per pass,
+// each 16-row group steps the row through position, frame and stream, and stores go through
+// 32-bit offsets (check_epilogue keeps every q / k / v offset below 2^31).
+template <int NPASS>
+struct QkvRows {
+  bf16* base[NPASS];
+  int col[NPASS], d0[NPASS];
+  bool rot[NPASS];
+  uint32_t p[NPASS], t[NPASS], s[NPASS];  // pass q's row in the current group: position, frame, stream
+
+  // n_first: the wave's first column; m_first: its first row
+  __device__ __forceinline__ void init(const Epi& e, int lane, int upr, int n_first, int m_first) {
+    const int D = e.n_heads * 64;
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+      const int gn = n_first + ((lane + 64 * q) % upr) * 8;
+      const int which = (gn >= D) + (gn >= 2 * D);
+      const int nn = gn - which * D;
+      base[q] = which == 0 ? e.q : (which == 1 ? e.k : e.v);
+      d0[q] = nn & 63;
+      col[q] = (nn >> 6) * (int)e.s_h + d0[q];
+      rot[q] = which < 2;
+      const uint32_t gm = (uint32_t)(m_first + (lane + 64 * q) / upr);
+      const uint32_t f = fast_div(gm, e.rpf_magic, e.rpf_shift);
+      p[q] = gm - f * (uint32_t)e.rows_per_frame;
+      s[q] = fast_div(f, e.fps_magic, e.fps_shift);
+      t[q] = f - s[q] * (uint32_t)e.frames_per_stream;
+    }
+  }
+  // a[q] by unrolled selects: q is only known at run time, and indexing the arrays with it would
+  // put them in scratch memory
+  template <typename T>
+  static __device__ __forceinline__ T pick(const T (&a)[NPASS], int q) {
+    T r = a[0];
+#pragma unroll
+    for (int i = 1; i < NPASS; ++i)
+      if (q == i) r = a[i];
+    return r;
+  }
+  // rotate (q and k) and store 8 values of pass q's row; tab / tab_rows: the LDS copy of the tables
+  __device__ __forceinline__ void store(const Epi& e, int q, float* v, const float* tab, int tab_rows) const {
+    const uint32_t pq = pick(p, q), tq = pick(t, q), sq = pick(s, q);
+    const int dq = pick(d0, q);
+    if (pick(rot, q)) {
+      const uint32_t pos = e.rope_by_frame ? tq : pq;
+      const float* cp = tab_rows ? tab + pos * ROPE_TP + dq : e.rope_cos + pos * 64 + dq;
+      const float* sp = tab_rows ? tab + (tab_rows + pos) * ROPE_TP + dq : e.rope_sinp + pos * 64 + dq;
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(cp), c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+      const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      rope_rotate8(v, c, sn);
+    }
+    const uint32_t off = sq * (uint32_t)e.s_b + tq * (uint32_t)e.s_t + pq * (uint32_t)e.s_p + (uint32_t)pick(col, q);
+    store8_bf16(pick(base, q) + off, v);
+  }
+  // on to the next 16-row group
+  __device__ __forceinline__ void advance(const Epi& e) {
+    const uint32_t rpf = (uint32_t)e.rows_per_frame, fps = (uint32_t)e.frames_per_stream;
+#pragma unroll
+    for (int q = 0; q < NPASS; ++q) {
+      p[q] += 16;
+      while (p[q] >= rpf) {
+        p[q] -= rpf;
+        if (++t[q] == fps) {
+          t[q] = 0;
+          ++s[q];
+        }
+      }
+    }
+  }
+};
 
 // Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N). tab / tab_rows:
 // an LDS copy of the QKV rotation tables (see rope_lds_rows), or null. with_bias = false: the

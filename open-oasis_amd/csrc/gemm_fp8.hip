@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
 // global_load_lds, 128 fp8 per row (one 16x16x128 MFMA step) in the same swizzled 128-byte
 // rows, plus each A row's 4 block-scale bytes per K tile (4 bytes per lane, one wave per 64
 // rows). Two stages; the epilogue stages 16 rows of a wave's tile at a time in that wave's LDS.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int KIND = -1>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
                                                                    const uint8_t* __restrict__ Ascale, int64_t lds,
                                                                    const uint8_t* __restrict__ B, int64_t ldb,
@@ -375,6 +375,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
     rope_to_lds(e, tab, tab_rows, tid, NW * 64);
     __syncthreads();
   }
+  // QKV + RoPE + head split: the lane's column decisions once, its rows stepped per group
+  constexpr bool QKV = KIND == OASIS_EPI_QKV_ROPE;
+  QkvRows<(16 * UPR + 63) / 64> qkv;
+  if constexpr (QKV) qkv.init(e, lane, UPR, n0 + wn * TN, m0 + wm * TM);
   // lanes 4i..4i+3 cover one aligned 32-column block when TN % 32 == 0 (the host checks it for
   // the GELU_TANH_FP8 epilogue)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
@@ -398,7 +402,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
         const f32x4 b0 = q1 ? hb[NBQ - 1][0] : hb[0][0], b1 = q1 ? hb[NBQ - 1][1] : hb[0][1];
         float v[8];
         scale_bias8(c0, c1, s0, s1, b0, b1, v);
-        if (e.kind == OASIS_EPI_PARTIAL_F32) {
+        if constexpr (QKV) {
+          qkv.store(e, u >> 6, v, tab, tab_rows);
+        } else if (e.kind == OASIS_EPI_PARTIAL_F32) {
           float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
           *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
           *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -407,6 +413,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
         }
       }
     }
+    if constexpr (QKV) qkv.advance(e);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -429,8 +436,13 @@ template <int BM, int BN, int WM, int WN>
 hipError_t launch8_big(const void* A, int64_t lda, const uint8_t* As, int64_t lds, const uint8_t* B, int64_t ldb,
                        const float* ws, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
-                     static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K, splits, e);
+  if (e.kind == OASIS_EPI_QKV_ROPE)
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_QKV_ROPE>), dim3(Mt * Nt * splits),
+                       dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
+                       splits, e);
+  else
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
+                       static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K, splits, e);
   return hipGetLastError();
 }
 

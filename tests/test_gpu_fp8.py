@@ -274,3 +274,61 @@ def test_gemm_fp8_large_token_tiles(M, N):
     with pytest.raises(L.OasisError, match="fp8 blocks"):
         L.call("oasis_gemm_fp8", L.ptr(Ad), K, L.ptr(q), K, L.ptr(s), M, N, K,
                ctypes.byref(_epi(kind=L.EPI_STORE_F32, out_f32=o, ld_out=N)), 5, 1, stream())
+
+
+@pytest.mark.parametrize("layout", ["temporal", "spatial", "vae"])
+def test_gemm_fp8_large_token_qkv_rope(layout):
+    """QKV + RoPE + head split on the 8-wave large-token fp8 tiles (their epilogue steps each
+    lane's row through positions, frames and streams 16 rows at a time) equals the 4-wave tile
+    bit for bit, over two streams of two frames, and matches the rotated fp64 product."""
+    H, D, K = 4, 256, 1024
+    B_, T, P = (1, 2, 576) if layout == "vae" else (2, 2, 144)
+    M, N = B_ * T * P, 3 * D
+    g = _gen(40 + len(layout))
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    if layout == "spatial":
+        ang = oracle.spatial_rope_angles(torch.rand(16, generator=g) * 2, 9, 16)
+    elif layout == "temporal":
+        ang = oracle.temporal_rope_angles(torch.rand(32, generator=g), T)
+    else:
+        ang = oracle.vae_rope_angles(torch.rand(8, generator=g) * 2, 18, 32)
+    cos, sinp = oracle.rope_cos_sinperm(ang, 64)
+    if layout == "temporal":
+        s_b, s_t, s_p, s_h = P * H * T * 64, 64, H * T * 64, T * 64
+    else:
+        s_b, s_t, s_p, s_h = T * H * P * 64, H * P * 64, 64, P * 64
+    q8, s8 = _quantize(W)
+    a8 = torch.zeros(M, K, dtype=torch.uint8, device="cuda")
+    a8s = torch.zeros(M, K // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_quantize_act_fp8", L.ptr(dev(A)), K, M, K, L.ptr(a8), K, L.ptr(a8s), K // 32, stream())
+    cos_d, sinp_d, bias_d = dev(cos), dev(sinp), dev(bias)
+
+    def run(tile):
+        q, k, v = (torch.zeros(M * D, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+        e = _epi(kind=L.EPI_QKV_ROPE, n_heads=H, bias=bias_d, q=q, k=k, v=v, rope_cos=cos_d, rope_sinp=sinp_d,
+                 rope_by_frame=int(layout == "temporal"), rows_per_frame=P, frames_per_stream=T,
+                 s_b=s_b, s_t=s_t, s_p=s_p, s_h=s_h)
+        print("fp8 qkv_rope %s tile %d M=%d" % (layout, tile, M), flush=True)
+        L.call("oasis_gemm_fp8_a8", L.ptr(a8), K, L.ptr(a8s), K // 32, L.ptr(q8), K, L.ptr(s8), M, N, K,
+               ctypes.byref(e), tile, 1, stream())
+        sync()
+        return q, k, v
+
+    ref = run(0)
+    for tile in (5, 6, 7):
+        got = run(tile)
+        for name, a, b in zip("qkv", got, ref):
+            assert torch.equal(a, b), "tile %d %s" % (tile, name)
+    y = (_ref(A, W) + bias.double()).float().reshape(B_, T, P, 3, H, 64)
+    pos_c = cos[torch.arange(T)] if layout == "temporal" else cos
+    pos_s = sinp[torch.arange(T)] if layout == "temporal" else sinp
+    if layout == "temporal":
+        c4, s4 = pos_c[None, :, None, None, :], pos_s[None, :, None, None, :]
+    else:
+        c4, s4 = pos_c[None, None, :, None, :], pos_s[None, None, :, None, :]
+    perm = (0, 2, 3, 1, 4) if layout == "temporal" else (0, 1, 3, 2, 4)
+    exp = (oracle.apply_rope_swap(y[:, :, :, 0], c4, s4), oracle.apply_rope_swap(y[:, :, :, 1], c4, s4), y[:, :, :, 2])
+    for name, got, r in zip("qkv", ref, exp):
+        assert_close(got, r.permute(*perm).contiguous(), 0.99999, 1e-2, "fp8 qkv_rope %s %s" % (layout, name))
