@@ -75,6 +75,8 @@ struct AttnArgs {
   // > 0: the output is a token-major [rows, frag_ks * 32] matrix stored in MFMA fragment order
   // (bf16): the row-major offset above names the element
   int frag_ks = 0;
+  // byte ranges read by the grid slice blockIdx.z == 1 (launched when any is set)
+  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
 };
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
@@ -106,6 +108,10 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
   constexpr int VPER = (VBL + NT - 1) / NT;
   __shared__ __attribute__((aligned(16))) bf16 Ks[KS * KPITCH];
   __shared__ __attribute__((aligned(16))) bf16 Vt[64 * VPITCH];
+  if (blockIdx.z) {  // the prefetching slice
+    prefetch_lines(a.pf);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wq = wave % NW, wk = wave / NW;  // query block, key-chunk parity
   // work id -> (head, query block) with a head's query blocks on consecutive ids: xcd_remap puts
@@ -279,6 +285,7 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
 template <int NW, int KC, int KS, typename T, int KSPLIT = 1>
 void flash_go(dim3 g, const T* q, const T* k, const T* v, T* o, const AttnArgs& a, hipStream_t s) {
   const dim3 b(NW * KSPLIT * 64);
+  if (oasis::prefetch_any(&a.pf)) g.z = 2;
   if constexpr (std::is_same<T, bf16>::value) {
     if (!a.bias && !a.causal) {
       hipLaunchKernelGGL((flash_kernel<NW, KC, KS, T, KSPLIT, true>), g, b, 0, s, q, k, v, o, a);
@@ -343,7 +350,11 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
 __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                        const bf16* __restrict__ v, bf16* __restrict__ out,
                                                        int64_t G, int T, int P, int H, float scale_log2, int qf,
-                                                       int fks) {
+                                                       int fks, oasis::Prefetch pf) {
+  if (blockIdx.z) {  // the prefetching slice
+    prefetch_lines(pf);
+    return;
+  }
   const int64_t grp = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int j = threadIdx.x & 15;
   if (grp >= G) return;  // whole 16-lane groups exit together; no cross-group shuffles
@@ -416,7 +427,8 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
 namespace {
 
 int attention_impl(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
-                   int64_t n_heads, float scale, hipStream_t stream, bool out_frag) {
+                   int64_t n_heads, float scale, hipStream_t stream, bool out_frag,
+                   const oasis::Prefetch* pf = nullptr) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "attention: null pointer");
   OASIS_REQUIRE(!out_frag || (n_frames * L) % 16 == 0, OASIS_ERR_SHAPE,
                 "attention: a fragment-order output needs a multiple of 16 rows");
@@ -435,6 +447,7 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int64
   a.o_sh = 64;
   a.o_si = n_heads * 64;
   a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
+  a.pf = oasis::prefetch_or_none(pf);
   return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                             static_cast<bf16*>(out), n_frames * n_heads, a, stream);
 }
@@ -480,13 +493,19 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
 
 namespace oasis {
 
+int attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L, int64_t n_heads,
+              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf) {
+  return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, stream, out_frag, pf);
+}
+
 int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
                    int64_t n_heads, float scale, hipStream_t stream) {
   return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, stream, true);
 }
 
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
-                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag) {
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag,
+                       const Prefetch* pf) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
   OASIS_REQUIRE(!out_frag || (B * (q_frame < 0 ? T : 1) * P) % 16 == 0, OASIS_ERR_SHAPE,
                 "temporal_attention: a fragment-order output needs a multiple of 16 rows");
@@ -512,13 +531,14 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
     a.o_sh = 64;
     a.o_si = P * n_heads * 64;
     a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
+    a.pf = prefetch_or_none(pf);
     return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                               static_cast<bf16*>(out), G, a, stream);
   }
-  hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16)), dim3(256), 0, stream,
-                     static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+  hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16), 1, prefetch_any(pf) ? 2 : 1), dim3(256), 0,
+                     stream, static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                      static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame,
-                     out_frag ? (int)(n_heads * 2) : 0);
+                     out_frag ? (int)(n_heads * 2) : 0, prefetch_or_none(pf));
   return check_launch("temporal_attention");
 }
 

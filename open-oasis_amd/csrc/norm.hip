@@ -185,11 +185,15 @@ __global__ __launch_bounds__(256) void residual_ln_block_kernel(float* __restric
                                                           const float* __restrict__ lb, int64_t ln_fs,
                                                           bf16* __restrict__ y, uint8_t* __restrict__ y8,
                                                           uint8_t* __restrict__ ys, float eps, int yf,
-                                                          float* __restrict__ mean_out) {
+                                                          float* __restrict__ mean_out, oasis::Prefetch pf) {
   constexpr int D = VPT * 256;
   constexpr int NC = VPT / 4 > 0 ? VPT / 4 : 1;   // 4-float groups per thread
   constexpr int W = VPT < 4 ? VPT : 4;            // floats per group
   __shared__ float red[2][4];
+  if (blockIdx.z) {  // the prefetching slice
+    prefetch_lines(pf);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const int64_t f = row / rpf;
@@ -539,17 +543,20 @@ hipError_t final_layer_np(int np, float* x, int64_t M, const float* part, int64_
 template <int NC>
 hipError_t residual_ln_np(int np, float* x, int64_t M, const float* part, int64_t ps, const float* bias,
                           const float* gate, int64_t gfs, int64_t rpf, const float* la, const float* lb, int64_t lfs,
-                          bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s, int yf, float* mean_out) {
-  // few rows: a 256-thread workgroup per row (VPT = NC floats per thread); many: a wave per row
+                          bf16* y, uint8_t* y8, uint8_t* ys, float eps, hipStream_t s, int yf, float* mean_out,
+                          const oasis::Prefetch& pf) {
+  // few rows: a 256-thread workgroup per row (VPT = NC floats per thread), plus the prefetching
+  // slice when pf names ranges; many: a wave per row
   const bool wave_rows = M >= 2048;
   const dim3 grid((unsigned)(wave_rows ? (M + 3) / 4 : M)), block(256);
+  const dim3 grid_pf((unsigned)M, 1, oasis::prefetch_any(&pf) ? 2 : 1);
 #define OASIS_RLN(NPV)                                                                                          \
   if (wave_rows)                                                                                                \
     hipLaunchKernelGGL((residual_ln_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, la, \
                        lb, lfs, y, y8, ys, eps);                                                                \
   else                                                                                                          \
-    hipLaunchKernelGGL((residual_ln_block_kernel<NC, NPV>), grid, block, 0, s, x, M, part, ps, bias, gate, gfs, rpf, \
-                       la, lb, lfs, y, y8, ys, eps, yf, mean_out)
+    hipLaunchKernelGGL((residual_ln_block_kernel<NC, NPV>), grid_pf, block, 0, s, x, M, part, ps, bias, gate, gfs,  \
+                       rpf, la, lb, lfs, y, y8, ys, eps, yf, mean_out, pf)
   switch (np) {
     case 0: OASIS_RLN(0); break;
     case 1: OASIS_RLN(1); break;
@@ -640,8 +647,9 @@ namespace oasis {
 int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
-                hipStream_t s, bool y_frag, float* mean_out) {
+                hipStream_t s, bool y_frag, float* mean_out, const Prefetch* pf) {
   OASIS_REQUIRE(x, OASIS_ERR_NULL, "residual_ln: null x");
+  const Prefetch pfv = prefetch_or_none(M < 2048 ? pf : nullptr);
   OASIS_REQUIRE(!mean_out || (M < 2048 && (y_bf16 || y8)), OASIS_ERR_ARG,
                 "residual_ln: row means are written for M < 2048 with an LN output");
   OASIS_REQUIRE(!y_frag || (M < 2048 && M % 16 == 0 && !y8), OASIS_ERR_ARG,
@@ -656,10 +664,10 @@ int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_part
   bf16* y = static_cast<bf16*>(y_bf16);
   hipError_t e;
   switch (D) {
-    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out); break;
-    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out); break;
-    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out); break;
-    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out); break;
+    case 256: e = residual_ln_np<1>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out, pfv); break;
+    case 512: e = residual_ln_np<2>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out, pfv); break;
+    case 1024: e = residual_ln_np<4>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out, pfv); break;
+    case 2048: e = residual_ln_np<8>(n_partials, x, M, partial, partial_stride, bias, gate, gate_fstride, rows_per_frame, ln_a, ln_b, ln_fstride, y, y8, y8_scale, eps, s, y_frag ? 1 : 0, mean_out, pfv); break;
     default:
       set_error("residual_ln: D=%lld must be one of 256, 512, 1024, 2048", (long long)D);
       return OASIS_ERR_SHAPE;

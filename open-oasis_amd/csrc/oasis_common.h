@@ -20,6 +20,28 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 
 // ---- error reporting (host) -------------------------------------------------
 namespace oasis {
+// Byte ranges that a kernel's extra workgroups (grid slice blockIdx.z == 1) read ahead of later
+// kernels, so that their operands come from the memory-side cache instead of HBM: one 4-byte word
+// per 128-byte line, the values dropped (prefetch_lines). Unused ranges have 0 bytes.
+struct Prefetch {
+  const void* p[4];
+  int64_t bytes[4];
+};
+inline bool prefetch_any(const Prefetch* pf) {
+  return pf && (pf->bytes[0] > 0 || pf->bytes[1] > 0 || pf->bytes[2] > 0 || pf->bytes[3] > 0);
+}
+inline Prefetch prefetch_or_none(const Prefetch* pf) {
+  return prefetch_any(pf) ? *pf : Prefetch{{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
+}
+// appends a range (ignored past four)
+inline void prefetch_add(Prefetch& pf, const void* p, int64_t bytes) {
+  for (int i = 0; i < 4; ++i)
+    if (pf.bytes[i] == 0) {
+      pf.p[i] = p;
+      pf.bytes[i] = bytes;
+      return;
+    }
+}
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 // acc = A[M,K] @ B[N,K]^T with the given epilogue (gemm.hip).
@@ -48,7 +70,7 @@ int gemm_fp8_launch(const void* A, int64_t lda, const uint8_t* A_scale, int64_t 
 int residual_ln(float* x, int64_t M, int64_t D, const float* partial, int n_partials, int64_t partial_stride,
                 const float* bias, const float* gate, int64_t gate_fstride, int64_t rows_per_frame, const float* ln_a,
                 const float* ln_b, int64_t ln_fstride, void* y_bf16, uint8_t* y8, uint8_t* y8_scale, float eps,
-                hipStream_t s, bool y_frag = false, float* mean_out = nullptr);
+                hipStream_t s, bool y_frag = false, float* mean_out = nullptr, const Prefetch* pf = nullptr);
 // The DiT's final layer in fp32 (norm.hip): the pending residual (n_partials split-K slices +
 // bias, gated), LN, modulate with the frame's (scale_p1, shift) rows, then v_out[M, 64] =
 // h @ W^T + b with W fp32 [64, D]. With chunk set, rows chunk_row0.. also take one DDIM step of
@@ -72,9 +94,15 @@ int gemv_adaln_pair(const float* x, int64_t ldx, int64_t R, const void* W16, int
 // Causal temporal attention (attention.hip); q_frame >= 0 computes only that query frame of
 // each group and writes it as a single frame: out [B*P, n_heads*64].
 // out_frag: out in MFMA fragment order (as a [rows, n_heads*64] matrix).
+// pf: byte ranges read by extra workgroups beside the attention.
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
-                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag = false);
-// oasis_attention (heads-first q/k/v per frame, token-major out) with out in fragment order.
+                       int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag = false,
+                       const Prefetch* pf = nullptr);
+// oasis_attention (heads-first q/k/v per frame, token-major out), out optionally in fragment
+// order, with byte ranges read by extra workgroups beside it.
+int attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L, int64_t n_heads,
+              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf);
+// oasis_attention with out in fragment order.
 int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
                    int64_t n_heads, float scale, hipStream_t stream);
 // QKV projection + temporal RoPE + causal attention of a two-frame temporal window in one
@@ -101,6 +129,42 @@ template <typename... P>
 inline bool oasis_aligned(size_t a, const P*... p) {
   const uintptr_t m = (0 | ... | reinterpret_cast<uintptr_t>(p));
   return (m & (a - 1)) == 0;
+}
+
+// Word 0 of line ll of a Prefetch's ranges taken back to back (0 past their end).
+OASIS_DEV uint32_t prefetch_word(const oasis::Prefetch& pf, int64_t ll) {
+  const int64_t l0 = pf.bytes[0] >> 7, l1 = l0 + (pf.bytes[1] >> 7), l2 = l1 + (pf.bytes[2] >> 7),
+                l3 = l2 + (pf.bytes[3] >> 7);
+  const uint32_t* p0 = static_cast<const uint32_t*>(pf.p[0]);
+  const uint32_t* p1 = static_cast<const uint32_t*>(pf.p[1]);
+  const uint32_t* p2 = static_cast<const uint32_t*>(pf.p[2]);
+  const uint32_t* p3 = static_cast<const uint32_t*>(pf.p[3]);
+  return ll < l0   ? p0[ll << 5]  // 32 words a line
+         : ll < l1 ? p1[(ll - l0) << 5]
+         : ll < l2 ? p2[(ll - l1) << 5]
+         : ll < l3 ? p3[(ll - l2) << 5]
+                   : 0u;
+}
+
+// keeps loaded words alive without using them: the loads stay and complete before this point
+OASIS_DEV void prefetch_sink(uint32_t x) { __asm__ volatile("" ::"v"(x)); }
+
+
+// The prefetching workgroups' part of a Prefetch: the grid slice blockIdx.z == 1 reads one 4-byte
+// word of every 128-byte line of the ranges, 8 lines per thread at a time, and drops the values.
+OASIS_DEV void prefetch_lines(const oasis::Prefetch& pf) {
+  const int64_t n = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  const int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t lines = (pf.bytes[0] >> 7) + (pf.bytes[1] >> 7) + (pf.bytes[2] >> 7) + (pf.bytes[3] >> 7);
+  uint32_t acc = 0;
+  for (int64_t l = i; l < lines; l += 8 * n) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = prefetch_word(pf, l + u * n);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  }
+  prefetch_sink(acc);
 }
 
 // ---- conversions ------------------------------------------------------------

@@ -58,7 +58,19 @@ struct Plan {
   // (the K/V-cache frame 5.960 ms against 5.985 with none, the T = 2 step 1.4728 against 1.4786):
   // O and FC2 at one frame, O alone at two; every other mask measured slower.
   int frag1, frag2;
+  // weights read ahead into the memory-side cache by extra workgroups of the short kernels before
+  // the projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1
+  // and FC2 weights of a sub-block, which kernel reads them (PF_NONE; PF_LN, the residual + LN at
+  // its start; PF_ATTN, its attention). OASIS_PREFETCH = "qkv,o,fc1,fc2" codes. The default (QKV's
+  // during the LN, the rest during the attention) is the fastest placement measured on MI355X: the
+  // T = 2 step 1.4373 against 1.4846 ms with none, the K/V-cache frame 5.702 against 5.890 ms.
+  int pf_host[4];
 };
+
+enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2 };
+// the VAE decoder's blocks (decodes of fewer than 2048 tokens): QKV's weights during the LN before
+// it, O's, FC1's and FC2's during the attention
+constexpr int kVaePrefetch[4] = {PF_LN, PF_ATTN, PF_ATTN, PF_ATTN};
 
 // Fragment-order operands, one bit each: the LN output QKV reads, the attention output O reads,
 // the LN output FC1 reads, and FC1's GELU output FC2 reads. FRAG_LN (with FRAG_O) carries the
@@ -96,6 +108,13 @@ const Plan& plan() {
       }
     }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
+    q.pf_host[0] = PF_LN;
+    q.pf_host[1] = q.pf_host[2] = q.pf_host[3] = PF_ATTN;
+    if (const char* env = getenv("OASIS_PREFETCH")) {
+      int h[4] = {0, 0, 0, 0};
+      sscanf(env, "%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3]);
+      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] == PF_LN || h[i] == PF_ATTN) ? h[i] : PF_NONE;
+    }
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
     q.frag2 = FRAG_O | FRAG_LN;
     if (const char* env = getenv("OASIS_FRAG")) {
@@ -188,6 +207,17 @@ int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64
                                   splits, s);
   }
   return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s);
+}
+
+// the prefetch ranges of one host kernel (PF_LN or PF_ATTN): the weights of the block's QKV, O,
+// FC1 and FC2 (bytes[r] of each) that the plan assigns to it
+oasis::Prefetch prefetch_for(const int (&hosts)[4], int host, bool on, const void* const (&wp)[4],
+                             const int64_t (&bytes)[4]) {
+  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
+  if (!on) return pf;
+  for (int r = 0; r < 4; ++r)
+    if (hosts[r] == host && wp[r]) oasis::prefetch_add(pf, wp[r], bytes[r]);
+  return pf;
 }
 
 int64_t ada_width(const oasis_dit_weights_t* w) { return (int64_t)w->n_sub * 6 * w->d_model + 2 * w->d_model; }
@@ -424,13 +454,20 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   const void* mlp_in = fp8 ? buf->mlp8 : buf->mlp;
   const void* mlp_sc = fp8 ? buf->mlp8_scale : nullptr;
 
+  const bool pf_on = !fp8 && M <= 320;
+  const int64_t wbytes[4] = {3 * D * D * 2, D * D * 2, Dm * D * 2, D * Dm * 2};
   for (int64_t j = j0; j < j1; ++j) {
     const bool spatial = (j % 2) == 0;
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
+    // the weights the projections below read, for the kernels that read them ahead
+    const void* const wp[4] = {f_qkv ? w->qkv_wf[j] : w->qkv_w[j], (f_o || f_ln) ? w->out_wf[j] : w->out_w[j],
+                               (f_ln || f_fc1) ? w->fc1_wf[j] : w->fc1_w[j], f_fc2 ? w->fc2_wf[j] : w->fc2_w[j]};
+    const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes);
+    const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes);
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
-                                 f_ln ? buf->ln_mean : nullptr));
+                                 f_ln ? buf->ln_mean : nullptr, &pf_qkv));
     // with OASIS_TEMPORAL_FUSED=1 or 2, two-frame temporal windows (the T = 2 step and the frame's
     // first, cache-filling pass; with 2 also the current-frame passes against the cache): QKV,
     // RoPE and the causal attention in one kernel
@@ -486,14 +523,14 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       else
         OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
                        s));
-      if (spatial && f_o)
-        OASIS_TRY(oasis::attention_frag(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s));
-      else if (spatial)
-        OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, stream));
+      if (spatial)
+        OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s, f_o, &pf_attn));
       else if (kv.mode == KV_NONE)
-        OASIS_TRY(oasis::temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, -1, s, f_o));
+        OASIS_TRY(oasis::temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, -1, s, f_o,
+                                            &pf_attn));
       else
-        OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s, f_o));
+        OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s, f_o,
+                                            &pf_attn));
     }
     if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     gelu.bias = w->fc1_b[j];
@@ -527,14 +564,15 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     } else {
       // O projection as split-K partials; bias + gated residual + LN + modulate fused after
       if (f_o)
-        OASIS_TRY(
-            oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use, s));
+        OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use,
+                                          s));
       else
         OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
       OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
                                    a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
       if (f_fc1)
-        OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
+        OASIS_TRY(
+            oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
       else
         OASIS_TRY(
             proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
@@ -725,17 +763,22 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
   const oasis_epilogue_t part = partial_epi(buf->partial, L, D);
 
   Pending pend;
+  const int64_t wbytes[4] = {3 * D * D * 2, D * D * 2, Dm * D * 2, D * Dm * 2};
   for (int i = 0; i < w->depth; ++i) {
     OASIS_REQUIRE(w->n1_w[i] && w->n1_b[i] && w->qkv_w[i] && w->qkv_b[i] && w->proj_w[i] && w->proj_b[i] &&
                       w->n2_w[i] && w->n2_b[i] && w->fc1_w[i] && w->fc1_b[i] && w->fc2_w[i] && w->fc2_b[i],
                   OASIS_ERR_NULL, "vae_decode: missing weights of block %d", i);
+    // weights read ahead, as in dit_blocks
+    const void* const wp[4] = {w->qkv_w[i], w->proj_w[i], w->fc1_w[i], w->fc2_w[i]};
+    const oasis::Prefetch pf_qkv = prefetch_for(kVaePrefetch, PF_LN, L < 2048, wp, wbytes);
+    const oasis::Prefetch pf_attn = prefetch_for(kVaePrefetch, PF_ATTN, L < 2048, wp, wbytes);
     // x + attn(LN(x)); x + MLP(LN(x)) (oasis_inference.py:1557-1608)
-    OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->n1_w[i],
-                                w->n1_b[i], 0, buf->h, kLnEps, stream));
+    OASIS_TRY(oasis::residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->n1_w[i],
+                                 w->n1_b[i], 0, buf->h, nullptr, nullptr, kLnEps, s, false, nullptr, &pf_qkv));
     qkv.bias = w->qkv_b[i];
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[i], D, L, 3 * D, D, qkv,
                                      pl.tile[ROLE_VQKV], 1, s));
-    OASIS_TRY(oasis_attention(buf->q, buf->k, buf->v, buf->attn, B, Lf, H, kAttnScale, stream));
+    OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B, Lf, H, kAttnScale, s, false, &pf_attn));
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, part,
                                      pl.tile[ROLE_VO], sp, s));
     OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, sp, L * D, w->proj_b[i], nullptr, 0, L, w->n2_w[i],
