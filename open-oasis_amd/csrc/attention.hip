@@ -76,7 +76,7 @@ struct AttnArgs {
   // (bf16): the row-major offset above names the element
   int frag_ks = 0;
   // byte ranges read by the grid slice blockIdx.z == 1 (launched when any is set)
-  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
+  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}, 7};
 };
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole

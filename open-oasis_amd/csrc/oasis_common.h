@@ -26,12 +26,13 @@ namespace oasis {
 struct Prefetch {
   const void* p[4];
   int64_t bytes[4];
+  int line_log2;  // bytes between the words read: 1 << line_log2 (7: one word per 128-byte line)
 };
 inline bool prefetch_any(const Prefetch* pf) {
   return pf && (pf->bytes[0] > 0 || pf->bytes[1] > 0 || pf->bytes[2] > 0 || pf->bytes[3] > 0);
 }
 inline Prefetch prefetch_or_none(const Prefetch* pf) {
-  return prefetch_any(pf) ? *pf : Prefetch{{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
+  return prefetch_any(pf) ? *pf : Prefetch{{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}, 7};
 }
 // appends a range (ignored past four)
 inline void prefetch_add(Prefetch& pf, const void* p, int64_t bytes) {
@@ -133,16 +134,17 @@ inline bool oasis_aligned(size_t a, const P*... p) {
 
 // Word 0 of line ll of a Prefetch's ranges taken back to back (0 past their end).
 OASIS_DEV uint32_t prefetch_word(const oasis::Prefetch& pf, int64_t ll) {
-  const int64_t l0 = pf.bytes[0] >> 7, l1 = l0 + (pf.bytes[1] >> 7), l2 = l1 + (pf.bytes[2] >> 7),
-                l3 = l2 + (pf.bytes[3] >> 7);
+  const int sh = pf.line_log2, ws = sh - 2;
+  const int64_t l0 = pf.bytes[0] >> sh, l1 = l0 + (pf.bytes[1] >> sh), l2 = l1 + (pf.bytes[2] >> sh),
+                l3 = l2 + (pf.bytes[3] >> sh);
   const uint32_t* p0 = static_cast<const uint32_t*>(pf.p[0]);
   const uint32_t* p1 = static_cast<const uint32_t*>(pf.p[1]);
   const uint32_t* p2 = static_cast<const uint32_t*>(pf.p[2]);
   const uint32_t* p3 = static_cast<const uint32_t*>(pf.p[3]);
-  return ll < l0   ? p0[ll << 5]  // 32 words a line
-         : ll < l1 ? p1[(ll - l0) << 5]
-         : ll < l2 ? p2[(ll - l1) << 5]
-         : ll < l3 ? p3[(ll - l2) << 5]
+  return ll < l0   ? p0[ll << ws]
+         : ll < l1 ? p1[(ll - l0) << ws]
+         : ll < l2 ? p2[(ll - l1) << ws]
+         : ll < l3 ? p3[(ll - l2) << ws]
                    : 0u;
 }
 
@@ -155,7 +157,8 @@ OASIS_DEV void prefetch_sink(uint32_t x) { __asm__ volatile("" ::"v"(x)); }
 OASIS_DEV void prefetch_lines(const oasis::Prefetch& pf) {
   const int64_t n = (int64_t)gridDim.x * gridDim.y * blockDim.x;
   const int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t lines = (pf.bytes[0] >> 7) + (pf.bytes[1] >> 7) + (pf.bytes[2] >> 7) + (pf.bytes[3] >> 7);
+  const int sh = pf.line_log2;
+  const int64_t lines = (pf.bytes[0] >> sh) + (pf.bytes[1] >> sh) + (pf.bytes[2] >> sh) + (pf.bytes[3] >> sh);
   uint32_t acc = 0;
   for (int64_t l = i; l < lines; l += 8 * n) {
     uint32_t v[8];

@@ -65,6 +65,12 @@ struct Plan {
   // during the LN, the rest during the attention) is the fastest placement measured on MI355X: the
   // T = 2 step 1.4373 against 1.4846 ms with none, the K/V-cache frame 5.702 against 5.890 ms.
   int pf_host[4];
+  // log2 of the bytes between the words read, for DiT passes of up to 160 tokens, of 161 to 320,
+  // and the VAE (OASIS_PF_LINE = "a,b,c", 6 to 8). A word every 128 bytes does not bring every
+  // byte into the cache: a word every 64 takes the K/V-cache frame from 5.731 to 5.656 ms, the
+  // one-frame passes having idle CUs to spare, and leaves the T = 2 step and the VAE unchanged;
+  // a word every 256 bytes is slower than none (step 1.4876, frame 5.952 ms).
+  int pf_line[3];
 };
 
 enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2 };
@@ -110,6 +116,14 @@ const Plan& plan() {
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
     q.pf_host[0] = PF_LN;
     q.pf_host[1] = q.pf_host[2] = q.pf_host[3] = PF_ATTN;
+    q.pf_line[0] = 6;
+    q.pf_line[1] = q.pf_line[2] = 7;
+    if (const char* env = getenv("OASIS_PF_LINE")) {
+      int l[3] = {0, 0, 0};
+      sscanf(env, "%d,%d,%d", &l[0], &l[1], &l[2]);
+      for (int i = 0; i < 3; ++i)
+        if (l[i] >= 6 && l[i] <= 8) q.pf_line[i] = l[i];
+    }
     if (const char* env = getenv("OASIS_PREFETCH")) {
       int h[4] = {0, 0, 0, 0};
       sscanf(env, "%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3]);
@@ -212,8 +226,8 @@ int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64
 // the prefetch ranges of one host kernel (PF_LN or PF_ATTN): the weights of the block's QKV, O,
 // FC1 and FC2 (bytes[r] of each) that the plan assigns to it
 oasis::Prefetch prefetch_for(const int (&hosts)[4], int host, bool on, const void* const (&wp)[4],
-                             const int64_t (&bytes)[4]) {
-  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}};
+                             const int64_t (&bytes)[4], int line_log2) {
+  oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}, line_log2};
   if (!on) return pf;
   for (int r = 0; r < 4; ++r)
     if (hosts[r] == host && wp[r]) oasis::prefetch_add(pf, wp[r], bytes[r]);
@@ -462,8 +476,9 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     // the weights the projections below read, for the kernels that read them ahead
     const void* const wp[4] = {f_qkv ? w->qkv_wf[j] : w->qkv_w[j], (f_o || f_ln) ? w->out_wf[j] : w->out_w[j],
                                (f_ln || f_fc1) ? w->fc1_wf[j] : w->fc1_w[j], f_fc2 ? w->fc2_wf[j] : w->fc2_w[j]};
-    const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes);
-    const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes);
+    const int pfl = pl.pf_line[M <= 160 ? 0 : 1];
+    const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes, pfl);
+    const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes, pfl);
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
@@ -770,8 +785,8 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
                   OASIS_ERR_NULL, "vae_decode: missing weights of block %d", i);
     // weights read ahead, as in dit_blocks
     const void* const wp[4] = {w->qkv_w[i], w->proj_w[i], w->fc1_w[i], w->fc2_w[i]};
-    const oasis::Prefetch pf_qkv = prefetch_for(kVaePrefetch, PF_LN, L < 2048, wp, wbytes);
-    const oasis::Prefetch pf_attn = prefetch_for(kVaePrefetch, PF_ATTN, L < 2048, wp, wbytes);
+    const oasis::Prefetch pf_qkv = prefetch_for(kVaePrefetch, PF_LN, L < 2048, wp, wbytes, pl.pf_line[2]);
+    const oasis::Prefetch pf_attn = prefetch_for(kVaePrefetch, PF_ATTN, L < 2048, wp, wbytes, pl.pf_line[2]);
     // x + attn(LN(x)); x + MLP(LN(x)) (oasis_inference.py:1557-1608)
     OASIS_TRY(oasis::residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->n1_w[i],
                                  w->n1_b[i], 0, buf->h, nullptr, nullptr, kLnEps, s, false, nullptr, &pf_qkv));
