@@ -54,9 +54,9 @@ struct Plan {
   int fused_temporal;
   // which operands are kept in MFMA fragment order, with their projection on gemm_frag: a mask of
   // the FRAG_* bits for passes of at most 160 tokens (frag1) and of 161 to 320 (frag2). OASIS_FRAG
-  // = "frag1[,frag2]" (0 for none). The defaults are the fastest masks on MI355X with cold weights
-  // (the K/V-cache frame 5.960 ms against 5.985 with none, the T = 2 step 1.4728 against 1.4786):
-  // O and FC2 at one frame, O alone at two; every other mask measured slower.
+  // = "frag1[,frag2]" (0 for none). The defaults, O and FC2 with the carried LayerNorm at both
+  // sizes, are the fastest masks measured on MI355X with the weights read ahead (pf_host): the T = 2
+  // step 1.4470 ms against 1.4644 without FC2 at two frames; the QKV bit changes nothing.
   int frag1, frag2;
   // weights read ahead into the memory-side cache by extra workgroups of the short kernels before
   // the projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1
@@ -130,7 +130,7 @@ const Plan& plan() {
       for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] == PF_LN || h[i] == PF_ATTN) ? h[i] : PF_NONE;
     }
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
-    q.frag2 = FRAG_O | FRAG_LN;
+    q.frag2 = FRAG_O | FRAG_FC2 | FRAG_LN;
     if (const char* env = getenv("OASIS_FRAG")) {
       int a = 0, b = 0;
       const int n = sscanf(env, "%d,%d", &a, &b);
