@@ -568,6 +568,11 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
   // the wave index read back as a scalar, so that the addresses built from it stay in SGPRs
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
+  if ((int)blockIdx.x >= Mt * Nt * splits) {  // workgroups past the tiles read e.pf ahead
+    const int w = blockIdx.x - Mt * Nt * splits, nw = gridDim.x - Mt * Nt * splits;
+    prefetch_part<16>(e.pf, (int64_t)w * 256 + tid, (int64_t)nw * 256);
+    return;
+  }
   // work id -> (split, n tile, m tile), the split outermost: an XCD's contiguous range of ids
   // covers one K slice of A rather than all of them. Up to 7 row tiles m runs fastest (the ids
   // cover all rows of a few weight slices); from 8 (576 tokens and up) in groups of 4 weight
@@ -1177,7 +1182,9 @@ template <int BM, int BN, int STG, int BMS = BM>
 hipError_t launch_wave(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int M, int N, int K, int splits,
                        const Epi& e, hipStream_t s) {
   const int Mt = (M + BMS - 1) / BMS, Nt = (N + BN - 1) / BN;
-  const dim3 grid(Mt * Nt * splits);
+  // with ranges to read ahead, workgroups past the tiles fill the CUs up to 256 (one tile each)
+  const int tiles = Mt * Nt * splits;
+  const dim3 grid(tiles + (prefetch_any(&e.pf) && tiles < 256 ? 256 - tiles : 0));
   switch ((K / splits) % 256 == 0 ? K / splits / 256 : 0) {
     case 1: launch_wave_nk<BM, BN, STG, 1, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
     case 2: launch_wave_nk<BM, BN, STG, 2, BMS>(grid, A, lda, B, ldb, M, N, K, splits, e, s); break;
@@ -1318,7 +1325,7 @@ int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits) {
 }
 
 int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
-                    const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s) {
+                    const oasis_epilogue_t& ex, int tile, int splits, hipStream_t s, const Prefetch* pf) {
   OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm: null operand");
   OASIS_REQUIRE(aligned16(A) && aligned16(B), OASIS_ERR_ARG, "gemm: A and B must be 16-byte aligned");
   OASIS_REQUIRE(ex.kind != OASIS_EPI_GATED_RES_LN && ex.kind != OASIS_EPI_GELU_TANH_LN, OASIS_ERR_ARG,
@@ -1334,7 +1341,8 @@ int gemm_launch_cfg(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, int6
   OASIS_REQUIRE(lda < (1ll << 22) && ldb < (1ll << 22), OASIS_ERR_SHAPE, "gemm: lda/ldb must be below 2^22");
   OASIS_REQUIRE(splits >= 1 && (K / BK) % splits == 0, OASIS_ERR_SHAPE,
                 "gemm: splits=%d must divide K/64=%lld", splits, (long long)(K / BK));
-  const Epi e = to_epi(ex);
+  Epi e = to_epi(ex);
+  e.pf = prefetch_or_none(pf);
   if (const int rc = check_epilogue(e, M, N, splits)) return rc;
   if (tile < 0) tile = auto_tile(M, N, K, splits, e.kind);
   OASIS_REQUIRE(tile < kNumTiles, OASIS_ERR_ARG, "gemm: tile config %d out of range", tile);

@@ -44,6 +44,7 @@ struct Epi {
   float ln_eps;
   int out_frag;
   int ln_group;  // *_LN: columns per statistics group (16 or 32), set by the fragment-order launcher
+  oasis::Prefetch pf;  // ranges read ahead by the wave-split kernel's workgroups past its tiles
   // n / rows_per_frame and n / frames_per_stream as (n * magic) >> shift (see DivMagic)
   uint64_t rpf_magic, fps_magic;
   int rpf_shift, fps_shift;
@@ -436,6 +437,7 @@ Epi to_epi(const oasis_epilogue_t& x) {
   e.ln_eps = x.ln_eps;
   e.out_frag = x.out_frag;
   e.ln_group = 16;
+  e.pf = oasis::prefetch_or_none(nullptr);
   return e;
 }
 

@@ -54,9 +54,11 @@ int gemm_frag_launch(const __bf16* A, int64_t a_rows, const __bf16* B, int64_t M
 // rows of A any fragment-order product of M rows may read (its row tiles rounded up: 48 rows at
 // most 160 tokens, 48 or 80 above)
 int64_t gemm_frag_rows(int64_t M);
-// explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32)
+// explicit tile configuration and split-K count (splits > 1 needs OASIS_EPI_PARTIAL_F32). pf: byte
+// ranges that workgroups past the tiles read ahead, on the CUs the wave-split tiles leave idle
+// (those tiles only; up to 256 workgroups in all).
 int gemm_launch_cfg(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
-                    const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s);
+                    const oasis_epilogue_t& epi, int tile, int splits, hipStream_t s, const Prefetch* pf = nullptr);
 // split-K count the default tile of a large-token (M >= 2048) split-K product wants
 int gemm_auto_splits(int64_t M, int64_t N, int64_t K, int max_splits);
 // acc = A[M,K] @ (Bq[N,K] (e4m3) * w_scale[N])^T with the given epilogue (gemm_fp8.hip).
@@ -152,22 +154,27 @@ OASIS_DEV uint32_t prefetch_word(const oasis::Prefetch& pf, int64_t ll) {
 OASIS_DEV void prefetch_sink(uint32_t x) { __asm__ volatile("" ::"v"(x)); }
 
 
-// The prefetching workgroups' part of a Prefetch: the grid slice blockIdx.z == 1 reads one 4-byte
-// word of every 128-byte line of the ranges, 8 lines per thread at a time, and drops the values.
-OASIS_DEV void prefetch_lines(const oasis::Prefetch& pf) {
-  const int64_t n = (int64_t)gridDim.x * gridDim.y * blockDim.x;
-  const int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+// Thread i of n reads lines i, i + n, ... of a Prefetch's ranges, U at a time, and drops the values.
+template <int U>
+OASIS_DEV void prefetch_part(const oasis::Prefetch& pf, int64_t i, int64_t n) {
   const int sh = pf.line_log2;
   const int64_t lines = (pf.bytes[0] >> sh) + (pf.bytes[1] >> sh) + (pf.bytes[2] >> sh) + (pf.bytes[3] >> sh);
   uint32_t acc = 0;
-  for (int64_t l = i; l < lines; l += 8 * n) {
-    uint32_t v[8];
+  for (int64_t l = i; l < lines; l += U * n) {
+    uint32_t v[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = prefetch_word(pf, l + u * n);
+    for (int u = 0; u < U; ++u) v[u] = prefetch_word(pf, l + u * n);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc ^= v[u];
+    for (int u = 0; u < U; ++u) acc ^= v[u];
   }
   prefetch_sink(acc);
+}
+
+// The prefetching workgroups' part of a Prefetch: the grid slice blockIdx.z == 1 reads one 4-byte
+// word of every line of the ranges, 8 lines per thread at a time.
+OASIS_DEV void prefetch_lines(const oasis::Prefetch& pf) {
+  prefetch_part<8>(pf, ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x,
+                   (int64_t)gridDim.x * gridDim.y * blockDim.x);
 }
 
 // ---- conversions ------------------------------------------------------------

@@ -61,19 +61,24 @@ struct Plan {
   // weights read ahead into the memory-side cache by extra workgroups of the short kernels before
   // the projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1
   // and FC2 weights of a sub-block, which kernel reads them (PF_NONE; PF_LN, the residual + LN at
-  // its start; PF_ATTN, its attention). OASIS_PREFETCH = "qkv,o,fc1,fc2" codes. The default (QKV's
-  // during the LN, the rest during the attention) is the fastest placement measured on MI355X: the
-  // T = 2 step 1.4373 against 1.4846 ms with none, the K/V-cache frame 5.702 against 5.890 ms.
+  // its start; PF_ATTN, its attention; PF_QKVG, the QKV GEMM's workgroups past its tiles, on the
+  // 16 CUs its 240 tiles leave idle, when it runs on a wave-split tile). OASIS_PREFETCH =
+  // "qkv,o,fc1,fc2" codes. The default, QKV's during the LN, O's during the QKV GEMM, FC1's and
+  // FC2's during the attention, is the fastest placement measured on MI355X (one box, two reps):
+  // the T = 2 step 1.4362 ms, against 1.4435 with O's during the attention and 1.4846 with none.
+  // A CU issues these one-word reads slowly: FC1's or FC2's 8.4 MB on the QKV GEMM's 16 spare CUs
+  // take the step to 1.61-1.86 ms.
   int pf_host[4];
   // log2 of the bytes between the words read, for DiT passes of up to 160 tokens, of 161 to 320,
-  // and the VAE (OASIS_PF_LINE = "a,b,c", 6 to 8). A word every 128 bytes does not bring every
+  // and the VAE (OASIS_PF_LINE = "a,b,c", 4 to 8). A word every 128 bytes does not bring every
   // byte into the cache: a word every 64 takes the K/V-cache frame from 5.731 to 5.656 ms, the
   // one-frame passes having idle CUs to spare, and leaves the T = 2 step and the VAE unchanged;
-  // a word every 256 bytes is slower than none (step 1.4876, frame 5.952 ms).
+  // a word every 256 bytes is slower than none (step 1.4876, frame 5.952 ms), and every 32 or 16
+  // bytes slower again (frame 5.68 and 6.02 ms).
   int pf_line[3];
 };
 
-enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2 };
+enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3 };
 // the VAE decoder's blocks (decodes of fewer than 2048 tokens): QKV's weights during the LN before
 // it, O's, FC1's and FC2's during the attention
 constexpr int kVaePrefetch[4] = {PF_LN, PF_ATTN, PF_ATTN, PF_ATTN};
@@ -115,19 +120,20 @@ const Plan& plan() {
     }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
     q.pf_host[0] = PF_LN;
-    q.pf_host[1] = q.pf_host[2] = q.pf_host[3] = PF_ATTN;
+    q.pf_host[1] = PF_QKVG;
+    q.pf_host[2] = q.pf_host[3] = PF_ATTN;
     q.pf_line[0] = 6;
     q.pf_line[1] = q.pf_line[2] = 7;
     if (const char* env = getenv("OASIS_PF_LINE")) {
       int l[3] = {0, 0, 0};
       sscanf(env, "%d,%d,%d", &l[0], &l[1], &l[2]);
       for (int i = 0; i < 3; ++i)
-        if (l[i] >= 6 && l[i] <= 8) q.pf_line[i] = l[i];
+        if (l[i] >= 4 && l[i] <= 8) q.pf_line[i] = l[i];
     }
     if (const char* env = getenv("OASIS_PREFETCH")) {
       int h[4] = {0, 0, 0, 0};
       sscanf(env, "%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3]);
-      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] == PF_LN || h[i] == PF_ATTN) ? h[i] : PF_NONE;
+      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] >= PF_LN && h[i] <= PF_QKVG) ? h[i] : PF_NONE;
     }
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
     q.frag2 = FRAG_O | FRAG_FC2 | FRAG_LN;
@@ -211,7 +217,8 @@ int check_dit(const oasis_dit_weights_t* w) {
 // One projection of sub-block j (role QKV/O/FC1/FC2): the bf16 GEMM on a bf16 A, or,
 // with e4m3 weights, the fp8 GEMM on A given as fp8 blocks (A e4m3 bytes, A_scale e8m0).
 int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64_t lda, const void* A_scale,
-         int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s) {
+         int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s,
+         const oasis::Prefetch* pf = nullptr) {
   const void* W = role == ROLE_QKV ? w->qkv_w[j] : role == ROLE_O ? w->out_w[j] : role == ROLE_FC1 ? w->fc1_w[j]
                                                                                                    : w->fc2_w[j];
   if (w->weight_format == OASIS_WEIGHTS_FP8) {
@@ -220,7 +227,7 @@ int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64
     return oasis::gemm_fp8_launch(A, lda, (const uint8_t*)A_scale, K / 32, (const uint8_t*)W, K, sc, M, N, K, e, -1,
                                   splits, s);
   }
-  return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s);
+  return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s, pf);
 }
 
 // the prefetch ranges of one host kernel (PF_LN or PF_ATTN): the weights of the block's QKV, O,
@@ -479,6 +486,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     const int pfl = pl.pf_line[M <= 160 ? 0 : 1];
     const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes, pfl);
     const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes, pfl);
+    const oasis::Prefetch pf_qkvg = prefetch_for(pl.pf_host, PF_QKVG, pf_on, wp, wbytes, pfl);
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
@@ -537,7 +545,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
         OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->qkv_wf[j], M, 3 * D, D, qkv, 1, s));
       else
         OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
-                       s));
+                       s, &pf_qkvg));
       if (spatial)
         OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s, f_o, &pf_attn));
       else if (kv.mode == KV_NONE)
