@@ -765,6 +765,11 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
   __shared__ __attribute__((aligned(16))) float lnbuf[LNF];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Mt = (M + TM - 1) / TM, Nt = N / TN;
+  if ((int)blockIdx.x >= Mt * Nt * splits) {  // workgroups past the tiles read e.pf ahead
+    const int w = blockIdx.x - Mt * Nt * splits, nw = gridDim.x - Mt * Nt * splits;
+    prefetch_part<8>(e.pf, (int64_t)w * (NW * 64) + tid, (int64_t)nw * (NW * 64));
+    return;
+  }
   const int ks = K / 32;  // k-steps per 16-row block
   const int pid = xcd_remap(blockIdx.x, Mt * Nt * splits);
   const int split = pid / (Mt * Nt);
@@ -1103,7 +1108,9 @@ bool try_frag(const dim3& g, const bf16* A, const bf16* B, int M, int N, int K, 
 template <int FM, int FN, int SPW>
 void launch_frag3(const bf16* A, const bf16* B, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
   const int Mt = (M + FM * 16 - 1) / (FM * 16), Nt = N / (FN * 16);
-  const dim3 g(Mt * Nt * splits);
+  // with ranges to read ahead, workgroups past the tiles fill the CUs up to 256 (one tile each)
+  const int tiles = Mt * Nt * splits;
+  const dim3 g(tiles + (prefetch_any(&e.pf) && tiles < 256 ? 256 - tiles : 0));
   if (try_frag<FM, FN, SPW, OASIS_EPI_PARTIAL_F32>(g, A, B, M, N, K, splits, e, s) ||
       try_frag<FM, FN, SPW, OASIS_EPI_GELU_TANH_FRAG>(g, A, B, M, N, K, splits, e, s) ||
       try_frag<FM, FN, SPW, OASIS_EPI_QKV_ROPE>(g, A, B, M, N, K, splits, e, s) ||
@@ -1367,7 +1374,7 @@ int64_t gemm_frag_rows(int64_t M) {
 }
 
 int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, int64_t N, int64_t K,
-                     const oasis_epilogue_t& ex, int splits, hipStream_t s) {
+                     const oasis_epilogue_t& ex, int splits, hipStream_t s, const Prefetch* pf) {
   OASIS_REQUIRE(A && B, OASIS_ERR_NULL, "gemm_frag: null operand");
   OASIS_REQUIRE(aligned16(A) && aligned16(B), OASIS_ERR_ARG, "gemm_frag: A and B must be 16-byte aligned");
   OASIS_REQUIRE(M > 0 && M <= 320 && M % 16 == 0, OASIS_ERR_SHAPE,
@@ -1388,6 +1395,7 @@ int gemm_frag_launch(const bf16* A, int64_t a_rows, const bf16* B, int64_t M, in
   // the statistics' group width: GATED_RES_LN sums whole 32-column groups on tiles at least 32
   // columns wide, else 16-column ones; GELU_TANH_LN derives the same from M and its K (= O's N)
   Epi eg = e;
+  eg.pf = prefetch_or_none(pf);
   if (e.kind == OASIS_EPI_GATED_RES_LN) eg.ln_group = fn >= 2 ? 32 : 16;
   if (e.kind == OASIS_EPI_GELU_TANH_LN) {
     int om, on;

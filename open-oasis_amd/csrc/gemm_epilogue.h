@@ -44,7 +44,7 @@ struct Epi {
   float ln_eps;
   int out_frag;
   int ln_group;  // *_LN: columns per statistics group (16 or 32), set by the fragment-order launcher
-  oasis::Prefetch pf;  // ranges read ahead by the wave-split kernel's workgroups past its tiles
+  oasis::Prefetch pf;  // ranges read ahead by the workgroups past the tiles (wave-split, fragment order)
   // n / rows_per_frame and n / frames_per_stream as (n * magic) >> shift (see DivMagic)
   uint64_t rpf_magic, fps_magic;
   int rpf_shift, fps_shift;

@@ -49,8 +49,10 @@ int check_launch(const char* what);
 int gemm_launch(const __bf16* A, int64_t lda, const __bf16* B, int64_t ldb, int64_t M, int64_t N, int64_t K,
                 const oasis_epilogue_t& epi, hipStream_t s);
 // both operands in MFMA fragment order (A with a_rows >= M rows), M <= 320 (gemm.hip)
+// pf: byte ranges that workgroups past the tiles read ahead, on the CUs the tiles leave idle (up
+// to 256 workgroups in all).
 int gemm_frag_launch(const __bf16* A, int64_t a_rows, const __bf16* B, int64_t M, int64_t N, int64_t K,
-                     const oasis_epilogue_t& epi, int splits, hipStream_t s);
+                     const oasis_epilogue_t& epi, int splits, hipStream_t s, const Prefetch* pf = nullptr);
 // rows of A any fragment-order product of M rows may read (its row tiles rounded up: 48 rows at
 // most 160 tokens, 48 or 80 above)
 int64_t gemm_frag_rows(int64_t M);

@@ -58,16 +58,18 @@ struct Plan {
   // sizes, are the fastest masks measured on MI355X with the weights read ahead (pf_host): the T = 2
   // step 1.4470 ms against 1.4644 without FC2 at two frames; the QKV bit changes nothing.
   int frag1, frag2;
-  // weights read ahead into the memory-side cache by extra workgroups of the short kernels before
-  // the projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1
-  // and FC2 weights of a sub-block, which kernel reads them (PF_NONE; PF_LN, the residual + LN at
-  // its start; PF_ATTN, its attention; PF_QKVG, the QKV GEMM's workgroups past its tiles, on the
-  // 16 CUs its 240 tiles leave idle, when it runs on a wave-split tile). OASIS_PREFETCH =
-  // "qkv,o,fc1,fc2" codes. The default, QKV's during the LN, O's during the QKV GEMM, FC1's and
-  // FC2's during the attention, is the fastest placement measured on MI355X (one box, two reps):
-  // the T = 2 step 1.4362 ms, against 1.4435 with O's during the attention and 1.4846 with none.
-  // A CU issues these one-word reads slowly: FC1's or FC2's 8.4 MB on the QKV GEMM's 16 spare CUs
-  // take the step to 1.61-1.86 ms.
+  // weights read ahead into the memory-side cache by extra workgroups of the kernels before the
+  // projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1 and
+  // FC2 weights of a sub-block, which kernel reads them (PF_NONE; PF_LN, the residual + LN at its
+  // start, and PF_ATTN, its attention, in a second grid slice; PF_QKVG and PF_OG, the QKV and O
+  // GEMMs' workgroups past their tiles, on the CUs the tiles leave idle: 16 of 256 for QKV's 240
+  // wave-split tiles, 64 for O's 192 fragment-order ones at two frames). OASIS_PREFETCH =
+  // "qkv,o,fc1,fc2" codes. A CU issues these one-word reads slowly, so each host takes what its
+  // idle CUs read in its own time. The default, QKV's during the LN, O's during the QKV GEMM, FC1's
+  // during O and FC2's during the attention, is the fastest placement measured on MI355X (one box,
+  // two reps each): the T = 2 step 1.4250 ms, against 1.4383 with FC1's during the attention too,
+  // 1.4580 with FC1's and FC2's during O, and 1.4846 with none; 1.61-1.86 ms with FC1's or FC2's
+  // on the QKV GEMM's 16 spare CUs.
   int pf_host[4];
   // log2 of the bytes between the words read, for DiT passes of up to 160 tokens, of 161 to 320,
   // and the VAE (OASIS_PF_LINE = "a,b,c", 4 to 8). A word every 128 bytes does not bring every
@@ -78,7 +80,7 @@ struct Plan {
   int pf_line[3];
 };
 
-enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3 };
+enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3, PF_OG = 4 };
 // the VAE decoder's blocks (decodes of fewer than 2048 tokens): QKV's weights during the LN before
 // it, O's, FC1's and FC2's during the attention
 constexpr int kVaePrefetch[4] = {PF_LN, PF_ATTN, PF_ATTN, PF_ATTN};
@@ -121,7 +123,8 @@ const Plan& plan() {
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
     q.pf_host[0] = PF_LN;
     q.pf_host[1] = PF_QKVG;
-    q.pf_host[2] = q.pf_host[3] = PF_ATTN;
+    q.pf_host[2] = PF_OG;
+    q.pf_host[3] = PF_ATTN;
     q.pf_line[0] = 6;
     q.pf_line[1] = q.pf_line[2] = 7;
     if (const char* env = getenv("OASIS_PF_LINE")) {
@@ -133,7 +136,7 @@ const Plan& plan() {
     if (const char* env = getenv("OASIS_PREFETCH")) {
       int h[4] = {0, 0, 0, 0};
       sscanf(env, "%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3]);
-      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] >= PF_LN && h[i] <= PF_QKVG) ? h[i] : PF_NONE;
+      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] >= PF_LN && h[i] <= PF_OG) ? h[i] : PF_NONE;
     }
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
     q.frag2 = FRAG_O | FRAG_FC2 | FRAG_LN;
@@ -487,6 +490,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes, pfl);
     const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes, pfl);
     const oasis::Prefetch pf_qkvg = prefetch_for(pl.pf_host, PF_QKVG, pf_on, wp, wbytes, pfl);
+    const oasis::Prefetch pf_og = prefetch_for(pl.pf_host, PF_OG, pf_on, wp, wbytes, pfl);
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
@@ -575,7 +579,8 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       o.ln_center = buf->ln_mean;
       o.ln_stats = buf->ln_stats;
       o.ln_mod = buf->ln_mod;
-      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, o, 1, s));
+      OASIS_TRY(
+          oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, o, 1, s, &pf_og));
       oasis_epilogue_t f1 = gelu;
       f1.kind = OASIS_EPI_GELU_TANH_LN;
       f1.rows_per_frame = P;
@@ -588,7 +593,7 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       // O projection as split-K partials; bias + gated residual + LN + modulate fused after
       if (f_o)
         OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->attn, FR, (const bf16*)w->out_wf[j], M, D, D, part, so_use,
-                                          s));
+                                          s, &pf_og));
       else
         OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D, part, pl.tile[ROLE_O], so, s));
       OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
