@@ -60,17 +60,22 @@ struct Plan {
   int frag1, frag2;
   // weights read ahead into the memory-side cache by extra workgroups of the kernels before the
   // projections, in the DiT's passes of at most 320 tokens (bf16 weights): for the QKV, O, FC1 and
-  // FC2 weights of a sub-block, which kernel reads them (PF_NONE; PF_LN, the residual + LN at its
-  // start, and PF_ATTN, its attention, in a second grid slice; PF_QKVG and PF_OG, the QKV and O
-  // GEMMs' workgroups past their tiles, on the CUs the tiles leave idle: 16 of 256 for QKV's 240
-  // wave-split tiles, 64 for O's 192 fragment-order ones at two frames). OASIS_PREFETCH =
-  // "qkv,o,fc1,fc2" codes. A CU issues these one-word reads slowly, so each host takes what its
-  // idle CUs read in its own time. The default, QKV's during the LN, O's during the QKV GEMM, FC1's
-  // during O and FC2's during the attention, is the fastest placement measured on MI355X (one box,
-  // two reps each): the T = 2 step 1.4250 ms, against 1.4383 with FC1's during the attention too,
-  // 1.4580 with FC1's and FC2's during O, and 1.4846 with none; 1.61-1.86 ms with FC1's or FC2's
-  // on the QKV GEMM's 16 spare CUs.
-  int pf_host[4];
+  // FC2 weights, which kernel of a sub-block reads them (PF_NONE; PF_LN, the residual + LN at its
+  // start, and PF_ATTN, its attention, in a second grid slice; PF_QKVG, PF_OG, PF_FC1G and PF_FC2G,
+  // the QKV, O, FC1 and FC2 GEMMs' workgroups past their tiles, on the CUs the tiles leave idle).
+  // A host that runs at or after a weight's projection reads the next sub-block's copy of it.
+  // OASIS_PREFETCH = "qkv,o,fc1,fc2" codes for both pass sizes, or eight for up to 160 tokens and
+  // for 161 to 320. A CU issues these one-word reads slowly, so each host takes what its idle CUs
+  // read in its own time. The defaults are the fastest placements measured on MI355X (one box, two
+  // reps each):
+  //  - two frames (256 tiles in FC1 and FC2, none idle): QKV's during the LN, O's during the QKV
+  //    GEMM (16 idle CUs), FC1's during O (64), FC2's during the attention: the T = 2 step 1.4250
+  //    ms, against 1.4383 with FC1's during the attention too, 1.4580 with FC1's and FC2's during
+  //    O, 1.4846 with none, and 1.61-1.86 ms with FC1's or FC2's on the QKV GEMM's 16 idle CUs;
+  //  - one frame (FC1 and FC2 leave 64 CUs idle): the next sub-block's QKV and this one's FC2
+  //    during FC1, O's during QKV, FC1's during O: the K/V-cache frame 5.486 ms, against 5.602
+  //    with the two-frame placement and 5.534 with only FC2's moved to FC1.
+  int pf_host[2][4];  // passes of up to 160 tokens, of 161 to 320
   // log2 of the bytes between the words read, for DiT passes of up to 160 tokens, of 161 to 320,
   // and the VAE (OASIS_PF_LINE = "a,b,c", 4 to 8). A word every 128 bytes does not bring every
   // byte into the cache: a word every 64 takes the K/V-cache frame from 5.731 to 5.656 ms, the
@@ -80,7 +85,11 @@ struct Plan {
   int pf_line[3];
 };
 
-enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3, PF_OG = 4 };
+enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3, PF_OG = 4, PF_FC1G = 5, PF_FC2G = 6 };
+// where each host runs in a sub-block, and where each of the four weights is read: a host that runs
+// at or after a weight's projection reads the next sub-block's copy of it
+constexpr int kHostPos[7] = {-1, 0, 2, 1, 3, 4, 5};
+constexpr int kWeightPos[4] = {1, 3, 4, 5};  // QKV, O, FC1, FC2
 // the VAE decoder's blocks (decodes of fewer than 2048 tokens): QKV's weights during the LN before
 // it, O's, FC1's and FC2's during the attention
 constexpr int kVaePrefetch[4] = {PF_LN, PF_ATTN, PF_ATTN, PF_ATTN};
@@ -121,10 +130,14 @@ const Plan& plan() {
       }
     }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
-    q.pf_host[0] = PF_LN;
-    q.pf_host[1] = PF_QKVG;
-    q.pf_host[2] = PF_OG;
-    q.pf_host[3] = PF_ATTN;
+    // one frame: the next sub-block's QKV and this one's FC2 during FC1, O's during QKV, FC1's
+    // during O; two frames: QKV's during the LN, O's during QKV, FC1's during O, FC2's during the
+    // attention
+    const int pf1[4] = {PF_FC1G, PF_QKVG, PF_OG, PF_FC1G}, pf2[4] = {PF_LN, PF_QKVG, PF_OG, PF_ATTN};
+    for (int r = 0; r < 4; ++r) {
+      q.pf_host[0][r] = pf1[r];
+      q.pf_host[1][r] = pf2[r];
+    }
     q.pf_line[0] = 6;
     q.pf_line[1] = q.pf_line[2] = 7;
     if (const char* env = getenv("OASIS_PF_LINE")) {
@@ -134,9 +147,12 @@ const Plan& plan() {
         if (l[i] >= 4 && l[i] <= 8) q.pf_line[i] = l[i];
     }
     if (const char* env = getenv("OASIS_PREFETCH")) {
-      int h[4] = {0, 0, 0, 0};
-      sscanf(env, "%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3]);
-      for (int i = 0; i < 4; ++i) q.pf_host[i] = (h[i] >= PF_LN && h[i] <= PF_OG) ? h[i] : PF_NONE;
+      int h[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      const int n = sscanf(env, "%d,%d,%d,%d,%d,%d,%d,%d", &h[0], &h[1], &h[2], &h[3], &h[4], &h[5], &h[6], &h[7]);
+      for (int i = 0; i < 8; ++i) {
+        const int v = n > 4 ? h[i] : h[i % 4];  // four codes: both pass sizes
+        q.pf_host[i / 4][i % 4] = (v >= PF_LN && v <= PF_FC2G) ? v : PF_NONE;
+      }
     }
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
     q.frag2 = FRAG_O | FRAG_FC2 | FRAG_LN;
@@ -236,11 +252,14 @@ int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64
 // the prefetch ranges of one host kernel (PF_LN or PF_ATTN): the weights of the block's QKV, O,
 // FC1 and FC2 (bytes[r] of each) that the plan assigns to it
 oasis::Prefetch prefetch_for(const int (&hosts)[4], int host, bool on, const void* const (&wp)[4],
-                             const int64_t (&bytes)[4], int line_log2) {
+                             const int64_t (&bytes)[4], int line_log2, const void* const* wp_next = nullptr) {
   oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}, line_log2};
   if (!on) return pf;
-  for (int r = 0; r < 4; ++r)
-    if (hosts[r] == host && wp[r]) oasis::prefetch_add(pf, wp[r], bytes[r]);
+  for (int r = 0; r < 4; ++r) {
+    if (hosts[r] != host) continue;
+    const void* p = kHostPos[host] < kWeightPos[r] ? wp[r] : (wp_next ? wp_next[r] : nullptr);
+    if (p) oasis::prefetch_add(pf, p, bytes[r]);
+  }
   return pf;
 }
 
@@ -484,13 +503,25 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
     const bool spatial = (j % 2) == 0;
     const float* a = ada + j * 6 * D;  // shift_a, scale_a+1, gate_a, shift_m, scale_m+1, gate_m
     // the weights the projections below read, for the kernels that read them ahead
-    const void* const wp[4] = {f_qkv ? w->qkv_wf[j] : w->qkv_w[j], (f_o || f_ln) ? w->out_wf[j] : w->out_w[j],
-                               (f_ln || f_fc1) ? w->fc1_wf[j] : w->fc1_w[j], f_fc2 ? w->fc2_wf[j] : w->fc2_w[j]};
-    const int pfl = pl.pf_line[M <= 160 ? 0 : 1];
-    const oasis::Prefetch pf_qkv = prefetch_for(pl.pf_host, PF_LN, pf_on, wp, wbytes, pfl);
-    const oasis::Prefetch pf_attn = prefetch_for(pl.pf_host, PF_ATTN, pf_on, wp, wbytes, pfl);
-    const oasis::Prefetch pf_qkvg = prefetch_for(pl.pf_host, PF_QKVG, pf_on, wp, wbytes, pfl);
-    const oasis::Prefetch pf_og = prefetch_for(pl.pf_host, PF_OG, pf_on, wp, wbytes, pfl);
+    auto weights_of = [&](int64_t i, const void** out) {
+      out[0] = f_qkv ? w->qkv_wf[i] : w->qkv_w[i];
+      out[1] = (f_o || f_ln) ? w->out_wf[i] : w->out_w[i];
+      out[2] = (f_ln || f_fc1) ? w->fc1_wf[i] : w->fc1_w[i];
+      out[3] = f_fc2 ? w->fc2_wf[i] : w->fc2_w[i];
+    };
+    const void* wp[4];
+    const void* wn[4] = {nullptr, nullptr, nullptr, nullptr};  // the next sub-block's, if any
+    weights_of(j, wp);
+    if (j + 1 < w->n_sub) weights_of(j + 1, wn);
+    const int pps = M <= 160 ? 0 : 1;
+    const int pfl = pl.pf_line[pps];
+    const int (&hosts)[4] = pl.pf_host[pps];
+    const oasis::Prefetch pf_qkv = prefetch_for(hosts, PF_LN, pf_on, wp, wbytes, pfl, wn);
+    const oasis::Prefetch pf_attn = prefetch_for(hosts, PF_ATTN, pf_on, wp, wbytes, pfl, wn);
+    const oasis::Prefetch pf_qkvg = prefetch_for(hosts, PF_QKVG, pf_on, wp, wbytes, pfl, wn);
+    const oasis::Prefetch pf_og = prefetch_for(hosts, PF_OG, pf_on, wp, wbytes, pfl, wn);
+    const oasis::Prefetch pf_fc1g = prefetch_for(hosts, PF_FC1G, pf_on, wp, wbytes, pfl, wn);
+    const oasis::Prefetch pf_fc2g = prefetch_for(hosts, PF_FC2G, pf_on, wp, wbytes, pfl, wn);
     // previous FC2 residual (if any) + LN + modulate (oasis_inference.py:1053-1056)
     OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, pend->n, M * D, pend->bias, pend->gate, fs, P, a + D, a,
                                  fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_qkv,
@@ -588,7 +619,8 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       f1.ln_mod = buf->ln_mod;
       f1.ln_eps = kLnEps;
       f1.out_frag = f_fc2 ? 1 : 0;
-      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, f1, 1, s));
+      OASIS_TRY(
+          oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, f1, 1, s, &pf_fc1g));
     } else {
       // O projection as split-K partials; bias + gated residual + LN + modulate fused after
       if (f_o)
@@ -599,16 +631,17 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, so_use, M * D, w->out_b[j], a + 2 * D, fs, P, a + 4 * D,
                                    a + 3 * D, fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
       if (f_fc1)
-        OASIS_TRY(
-            oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s));
+        OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, gelu, 1, s,
+                                          &pf_fc1g));
       else
-        OASIS_TRY(
-            proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s));
+        OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s,
+                       &pf_fc1g));
     }
     if (f_fc2)
-      OASIS_TRY(oasis::gemm_frag_launch((const bf16*)buf->mlp, FR, (const bf16*)w->fc2_wf[j], M, D, Dm, part, sf, s));
+      OASIS_TRY(
+          oasis::gemm_frag_launch((const bf16*)buf->mlp, FR, (const bf16*)w->fc2_wf[j], M, D, Dm, part, sf, s, &pf_fc2g));
     else
-      OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s));
+      OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm, part, pl.tile[ROLE_FC2], sf, s, &pf_fc2g));
     pend->bias = w->fc2_b[j];
     pend->gate = a + 5 * D;
     pend->n = sf;
