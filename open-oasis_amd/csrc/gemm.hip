@@ -888,9 +888,9 @@ __global__ __launch_bounds__(512) void gemm_frag_kernel(const bf16* __restrict__
       }
     }
     // element (row, col) of a wave's modulate-block rows sits at lane (row / 4) * 16 + col % 16,
-    // register row % 4 of block col / 16
+    // register row % 4 of block col / 16; only the first vrows rows (2 per frame) are read
     auto sum_vrows = [&](int first, int stride) {
-      for (int u = first; u < 16 * TN; u += stride) {
+      for (int u = first; u < vrows * TN; u += stride) {
         const int row = u / TN, col = u - row * TN;
         const int off = ((col >> 4) * 64 + (row >> 2) * 16 + (col & 15)) * 4 + (row & 3);
         float sum = 0.f;
