@@ -1283,6 +1283,13 @@ const TileCfg kTiles[] = {
     {48, 64, launch_wave<48, 64, 2>, 1, 256, 2048},                       // 10
     {64, 64, launch_wave<64, 64, 2>, 1, 256, 2048},                       // 11
     {32, 64, launch_wave<32, 64, 2>, 1, 256, 2048},                       // 12
+    // large-token products of N = 1024 run unsplit (the O projection with its gated residual in
+    // the epilogue): 256 workgroups at 4608 tokens, 6 waves of 48 x 64 or 8 of 144 x 16
+    {144, 128, launch_big<144, 128, 3, 2, 2>},                            // 13
+    {288, 64, launch_big<288, 64, 2, 4, 2>, 1},                           // 14
+    {144, 128, launch_big<144, 128, 3, 2, 3>},                            // 15: 3 stages
+    {144, 128, launch_big<144, 128, 3, 2, 4>},                            // 16: 4 stages
+    {288, 128, launch_big<288, 128, 2, 4, 3>},                            // 17: 3 stages
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
 // global_load_lds, 128 fp8 per row (one 16x16x128 MFMA step) in the same swizzled 128-byte
 // rows, plus each A row's 4 block-scale bytes per K tile (4 bytes per lane, one wave per 64
 // rows). Two stages; the epilogue stages 16 rows of a wave's tile at a time in that wave's LDS.
-template <int BM, int BN, int WM, int WN, int KIND = -1>
+template <int BM, int BN, int WM, int WN, int KIND = -1, int STAGES = 2>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
                                                                    const uint8_t* __restrict__ Ascale, int64_t lds,
                                                                    const uint8_t* __restrict__ B, int64_t ldb,
@@ -259,9 +259,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   constexpr int LPW = (NBLK + NW - 1) / NW;
   constexpr int SWAVES = (BM + 63) / 64;  // waves that load the A scales (64 rows each)
   static_assert(SWAVES <= NW, "scale rows");
+  static_assert(STAGES >= 2 && (STAGES - 2) * (LPW + 1) <= 63, "vmcnt range");
   constexpr int DATA = (BM + BN) * P8;
-  constexpr int STAGE = DATA + SWAVES * 256;
-  constexpr int RING = 2 * STAGE;
+  // every wave issues LPW + 1 loads per stage (a wave past the scale rows reloads a clamped scale
+  // word into a slot of its own), so one vmcnt bound holds for all waves
+  constexpr int STAGE = DATA + NW * 256;
+  constexpr int RING = STAGES * STAGE;
   constexpr int EP = TN + 4;
   constexpr int EPI_BYTES = NW * 16 * EP * 4;
   constexpr int SMEM = RING > EPI_BYTES ? RING : EPI_BYTES;
@@ -302,7 +305,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
     char* base = smem + buf * STAGE;
 #pragma unroll
     for (int u = 0; u < LPW; ++u) buffer_load_lds16(from_a[u] ? Ars : Brs, off[u], kt * BK8, base + dst[u]);
-    if (wave < SWAVES) load_lds4(ssrc + kt * (BK8 / 32), base + DATA + wave * 256);
+    load_lds4(ssrc + kt * (BK8 / 32), base + DATA + wave * 256);
   };
 
   v4f acc[FM][FN];
@@ -338,12 +341,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
                                                                       kScaleOne);
   };
 
-  issue(0, 0);
+  constexpr int VM = (STAGES - 2) * (LPW + 1);  // stages that may stay in flight: tile k is in LDS
+  constexpr int WAIT = (VM & 15) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(min(s, nk - 1), s);
   for (int k = 0; k < nk; ++k) {
-    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0): tile k is in LDS
+    __builtin_amdgcn_s_waitcnt(WAIT);
     __builtin_amdgcn_s_barrier();
-    issue(min(k + 1, nk - 1), (k + 1) & 1);  // into the buffer read at k - 1
-    compute(k & 1);
+    issue(min(k + STAGES - 1, nk - 1), (k + STAGES - 1) % STAGES);  // into the buffer read at k - 1
+    compute(k % STAGES);
   }
   __builtin_amdgcn_s_waitcnt(0);
 
@@ -432,16 +438,16 @@ hipError_t launch8(const void* A, int64_t lda, const uint8_t* As, int64_t lds, c
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int STAGES = 2>
 hipError_t launch8_big(const void* A, int64_t lda, const uint8_t* As, int64_t lds, const uint8_t* B, int64_t ldb,
                        const float* ws, int M, int N, int K, int splits, const Epi& e, hipStream_t s) {
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
   if (e.kind == OASIS_EPI_QKV_ROPE)
-    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_QKV_ROPE>), dim3(Mt * Nt * splits),
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_QKV_ROPE, STAGES>), dim3(Mt * Nt * splits),
                        dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
                        splits, e);
   else
-    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, -1, STAGES>), dim3(Mt * Nt * splits), dim3(WM * WN * 64), 0, s,
                        static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K, splits, e);
   return hipGetLastError();
 }
@@ -455,17 +461,21 @@ struct Tile8 {
 #define OASIS_T8(BM, BN, WM, WN)                                                                       \
   {BM, BN, 2, launch8<BM, BN, WM, WN, 2, false>, launch8<BM, BN, WM, WN, 1, false>,                   \
    launch8<BM, BN, WM, WN, 2, true>, launch8<BM, BN, WM, WN, 1, true>, 0}
-#define OASIS_T8_BIG(BM, BN, WM, WN, NO_FP8_EPI) \
-  {BM, BN, 1, nullptr, nullptr, launch8_big<BM, BN, WM, WN>, launch8_big<BM, BN, WM, WN>, NO_FP8_EPI}
+#define OASIS_T8_BIG(BM, BN, WM, WN, NO_FP8_EPI, ST) \
+  {BM, BN, 1, nullptr, nullptr, launch8_big<BM, BN, WM, WN, ST>, launch8_big<BM, BN, WM, WN, ST>, NO_FP8_EPI}
 const Tile8 kTiles8[] = {
     OASIS_T8(128, 128, 2, 2),              // 0
     OASIS_T8(128, 64, 2, 2),               // 1
     OASIS_T8(64, 128, 2, 2),               // 2
     OASIS_T8(64, 64, 2, 2),                // 3
     OASIS_T8(32, 64, 1, 4),                // 4
-    OASIS_T8_BIG(288, 256, 2, 4, 0),       // 5  (fp8 A only)
-    OASIS_T8_BIG(288, 192, 2, 4, 1),       // 6
-    OASIS_T8_BIG(288, 128, 2, 4, 0),       // 7
+    OASIS_T8_BIG(288, 256, 2, 4, 0, 2),    // 5  (fp8 A only; two stages)
+    OASIS_T8_BIG(288, 192, 2, 4, 1, 2),    // 6
+    OASIS_T8_BIG(288, 128, 2, 4, 0, 2),    // 7
+    OASIS_T8_BIG(144, 128, 3, 2, 0, 2),    // 8  (N = 1024 unsplit at 4608 tokens: 256 tiles)
+    OASIS_T8_BIG(288, 64, 2, 4, 1, 2),     // 9
+    OASIS_T8_BIG(144, 128, 3, 2, 0, 3),    // 10 (three stages)
+    OASIS_T8_BIG(144, 128, 3, 2, 0, 4),    // 11 (four stages)
 };
 #undef OASIS_T8
 #undef OASIS_T8_BIG

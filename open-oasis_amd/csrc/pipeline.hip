@@ -47,6 +47,7 @@ enum { ROLE_QKV, ROLE_O, ROLE_FC1, ROLE_FC2, ROLE_VQKV, ROLE_VO, ROLE_VFC1, ROLE
 struct Plan {
   int tile[ROLE_N];
   int splits[ROLE_N];
+  int tile8[ROLE_N];  // fp8-weight tiles (kTiles8 ids of gemm_fp8.hip; OASIS_GEMM_PLAN8="fc1:10,...")
   // two-frame temporal windows on temporal_qkv.hip (OASIS_TEMPORAL_FUSED): 0 for none (default:
   // the wave-split QKV GEMM + temporal attention pair times as fast or faster on MI355X, 1.592
   // against 1.601 ms per step and 160.9 against 160.6 FPS per frame), 1 for the T = 2 passes,
@@ -83,6 +84,19 @@ struct Plan {
   // a word every 256 bytes is slower than none (step 1.4876, frame 5.952 ms), and every 32 or 16
   // bytes slower again (frame 5.68 and 6.02 ms).
   int pf_line[3];
+  // Large-token passes whose unsplit 144 x 128 tiles fill the 256 CUs (4465+ tokens at D = 1024):
+  // the O and FC2 projections (N = D) unsplit on these tiles (bf16 kTiles id, fp8 kTiles8 id) with
+  // the bias + gated residual into x in their epilogue, so that no split-K partials are written and
+  // read back and the LayerNorm + modulate after them runs alone. OASIS_O_UNSPLIT and
+  // OASIS_FC2_UNSPLIT = "bf16_tile,fp8_tile" (-1: split-K partials + residual_ln). The defaults
+  // are the fastest measured on MI355X (one box, two reps each), against split-K on 288 x 128:
+  //  - bf16 tile 16 (144 x 128, 6 waves, 4 stages), fp8 tile 10 (the same, 3 stages): the config-2
+  //    sub-block 0.204 -> 0.188 ms, the config-4 step 6.31 -> 5.91 ms (bf16) and 5.61 -> 5.22 ms (fp8);
+  //  - two stages (bf16 tile 13, fp8 8): 6.59 / 5.65 ms with FC2 unsplit; O alone 6.22 / 5.44 ms;
+  //  - 8 waves of 144 x 16 on 288 x 64 (bf16 14, fp8 9): O alone 6.53 / 5.65 ms;
+  //  - FC1 or QKV on the 144 x 128 tiles too (four rounds of 256 tiles): 6.52-7.04 / 5.52-5.99 ms.
+  int o_unsplit[2];
+  int fc2_unsplit[2];
 };
 
 enum { PF_NONE = 0, PF_LN = 1, PF_ATTN = 2, PF_QKVG = 3, PF_OG = 4, PF_FC1G = 5, PF_FC2G = 6 };
@@ -129,6 +143,22 @@ const Plan& plan() {
           }
       }
     }
+    for (int i = 0; i < ROLE_N; ++i) q.tile8[i] = -1;
+    if (const char* env = getenv("OASIS_GEMM_PLAN8")) {
+      std::string str(env);
+      size_t pos = 0;
+      while (pos < str.size()) {
+        size_t end = str.find(',', pos);
+        if (end == std::string::npos) end = str.size();
+        const std::string item = str.substr(pos, end - pos);
+        pos = end + 1;
+        const size_t c1 = item.find(':');
+        int tile = -1;
+        if (c1 == std::string::npos || sscanf(item.c_str() + c1 + 1, "%d", &tile) < 1) continue;
+        for (int i = 0; i < ROLE_N; ++i)
+          if (item.substr(0, c1) == names[i]) q.tile8[i] = tile;
+      }
+    }
     if (const char* env = getenv("OASIS_TEMPORAL_FUSED")) q.fused_temporal = atoi(env);
     // one frame: the next sub-block's QKV and this one's FC2 during FC1, O's during QKV, FC1's
     // during O; two frames: QKV's during the LN, O's during QKV, FC1's during O, FC2's during the
@@ -154,6 +184,10 @@ const Plan& plan() {
         q.pf_host[i / 4][i % 4] = (v >= PF_LN && v <= PF_FC2G) ? v : PF_NONE;
       }
     }
+    q.o_unsplit[0] = q.fc2_unsplit[0] = 16;
+    q.o_unsplit[1] = q.fc2_unsplit[1] = 10;
+    if (const char* env = getenv("OASIS_O_UNSPLIT")) sscanf(env, "%d,%d", &q.o_unsplit[0], &q.o_unsplit[1]);
+    if (const char* env = getenv("OASIS_FC2_UNSPLIT")) sscanf(env, "%d,%d", &q.fc2_unsplit[0], &q.fc2_unsplit[1]);
     q.frag1 = FRAG_O | FRAG_FC2 | FRAG_LN;
     q.frag2 = FRAG_O | FRAG_FC2 | FRAG_LN;
     if (const char* env = getenv("OASIS_FRAG")) {
@@ -237,14 +271,14 @@ int check_dit(const oasis_dit_weights_t* w) {
 // with e4m3 weights, the fp8 GEMM on A given as fp8 blocks (A e4m3 bytes, A_scale e8m0).
 int proj(const oasis_dit_weights_t* w, int role, int64_t j, const void* A, int64_t lda, const void* A_scale,
          int64_t M, int64_t N, int64_t K, const oasis_epilogue_t& e, int tile, int splits, hipStream_t s,
-         const oasis::Prefetch* pf = nullptr) {
+         const oasis::Prefetch* pf = nullptr, int tile8 = -1) {
   const void* W = role == ROLE_QKV ? w->qkv_w[j] : role == ROLE_O ? w->out_w[j] : role == ROLE_FC1 ? w->fc1_w[j]
                                                                                                    : w->fc2_w[j];
   if (w->weight_format == OASIS_WEIGHTS_FP8) {
     const float* sc = role == ROLE_QKV ? w->qkv_s[j] : role == ROLE_O ? w->out_s[j] : role == ROLE_FC1 ? w->fc1_s[j]
                                                                                                        : w->fc2_s[j];
-    return oasis::gemm_fp8_launch(A, lda, (const uint8_t*)A_scale, K / 32, (const uint8_t*)W, K, sc, M, N, K, e, -1,
-                                  splits, s);
+    return oasis::gemm_fp8_launch(A, lda, (const uint8_t*)A_scale, K / 32, (const uint8_t*)W, K, sc, M, N, K, e,
+                                  tile8 >= 0 ? tile8 : plan().tile8[role], splits, s);
   }
   return oasis::gemm_launch_cfg((const bf16*)A, lda, (const bf16*)W, K, M, N, K, e, tile, splits, s, pf);
 }
@@ -380,6 +414,30 @@ struct Pending {
   int n = 0;
 };
 
+// x[m, :] += acc + bias: a projection's residual in its epilogue
+oasis_epilogue_t residual_epi(float* x, int64_t ld, const float* bias) {
+  oasis_epilogue_t e = epi_zero();
+  e.kind = OASIS_EPI_RESIDUAL;
+  e.bias = bias;
+  e.out_f32 = x;
+  e.ld_out = ld;
+  return e;
+}
+
+// x[m, :] += gate[m / rows_per_frame, :] * (acc + bias): a projection's gated residual in its epilogue
+oasis_epilogue_t gated_res_epi(float* x, int64_t ld, const float* bias, const float* gate, int64_t gate_fstride,
+                               int64_t rows_per_frame) {
+  oasis_epilogue_t e = epi_zero();
+  e.kind = OASIS_EPI_GATED_RES;
+  e.bias = bias;
+  e.out_f32 = x;
+  e.ld_out = ld;
+  e.gate = gate;
+  e.gate_fstride = gate_fstride;
+  e.rows_per_frame = rows_per_frame;
+  return e;
+}
+
 oasis_epilogue_t partial_epi(float* part, int64_t M, int64_t N) {
   oasis_epilogue_t e = epi_zero();
   e.kind = OASIS_EPI_PARTIAL_F32;
@@ -482,6 +540,10 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   qkv.rows_per_frame = P;
   qkv.frames_per_stream = T;
   const bool fp8 = w->weight_format == OASIS_WEIGHTS_FP8;
+  // O and FC2 unsplit with their gated residual in the epilogue where 144 x 128 tiles fill the CUs
+  const bool unsplit_fill = (M + 143) / 144 * ((D + 127) / 128) >= 256;
+  const bool o_res = unsplit_fill && !f_o && !f_ln && !f_fc1 && (fp8 ? pl.o_unsplit[1] : pl.o_unsplit[0]) >= 0;
+  const bool fc2_res = unsplit_fill && !f_fc2 && (fp8 ? pl.fc2_unsplit[1] : pl.fc2_unsplit[0]) >= 0;
   oasis_epilogue_t gelu = epi_zero();
   gelu.kind = fp8 ? OASIS_EPI_GELU_TANH_FP8 : (f_fc2 ? OASIS_EPI_GELU_TANH_FRAG : OASIS_EPI_GELU_TANH);
   gelu.out_bf16 = buf->mlp;
@@ -621,6 +683,15 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       f1.out_frag = f_fc2 ? 1 : 0;
       OASIS_TRY(
           oasis::gemm_frag_launch((const bf16*)buf->h, FR, (const bf16*)w->fc1_wf[j], M, Dm, D, f1, 1, s, &pf_fc1g));
+    } else if (o_res) {
+      // O unsplit with bias + gated residual into x in its epilogue, then LN + modulate alone
+      OASIS_TRY(proj(w, ROLE_O, j, fp8 ? (const void*)a8 : buf->attn, D, a8s, M, D, D,
+                     gated_res_epi(buf->x, D, w->out_b[j], a + 2 * D, fs, P), pl.o_unsplit[0], 1, s, nullptr,
+                     pl.o_unsplit[1]));
+      OASIS_TRY(oasis::residual_ln(buf->x, M, D, buf->partial, 0, M * D, nullptr, nullptr, fs, P, a + 4 * D, a + 3 * D,
+                                   fs, (void*)ln_out, fp8 ? a8 : nullptr, a8s, kLnEps, s, f_fc1));
+      OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s,
+                     &pf_fc1g));
     } else {
       // O projection as split-K partials; bias + gated residual + LN + modulate fused after
       if (f_o)
@@ -636,6 +707,13 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       else
         OASIS_TRY(proj(w, ROLE_FC1, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, Dm, D, gelu, pl.tile[ROLE_FC1], 1, s,
                        &pf_fc1g));
+    }
+    if (fc2_res) {  // FC2 unsplit: its gated residual lands in x, nothing stays pending
+      OASIS_TRY(proj(w, ROLE_FC2, j, mlp_in, Dm, mlp_sc, M, D, Dm,
+                     gated_res_epi(buf->x, D, w->fc2_b[j], a + 5 * D, fs, P), pl.fc2_unsplit[0], 1, s, nullptr,
+                     pl.fc2_unsplit[1]));
+      *pend = Pending();
+      continue;
     }
     if (f_fc2)
       OASIS_TRY(
@@ -822,6 +900,10 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
   gelu.out_bf16 = buf->mlp;
   gelu.ld_out = Dm;
   const oasis_epilogue_t part = partial_epi(buf->partial, L, D);
+  // batched decodes whose unsplit 144 x 128 tiles fill the CUs: O and FC2 unsplit (as dit_blocks)
+  const bool unsplit_fill = (L + 143) / 144 * ((D + 127) / 128) >= 256;
+  const bool o_res = unsplit_fill && pl.tile[ROLE_VO] < 0 && pl.splits[ROLE_VO] <= 0 && pl.o_unsplit[0] >= 0;
+  const bool fc2_res = unsplit_fill && pl.tile[ROLE_VFC2] < 0 && pl.splits[ROLE_VFC2] <= 0 && pl.fc2_unsplit[0] >= 0;
 
   Pending pend;
   const int64_t wbytes[4] = {3 * D * D * 2, D * D * 2, Dm * D * 2, D * Dm * 2};
@@ -840,17 +922,30 @@ int vae_decode(const oasis_vae_weights_t* w, const oasis_vae_buffers_t* buf, int
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->qkv_w[i], D, L, 3 * D, D, qkv,
                                      pl.tile[ROLE_VQKV], 1, s));
     OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B, Lf, H, kAttnScale, s, false, &pf_attn));
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, part,
-                                     pl.tile[ROLE_VO], sp, s));
-    OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, sp, L * D, w->proj_b[i], nullptr, 0, L, w->n2_w[i],
-                                w->n2_b[i], 0, buf->h, kLnEps, stream));
+    if (o_res) {  // unsplit, the residual added in the epilogue (as the DiT's large-token passes)
+      OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D,
+                                       residual_epi(buf->x, D, w->proj_b[i]), pl.o_unsplit[0], 1, s));
+      OASIS_TRY(oasis_residual_ln(buf->x, L, D, nullptr, 0, L * D, nullptr, nullptr, 0, L, w->n2_w[i], w->n2_b[i], 0,
+                                  buf->h, kLnEps, stream));
+    } else {
+      OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->attn, D, (const bf16*)w->proj_w[i], D, L, D, D, part,
+                                       pl.tile[ROLE_VO], sp, s));
+      OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, sp, L * D, w->proj_b[i], nullptr, 0, L, w->n2_w[i],
+                                  w->n2_b[i], 0, buf->h, kLnEps, stream));
+    }
     gelu.bias = w->fc1_b[i];
     OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->h, D, (const bf16*)w->fc1_w[i], D, L, Dm, D, gelu,
                                      pl.tile[ROLE_VFC1], 1, s));
-    OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[i], Dm, L, D, Dm, part,
-                                     pl.tile[ROLE_VFC2], sf, s));
-    pend.bias = w->fc2_b[i];
-    pend.n = sf;
+    if (fc2_res) {
+      OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[i], Dm, L, D, Dm,
+                                       residual_epi(buf->x, D, w->fc2_b[i]), pl.fc2_unsplit[0], 1, s));
+      pend = Pending();
+    } else {
+      OASIS_TRY(oasis::gemm_launch_cfg((const bf16*)buf->mlp, Dm, (const bf16*)w->fc2_w[i], Dm, L, D, Dm, part,
+                                       pl.tile[ROLE_VFC2], sf, s));
+      pend.bias = w->fc2_b[i];
+      pend.n = sf;
+    }
   }
   OASIS_TRY(oasis_residual_ln(buf->x, L, D, buf->partial, pend.n, L * D, pend.bias, nullptr, 0, L, w->norm_w, w->norm_b,
                               0, buf->h, kLnEps, stream));

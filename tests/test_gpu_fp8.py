@@ -222,7 +222,7 @@ def test_gemm_fp8_a8_equals_in_kernel_quantization():
 
 @pytest.mark.parametrize("M,N", [(600, 520), (4608, 1024)])
 def test_gemm_fp8_large_token_tiles(M, N):
-    """The 8-wave large-token fp8 tiles (fp8 A only) equal the 4-wave tiles bit for bit (the same
+    """The 6- and 8-wave large-token fp8 tiles (fp8 A only) equal the 4-wave tiles bit for bit (the same
     MFMA sequence per output), on a ragged shape and on the config-4 projection shape, for plain,
     split-K and GELU -> fp8-block epilogues; a tile whose lanes do not cover 32-column blocks
     refuses the fp8 epilogue, and the large tiles refuse bf16 A."""
@@ -259,10 +259,10 @@ def test_gemm_fp8_large_token_tiles(M, N):
     ref = run(0)
     ref_part = run(0, 2)
     ref8 = run(0, kind="gelu8") if N % 32 == 0 else None
-    for tile in (5, 6, 7):
+    for tile in (5, 6, 7, 8, 9, 10, 11):
         assert torch.equal(run(tile), ref), "tile %d" % tile
         assert torch.equal(run(tile, 2), ref_part), "tile %d split-K x2" % tile
-        if ref8 is not None and tile != 6:
+        if ref8 is not None and tile not in (6, 9):
             m8, m8s = run(tile, kind="gelu8")
             assert torch.equal(m8, ref8[0]) and torch.equal(m8s, ref8[1]), "tile %d gelu8" % tile
     cos, rel = metrics(ref, _ref(A, W) + bias.double())
@@ -317,7 +317,7 @@ def test_gemm_fp8_large_token_qkv_rope(layout):
         return q, k, v
 
     ref = run(0)
-    for tile in (5, 6, 7):
+    for tile in (5, 6, 7, 10, 11):
         got = run(tile)
         for name, a, b in zip("qkv", got, ref):
             assert torch.equal(a, b), "tile %d %s" % (tile, name)

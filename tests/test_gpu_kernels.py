@@ -107,12 +107,13 @@ def test_gemm_gated_and_plain_residual():
 @pytest.mark.parametrize("layout,tile", [("spatial", -1), ("temporal", -1), ("vae", -1), ("spatial", 11),
                                          ("temporal", 11), ("spatial", 12), ("vae", 11), ("spatial", 5),
                                          ("temporal", 5), ("temporal", 6), ("spatial", 6), ("temporal", 7),
-                                         ("vae", 6)])
+                                         ("vae", 6), ("temporal", 16), ("spatial", 16)])
 def test_gemm_qkv_rope(layout, tile):
     """QKV + RoPE + head split into each attention layout: the default tile (K = 256), the
     wave-split tiles 11 / 12 with the kernels specialised for this epilogue (K = 1024), and the
-    large-token tiles 5-7 (288 x 256 / 192 / 128; their epilogue steps each lane's row through
-    positions, frames and streams 16 rows at a time, here over two streams of two frames)."""
+    large-token tiles 5-7 and 16 (288 x 256 / 192 / 128, 144 x 128; their epilogue steps each
+    lane's row through positions, frames and streams 16 rows at a time, here over two streams of
+    two frames)."""
     H, D = 4, 256
     K = 256 if tile < 0 else 1024
     if layout == "vae":
@@ -567,7 +568,7 @@ def test_rope_layout_shared_positions(H, T):
 
 
 # ---------------------------------------------------------------- tile configs, split-K, fused LN
-@pytest.mark.parametrize("tile", list(range(13)))
+@pytest.mark.parametrize("tile", list(range(18)))
 def test_gemm_tile_configs(tile):
     M, N, K = 288, 1024, 1024
     g = _gen(30 + tile)
