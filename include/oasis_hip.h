@@ -316,6 +316,17 @@ int oasis_temporal_attention(const void* q, const void* k, const void* v, void* 
                              int64_t B, int64_t T, int64_t P, int64_t n_heads, float scale,
                              oasis_stream_t stream);
 
+/* oasis_attention and oasis_temporal_attention writing their output as fp8 activation blocks
+ * (e4m3 bytes out8 [rows, n_heads*64], e8m0 scales out8_scale [rows, n_heads*2]): the bytes
+ * oasis_quantize_act_fp8 would make of the bf16 output, in the same launch. The fp8-weight
+ * step's O projection reads them. (No counterpart in the reference, whose attention output is
+ * bf16; it fuses the fp8 path's activation quantization, config 4.) */
+int oasis_attention_fp8(const void* q, const void* k, const void* v, void* out8, void* out8_scale,
+                        int64_t n_frames, int64_t L, int64_t n_heads, float scale, oasis_stream_t stream);
+int oasis_temporal_attention_fp8(const void* q, const void* k, const void* v, void* out8, void* out8_scale,
+                                 int64_t B, int64_t T, int64_t P, int64_t n_heads, float scale,
+                                 oasis_stream_t stream);
+
 /* Temporal sub-block front half for a two-frame window in one launch: QKV projection,
  * temporal RoPE and causal attention over the frames of each (stream, position, head).
  *   h: bf16 LN output [B*T*P, ldh] (row (b*T + t)*P + p); w_qkv: bf16 [3D, D], D = 64 n_heads;

@@ -128,6 +128,8 @@ SIGNATURES = {
                           c_f, c_p],
     "oasis_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_temporal_attention": [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
+    "oasis_attention_fp8": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_f, c_p],
+    "oasis_temporal_attention_fp8": [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_f, c_p],
     "oasis_temporal_qkv_attention": [c_p, c_i64, c_p, c_p, c_i64, c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_f,
                                      c_p],
     "oasis_gemv_bf16": [c_p, c_i64, c_i64, c_p, c_i64, c_i64, c_p, c_p, c_i64, c_i, c_i, c_i, c_p],

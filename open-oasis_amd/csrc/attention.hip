@@ -77,7 +77,21 @@ struct AttnArgs {
   int frag_ks = 0;
   // byte ranges read by the grid slice blockIdx.z == 1 (launched when any is set)
   oasis::Prefetch pf = {{nullptr, nullptr, nullptr, nullptr}, {0, 0, 0, 0}, 7};
+  // set: the output goes out as fp8 activation blocks instead (e4m3 bytes at o8 + the row-major
+  // offset, the e8m0 scale of each 32-column block at o8s + offset / 32), the bf16-rounded values
+  // quantized as oasis_quantize_act_fp8 would; the row-major offsets are multiples of 64 there
+  uint8_t* o8 = nullptr;
+  uint8_t* o8s = nullptr;
 };
+
+// Four consecutive bf16-rounded outputs r of a 32-column block whose max |v| over the block is
+// amax -> e4m3 bytes (a u32) at q, and the block's e8m0 scale byte at *sc when sc is set.
+__device__ __forceinline__ void store_fp8x4(uint8_t* q, uint8_t* sc, const float* r, float amax) {
+  const int sb = fp8_block_scale(amax);
+  const float inv = fp8_block_inv(sb);
+  *reinterpret_cast<uint32_t*>(q) = pack4_fp8(r[0] * inv, r[1] * inv, r[2] * inv, r[3] * inv);
+  if (sc) *sc = (uint8_t)sb;
+}
 
 // KS keys are staged in LDS at a time (K rows and V^T columns; KS >= Lk stages the whole
 // sequence once, with no barrier in the key loop) and consumed in KC-key chunks.
@@ -273,6 +287,25 @@ __global__ __launch_bounds__(NW * KSPLIT * 64) void flash_kernel(const T* __rest
   const int fo = f / a.f_inner, fi = f - fo * a.f_inner;
   const int64_t off = fo * a.o_sfo + fi * a.o_sf + h * a.o_sh + (int64_t)my_q * a.o_si;
   const int64_t ocols = (int64_t)a.frag_ks * 32, orow = a.frag_ks ? off / ocols : 0;
+  if (a.o8) {
+    // dims 0..31 of the head are o[0..1] of the 4 lanes sharing lr (lane groups g), 32..63 o[2..3]
+    float r[4][4], m[2] = {0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r[dt][i] = bf2f(f2bf(o[dt][i] * inv));
+        m[dt >> 1] = fmaxf(m[dt >> 1], fabsf(r[dt][i]));
+      }
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) m[h2] = max_xor32(max_xor16(m[h2]));
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int64_t e = off + dt * 16 + 4 * g;
+      store_fp8x4(a.o8 + e, (g == 0 && (dt & 1) == 0) ? a.o8s + e / 32 : nullptr, r[dt], m[dt >> 1]);
+    }
+    return;
+  }
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const int d = dt * 16 + 4 * g;
@@ -350,7 +383,8 @@ int flash_launch(const T* q, const T* k, const T* v, T* o, int64_t n_bh, const A
 __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                        const bf16* __restrict__ v, bf16* __restrict__ out,
                                                        int64_t G, int T, int P, int H, float scale_log2, int qf,
-                                                       int fks, oasis::Prefetch pf) {
+                                                       int fks, oasis::Prefetch pf, uint8_t* __restrict__ out8,
+                                                       uint8_t* __restrict__ out8s) {
   if (blockIdx.z) {  // the prefetching slice
     prefetch_lines(pf);
     return;
@@ -363,6 +397,20 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
   const int p = (int)(bp % P);
   const int64_t b = bp / P;
   const int64_t base = grp * T * 64 + j * 4;
+  // output row `row`, this lane's 4 dims: bf16 (row-major or fragment order) or, with out8, fp8
+  // blocks (the 8 lanes of an aligned 32-dim half of the head share a block)
+  auto put = [&](int64_t row, float a0, float a1, float a2, float a3) {
+    const int col = h * 64 + j * 4;
+    if (out8) {
+      const float r[4] = {bf2f(f2bf(a0)), bf2f(f2bf(a1)), bf2f(f2bf(a2)), bf2f(f2bf(a3))};
+      const float amax = oct_max(fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3]))));
+      const int64_t e = row * (int64_t)(H * 64) + col;
+      store_fp8x4(out8 + e, (j & 7) == 0 ? out8s + e / 32 : nullptr, r, amax);
+      return;
+    }
+    bf16* dst = fks ? out + frag_index(row, col, fks) : out + row * (int64_t)(H * 64) + col;
+    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(a0), f2bf(a1), f2bf(a2), f2bf(a3)};
+  };
   // qf >= 0: only query frame qf is computed, written as the single frame of a T=1 output
   // (out row b*P + p); the K/V cache path runs the current frame against cached context K/V.
   if (T == 2) {  // the DiT's 2-frame window: one round trip for all six rows
@@ -385,14 +433,10 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     const float inv = 1.0f / (p0 + p1);
     const int T_out = qf < 0 ? T : 1;
     const int64_t row0 = b * T_out * P + p, row1 = qf < 0 ? row0 + P : row0;
-    const int col = h * 64 + j * 4;
-    bf16* dst0 = fks ? out + frag_index(row0, col, fks) : out + row0 * (int64_t)(H * 64) + col;
-    bf16* dst1 = fks ? out + frag_index(row1, col, fks) : out + row1 * (int64_t)(H * 64) + col;
-    if (qf <= 0) *reinterpret_cast<bf16x4*>(dst0) = v0;
+    if (qf <= 0) put(row0, bf2f(v0[0]), bf2f(v0[1]), bf2f(v0[2]), bf2f(v0[3]));
     if (qf == 0) return;
-    *reinterpret_cast<bf16x4*>(dst1) =
-        bf16x4{f2bf((p0 * bf2f(v0[0]) + p1 * bf2f(v1[0])) * inv), f2bf((p0 * bf2f(v0[1]) + p1 * bf2f(v1[1])) * inv),
-               f2bf((p0 * bf2f(v0[2]) + p1 * bf2f(v1[2])) * inv), f2bf((p0 * bf2f(v0[3]) + p1 * bf2f(v1[3])) * inv)};
+    put(row1, (p0 * bf2f(v0[0]) + p1 * bf2f(v1[0])) * inv, (p0 * bf2f(v0[1]) + p1 * bf2f(v1[1])) * inv,
+        (p0 * bf2f(v0[2]) + p1 * bf2f(v1[2])) * inv, (p0 * bf2f(v0[3]) + p1 * bf2f(v1[3])) * inv);
     return;
   }
   for (int t = qf < 0 ? 0 : qf; t < (qf < 0 ? T : qf + 1); ++t) {
@@ -415,10 +459,7 @@ __global__ __launch_bounds__(256) void temporal_kernel(const bf16* __restrict__ 
     }
     const float inv = 1.0f / l;
     const int64_t frame = qf < 0 ? b * T + t : b;
-    bf16* dst = fks ? out + frag_index(frame * P + p, h * 64 + j * 4, fks)
-                    : out + (frame * P + p) * (int64_t)(H * 64) + h * 64 + j * 4;
-    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(acc[0] * inv), f2bf(acc[1] * inv), f2bf(acc[2] * inv),
-                                              f2bf(acc[3] * inv)};
+    put(frame * P + p, acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
   }
 }
 
@@ -428,8 +469,10 @@ namespace {
 
 int attention_impl(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
                    int64_t n_heads, float scale, hipStream_t stream, bool out_frag,
-                   const oasis::Prefetch* pf = nullptr) {
+                   const oasis::Prefetch* pf = nullptr, uint8_t* out8 = nullptr, uint8_t* out8_scale = nullptr) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "attention: null pointer");
+  OASIS_REQUIRE(!out8 || (out8_scale && !out_frag), OASIS_ERR_ARG,
+                "attention: an fp8 output needs its scales and a row-major layout");
   OASIS_REQUIRE(!out_frag || (n_frames * L) % 16 == 0, OASIS_ERR_SHAPE,
                 "attention: a fragment-order output needs a multiple of 16 rows");
   OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "attention: pointers must be 16-byte aligned");
@@ -448,6 +491,8 @@ int attention_impl(const void* q, const void* k, const void* v, void* out, int64
   a.o_si = n_heads * 64;
   a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
   a.pf = oasis::prefetch_or_none(pf);
+  a.o8 = out8;
+  a.o8s = out8_scale;
   return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                             static_cast<bf16*>(out), n_frames * n_heads, a, stream);
 }
@@ -494,8 +539,8 @@ extern "C" int oasis_sdpa(const void* Q, const void* K, const void* V, void* out
 namespace oasis {
 
 int attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L, int64_t n_heads,
-              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf) {
-  return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, stream, out_frag, pf);
+              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf, uint8_t* out8, uint8_t* out8_scale) {
+  return attention_impl(q, k, v, out, n_frames, L, n_heads, scale, stream, out_frag, pf, out8, out8_scale);
 }
 
 int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
@@ -505,8 +550,10 @@ int attention_frag(const void* q, const void* k, const void* v, void* out, int64
 
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
                        int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag,
-                       const Prefetch* pf) {
+                       const Prefetch* pf, uint8_t* out8, uint8_t* out8_scale) {
   OASIS_REQUIRE(q && k && v && out, OASIS_ERR_NULL, "temporal_attention: null pointer");
+  OASIS_REQUIRE(!out8 || (out8_scale && !out_frag), OASIS_ERR_ARG,
+                "temporal_attention: an fp8 output needs its scales and a row-major layout");
   OASIS_REQUIRE(!out_frag || (B * (q_frame < 0 ? T : 1) * P) % 16 == 0, OASIS_ERR_SHAPE,
                 "temporal_attention: a fragment-order output needs a multiple of 16 rows");
   OASIS_REQUIRE(oasis_aligned(16, q, k, v, out), OASIS_ERR_ARG, "temporal_attention: pointers must be 16-byte aligned");
@@ -532,13 +579,15 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
     a.o_si = P * n_heads * 64;
     a.frag_ks = out_frag ? (int)(n_heads * 2) : 0;
     a.pf = prefetch_or_none(pf);
+    a.o8 = out8;
+    a.o8s = out8_scale;
     return flash_launch<bf16>(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                               static_cast<bf16*>(out), G, a, stream);
   }
   hipLaunchKernelGGL(temporal_kernel, dim3((unsigned)((G + 15) / 16), 1, prefetch_any(pf) ? 2 : 1), dim3(256), 0,
                      stream, static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                      static_cast<bf16*>(out), G, (int)T, (int)P, (int)n_heads, scale * LOG2E, q_frame < 0 ? -1 : q_frame,
-                     out_frag ? (int)(n_heads * 2) : 0, prefetch_or_none(pf));
+                     out_frag ? (int)(n_heads * 2) : 0, prefetch_or_none(pf), out8, out8_scale);
   return check_launch("temporal_attention");
 }
 
@@ -547,4 +596,19 @@ int temporal_attention(const void* q, const void* k, const void* v, void* out, i
 extern "C" int oasis_temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T,
                                         int64_t P, int64_t n_heads, float scale, oasis_stream_t stream) {
   return oasis::temporal_attention(q, k, v, out, B, T, P, n_heads, scale, -1, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int oasis_attention_fp8(const void* q, const void* k, const void* v, void* out8, void* out8_scale,
+                                   int64_t n_frames, int64_t L, int64_t n_heads, float scale, oasis_stream_t stream) {
+  OASIS_REQUIRE(out8 && out8_scale, OASIS_ERR_NULL, "attention_fp8: null output");
+  return attention_impl(q, k, v, out8, n_frames, L, n_heads, scale, static_cast<hipStream_t>(stream), false, nullptr,
+                        static_cast<uint8_t*>(out8), static_cast<uint8_t*>(out8_scale));
+}
+
+extern "C" int oasis_temporal_attention_fp8(const void* q, const void* k, const void* v, void* out8, void* out8_scale,
+                                            int64_t B, int64_t T, int64_t P, int64_t n_heads, float scale,
+                                            oasis_stream_t stream) {
+  OASIS_REQUIRE(out8 && out8_scale, OASIS_ERR_NULL, "temporal_attention_fp8: null output");
+  return oasis::temporal_attention(q, k, v, out8, B, T, P, n_heads, scale, -1, static_cast<hipStream_t>(stream), false,
+                                   nullptr, static_cast<uint8_t*>(out8), static_cast<uint8_t*>(out8_scale));
 }

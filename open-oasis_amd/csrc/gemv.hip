@@ -21,13 +21,15 @@
 namespace {
 
 constexpr int KSTEP = 64;   // k per pipeline step (two MFMAs)
-constexpr int UNROLL = 4;   // pipeline steps whose loads are issued together
+// pipeline steps whose loads are issued together (gemv_tiles' UNROLL): 4 with one 16-row group of
+// x; 8 with two, whose staged x (132 KB at 32 rows) leaves one workgroup per CU, so each wave keeps
+// more in flight (the config-4 adaLN pass over 32 rows 180 -> 171 us)
 
 // TILED: W in 16-row MFMA tile order (for tile t and 32-wide K step s, the 64 lanes' 16-byte
 // pieces back to back, lane l holding row 16t + (l & 15), columns 32s + 8(l >> 4) .. +7), so a
 // wave's load instruction reads 1 KB contiguous; else row-major [N, K].
 // block / nblocks: this workgroup's index among the nblocks that share the tiles
-template <int RG, int KS, bool TILED>
+template <int RG, int KS, bool TILED, int UNROLL = RG == 1 ? 4 : 8>
 __device__ __forceinline__ void gemv_tiles(const float* __restrict__ x, int64_t ldx, int R, const bf16* __restrict__ W,
                                            int N, int K, const float* __restrict__ b, float* __restrict__ out,
                                            int64_t ld_out, int act_in, int act_out, int accumulate, int block,

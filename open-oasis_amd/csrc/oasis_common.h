@@ -100,13 +100,18 @@ int gemv_adaln_pair(const float* x, int64_t ldx, int64_t R, const void* W16, int
 // each group and writes it as a single frame: out [B*P, n_heads*64].
 // out_frag: out in MFMA fragment order (as a [rows, n_heads*64] matrix).
 // pf: byte ranges read by extra workgroups beside the attention.
+// out8 / out8_scale: the output as fp8 activation blocks instead of bf16 (row-major, e4m3 bytes
+// [rows, n_heads*64] and e8m0 scales [rows, n_heads*2]), as oasis_quantize_act_fp8 of the bf16
+// output would give; out is then not written.
 int temporal_attention(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t T, int64_t P,
                        int64_t n_heads, float scale, int q_frame, hipStream_t stream, bool out_frag = false,
-                       const Prefetch* pf = nullptr);
+                       const Prefetch* pf = nullptr, uint8_t* out8 = nullptr, uint8_t* out8_scale = nullptr);
 // oasis_attention (heads-first q/k/v per frame, token-major out), out optionally in fragment
-// order, with byte ranges read by extra workgroups beside it.
+// order or as fp8 activation blocks (as temporal_attention), with byte ranges read by extra
+// workgroups beside it.
 int attention(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L, int64_t n_heads,
-              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf);
+              float scale, hipStream_t stream, bool out_frag, const Prefetch* pf, uint8_t* out8 = nullptr,
+              uint8_t* out8_scale = nullptr);
 // oasis_attention with out in fragment order.
 int attention_frag(const void* q, const void* k, const void* v, void* out, int64_t n_frames, int64_t L,
                    int64_t n_heads, float scale, hipStream_t stream);

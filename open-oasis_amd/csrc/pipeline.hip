@@ -643,16 +643,19 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
       else
         OASIS_TRY(proj(w, ROLE_QKV, j, fp8 ? (const void*)a8 : buf->h, D, a8s, M, 3 * D, D, qkv, pl.tile[ROLE_QKV], 1,
                        s, &pf_qkvg));
+      // with fp8 weights the attention writes O's A operand as fp8 blocks itself
+      uint8_t* o8 = fp8 ? a8 : nullptr;
+      uint8_t* o8s = fp8 ? a8s : nullptr;
       if (spatial)
-        OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s, f_o, &pf_attn));
+        OASIS_TRY(oasis::attention(buf->q, buf->k, buf->v, buf->attn, B * T, P, H, kAttnScale, s, f_o, &pf_attn, o8,
+                                   o8s));
       else if (kv.mode == KV_NONE)
         OASIS_TRY(oasis::temporal_attention(buf->q, buf->k, buf->v, buf->attn, B, T, P, H, kAttnScale, -1, s, f_o,
-                                            &pf_attn));
+                                            &pf_attn, o8, o8s));
       else
         OASIS_TRY(oasis::temporal_attention(buf->q, kc, vc, buf->attn, B, 2, P, H, kAttnScale, qf, s, f_o,
-                                            &pf_attn));
+                                            &pf_attn, o8, o8s));
     }
-    if (fp8) OASIS_TRY(oasis_quantize_act_fp8(buf->attn, D, M, D, a8, D, a8s, D / 32, stream));
     gelu.bias = w->fc1_b[j];
     if (f_ln) {
       // O + bias + gated residual into x in the epilogue, which also leaves FC1 the centred rows

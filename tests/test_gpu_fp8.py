@@ -185,6 +185,36 @@ def test_quantize_act_fp8_matches_oracle():
     assert torch.equal(deq, oracle.quantize_act_blocks(x))
 
 
+@pytest.mark.parametrize("kind,F,T,H", [("spatial", 2, 1, 16), ("spatial", 1, 1, 4), ("temporal", 2, 2, 4),
+                                         ("temporal", 2, 4, 4), ("temporal", 1, 13, 4), ("temporal", 1, 32, 2)])
+def test_attention_fp8_output_equals_quantized_bf16(kind, F, T, H):
+    """The attention kernels' fp8-block output (the fp8 step's O operand, written in the attention
+    launch) is bit for bit oasis_quantize_act_fp8 of their bf16 output: the spatial flash kernel,
+    the temporal VALU kernel (T = 2 and its general loop) and the causal flash kernel (T >= 8)."""
+    P = 144
+    rows = F * T * P
+    D = H * 64
+    g = _gen(300 + F * 7 + T * 13 + H)
+    q, k, v = (dev((torch.randn(rows * D, generator=g) * 2).to(torch.bfloat16)) for _ in range(3))
+    out = torch.zeros(rows, D, device="cuda", dtype=torch.bfloat16)
+    o8 = torch.full((rows, D), 0x7F, dtype=torch.uint8, device="cuda")
+    o8s = torch.full((rows, D // 32), 0xEE, dtype=torch.uint8, device="cuda")
+    if kind == "spatial":
+        print("attention fp8 spatial F=%d H=%d" % (F, H), flush=True)
+        L.call("oasis_attention", L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), F, P, H, 0.125, stream())
+        L.call("oasis_attention_fp8", L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(o8), L.ptr(o8s), F, P, H, 0.125, stream())
+    else:
+        print("attention fp8 temporal B=%d T=%d H=%d" % (F, T, H), flush=True)
+        L.call("oasis_temporal_attention", L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(out), F, T, P, H, 0.125, stream())
+        L.call("oasis_temporal_attention_fp8", L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(o8), L.ptr(o8s), F, T, P, H,
+               0.125, stream())
+    ref8 = torch.zeros(rows, D, dtype=torch.uint8, device="cuda")
+    ref8s = torch.zeros(rows, D // 32, dtype=torch.uint8, device="cuda")
+    L.call("oasis_quantize_act_fp8", L.ptr(out), D, rows, D, L.ptr(ref8), D, L.ptr(ref8s), D // 32, stream())
+    sync()
+    assert torch.equal(o8, ref8) and torch.equal(o8s, ref8s), (kind, F, T, H)
+
+
 def test_gemm_fp8_a8_equals_in_kernel_quantization():
     """Pre-quantized A blocks give bit-identical results to quantizing A inside the GEMM,
     and the fp8 GELU epilogue writes the blocks the next fp8 GEMM reads."""
