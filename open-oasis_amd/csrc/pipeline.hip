@@ -541,9 +541,14 @@ int dit_blocks(const oasis_dit_weights_t* w, const oasis_dit_buffers_t* buf, int
   qkv.frames_per_stream = T;
   const bool fp8 = w->weight_format == OASIS_WEIGHTS_FP8;
   // O and FC2 unsplit with their gated residual in the epilogue where 144 x 128 tiles fill the CUs
+  // (unless OASIS_GEMM_PLAN / OASIS_GEMM_PLAN8 place that role themselves)
   const bool unsplit_fill = (M + 143) / 144 * ((D + 127) / 128) >= 256;
-  const bool o_res = unsplit_fill && !f_o && !f_ln && !f_fc1 && (fp8 ? pl.o_unsplit[1] : pl.o_unsplit[0]) >= 0;
-  const bool fc2_res = unsplit_fill && !f_fc2 && (fp8 ? pl.fc2_unsplit[1] : pl.fc2_unsplit[0]) >= 0;
+  auto unsplit = [&](int role, const int (&tiles)[2]) {
+    return unsplit_fill && pl.splits[role] <= 0 && (fp8 ? tiles[1] >= 0 && pl.tile8[role] < 0
+                                                           : tiles[0] >= 0 && pl.tile[role] < 0);
+  };
+  const bool o_res = !f_o && !f_ln && !f_fc1 && unsplit(ROLE_O, pl.o_unsplit);
+  const bool fc2_res = !f_fc2 && unsplit(ROLE_FC2, pl.fc2_unsplit);
   oasis_epilogue_t gelu = epi_zero();
   gelu.kind = fp8 ? OASIS_EPI_GELU_TANH_FP8 : (f_fc2 ? OASIS_EPI_GELU_TANH_FRAG : OASIS_EPI_GELU_TANH);
   gelu.out_bf16 = buf->mlp;
