@@ -320,25 +320,37 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
     const i32x4 x1 = *reinterpret_cast<const i32x4*>(base + r * P8 + ((((4 + g) ^ (r >> 1)) & 7) << 4));
     return i32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
   };
+  // B fragments first; then A fragment i + 1 and its scale byte are read while the MFMAs of
+  // fragment i issue (a wait and scheduling barriers keep that order), so only two A fragments
+  // are live beside the 4 * FM * FN accumulator registers and each read lands under FN MFMAs
   auto compute = [&](int buf) {
     const char* base = smem + buf * STAGE;
     const uint8_t* sb = reinterpret_cast<const uint8_t*>(base + DATA);
-    i32x8 af[FM], bfr[FN];
-    int sa[FM];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int r = wm * TM + i * 16 + lr;
-      af[i] = frag(base, r);
-      sa[i] = sb[r * 4 + g];
-    }
+    i32x8 bfr[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) bfr[j] = frag(base, BM + wn * TN + j * 16 + lr);
+    i32x8 a = frag(base, wm * TM + lr);
+    int sa = sb[(wm * TM + lr) * 4 + g];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+      // fragment i (and, at i = 0, the B fragments) landed before fragment i + 1's reads are issued,
+      // so the wait never covers the reads that the MFMAs below are meant to hide
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      i32x8 an = a;
+      int sn = sa;
+      if (i + 1 < FM) {
+        const int rn = wm * TM + (i + 1) * 16 + lr;
+        an = frag(base, rn);
+        sn = sb[rn * 4 + g];
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bfr[j], acc[i][j], 0, 0, 0, sa[i], 0,
-                                                                      kScaleOne);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bfr[j], acc[i][j], 0, 0, 0, sa, 0, kScaleOne);
+      __builtin_amdgcn_sched_barrier(0);
+      a = an;
+      sa = sn;
+    }
   };
 
   constexpr int VM = (STAGES - 2) * (LPW + 1);  // stages that may stay in flight: tile k is in LDS
