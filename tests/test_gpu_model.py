@@ -66,11 +66,13 @@ def test_temporal_sub_block_config2():
     _check_sub_block(c["x"][0], c["cond"][0], w, "t", 32, "config2 temporal sub-block T=32")
 
 
-@pytest.mark.parametrize("kind,T", [("s", 1), ("t", 1), ("s", 4), ("t", 4), ("t", 13)])
+@pytest.mark.parametrize("kind,T", [("s", 1), ("t", 1), ("s", 4), ("t", 4), ("t", 13), ("t", 16), ("s", 33)])
 def test_sub_blocks_between_sizes(kind, T):
     """Sub-blocks at the token counts between configs: one 144-token frame (the K/V-cache
     steps' tile and split choices), 576 tokens (tile 2 with the QKV + RoPE epilogue in both
-    layouts) and 1872 tokens (the largest count below the 8-wave tall tiles)."""
+    layouts), 1872 tokens (the largest count below the 8-wave tall tiles), 2304 tokens (the tall
+    tiles with O and FC2 as split-K partials, below where unsplit 144 x 128 tiles fill the CUs) and
+    4752 tokens (O and FC2 unsplit, 264 tiles: a second partial round)."""
     c0, c2 = synth.config0(), synth.config2()
     dr = synth.Draw(70 + T)
     x, cond = dr.normal(T, 144, 1024), dr.normal(T, 1024)
