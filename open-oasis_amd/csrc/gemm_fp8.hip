@@ -239,11 +239,12 @@ __global__ __launch_bounds__(256) void gemm_fp8_kernel(const void* __restrict__ 
   }
 }
 
-// Large-token fp8 variant (2048+ tokens, A already in e4m3 blocks): 8 waves share a tall tile
-// (288 x 256 and the like, as the bf16 gemm_big_kernel) and the K tiles reach LDS through
-// global_load_lds, 128 fp8 per row (one 16x16x128 MFMA step) in the same swizzled 128-byte
-// rows, plus each A row's 4 block-scale bytes per K tile (4 bytes per lane, one wave per 64
-// rows). Two stages; the epilogue stages 16 rows of a wave's tile at a time in that wave's LDS.
+// Large-token fp8 variant (2048+ tokens, A already in e4m3 blocks): 6 or 8 waves share a tall
+// tile (288 x 256, 144 x 128 and the like, as the bf16 gemm_big_kernel) and the K tiles reach LDS
+// through global_load_lds, 128 fp8 per row (one 16x16x128 MFMA step) in the same swizzled 128-byte
+// rows, plus each A row's 4 block-scale bytes per K tile (4 bytes per lane, the first waves' lanes
+// one row each). STAGES K tiles in the ring (two for the 288-row tiles, which is what 160 KB holds);
+// the epilogue stages 16 rows of a wave's tile at a time in that wave's LDS.
 template <int BM, int BN, int WM, int WN, int KIND = -1, int STAGES = 2>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_t* __restrict__ A, int64_t lda,
                                                                    const uint8_t* __restrict__ Ascale, int64_t lds,
