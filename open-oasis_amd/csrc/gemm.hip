@@ -487,6 +487,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
   QkvRows<(16 * UPR + 63) / 64> qkv;
   if constexpr (QKV) qkv.init(e, lane, UPR, n0 + wn * TN, m0 + wm * TM);
 
+  // residual kinds: x (and gate) fetched a 16-row group ahead
+  constexpr bool RES = KIND == OASIS_EPI_GATED_RES || KIND == OASIS_EPI_RESIDUAL;
+  ResAhead<UPR, RES ? KIND : OASIS_EPI_RESIDUAL> res;
+  if constexpr (RES) res.fetch(e, lane, m0 + wm * TM, n0 + wn * TN, M, N, 0);
+
   // each lane takes 8 consecutive columns of one row; lanes 4i..4i+3 cover one aligned 32-column
   // block when TN % 32 == 0 (the fp8 epilogue's shuffles rely on it; the host checks)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
@@ -499,7 +504,23 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_big_kernel(const bf16* __re
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int u = lane; u < 16 * UPR; u += 64) {
+    if constexpr (RES) {
+      if (i + 1 < FM) res.fetch(e, lane, m0 + wm * TM + (i + 1) * 16, n0 + wn * TN, M, N, (i + 1) & 1);
+#pragma unroll
+      for (int q = 0; q < res.UPL; ++q) {
+        const int r = res.row(lane, q), c8 = res.col(lane, q);
+        const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
+        if (!res.live(lane, q) || gm >= M || gn >= N) continue;
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
+        const f32x4 b0 = q > 0 && NBQ > 1 ? hb[NBQ - 1][0] : hb[0][0];
+        const f32x4 b1 = q > 0 && NBQ > 1 ? hb[NBQ - 1][1] : hb[0][1];
+        const float v[8] = {c0[0] + b0[0], c0[1] + b0[1], c0[2] + b0[2], c0[3] + b0[3],
+                            c1[0] + b1[0], c1[1] + b1[1], c1[2] + b1[2], c1[3] + b1[3]};
+        res.store(e, q, i & 1, gm, gn, v);
+      }
+    }
+    for (int u = lane; !RES && u < 16 * UPR; u += 64) {
       const int r = u / UPR, c8 = (u - r * UPR) * 8;
       const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
       const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
@@ -1221,6 +1242,14 @@ hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, in
     case OASIS_EPI_PARTIAL_F32:
       hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_PARTIAL_F32>), grid, block, 0, s, A,
                          lda, B, ldb, M, N, K, splits, e);
+      break;
+    case OASIS_EPI_GATED_RES:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_GATED_RES>), grid, block, 0, s, A, lda,
+                         B, ldb, M, N, K, splits, e);
+      break;
+    case OASIS_EPI_RESIDUAL:
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_RESIDUAL>), grid, block, 0, s, A, lda,
+                         B, ldb, M, N, K, splits, e);
       break;
     default:
       hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN>), grid, block, 0, s, A, lda, B, ldb, M, N, K,

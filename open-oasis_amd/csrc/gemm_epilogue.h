@@ -255,6 +255,57 @@ struct QkvRows {
   }
 };
 
+// The residual epilogues (GATED_RES, RESIDUAL) in the large-token kernels' per-wave epilogue, with
+// the lane-to-unit map of QkvRows: the x (and gate) vectors of a 16-row group are fetched one group
+// ahead, into buffer b = group & 1, so that only the first group's memory round trip is exposed.
+// No other lane or workgroup writes the x elements a lane fetches.
+template <int UPR, int KIND>
+struct ResAhead {
+  static_assert(KIND == OASIS_EPI_GATED_RES || KIND == OASIS_EPI_RESIDUAL, "residual kinds");
+  static constexpr int UPL = (16 * UPR + 63) / 64;
+  f32x4 x[2][UPL][2], g[2][UPL][2];
+
+  // the unit of pass q: its row within the group and its first column within the wave's tile
+  static __device__ __forceinline__ int row(int lane, int q) { return (lane + 64 * q) / UPR; }
+  static __device__ __forceinline__ int col(int lane, int q) { return ((lane + 64 * q) % UPR) * 8; }
+  static __device__ __forceinline__ bool live(int lane, int q) { return lane + 64 * q < 16 * UPR; }
+
+  // row0 / col0: the group's first row and the wave's first column
+  __device__ __forceinline__ void fetch(const Epi& e, int lane, int row0, int col0, int M, int N, int b) {
+#pragma unroll
+    for (int q = 0; q < UPL; ++q) {
+      const int gm = row0 + row(lane, q), gn = col0 + col(lane, q);
+      if (!live(lane, q) || gm >= M || gn >= N) continue;
+      const float* d = e.out_f32 + (int64_t)gm * e.ld_out + gn;
+      x[b][q][0] = *reinterpret_cast<const f32x4*>(d);
+      x[b][q][1] = *reinterpret_cast<const f32x4*>(d + 4);
+      if constexpr (KIND == OASIS_EPI_GATED_RES) {
+        const int64_t f = fast_div((uint32_t)gm, e.rpf_magic, e.rpf_shift);
+        const float* gp = e.gate + f * e.gate_fstride + gn;
+        g[b][q][0] = *reinterpret_cast<const f32x4*>(gp);
+        g[b][q][1] = *reinterpret_cast<const f32x4*>(gp + 4);
+      }
+    }
+  }
+  // x[gm, gn .. gn + 8) += (gate *) v with the vectors fetched for pass q into buffer b
+  __device__ __forceinline__ void store(const Epi& e, int q, int b, int64_t gm, int gn, const float* v) const {
+    f32x4 x0 = x[b][q][0], x1 = x[b][q][1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (KIND == OASIS_EPI_GATED_RES) {
+        x0[j] += g[b][q][0][j] * v[j];
+        x1[j] += g[b][q][1][j] * v[j + 4];
+      } else {
+        x0[j] += v[j];
+        x1[j] += v[j + 4];
+      }
+    }
+    float* d = e.out_f32 + gm * e.ld_out + gn;
+    *reinterpret_cast<f32x4*>(d) = x0;
+    *reinterpret_cast<f32x4*>(d + 4) = x1;
+  }
+};
+
 // Applies the epilogue to 8 consecutive columns [n0, n0+8) of row m (all < N). tab / tab_rows:
 // an LDS copy of the QKV rotation tables (see rope_lds_rows), or null. with_bias = false: the
 // caller has already added the bias. kind >= 0: the epilogue kind known at compile time (it must

@@ -398,6 +398,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
   constexpr bool QKV = KIND == OASIS_EPI_QKV_ROPE;
   QkvRows<(16 * UPR + 63) / 64> qkv;
   if constexpr (QKV) qkv.init(e, lane, UPR, n0 + wn * TN, m0 + wm * TM);
+  // residual kinds: x (and gate) fetched a 16-row group ahead
+  constexpr bool RES = KIND == OASIS_EPI_GATED_RES || KIND == OASIS_EPI_RESIDUAL;
+  ResAhead<UPR, RES ? KIND : OASIS_EPI_RESIDUAL> res;
+  if constexpr (RES) res.fetch(e, lane, m0 + wm * TM, n0 + wn * TN, M, N, 0);
   // lanes 4i..4i+3 cover one aligned 32-column block when TN % 32 == 0 (the host checks it for
   // the GELU_TANH_FP8 epilogue)
   float* st = reinterpret_cast<float*>(smem) + wave * 16 * EP;
@@ -410,7 +414,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int u = lane; u < 16 * UPR; u += 64) {
+    if constexpr (RES) {
+      if (i + 1 < FM) res.fetch(e, lane, m0 + wm * TM + (i + 1) * 16, n0 + wn * TN, M, N, (i + 1) & 1);
+#pragma unroll
+      for (int q = 0; q < res.UPL; ++q) {
+        const int r = res.row(lane, q), c8 = res.col(lane, q);
+        const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
+        if (!res.live(lane, q) || gm >= M || gn >= N) continue;
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(st + r * EP + c8);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(st + r * EP + c8 + 4);
+        const bool q1 = q > 0 && NBQ > 1;
+        const f32x4 s0 = q1 ? hs[NBQ - 1][0] : hs[0][0], s1 = q1 ? hs[NBQ - 1][1] : hs[0][1];
+        const f32x4 b0 = q1 ? hb[NBQ - 1][0] : hb[0][0], b1 = q1 ? hb[NBQ - 1][1] : hb[0][1];
+        float v[8];
+        scale_bias8(c0, c1, s0, s1, b0, b1, v);
+        res.store(e, q, i & 1, gm, gn, v);
+      }
+    }
+    for (int u = lane; !RES && u < 16 * UPR; u += 64) {
       const int r = u / UPR, c8 = (u - r * UPR) * 8;
       const int gm = m0 + wm * TM + i * 16 + r, gn = n0 + wn * TN + c8;
       if (gm < M && gn < N) {
@@ -457,6 +478,14 @@ hipError_t launch8_big(const void* A, int64_t lda, const uint8_t* As, int64_t ld
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
   if (e.kind == OASIS_EPI_QKV_ROPE)
     hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_QKV_ROPE, STAGES>), dim3(Mt * Nt * splits),
+                       dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
+                       splits, e);
+  else if (e.kind == OASIS_EPI_GATED_RES)
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_GATED_RES, STAGES>), dim3(Mt * Nt * splits),
+                       dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
+                       splits, e);
+  else if (e.kind == OASIS_EPI_RESIDUAL)
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_RESIDUAL, STAGES>), dim3(Mt * Nt * splits),
                        dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
                        splits, e);
   else

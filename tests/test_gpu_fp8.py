@@ -267,8 +267,19 @@ def test_gemm_fp8_large_token_tiles(M, N):
     a8s = torch.zeros(M, K // 32, dtype=torch.uint8, device="cuda")
     L.call("oasis_quantize_act_fp8", L.ptr(Ad), K, M, K, L.ptr(a8), K, L.ptr(a8s), K // 32, stream())
 
+    # residual epilogues into x0, gates of 100-row frames (the gate row changes inside tiles)
+    P = 100
+    x0 = torch.randn(M, N, generator=g)
+    ada = dev(torch.randn((M + P - 1) // P, 2 * N, generator=g))
+
     def run(tile, splits=1, kind=None):
-        if kind == "gelu8":
+        if kind in ("gated", "res"):
+            o = dev(x0)
+            e = _epi(kind=L.EPI_GATED_RES, bias=dev(bias), out_f32=o, ld_out=N, gate=ada[0, N:], gate_fstride=2 * N,
+                     rows_per_frame=P) if kind == "gated" else _epi(kind=L.EPI_RESIDUAL, bias=dev(bias), out_f32=o,
+                                                                     ld_out=N)
+            out = o
+        elif kind == "gelu8":
             m8 = torch.zeros(M, N, dtype=torch.uint8, device="cuda")
             m8s = torch.zeros(M, N // 32, dtype=torch.uint8, device="cuda")
             e = _epi(kind=L.EPI_GELU_TANH_FP8, bias=dev(bias), out_fp8=m8, out_scale=m8s, ld_out=N, ld_scale=N // 32)
@@ -289,14 +300,20 @@ def test_gemm_fp8_large_token_tiles(M, N):
     ref = run(0)
     ref_part = run(0, 2)
     ref8 = run(0, kind="gelu8") if N % 32 == 0 else None
+    ref_gated, ref_res = run(0, kind="gated"), run(0, kind="res")
     for tile in (5, 6, 7, 8, 9, 10, 11):
         assert torch.equal(run(tile), ref), "tile %d" % tile
         assert torch.equal(run(tile, 2), ref_part), "tile %d split-K x2" % tile
+        assert torch.equal(run(tile, kind="gated"), ref_gated), "tile %d gated residual" % tile
+        assert torch.equal(run(tile, kind="res"), ref_res), "tile %d residual" % tile
         if ref8 is not None and tile not in (6, 9):
             m8, m8s = run(tile, kind="gelu8")
             assert torch.equal(m8, ref8[0]) and torch.equal(m8s, ref8[1]), "tile %d gelu8" % tile
     cos, rel = metrics(ref, _ref(A, W) + bias.double())
     assert rel <= 1e-4, rel
+    gates = ada[:, N:].cpu().repeat_interleave(P, 0)[:M]
+    assert metrics(ref_gated, x0 + gates * ref.cpu())[1] <= 1e-6
+    assert metrics(ref_res, x0 + ref.cpu())[1] <= 1e-6
     if N % 32 == 0:
         with pytest.raises(L.OasisError, match="GELU_TANH_FP8"):
             run(6, kind="gelu8")

@@ -675,6 +675,35 @@ def test_gemm_large_token_tiles_ragged(tile):
     assert_close(out, Ad.float() @ Bd.float().t(), 0.999999, 1e-4, "tile %d 4608x4096x1024" % tile)
 
 
+@pytest.mark.parametrize("tile", [2, 3, 4, 5, 6, 7, 13, 14, 15, 16, 17])
+def test_gemm_staged_epilogue_residuals(tile):
+    """The per-wave staged epilogue's residual kinds (x and gate fetched a 16-row group ahead) on
+    every tile of that kernel, on a ragged shape (the last tile row and column partial, lanes with
+    no unit where a wave's tile is 16 or 48 columns wide) whose 100-row frames change the gate row
+    inside tiles and 16-row groups: gated residual, then plain residual, into the same x."""
+    M, N, K, P = 600, 520, 320, 100
+    g = _gen(150 + tile)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    x0 = torch.randn(M, N, generator=g)
+    fstride = 2 * N
+    ada = torch.randn(M // P, fstride, generator=g)
+    x, ada_d = dev(x0), dev(ada)
+    Ad, Bd = dev(A), dev(B)
+    e = _epi(kind=L.EPI_GATED_RES, bias=dev(bias), out_f32=x, ld_out=N, gate=ada_d[0, N:], gate_fstride=fstride,
+             rows_per_frame=P)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), K, L.ptr(Bd), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    sync()
+    y = A.float() @ B.float().t() + bias
+    ref = x0 + ada[:, N:].repeat_interleave(P, 0) * y
+    assert_close(x, ref, 0.999999, 1e-5, "tile %d gated residual" % tile)
+    e = _epi(kind=L.EPI_RESIDUAL, bias=dev(bias), out_f32=x, ld_out=N)
+    L.call("oasis_gemm_bf16_config", L.ptr(Ad), K, L.ptr(Bd), K, M, N, K, ctypes.byref(e), tile, 1, stream())
+    sync()
+    assert_close(x, ref + y, 0.999999, 1e-5, "tile %d residual" % tile)
+
+
 def test_gemm_fp8_epilogue_needs_aligned_lanes():
     """A tile whose epilogue lanes do not cover whole 32-column blocks refuses GELU_TANH_FP8."""
     M, N, K = 288, 384, 64
