@@ -633,6 +633,18 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
       bv[q][j + 4] = b1[j];
     }
   }
+  // QKV + RoPE: the rotation table rows of this thread's epilogue units, fetched before the K loop
+  // as well (the row's table position does not depend on the product)
+  constexpr bool QKV = KIND == OASIS_EPI_QKV_ROPE;
+  float rc[QKV ? UPT : 1][8], rs[QKV ? UPT : 1][8];
+  if constexpr (QKV) {
+#pragma unroll
+    for (int q = 0; q < UPT; ++q) {
+      const int u = tid + q * 256, r = u / UPR;
+      const int gm = min(m0 + r, M - 1), gn = min(n0 + (u % UPR) * 8, N - 8);
+      qkv_rope_tables(e, gm, gn, rc[q], rs[q]);
+    }
+  }
 
   // lane's row in each 8-row block: r = 8 blk + lane / 8, K chunk (lane % 8) ^ ((r >> 1) & 7).
   // Loads are buffer loads: a scalar base (the tile's first A row / weight row at this wave's K
@@ -738,6 +750,8 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const bf16* __restrict__
         float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
         *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+      } else if constexpr (QKV) {
+        qkv_rope_store(e, gm, gn, v, rc[q], rs[q]);
       } else {
         epilogue8(e, gm, gn, v, nullptr, 0, false, KIND);
       }
