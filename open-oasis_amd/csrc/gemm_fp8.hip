@@ -444,12 +444,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_fp8_big_kernel(const uint8_
         scale_bias8(c0, c1, s0, s1, b0, b1, v);
         if constexpr (QKV) {
           qkv.store(e, u >> 6, v, tab, tab_rows);
-        } else if (e.kind == OASIS_EPI_PARTIAL_F32) {
+        } else if (KIND == OASIS_EPI_PARTIAL_F32 || (KIND < 0 && e.kind == OASIS_EPI_PARTIAL_F32)) {
           float* d = e.out_f32 + (int64_t)split * e.split_stride + (int64_t)gm * e.ld_out + gn;
           *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
           *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
         } else {
-          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false);
+          epilogue8(e, gm, gn, v, tab_rows ? tab : nullptr, tab_rows, false, KIND);
         }
       }
     }
@@ -478,6 +478,14 @@ hipError_t launch8_big(const void* A, int64_t lda, const uint8_t* As, int64_t ld
   const int Mt = (M + BM - 1) / BM, Nt = (N + BN - 1) / BN;
   if (e.kind == OASIS_EPI_QKV_ROPE)
     hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_QKV_ROPE, STAGES>), dim3(Mt * Nt * splits),
+                       dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
+                       splits, e);
+  else if (e.kind == OASIS_EPI_GELU_TANH_FP8)
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_GELU_TANH_FP8, STAGES>), dim3(Mt * Nt * splits),
+                       dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
+                       splits, e);
+  else if (e.kind == OASIS_EPI_PARTIAL_F32)
+    hipLaunchKernelGGL((gemm_fp8_big_kernel<BM, BN, WM, WN, OASIS_EPI_PARTIAL_F32, STAGES>), dim3(Mt * Nt * splits),
                        dim3(WM * WN * 64), 0, s, static_cast<const uint8_t*>(A), lda, As, lds, B, ldb, ws, M, N, K,
                        splits, e);
   else if (e.kind == OASIS_EPI_GATED_RES)
