@@ -54,8 +54,8 @@ def _event_ms(fn, stream, n, graph=None):
 # HBM-side bytes per launch (L2-miss fetch + write) of the roofline kernels, from
 # `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of `bench.py --probe`, each
 # scaled by what the same counter reads for a plain device copy of known size.
-TRAFFIC = {"fc1_ln": 16877323, "fc1_row": 15622976, "gemv": 405109773, "fc1_4608_bf16": 90365516,
-           "fc1_4608_fp8": 46790181}
+TRAFFIC = {"fc1_ln": 16877545, "fc1_row": 15622976, "gemv": 405109565, "fc1_4608_bf16": 90367489,
+           "fc1_4608_fp8": 46325337}
 
 
 def _fc1_timing(pkg, dit, ws, stream, n=100, graph=True):
