@@ -1253,6 +1253,10 @@ hipError_t launch_big(const bf16* A, int64_t lda, const bf16* B, int64_t ldb, in
       hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_GELU_TANH>), grid, block, 0, s, A, lda,
                          B, ldb, M, N, K, splits, e);
       break;
+    case OASIS_EPI_GELU_ERF:  // the VAE's FC1
+      hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_GELU_ERF>), grid, block, 0, s, A, lda,
+                         B, ldb, M, N, K, splits, e);
+      break;
     case OASIS_EPI_PARTIAL_F32:
       hipLaunchKernelGGL((gemm_big_kernel<BM, BN, WM, WN, STAGES, GN, OASIS_EPI_PARTIAL_F32>), grid, block, 0, s, A,
                          lda, B, ldb, M, N, K, splits, e);

@@ -350,6 +350,8 @@ OASIS_DEV float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
+// erf-GELU as the reference computes it in fp32 (torch's exact GELU): 0.5 x (1 + erf(x / sqrt 2)),
+// so past x ~ -5.5 it is 0 there as here
 OASIS_DEV float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
 
 OASIS_DEV float silu(float x) { return x / (1.0f + __expf(-x)); }

@@ -81,6 +81,31 @@ def test_gemm_bf16_epilogues(kind):
     assert_close(out, ref, 0.99999, 1e-2, "gemm epilogue " + kind)
 
 
+@pytest.mark.parametrize("tile", [-1, 5])
+def test_gelu_erf_epilogue_values(tile):
+    """The erf-GELU epilogue on chosen inputs (an identity weight passes A through, K = 256): over
+    [-12, 12] every output within one bf16 step of torch's exact GELU in fp32 (the reference's),
+    or within 1e-6 where that is below 1e-4 (its negative tail: 0 past x ~ -5.5), and at most 2%
+    of the others not torch's value rounded to bf16; on the default tile and the large-token tile (the
+    compile-time GELU_ERF epilogue of the VAE's FC1)."""
+    M, K = 320, 256
+    x = torch.linspace(-12.0, 12.0, M * K).reshape(M, K).to(torch.bfloat16)
+    B = torch.eye(K).to(torch.bfloat16)
+    out = torch.zeros(M, K, device="cuda", dtype=torch.bfloat16)
+    e = _epi(kind=L.EPI_GELU_ERF, out_bf16=out, ld_out=K)
+    L.call("oasis_gemm_bf16_config", L.ptr(dev(x)), K, L.ptr(dev(B)), K, M, K, K, ctypes.byref(e), tile, 1, stream())
+    sync()
+    ref = torch.nn.functional.gelu(x.float()).double()
+    got = out.cpu().double()
+    tol = torch.where(ref.abs() < 1e-4, torch.full_like(ref, 1e-6), ref.abs() * 2.0 ** -7)
+    assert ((got - ref).abs() <= tol).all(), ((got - ref).abs() / tol).max()
+    body = ref.abs() >= 1e-4
+    off = (got != ref.to(torch.bfloat16).double())[body].double().mean().item()
+    print("gelu_erf tile %d: %.5f of outputs (|GELU| >= 1e-4) not torch's GELU rounded to bf16" % (tile, off),
+          flush=True)
+    assert off <= 0.02, off
+
+
 def test_gemm_gated_and_plain_residual():
     M, N, K, P = 288, 1024, 4096, 144
     g = _gen(4)
